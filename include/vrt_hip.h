@@ -1,0 +1,214 @@
+/*
+ * vrt_hip.h -- C ABI of the MI355X (gfx950) HIP implementation of Vortex-RT's Gemma 3
+ * Q8_0 token loop. Plain pointers and sizes only; every function returns VRT_OK (0) or a
+ * nonzero status whose message is available from vrt_last_error() on the calling thread.
+ *
+ * Each declaration names the reference interface it replaces. The reference exposes a
+ * C++ class API (namespace vortexrt) over Vulkan; the headers under include/vortexrt keep that C++
+ * surface and is implemented on top of these functions (libvortexrt.so).
+ *
+ * Conventions
+ *  - Device pointers come from vrt_alloc (or any HIP allocation on the context's device).
+ *  - Kernel entry points are stream-ordered on the context's single stream; vrt_sync()
+ *    gives the reference's synchronous semantics (every reference run* call blocks on a
+ *    fence, src/q8_matvec.cpp:1321-1350). vrt_memcpy is synchronous.
+ *  - Argument validation mirrors the reference's and happens on the host before any
+ *    launch, so an invalid call never reaches the GPU.
+ *  - A context or executor handle must not be used from two threads at once.
+ */
+#ifndef VRT_HIP_H
+#define VRT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VRT_OK 0
+#define VRT_ERR_INVALID 1   /* argument check failed (the reference throws std::runtime_error) */
+#define VRT_ERR_HIP 2       /* HIP runtime error */
+#define VRT_ERR_STATE 3     /* executor state: non-contiguous position, context exceeded, ... */
+#define VRT_ERR_NUMERIC 4   /* non-finite hidden state, softmax failure, invalid argmax */
+
+typedef struct vrt_ctx vrt_ctx;
+typedef struct vrt_g3 vrt_g3;
+
+/* include/vortexrt/argmax.hpp:12-17 (ArgmaxResult, 8 bytes). */
+typedef struct vrt_argmax_result {
+    uint32_t index;
+    float value;
+} vrt_argmax_result;
+
+/* include/vortexrt/vulkan_context.hpp:13-32 (DeviceCapabilities), HIP fields. */
+typedef struct vrt_device_info {
+    char name[256];
+    char arch[64];
+    uint32_t device_index;
+    uint32_t vendor_id;
+    uint32_t device_id;
+    uint32_t subgroup_size;       /* wavefront size: 64 */
+    uint32_t compute_units;
+    uint32_t fp16, int8, storage8, storage16;
+    uint64_t device_local_bytes;
+    uint64_t l2_bytes;
+} vrt_device_info;
+
+/* Thread-local message of the last failing call on this thread. */
+const char* vrt_last_error(void);
+
+/* ---- context and memory ------------------------------------------------------------ */
+
+/* VulkanContext(std::string device_selector), include/vortexrt/vulkan_context.hpp:45 and
+ * src/vulkan_context.cpp:116-317: selector is "" (then env VORTEXRT_DEVICE, then device 0),
+ * a decimal index, or a case-insensitive substring of the device name. */
+int vrt_ctx_create(const char* selector, vrt_ctx** out);
+int vrt_ctx_destroy(vrt_ctx* ctx);
+/* VulkanContext::capabilities(), include/vortexrt/vulkan_context.hpp:56. */
+int vrt_ctx_info(const vrt_ctx* ctx, vrt_device_info* out);
+
+#define VRT_MEM_DEVICE 0      /* VK_MEMORY_PROPERTY_DEVICE_LOCAL_BIT -> hipMalloc */
+#define VRT_MEM_HOST 1        /* HOST_VISIBLE | HOST_COHERENT -> pinned hipHostMalloc */
+
+/* Buffer(ctx, size, usage, memory_properties), include/vortexrt/buffer.hpp:13-17. The
+ * allocation is zero-filled and rounded up to 256 bytes plus 256 bytes of slack. */
+int vrt_alloc(vrt_ctx* ctx, uint64_t bytes, uint32_t kind, void** out);
+int vrt_free(vrt_ctx* ctx, void* ptr);
+/* Buffer::upload / Buffer::download, include/vortexrt/buffer.hpp:32-33: synchronous copy
+ * between any two addresses (host or device). */
+int vrt_memcpy(vrt_ctx* ctx, void* dst, const void* src, uint64_t bytes);
+int vrt_memset(vrt_ctx* ctx, void* dst, int value, uint64_t bytes);
+/* Waits for all work on the context's stream (the reference's vkWaitForFences). */
+int vrt_sync(vrt_ctx* ctx);
+/* The hipStream_t every kernel of this context is launched on. */
+int vrt_stream(vrt_ctx* ctx, void** stream);
+
+/* Timing on the context's stream (hipEvent pairs). */
+int vrt_event_create(vrt_ctx* ctx, void** ev);
+int vrt_event_record(vrt_ctx* ctx, void* ev);
+int vrt_event_elapsed_ms(void* start, void* stop, float* ms);
+int vrt_event_destroy(void* ev);
+
+/* ---- Q8_0 kernels ------------------------------------------------------------------- */
+/* Weights are GGUF Q8_0: rows of input_dim/32 blocks of 34 bytes {f16 scale LE, int8[32]}.
+ * weight_byte_offset must be 4-byte aligned and input_dim a nonzero multiple of 32
+ * (src/q8_matvec.cpp:801-820). weights_bytes is the readable size at `weights`. */
+
+/* Q8MatVecPipeline::run, include/vortexrt/q8_matvec.hpp:35-41: y = W x. */
+int vrt_q8_matvec(vrt_ctx* ctx, const void* weights, uint64_t weights_bytes, uint32_t weight_byte_offset,
+                  const float* x, float* y, uint32_t input_dim, uint32_t output_dim);
+
+/* Q8MatVecPipeline::run_staged_pair / run_staged_triplet, include/vortexrt/q8_matvec.hpp:
+ * 74-100: n (1..8) matrices sharing x, outputs packed contiguously in call order. */
+int vrt_q8_matvec_multi(vrt_ctx* ctx, const void* weights, uint64_t weights_bytes, uint32_t n,
+                        const uint32_t* weight_byte_offsets, const uint32_t* output_dims,
+                        uint32_t input_dim, const float* x, float* y_packed);
+
+/* Q8MatVecPipeline::run_staged_ffn, include/vortexrt/q8_matvec.hpp:57-72 and
+ * src/q8_matvec.cpp:1360-2004: gate = Wg x, up = Wu x, h = gelu_tanh(gate) * up,
+ * y = Wd h. workspace holds [gate | up] (2 * ffn_dim floats); gate ends up holding h
+ * as in the reference's workspace. */
+int vrt_q8_ffn(vrt_ctx* ctx, const void* weights, uint64_t weights_bytes,
+               uint32_t gate_offset, uint32_t up_offset, uint32_t down_offset,
+               uint32_t input_dim, uint32_t ffn_dim, uint32_t output_dim,
+               const float* x, float* workspace, uint64_t workspace_bytes, float* y);
+
+/* shaders/gelu_mul.comp: gate[i] = gelu_tanh(gate[i]) * up[i]. */
+int vrt_gelu_mul(vrt_ctx* ctx, float* gate, const float* up, uint32_t n);
+
+/* ArgmaxPipeline::run, include/vortexrt/argmax.hpp:29-32 and shaders/argmax.comp:
+ * NaN never wins, larger wins, equal values -> lower index. out is device-visible. */
+int vrt_argmax(vrt_ctx* ctx, const float* x, uint32_t n, vrt_argmax_result* out);
+
+/* Quantiser of record (src/q8_test_main.cpp:18-131; variant 1 = src/ffn_test_main.cpp:
+ * 112-215) on the GPU, bit-exact: n floats (multiple of 32) -> n/32 blocks. */
+int vrt_q8_quantize(vrt_ctx* ctx, const float* x, uint64_t n, uint32_t variant, void* out_blocks);
+
+/* GgufFile::read_q8_0_row dequant (src/gguf.cpp:620-635) on the GPU: n_blocks -> floats. */
+int vrt_q8_dequantize(vrt_ctx* ctx, const void* blocks, uint64_t n_blocks, float* out);
+
+/* ---- Gemma 3 executor --------------------------------------------------------------- */
+
+/* Gemma3Config, include/vortexrt/gemma3.hpp:19-33. */
+typedef struct vrt_g3_config {
+    uint32_t context_length;
+    uint32_t embedding_length;
+    uint32_t block_count;
+    uint32_t feed_forward_length;
+    uint32_t head_count;
+    uint32_t head_count_kv;
+    uint32_t head_dim;
+    uint32_t value_dim;
+    uint32_t vocab_size;
+    uint32_t sliding_window;
+    float rms_epsilon;
+    float global_rope_base;
+    float local_rope_base;
+} vrt_g3_config;
+
+/* Per-block tensors (src/gemma3.cpp:456-505): Q8_0 byte offsets into the arena and host
+ * pointers to the F32 norm weights (copied to the device by vrt_g3_create). */
+typedef struct vrt_g3_layer {
+    uint64_t attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down;
+    const float* attn_norm;             /* [embedding_length] */
+    const float* attn_q_norm;           /* [head_dim] */
+    const float* attn_k_norm;           /* [head_dim] */
+    const float* post_attention_norm;   /* [embedding_length] */
+    const float* ffn_norm;              /* [embedding_length] */
+    const float* post_ffw_norm;         /* [embedding_length] */
+} vrt_g3_layer;
+
+typedef struct vrt_g3_desc {
+    vrt_g3_config config;
+    const void* arena;          /* device copy of the GGUF tensor-data section (caller-owned) */
+    uint64_t arena_bytes;
+    uint64_t token_embd;        /* byte offset of token_embd.weight (tied LM head) */
+    const float* output_norm;   /* host [embedding_length] */
+    const vrt_g3_layer* layers; /* [block_count] */
+    uint32_t eos_token_id;      /* tokenizer.ggml.eos_token_id (src/gemma3.cpp:443-446) */
+} vrt_g3_desc;
+
+/* Device half of the Gemma3Model constructor (src/gemma3.cpp:510-654): KV cache, RoPE
+ * tables (src/gemma3.cpp:1309-1369 evaluated on the host), norm weights, workspaces and
+ * the captured decode-step graph. Shapes are validated as the reference does
+ * (src/gemma3.cpp:219-257). */
+int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out);
+int vrt_g3_destroy(vrt_g3* g3);
+
+/* Gemma3Model::reset_cache, src/gemma3.cpp:1454-1460. */
+int vrt_g3_reset(vrt_g3* g3);
+
+/* Gemma3Model::decode_token, src/gemma3.cpp:1462-1882. top_k == 0 skips the LM head;
+ * top_k >= 1 runs the tied LM head fused with greedy argmax (result in *out); top_k > 1
+ * also keeps the logits for vrt_g3_logits. hidden_out (embedding_length floats, host) may
+ * be NULL. On any error the KV cache is reset, as in the reference. */
+int vrt_g3_decode(vrt_g3* g3, uint32_t token, uint32_t position, uint32_t top_k,
+                  vrt_argmax_result* out, float* hidden_out);
+
+/* Logits of the last step that ran the LM head with top_k > 1 (host copy, n floats). */
+int vrt_g3_logits(vrt_g3* g3, float* host_logits, uint32_t n);
+
+/* Gemma3Model::generate_greedy_tokens, src/gemma3.cpp:2080-2149: the whole loop runs on
+ * the device (graph replays, the next token chosen on the device) with one host sync.
+ * out_tokens holds up to max_new ids; generation stops after EOS as in the reference. */
+int vrt_g3_generate(vrt_g3* g3, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                    uint32_t* out_tokens, uint32_t* n_out);
+
+/* Teacher-forced run (validation): resets, then step i consumes tokens[i] at position i;
+ * steps i >= first_logit_step run the LM head and record their greedy result in out[i]. */
+int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first_logit_step,
+                  vrt_argmax_result* out);
+
+/* Executor options. */
+#define VRT_G3_OPT_USE_GRAPH 1      /* 1 (default): replay the captured step graph */
+int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
+
+/* Launches the tied LM head + argmax kernel `iters` times back to back between two
+ * hipEvents on the context stream (current hidden state) and reports the mean duration. */
+int vrt_g3_time_lm_head(vrt_g3* g3, uint32_t iters, float* mean_us);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

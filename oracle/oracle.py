@@ -1,0 +1,235 @@
+"""ctypes loader for the CPU oracle (oracle/_build/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, never by the product path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+
+def build(force: bool = False) -> str:
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE] + (["-B"] if force else []), check=True)
+    return LIB_PATH
+
+
+class G3Info(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "context_length", "embedding_length", "block_count", "feed_forward_length", "head_count",
+        "head_count_kv", "head_dim", "value_dim", "vocab_size", "sliding_window")] + \
+        [("rms_epsilon", C.c_float), ("global_rope_base", C.c_float), ("local_rope_base", C.c_float),
+         ("eos_id", C.c_uint32), ("bos_id", C.c_uint32)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        P, F, U32, U64, I = C.c_void_p, C.c_float, C.c_uint32, C.c_uint64, C.c_int
+        sig = {
+            "or_f32_to_f16": (C.c_uint16, [F]),
+            "or_f16_to_f32": (F, [C.c_uint16]),
+            "or_q8_quantize_a": (None, [P, U64, U32, P]),
+            "or_q8_quantize_b": (None, [P, U64, U32, P]),
+            "or_q8_dequant": (None, [P, U64, P]),
+            "or_q8_matvec_lanes": (None, [P, P, P, U32, U64, U32]),
+            "or_q8_matvec_f64": (None, [P, P, P, U32, U64]),
+            "or_gelu_tanh": (F, [F]),
+            "or_gelu_mul": (None, [P, P, U32]),
+            "or_argmax": (None, [P, U64, P, P]),
+            "or_rms_norm_into": (None, [P, P, P, U32, F]),
+            "or_rms_norm_inplace": (None, [P, P, U32, F]),
+            "or_rms_norm_heads": (None, [P, P, U32, U32, F]),
+            "or_rope_inv_freq": (None, [U32, F, P]),
+            "or_rope_table": (None, [P, U32, U32, P, P]),
+            "or_apply_rope": (None, [P, U32, U32, P, P]),
+            "or_attention": (I, [P, P, P, U32, U32, U32, F, P]),
+            "or_g3_open": (P, [C.c_char_p, U32, C.c_char_p, C.c_size_t]),
+            "or_g3_close": (None, [P]),
+            "or_g3_get_info": (None, [P, P]),
+            "or_g3_reset": (None, [P]),
+            "or_g3_decode": (I, [P, U32, U32, I, P, P, P, P]),
+            "or_g3_generate": (I, [P, P, U32, U32, P, P]),
+            "or_g3_error": (C.c_char_p, [P]),
+            "or_num_threads": (I, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def f32_to_f16(x: float) -> int:
+    return int(lib().or_f32_to_f16(C.c_float(x)))
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().or_f16_to_f32(C.c_uint16(h)))
+
+
+def quantize(w: np.ndarray, variant: str = "a") -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    out = np.empty(w.size // 32 * 34, dtype=np.uint8)
+    fn = lib().or_q8_quantize_a if variant == "a" else lib().or_q8_quantize_b
+    fn(_p(w), w.size // 32, 32, _p(out))
+    return out
+
+
+def dequant(blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(blocks.size // 34 * 32, dtype=np.float32)
+    lib().or_q8_dequant(_p(blocks), blocks.size // 34, _p(out))
+    return out
+
+
+def matvec_lanes(w: np.ndarray, x: np.ndarray, rows: int, lanes: int = 8) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    lib().or_q8_matvec_lanes(_p(w), _p(x), _p(y), x.size, rows, lanes)
+    return y
+
+
+def matvec_f64(w: np.ndarray, x: np.ndarray, rows: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float64)
+    lib().or_q8_matvec_f64(_p(w), _p(x), _p(y), x.size, rows)
+    return y
+
+
+def gelu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.array(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    lib().or_gelu_mul(_p(g), _p(u), g.size)
+    return g
+
+
+def argmax(v: np.ndarray):
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    i, val = C.c_uint32(), C.c_float()
+    lib().or_argmax(_p(v), v.size, C.byref(i), C.byref(val))
+    return int(i.value), float(val.value)
+
+
+def rms_norm_into(x, w, eps=1e-6):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_rms_norm_into(_p(x), _p(w), _p(out), x.size, C.c_float(eps))
+    return out
+
+
+def rms_norm_inplace(x, w, eps=1e-6):
+    v = np.array(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    lib().or_rms_norm_inplace(_p(v), _p(w), v.size, C.c_float(eps))
+    return v
+
+
+def rms_norm_heads(x, w, heads, eps=1e-6):
+    v = np.array(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    lib().or_rms_norm_heads(_p(v), _p(w), heads, w.size, C.c_float(eps))
+    return v
+
+
+def rope_inv_freq(head_dim, theta):
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    lib().or_rope_inv_freq(head_dim, C.c_float(theta), _p(out))
+    return out
+
+
+def rope_table(inv, pos):
+    inv = np.ascontiguousarray(inv, dtype=np.float32)
+    c = np.empty_like(inv)
+    s = np.empty_like(inv)
+    lib().or_rope_table(_p(inv), inv.size, pos, _p(c), _p(s))
+    return c, s
+
+
+def apply_rope(x, heads, head_dim, c, s):
+    v = np.array(x, dtype=np.float32)
+    c = np.ascontiguousarray(c, dtype=np.float32)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    lib().or_apply_rope(_p(v), heads, head_dim, _p(c), _p(s))
+    return v
+
+
+def attention(q, keys, values, heads, head_dim, scale):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    keys = np.ascontiguousarray(keys, dtype=np.float32)
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(heads * head_dim, dtype=np.float32)
+    rc = lib().or_attention(_p(q), _p(keys), _p(values), keys.shape[0], heads, head_dim, C.c_float(scale), _p(out))
+    if rc:
+        raise RuntimeError("Gemma 3 attention softmax failed")
+    return out
+
+
+class Model:
+    """The whole-model oracle (src/gemma3.cpp executor restated) over a GGUF file."""
+
+    def __init__(self, path: str, lanes: int = 8):
+        err = C.create_string_buffer(512)
+        self.h = lib().or_g3_open(str(path).encode(), lanes, err, 512)
+        if not self.h:
+            raise RuntimeError(err.value.decode())
+        info = G3Info()
+        lib().or_g3_get_info(self.h, C.byref(info))
+        self.info = info
+
+    def close(self):
+        if self.h:
+            lib().or_g3_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def reset(self):
+        lib().or_g3_reset(self.h)
+
+    def decode(self, token: int, pos: int, want_logits: bool = True, logits: bool = False):
+        d = self.info.embedding_length
+        hidden = np.empty(d, dtype=np.float32)
+        lg = np.empty(self.info.vocab_size, dtype=np.float32) if logits else None
+        ai, av = C.c_uint32(), C.c_float()
+        rc = lib().or_g3_decode(self.h, token, pos, 1 if want_logits else 0, _p(hidden),
+                                _p(lg) if lg is not None else None, C.byref(ai), C.byref(av))
+        if rc:
+            raise RuntimeError(lib().or_g3_error(self.h).decode())
+        return dict(hidden=hidden, logits=lg, index=int(ai.value) if want_logits else None,
+                    value=float(av.value) if want_logits else None)
+
+    def generate(self, prompt, max_new: int):
+        pr = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max(max_new, 1), dtype=np.uint32)
+        n = C.c_uint32()
+        rc = lib().or_g3_generate(self.h, _p(pr), pr.size, max_new, _p(out), C.byref(n))
+        if rc:
+            raise RuntimeError(lib().or_g3_error(self.h).decode())
+        return out[: n.value].copy()
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())

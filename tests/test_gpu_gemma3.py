@@ -1,0 +1,143 @@
+"""GPU parity of the Gemma 3 executor (vrt_g3_*) against the CPU oracle's restatement of
+src/gemma3.cpp.
+
+Bars: teacher-forced greedy tokens identical; logits within 1e-3 of max|logit| (the relative
+tolerance the workload states for fp32 logits); final hidden within 1e-4 of max|hidden|;
+graph replay bit-identical to eager launches.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import synth
+import vrt
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+HIDDEN_TOL = 1e-4
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a.astype(np.float64) - b.astype(np.float64))) / max(np.max(np.abs(b)), 1e-30))
+
+
+def _oracle_forced(path, tokens, first_logit):
+    m = oracle.Model(path)
+    out = []
+    for i, t in enumerate(tokens):
+        r = m.decode(int(t), i, want_logits=i >= first_logit, logits=i >= first_logit)
+        out.append(r)
+    m.close()
+    return out
+
+
+def _top2_gap(logits):
+    s = np.sort(logits)
+    return float(s[-1] - s[-2])
+
+
+@pytest.fixture(scope="module")
+def tiny_g3(ctx, tiny_model):
+    g = vrt.Gemma3(ctx, tiny_model)
+    yield g
+    g.close()
+
+
+def test_tiny_teacher_forced_tokens_and_logits(ctx, tiny_model, tiny_g3):
+    """40 positions with window 8: local layers evict, the global layer (block 5) keeps all."""
+    toks = synth.uniform_ids(21, 40, 2, 1000)
+    print(f"[g3] tiny forced n={toks.size}", flush=True)
+    got = tiny_g3.forced(toks, 0)
+    ref = _oracle_forced(tiny_model, toks, 0)
+    for i, r in enumerate(ref):
+        assert got["index"][i] == r["index"], f"step {i}: gpu {got['index'][i]} oracle {r['index']} gap {_top2_gap(r['logits'])}"
+    # logits through the decode_token path (top_k > 1 keeps them)
+    tiny_g3.reset()
+    for i, t in enumerate(toks[:12]):
+        (idx, val), hid = tiny_g3.decode(int(t), i, top_k=8, hidden=True)
+        lg = tiny_g3.logits()
+        assert _rel(lg, ref[i]["logits"]) <= LOGIT_TOL
+        assert _rel(hid, ref[i]["hidden"]) <= HIDDEN_TOL
+        assert idx == ref[i]["index"]
+
+
+def test_tiny_generate_matches_oracle(ctx, tiny_model, tiny_g3):
+    prompt = synth.uniform_ids(5, 5, 2, 1000)
+    got = tiny_g3.generate(prompt, 30)
+    m = oracle.Model(tiny_model)
+    ref = m.generate(prompt, 30)
+    m.close()
+    assert np.array_equal(got, ref)
+
+
+def test_graph_replay_equals_eager(ctx, tiny_g3):
+    toks = synth.uniform_ids(8, 20, 2, 1000)
+    tiny_g3.set_graph(True)
+    a = tiny_g3.forced(toks, 0)
+    tiny_g3.set_graph(False)
+    b = tiny_g3.forced(toks, 0)
+    tiny_g3.set_graph(True)
+    c = tiny_g3.forced(toks, 0)
+    assert np.array_equal(a["index"], b["index"]) and np.array_equal(a["value"].view(np.uint32), b["value"].view(np.uint32))
+    assert np.array_equal(a["value"].view(np.uint32), c["value"].view(np.uint32))
+
+
+def test_no_window_keeps_full_history(ctx, tiny_model_nowindow):
+    g = vrt.Gemma3(ctx, tiny_model_nowindow)
+    toks = synth.uniform_ids(31, 24, 2, 1000)
+    got = g.forced(toks, 4)
+    ref = _oracle_forced(tiny_model_nowindow, toks, 4)
+    g.close()
+    for i in range(4, toks.size):
+        assert got["index"][i] == ref[i]["index"]
+
+
+def test_decode_errors_reset(ctx, tiny_g3):
+    tiny_g3.reset()
+    tiny_g3.decode(5, 0, top_k=1)
+    with pytest.raises(vrt.VrtError, match="contiguous"):
+        tiny_g3.decode(5, 2, top_k=1)
+    with pytest.raises(vrt.VrtError, match="vocabulary"):
+        tiny_g3.decode(1000, 1, top_k=1)
+    # the vocabulary error reset the cache: position 0 is next again
+    tiny_g3.decode(5, 0, top_k=0)
+    with pytest.raises(vrt.VrtError, match="context length"):
+        tiny_g3.generate(np.arange(2, 200, dtype=np.uint32), 100)
+
+
+@pytest.fixture(scope="module")
+def full_model(model_dir):
+    path = os.path.join(str(model_dir), "gemma3_270m_seed0.gguf")
+    if not os.path.exists(path):
+        print("[g3] writing Gemma-3-270M-shape model", flush=True)
+        synth.write_gemma3_gguf(path, seed=0, **synth.GEMMA3_270M)
+    return path
+
+
+def test_full_shape_greedy_and_logits(ctx, full_model):
+    """Config 2 shapes: 8-token prompt, greedy continuation compared token by token and the
+    last step's logits within 1e-3."""
+    g = vrt.Gemma3(ctx, full_model)
+    prompt = synth.uniform_ids(0, 8, 2, 262144)
+    n_new = 12
+    print("[g3] full-shape generate", flush=True)
+    got = g.generate(prompt, n_new)
+    m = oracle.Model(full_model)
+    ref = m.generate(prompt, n_new)
+    assert np.array_equal(got, ref), f"gpu {got} oracle {ref}"
+    # teacher-forced logits at the last position
+    seq = np.concatenate([prompt, ref[:-1]]).astype(np.uint32)
+    m.reset()
+    g.reset()
+    for i, t in enumerate(seq):
+        last = i == seq.size - 1
+        r = m.decode(int(t), i, want_logits=last, logits=last)
+        (idx, _), hid = g.decode(int(t), i, top_k=8 if last else 0, hidden=True)
+        assert _rel(hid, r["hidden"]) <= HIDDEN_TOL
+    assert _rel(g.logits(), r["logits"]) <= LOGIT_TOL
+    assert idx == r["index"]
+    m.close()
+    g.close()

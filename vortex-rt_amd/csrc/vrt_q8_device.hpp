@@ -1,0 +1,295 @@
+// vrt_q8_device.hpp -- gfx950 device primitives for Q8_0 matrix-vector work.
+//
+// Q8_0 (GGUF type 8): 34-byte blocks {f16 scale little-endian, int8 q[32]} along K, rows
+// contiguous. y[r] = sum_b f16(s_rb) * sum_k q_rbk * x[32b + k]   (shaders/q8_matvec*.comp).
+//
+// Activation limbs. Every 32-element block j of x is rewritten once per launch as
+//     x_k ~= s_j * (a_k + b_k / 254 + c_k / 254^2),   s_j = amax_j / 127,  a, b, c int8,
+// with |error| <= s_j * 0.5 / 254^2 = amax_j * 6.1e-8 (fp32 resolution). The block dot then
+// runs on the integer dot unit: A = sum q*a, B = sum q*b, C = sum q*c via v_dot4_i32_i8
+// (exact int32), and y_block = d_w * s_j * (A + B/254 + C/254^2) in fp32. That is 24 dot4 +
+// 8 byte-realigns per 34-byte block instead of 32 int->float converts and 32 FMAs, which
+// keeps the streaming kernels under the VALU ceiling at full HBM rate.
+//
+// Lane layout. A wave is split into 64/S row slots of S lanes; slot lane t owns blocks
+// t, t+S, ... (NB of them) for the whole launch, so its limbs live in registers. Every
+// lane reads its block with nine aligned dword loads (plus the 2-byte scale); neighbouring
+// lanes read neighbouring blocks, so a slot streams its row contiguously.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vrt {
+
+constexpr int kWave = 64;
+
+// ---- cross-lane reductions -------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float swz_xor16(float v) {
+    // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10 (within 32 lanes).
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+
+// Sum over each aligned group of S lanes (S a power of two <= 64). Every lane of a group
+// ends with the group total (S <= 32); for S == 64 lanes 0..31 and 32..63 each hold
+// half sums, so use wave_sum for a full-wave total.
+template <int S>
+__device__ __forceinline__ float slot_sum(float v) {
+    if constexpr (S >= 2) v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    if constexpr (S >= 4) v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    if constexpr (S >= 8) v += dpp_mov<0x141>(v);   // row_half_mirror
+    if constexpr (S >= 16) v += dpp_mov<0x140>(v);  // row_mirror
+    if constexpr (S >= 32) v += swz_xor16(v);
+    return v;
+}
+
+// Full-wave sum, wave-uniform result.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = slot_sum<32>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+// ---- argmax rule (shaders/argmax.comp:30-43) --------------------------------------------
+
+__device__ __forceinline__ bool am_better(float cv, uint32_t ci, float bv, uint32_t bi) {
+    if (__builtin_isnan(cv)) return false;
+    return cv > bv || (cv == bv && ci < bi);
+}
+
+// Wave-wide argmax under am_better; result valid in every lane.
+__device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off);
+        const uint32_t oi = __shfl_xor(i, off);
+        if (am_better(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+}
+
+// ---- f16 -------------------------------------------------------------------------------
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);   // v_cvt_f32_f16, exact
+}
+
+// ---- Q8_0 block loads ------------------------------------------------------------------
+
+struct Q8Raw {
+    uint32_t d[9];   // dwords covering the 32 quants, starting at (block + 2) & ~3
+    uint32_t sbits;  // f16 scale bits
+    uint32_t sh;     // byte shift of the quants inside d: 0 or 2
+};
+
+// blk: start of a 34-byte block (2-byte aligned); end: one past the last readable byte.
+// Reads stay inside [blk, blk + 34) except for up to 2 bytes past the block, which are
+// read only when they lie before `end`.
+__device__ __forceinline__ void q8_load(const uint8_t* blk, const uint8_t* end, Q8Raw& r) {
+    const uintptr_t q = reinterpret_cast<uintptr_t>(blk) + 2u;
+    const uint32_t* lb = reinterpret_cast<const uint32_t*>(q & ~uintptr_t(3));
+    r.sh = static_cast<uint32_t>(q & 3u);
+    r.sbits = *reinterpret_cast<const uint16_t*>(blk);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r.d[j] = __builtin_nontemporal_load(lb + j);
+    r.d[8] = 0u;
+    if (r.sh) {
+        const uint8_t* tail = reinterpret_cast<const uint8_t*>(lb + 8);
+        r.d[8] = (tail + 4 <= end) ? __builtin_nontemporal_load(lb + 8)
+                                   : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tail));
+    }
+}
+
+// ---- activation limbs --------------------------------------------------------------------
+
+struct XLimb {
+    int a[8], b[8], c[8];   // 32 int8 each, packed 4 per dword in k order
+    float s;                // block scale: amax/127; 0 for an all-zero block; NaN if non-finite
+};
+
+// LDS image of the limbs for a K-vector: la/lb/lc int8[K], ls float[K/32].
+struct LimbLds {
+    int8_t* a;
+    int8_t* b;
+    int8_t* c;
+    float* s;
+};
+
+// Cooperative limb build for xs[0..K) (LDS) by all threads of the block. Each wave covers
+// two 32-element blocks per pass (one lane per element). Ends with __syncthreads().
+__device__ __forceinline__ void build_limbs(const float* xs, uint32_t K, LimbLds L) {
+    const uint32_t nblk = K >> 5;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t nwaves = blockDim.x >> 6;
+    for (uint32_t pair = wave; pair * 2u < nblk; pair += nwaves) {
+        const uint32_t blk = pair * 2u + (lane >> 5);
+        const bool live = blk < nblk;
+        const float v = live ? xs[blk * 32u + (lane & 31u)] : 0.0f;
+        // block amax and a non-finite flag over the 32 lanes of this half-wave
+        float m = fabsf(v);
+        float bad = __builtin_isfinite(v) ? 0.0f : 1.0f;
+        for (int off = 16; off > 0; off >>= 1) {
+            m = fmaxf(m, __shfl_xor(m, off));
+            bad = fmaxf(bad, __shfl_xor(bad, off));
+        }
+        int8_t qa = 0, qb = 0, qc = 0;
+        float s = 0.0f;
+        if (bad != 0.0f) {
+            s = __builtin_nanf("");
+        } else if (m >= 1e-30f) {
+            s = m * (1.0f / 127.0f);
+            const float inv = 127.0f / m;
+            const float r = v * inv;
+            const float a = rintf(r);
+            const float e1 = (r - a) * 254.0f;
+            const float b = fminf(fmaxf(rintf(e1), -127.0f), 127.0f);
+            const float e2 = (e1 - b) * 254.0f;
+            const float c = fminf(fmaxf(rintf(e2), -127.0f), 127.0f);
+            qa = static_cast<int8_t>(fminf(fmaxf(a, -127.0f), 127.0f));
+            qb = static_cast<int8_t>(b);
+            qc = static_cast<int8_t>(c);
+        }
+        if (live) {
+            const uint32_t k = blk * 32u + (lane & 31u);
+            L.a[k] = qa;
+            L.b[k] = qb;
+            L.c[k] = qc;
+            if ((lane & 31u) == 0u) L.s[blk] = s;
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void load_limb(const LimbLds& L, uint32_t blk, XLimb& x) {
+    const int* pa = reinterpret_cast<const int*>(L.a + blk * 32u);
+    const int* pb = reinterpret_cast<const int*>(L.b + blk * 32u);
+    const int* pc = reinterpret_cast<const int*>(L.c + blk * 32u);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { x.a[j] = pa[j]; x.b[j] = pb[j]; x.c[j] = pc[j]; }
+    x.s = L.s[blk];
+}
+
+// One block's contribution: d_w * s_x * (A + B/254 + C/254^2).
+__device__ __forceinline__ float q8_dot(const Q8Raw& r, const XLimb& x) {
+    int A = 0, B = 0, Cc = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = static_cast<int>(__builtin_amdgcn_alignbyte(r.d[j + 1], r.d[j], r.sh));
+        A = __builtin_amdgcn_sdot4(q, x.a[j], A, false);
+        B = __builtin_amdgcn_sdot4(q, x.b[j], B, false);
+        Cc = __builtin_amdgcn_sdot4(q, x.c[j], Cc, false);
+    }
+    const float t = fmaf(static_cast<float>(Cc), 1.0f / 64516.0f,
+                         fmaf(static_cast<float>(B), 1.0f / 254.0f, static_cast<float>(A)));
+    return half_bits_to_float(r.sbits) * x.s * t;
+}
+
+// ---- row streaming ----------------------------------------------------------------------
+
+// A virtual row space over up to kMaxSeg Q8_0 matrices sharing K. Either the segments are
+// concatenated (rows of segment 0, then 1, ...) or, with `interleave`, virtual row v is
+// row v>>1 of segment v&1 (gate/up pairs).
+constexpr int kMaxSeg = 8;
+
+struct RowSpace {
+    const uint8_t* base[kMaxSeg];
+    uint32_t rows[kMaxSeg];
+    uint32_t first[kMaxSeg];   // first virtual row of each segment (concatenated mode)
+    uint32_t nseg;
+    uint32_t total;
+    uint32_t interleave;
+};
+
+__device__ __forceinline__ const uint8_t* row_ptr(const RowSpace& rs, uint32_t v, uint64_t row_bytes,
+                                                  uint32_t& seg, uint32_t& local) {
+    // Unrolled compare-select over the segment table keeps RowSpace in registers.
+    const uint8_t* base;
+    if (rs.interleave) {
+        seg = v & 1u;
+        local = v >> 1;
+        base = seg ? rs.base[1] : rs.base[0];
+    } else {
+        seg = 0;
+        base = rs.base[0];
+        uint32_t first = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxSeg; ++i) {
+            if (static_cast<uint32_t>(i) < rs.nseg && v >= rs.first[i]) {
+                seg = static_cast<uint32_t>(i);
+                base = rs.base[i];
+                first = rs.first[i];
+            }
+        }
+        local = v - first;
+    }
+    return base + static_cast<uint64_t>(local) * row_bytes;
+}
+
+// Streams virtual rows [v_begin, v_end) with the calling wave: row groups of 64/S rows,
+// wave w of the block takes groups w, w + nwaves, ... and keeps U groups in flight.
+// sink(v, value) is called on the lane that owns row v's total (slot lane 0).
+template <int S, int NB, int U, typename Sink>
+__device__ __forceinline__ void stream_rows(const RowSpace& rs, uint64_t row_bytes, uint32_t nblk,
+                                            const uint8_t* w_end, const XLimb (&xl)[NB],
+                                            uint32_t v_begin, uint32_t v_end, Sink&& sink) {
+    constexpr uint32_t RPW = 64u / S;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t slot = lane / S;
+    const uint32_t sl = lane % S;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t nwaves = blockDim.x >> 6;
+    const uint32_t ngroups = (v_end - v_begin + RPW - 1u) / RPW;
+    for (uint32_t g0 = wave; g0 < ngroups; g0 += U * nwaves) {
+        Q8Raw raw[U][NB];
+        uint32_t vrow[U];
+        bool live[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t g = g0 + static_cast<uint32_t>(u) * nwaves;
+            vrow[u] = v_begin + g * RPW + slot;
+            live[u] = g < ngroups && vrow[u] < v_end;
+            uint32_t seg, local;
+            const uint8_t* rp = live[u] ? row_ptr(rs, vrow[u], row_bytes, seg, local) : nullptr;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+                if (live[u] && b < nblk) q8_load(rp + 34u * b, w_end, raw[u][n]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+                if (live[u] && b < nblk) acc += q8_dot(raw[u][n], xl[n]);
+            }
+            float tot;
+            if constexpr (S == 64) {
+                const float h = slot_sum<32>(acc);
+                tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 0)) +
+                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 32));
+            } else {
+                tot = slot_sum<S>(acc);
+            }
+            if (live[u] && sl == 0u) sink(vrow[u], tot);
+        }
+    }
+}
+
+}  // namespace vrt

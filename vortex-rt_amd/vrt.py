@@ -1,0 +1,372 @@
+"""ctypes binding of libvrt_hip.so (include/vrt_hip.h) for tests and the bench.
+
+Loads the in-tree build (_build/libvrt_hip.so) and raises if it is missing: there is no
+fallback path. Device memory is owned by DeviceBuffer objects (vrt_alloc / vrt_free).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "_build", "libvrt_hip.so")
+
+VRT_OK, VRT_ERR_INVALID, VRT_ERR_HIP, VRT_ERR_STATE, VRT_ERR_NUMERIC = 0, 1, 2, 3, 4
+MEM_DEVICE, MEM_HOST = 0, 1
+OPT_USE_GRAPH = 1
+
+
+class VrtError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+class ArgmaxResult(C.Structure):
+    _fields_ = [("index", C.c_uint32), ("value", C.c_float)]
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64), ("device_index", C.c_uint32),
+                ("vendor_id", C.c_uint32), ("device_id", C.c_uint32), ("subgroup_size", C.c_uint32),
+                ("compute_units", C.c_uint32), ("fp16", C.c_uint32), ("int8", C.c_uint32),
+                ("storage8", C.c_uint32), ("storage16", C.c_uint32), ("device_local_bytes", C.c_uint64),
+                ("l2_bytes", C.c_uint64)]
+
+
+class G3Config(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "context_length", "embedding_length", "block_count", "feed_forward_length", "head_count",
+        "head_count_kv", "head_dim", "value_dim", "vocab_size", "sliding_window")] + \
+        [("rms_epsilon", C.c_float), ("global_rope_base", C.c_float), ("local_rope_base", C.c_float)]
+
+
+class G3Layer(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                                          "ffn_down")] + \
+        [(n, C.c_void_p) for n in ("attn_norm", "attn_q_norm", "attn_k_norm", "post_attention_norm", "ffn_norm",
+                                   "post_ffw_norm")]
+
+
+class G3Desc(C.Structure):
+    _fields_ = [("config", G3Config), ("arena", C.c_void_p), ("arena_bytes", C.c_uint64),
+                ("token_embd", C.c_uint64), ("output_norm", C.c_void_p), ("layers", C.POINTER(G3Layer)),
+                ("eos_token_id", C.c_uint32)]
+
+
+# Every symbol include/vrt_hip.h declares, with its ctypes signature.
+_P, _U32, _U64, _I, _F = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int, C.c_float
+SIGNATURES = {
+    "vrt_last_error": (C.c_char_p, []),
+    "vrt_ctx_create": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "vrt_ctx_destroy": (_I, [_P]),
+    "vrt_ctx_info": (_I, [_P, C.POINTER(DeviceInfo)]),
+    "vrt_alloc": (_I, [_P, _U64, _U32, C.POINTER(_P)]),
+    "vrt_free": (_I, [_P, _P]),
+    "vrt_memcpy": (_I, [_P, _P, _P, _U64]),
+    "vrt_memset": (_I, [_P, _P, _I, _U64]),
+    "vrt_sync": (_I, [_P]),
+    "vrt_stream": (_I, [_P, C.POINTER(_P)]),
+    "vrt_event_create": (_I, [_P, C.POINTER(_P)]),
+    "vrt_event_record": (_I, [_P, _P]),
+    "vrt_event_elapsed_ms": (_I, [_P, _P, C.POINTER(_F)]),
+    "vrt_event_destroy": (_I, [_P]),
+    "vrt_q8_matvec": (_I, [_P, _P, _U64, _U32, _P, _P, _U32, _U32]),
+    "vrt_q8_matvec_multi": (_I, [_P, _P, _U64, _U32, _P, _P, _U32, _P, _P]),
+    "vrt_q8_ffn": (_I, [_P, _P, _U64, _U32, _U32, _U32, _U32, _U32, _U32, _P, _P, _U64, _P]),
+    "vrt_gelu_mul": (_I, [_P, _P, _P, _U32]),
+    "vrt_argmax": (_I, [_P, _P, _U32, _P]),
+    "vrt_q8_quantize": (_I, [_P, _P, _U64, _U32, _P]),
+    "vrt_q8_dequantize": (_I, [_P, _P, _U64, _P]),
+    "vrt_g3_create": (_I, [_P, C.POINTER(G3Desc), C.POINTER(_P)]),
+    "vrt_g3_destroy": (_I, [_P]),
+    "vrt_g3_reset": (_I, [_P]),
+    "vrt_g3_decode": (_I, [_P, _U32, _U32, _U32, C.POINTER(ArgmaxResult), _P]),
+    "vrt_g3_logits": (_I, [_P, _P, _U32]),
+    "vrt_g3_generate": (_I, [_P, _P, _U32, _U32, _P, C.POINTER(_U32)]),
+    "vrt_g3_forced": (_I, [_P, _P, _U32, _U32, _P]),
+    "vrt_g3_set_option": (_I, [_P, _U32, _U32]),
+    "vrt_g3_time_lm_head": (_I, [_P, _U32, C.POINTER(_F)]),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() first")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != VRT_OK:
+        raise VrtError(rc, lib().vrt_last_error().decode(errors="replace"))
+
+
+def ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, DeviceBuffer):
+        return a.ptr
+    if isinstance(a, int):
+        return a
+    return a.ctypes.data_as(C.c_void_p).value
+
+
+class Context:
+    """VulkanContext replacement (include/vortexrt/vulkan_context.hpp:43-60)."""
+
+    def __init__(self, selector: str = ""):
+        h = C.c_void_p()
+        check(lib().vrt_ctx_create(selector.encode(), C.byref(h)))
+        self.h = h.value
+        info = DeviceInfo()
+        check(lib().vrt_ctx_info(self.h, C.byref(info)))
+        self.info = info
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().vrt_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def sync(self):
+        check(lib().vrt_sync(self.h))
+
+    def alloc(self, nbytes: int, kind: int = MEM_DEVICE) -> "DeviceBuffer":
+        return DeviceBuffer(self, nbytes, kind)
+
+    def upload(self, arr: np.ndarray, kind: int = MEM_DEVICE) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        b = DeviceBuffer(self, arr.nbytes, kind)
+        b.write(arr)
+        return b
+
+    def event(self):
+        h = C.c_void_p()
+        check(lib().vrt_event_create(self.h, C.byref(h)))
+        return h.value
+
+    def record(self, ev):
+        check(lib().vrt_event_record(self.h, ev))
+
+    @staticmethod
+    def elapsed_ms(a, b) -> float:
+        ms = C.c_float()
+        check(lib().vrt_event_elapsed_ms(a, b, C.byref(ms)))
+        return float(ms.value)
+
+
+class DeviceBuffer:
+    """Buffer replacement (include/vortexrt/buffer.hpp:11-42)."""
+
+    def __init__(self, ctx: Context, nbytes: int, kind: int = MEM_DEVICE):
+        self.ctx, self.nbytes, self.kind = ctx, int(nbytes), kind
+        p = C.c_void_p()
+        check(lib().vrt_alloc(ctx.h, self.nbytes, kind, C.byref(p)))
+        self.ptr = p.value
+
+    def write(self, arr: np.ndarray, offset: int = 0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        check(lib().vrt_memcpy(self.ctx.h, self.ptr + offset, ptr(arr), arr.nbytes))
+
+    def read(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib().vrt_memcpy(self.ctx.h, ptr(out), self.ptr + offset, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().vrt_free(self.ctx.h, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---- kernels ------------------------------------------------------------------------------
+
+def q8_matvec(ctx, w: DeviceBuffer, off: int, x: DeviceBuffer, y: DeviceBuffer, k: int, rows: int, w_bytes=None):
+    check(lib().vrt_q8_matvec(ctx.h, w.ptr, w.nbytes if w_bytes is None else w_bytes, off, x.ptr, y.ptr, k, rows))
+
+
+def q8_matvec_multi(ctx, w: DeviceBuffer, offs, dims, k: int, x: DeviceBuffer, y: DeviceBuffer):
+    o = np.asarray(offs, dtype=np.uint32)
+    d = np.asarray(dims, dtype=np.uint32)
+    check(lib().vrt_q8_matvec_multi(ctx.h, w.ptr, w.nbytes, len(o), ptr(o), ptr(d), k, x.ptr, y.ptr))
+
+
+def q8_ffn(ctx, w, gate_off, up_off, down_off, k, ffn, out, x, ws, y):
+    check(lib().vrt_q8_ffn(ctx.h, w.ptr, w.nbytes, gate_off, up_off, down_off, k, ffn, out, x.ptr, ws.ptr, ws.nbytes,
+                           y.ptr))
+
+
+def gelu_mul(ctx, gate: DeviceBuffer, up: DeviceBuffer, n: int):
+    check(lib().vrt_gelu_mul(ctx.h, gate.ptr, up.ptr, n))
+
+
+def argmax(ctx, x: DeviceBuffer, n: int, out: DeviceBuffer):
+    check(lib().vrt_argmax(ctx.h, x.ptr, n, out.ptr))
+
+
+def q8_quantize(ctx, x: DeviceBuffer, n: int, variant: int, out: DeviceBuffer):
+    check(lib().vrt_q8_quantize(ctx.h, x.ptr, n, variant, out.ptr))
+
+
+def q8_dequantize(ctx, blocks: DeviceBuffer, nblocks: int, out: DeviceBuffer):
+    check(lib().vrt_q8_dequantize(ctx.h, blocks.ptr, nblocks, out.ptr))
+
+
+# ---- Gemma 3 executor ----------------------------------------------------------------------
+
+class Gemma3:
+    """Executor over a GGUF file: parses it (gguf.py), uploads the tensor-data section as the
+    device arena and builds the vrt_g3 executor (Gemma3Model's device half)."""
+
+    def __init__(self, ctx: Context, path: str):
+        import gguf as G
+        self.ctx = ctx
+        f = G.GgufFile.open(path)
+        self.file = f
+        if f.meta_str("general.architecture") != "gemma3":
+            raise RuntimeError("Gemma3Model requires general.architecture=gemma3")
+
+        def req(key):
+            v = f.meta_u64(key)
+            if v is None or v > 0xFFFFFFFF:
+                raise RuntimeError("Missing/invalid Gemma 3 metadata: " + key)
+            return v
+
+        cfg = G3Config()
+        cfg.context_length = req("gemma3.context_length")
+        cfg.embedding_length = req("gemma3.embedding_length")
+        cfg.block_count = req("gemma3.block_count")
+        cfg.feed_forward_length = req("gemma3.feed_forward_length")
+        cfg.head_count = req("gemma3.attention.head_count")
+        cfg.head_count_kv = req("gemma3.attention.head_count_kv")
+        cfg.head_dim = req("gemma3.attention.key_length")
+        cfg.value_dim = req("gemma3.attention.value_length")
+        eps = f.meta_f64("gemma3.attention.layer_norm_rms_epsilon")
+        if eps is None:
+            raise RuntimeError("Missing Gemma 3 metadata: gemma3.attention.layer_norm_rms_epsilon")
+        cfg.rms_epsilon = eps
+        sw = f.meta_u64("gemma3.attention.sliding_window")
+        cfg.sliding_window = sw if sw is not None and sw <= 0xFFFFFFFF else 0
+        rb = f.meta_f64("gemma3.rope.freq_base")
+        cfg.global_rope_base = rb if rb is not None and np.isfinite(rb) and rb > 0 else 1.0e6
+        cfg.local_rope_base = 1.0e4
+        emb = f.tensors.get("token_embd.weight")
+        if emb is None or emb.type != 8 or len(emb.dims) != 2 or emb.dims[0] != cfg.embedding_length:
+            raise RuntimeError("Unsupported token_embd.weight layout")
+        cfg.vocab_size = emb.dims[1]
+        self.config = cfg
+        self.eos = f.meta_u64("tokenizer.ggml.eos_token_id")
+        self.eos = 1 if self.eos is None else self.eos
+        data = f.data_view()
+        self.arena = DeviceBuffer(ctx, len(data))
+        # upload in chunks from the memory map
+        chunk = 64 << 20
+        arr = np.frombuffer(data, dtype=np.uint8)
+        for o in range(0, len(arr), chunk):
+            part = np.ascontiguousarray(arr[o:o + chunk])
+            check(lib().vrt_memcpy(ctx.h, self.arena.ptr + o, ptr(part), part.nbytes))
+        self._keep = []
+
+        def f32(name):
+            t = f.tensors.get(name)
+            if t is None:
+                raise RuntimeError("Missing Gemma 3 tensor: " + name)
+            a = f.read_f32(name)
+            self._keep.append(a)
+            return ptr(a)
+
+        layers = (G3Layer * cfg.block_count)()
+        for l in range(cfg.block_count):
+            p = f"blk.{l}."
+            Ly = layers[l]
+            for fld, nm in (("attn_q", "attn_q"), ("attn_k", "attn_k"), ("attn_v", "attn_v"),
+                            ("attn_output", "attn_output"), ("ffn_gate", "ffn_gate"), ("ffn_up", "ffn_up"),
+                            ("ffn_down", "ffn_down")):
+                t = f.tensors.get(p + nm + ".weight")
+                if t is None or t.type != 8:
+                    raise RuntimeError("Missing Gemma 3 tensor: " + p + nm + ".weight")
+                setattr(Ly, fld, t.offset)
+            for fld, nm in (("attn_norm", "attn_norm"), ("attn_q_norm", "attn_q_norm"),
+                            ("attn_k_norm", "attn_k_norm"), ("post_attention_norm", "post_attention_norm"),
+                            ("ffn_norm", "ffn_norm"), ("post_ffw_norm", "post_ffw_norm")):
+                setattr(Ly, fld, f32(p + nm + ".weight"))
+        desc = G3Desc()
+        desc.config = cfg
+        desc.arena = self.arena.ptr
+        desc.arena_bytes = len(data)
+        desc.token_embd = emb.offset
+        desc.output_norm = f32("output_norm.weight")
+        desc.layers = layers
+        desc.eos_token_id = self.eos
+        h = C.c_void_p()
+        check(lib().vrt_g3_create(ctx.h, C.byref(desc), C.byref(h)))
+        self.h = h.value
+        self._keep.clear()
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().vrt_g3_destroy(self.h)
+            self.h = None
+        if getattr(self, "arena", None) is not None:
+            self.arena.free()
+            self.arena = None
+
+    def __del__(self):
+        self.close()
+
+    def set_graph(self, on: bool):
+        check(lib().vrt_g3_set_option(self.h, OPT_USE_GRAPH, 1 if on else 0))
+
+    def reset(self):
+        check(lib().vrt_g3_reset(self.h))
+
+    def decode(self, token: int, pos: int, top_k: int = 1, hidden: bool = False):
+        r = ArgmaxResult()
+        hbuf = np.empty(self.config.embedding_length, dtype=np.float32) if hidden else None
+        check(lib().vrt_g3_decode(self.h, token, pos, top_k, C.byref(r), ptr(hbuf)))
+        return (int(r.index), float(r.value)), hbuf
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.config.vocab_size, dtype=np.float32)
+        check(lib().vrt_g3_logits(self.h, ptr(out), out.size))
+        return out
+
+    def generate(self, prompt, max_new: int) -> np.ndarray:
+        pr = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max(1, max_new), dtype=np.uint32)
+        n = C.c_uint32()
+        check(lib().vrt_g3_generate(self.h, ptr(pr), pr.size, max_new, ptr(out), C.byref(n)))
+        return out[: n.value].copy()
+
+    def forced(self, tokens, first_logit_step: int):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.zeros(t.size, dtype=np.dtype([("index", np.uint32), ("value", np.float32)]))
+        check(lib().vrt_g3_forced(self.h, ptr(t), t.size, first_logit_step, ptr(out)))
+        return out
+
+    def time_lm_head(self, iters: int) -> float:
+        us = C.c_float()
+        check(lib().vrt_g3_time_lm_head(self.h, iters, C.byref(us)))
+        return float(us.value)
