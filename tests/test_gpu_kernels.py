@@ -231,7 +231,11 @@ def test_quantize_bit_exact(ctx):
         vrt.q8_quantize(ctx, xd, x.size, variant, out)
         ctx.sync()
         got = out.read(np.uint8, x.size // 32 * 34)
-        assert np.array_equal(got, oracle.quantize(x, name))
+        ref = oracle.quantize(x, name)
+        bad = np.nonzero((got != ref).reshape(-1, 34).any(axis=1))[0]
+        assert bad.size == 0, f"variant {name}: {bad.size} blocks differ, first {bad[:8]} " \
+                              f"x={x.reshape(-1, 32)[bad[0]][:4]} gpu={got.reshape(-1, 34)[bad[0]][:6]} " \
+                              f"ref={ref.reshape(-1, 34)[bad[0]][:6]}"
         assert np.array_equal(got, synth.quantize_q8_0(x, name))
 
 

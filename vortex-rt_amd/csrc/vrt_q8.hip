@@ -221,7 +221,8 @@ __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ x, u
     const uint32_t k = threadIdx.x & 31u;
     const bool live = blk < nblocks;
     const float v = live ? x[blk * 32u + k] : 0.0f;
-    float amax = fabsf(v);  // std::max(abs_max, fabs(v)) skips NaN, as fmaxf does
+    // abs_max starts at 0 and std::max(abs_max, fabs(v)) never takes a NaN: fmaxf(0, .)
+    float amax = fmaxf(0.0f, fabsf(v));
     for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
     if (!live) return;
     float scale = amax / 127.0f;

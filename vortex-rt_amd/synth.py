@@ -112,7 +112,10 @@ def quantize_q8_0(w: np.ndarray, variant: str = "a") -> np.ndarray:
     with np.errstate(divide="ignore", invalid="ignore"):
         r = (v / div[:, None]).astype(np.float32)
     n = np.rint(r)
-    q = np.where(np.isnan(n), -127, np.clip(np.nan_to_num(n, nan=0.0, posinf=127.0, neginf=-127.0), -127, 127))
+    # static_cast<int> of NaN or |n| >= 2^31 is INT_MIN on x86-64, which the clamp maps to -127
+    with np.errstate(invalid="ignore"):
+        out_of_range = ~(np.abs(n) < np.float32(2147483648.0))
+    q = np.where(out_of_range, -127, np.clip(np.where(out_of_range, 0, n), -127, 127))
     out = np.empty((nb, 34), dtype=np.uint8)
     out[:, 0:2] = half.view(np.uint8).reshape(nb, 2)
     out[:, 2:] = q.astype(np.int8).view(np.uint8)
