@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""Decode throughput of the Gemma-3-270M-shape Q8_0 batch-1 token loop on one MI355X.
+
+Workload: random-init Gemma-3-270M-architecture model (18 blocks, d 640, 4 query heads and
+1 KV head of 256, FFN 2048, vocab 262144 tied Q8_0 LM head, window 512), an 8-token prompt
+of uniform ids in [2, 262144) from seed 0, then greedy decode with an fp32 KV cache. One
+"step" is one decode_token (all 18 blocks + LM head + argmax) producing one token. The
+prompt is prefilled first (untimed); --steps decode steps at positions 8, 9, ... are timed
+with hipEvents on the library's stream. Inputs are resident in HBM before timing.
+
+Algorithmic bytes per step at position p: every Q8_0 weight byte, the fp32 norm weights, one
+embedding row, plus the fp32 KV rows attention reads (min(p+1, window) positions for local
+blocks, p+1 for global ones), each counted once.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for sub in ("vortex-rt_amd", "oracle"):
+    sys.path.insert(0, os.path.join(REPO, sub))
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "decode tokens/s + achieved HBM GB/s (% of roofline), Gemma3-270M-shape Q8_0, 1 GPU"
+
+
+def step_bytes(cfg, pos: int) -> int:
+    d, H, hd, F, V, L = (cfg.embedding_length, cfg.head_count, cfg.head_dim, cfg.feed_forward_length,
+                         cfg.vocab_size, cfg.block_count)
+    q8 = lambda rows, k: rows * (k // 32) * 34
+    layer = q8(H * hd, d) + 2 * q8(hd, d) + q8(d, H * hd) + 2 * q8(F, d) + q8(d, F)
+    norms = (L * (4 * d + 2 * hd) + d) * 4
+    total = L * layer + q8(V, d) + norms + (d // 32) * 34
+    for l in range(L):
+        glob = (l + 1) % 6 == 0
+        slots = cfg.context_length if (glob or cfg.sliding_window == 0) else cfg.sliding_window
+        total += min(pos + 1, slots) * hd * 4 * 2
+    return total
+
+
+def lm_head_bytes(cfg) -> int:
+    return cfg.vocab_size * (cfg.embedding_length // 32) * 34
+
+
+def load_traffic():
+    """HBM bytes per LM-head launch from the committed rocprofv3 PMC summary, if present."""
+    p = os.path.join(REPO, "profiles", "lm_head_pmc.json")
+    try:
+        with open(p) as fp:
+            return json.load(fp).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(path, prompt, target_s: float = 12.0):
+    """The oracle (scalar C, OpenMP over matvec rows) timed on this host: prompt steps without
+    the LM head, then greedy decode steps (each with the LM head) until ~target_s of work."""
+    import oracle
+    m = oracle.Model(path)
+    pos = 0
+    for i, t in enumerate(prompt):
+        r = m.decode(int(t), pos, want_logits=(i == len(prompt) - 1))
+        pos += 1
+    tok = r["index"]
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        r = m.decode(int(tok), pos, want_logits=True)
+        times.append(time.perf_counter() - t0)
+        tok = r["index"]
+        pos += 1
+        if time.perf_counter() - t_all > target_s or len(times) >= 64:
+            break
+    m.close()
+    n = len(times)
+    return {"value": n / sum(times), "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"{n} greedy decode steps at positions {len(prompt)}..{len(prompt) + n - 1} of the same "
+                      f"model and prompt (oracle/vrt_oracle.c, {oracle.num_threads()} OpenMP threads); "
+                      f"the reference's Lavapipe path is not available on this host"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the batch-1 token loop is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import synth
+    import vrt
+
+    if not os.path.exists(args.model):
+        os.makedirs(os.path.dirname(args.model), exist_ok=True)
+        t0 = time.time()
+        synth.write_gemma3_gguf(args.model, seed=0, **synth.GEMMA3_270M)
+        print(f"[bench] wrote {args.model} in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    ctx = vrt.Context("")
+    g = vrt.Gemma3(ctx, args.model)
+    cfg = g.config
+    prompt = synth.uniform_ids(0, 8, 2, cfg.vocab_size)
+    n_prompt = prompt.size
+    print(f"[bench] device {ctx.info.name.decode()} ({ctx.info.arch.decode()}, {ctx.info.compute_units} CUs)",
+          file=sys.stderr, flush=True)
+
+    # warm-up: a full generation of `warmup` decode steps (graph capture happens here)
+    warm = g.generate(prompt, args.warmup + 1)
+
+    # timed: prefill untimed, then exactly `steps` decode steps between two events
+    g.start(prompt, args.steps + 1)
+    g.step(n_prompt)
+    ctx.sync()
+    ev0, ev1 = ctx.event(), ctx.event()
+    ctx.sync()
+    ctx.record(ev0)
+    g.step(args.steps)
+    ctx.record(ev1)
+    ms = ctx.elapsed_ms(ev0, ev1)
+    ctx.sync()
+    toks = g.collect()
+    if toks.size < args.steps + 1:
+        print(f"[bench] EOS after {toks.size} tokens; timed steps after it were skipped", file=sys.stderr)
+    k = min(warm.size, toks.size)
+    if not np.array_equal(warm[:k], toks[:k]):
+        raise SystemExit("[bench] nondeterministic greedy tokens between warm-up and timed run")
+
+    ms_per_step = ms / args.steps
+    tok_s = args.steps / (ms / 1e3)
+    total_bytes = sum(step_bytes(cfg, n_prompt + i) for i in range(args.steps))
+    gbps = total_bytes / (ms / 1e3) / 1e9
+
+    # dominant kernel: tied LM head + argmax, timed alone with events on the same stream
+    lm_us = g.time_lm_head(50)
+    lm_bytes = lm_head_bytes(cfg)
+    lm_gbps = lm_bytes / (lm_us * 1e-6) / 1e9
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 weights x fp32 activations (int8 dot4 on 3 int8 activation limbs), fp32 KV",
+        "data": "synthetic (random-init weights N(0,0.02) quantised to Q8_0, seed 0)",
+        "config": {
+            "workload": f"Gemma-3-270M-shape Q8_0 batch-1 greedy decode: {n_prompt}-token prompt (untimed prefill), "
+                        f"{args.steps} timed decode steps at positions {n_prompt}..{n_prompt + args.steps - 1}",
+            "layers": cfg.block_count, "d_model": cfg.embedding_length, "heads": cfg.head_count,
+            "kv_heads": cfg.head_count_kv, "head_dim": cfg.head_dim, "ffn": cfg.feed_forward_length,
+            "vocab": cfg.vocab_size, "sliding_window": cfg.sliding_window, "batch": 1,
+            "parallelism": "single GPU",
+        },
+        "hbm_gbps": round(gbps, 1),
+        "step_roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "bytes_per_step_mean": int(total_bytes / args.steps),
+        "roofline": {
+            "kernel": "k_lm (tied 262144x640 Q8_0 LM head fused with greedy argmax)",
+            "bound": "hbm",
+            "achieved": round(lm_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(lm_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": load_traffic(),
+            "mean_launch_us": round(lm_us, 3),
+            "algorithmic_bytes_per_launch": lm_bytes,
+        },
+        "cpu_baseline": None,
+    }
+    g.close()
+    ctx.close()
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.model, prompt)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

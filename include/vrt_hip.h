@@ -195,6 +195,14 @@ int vrt_g3_logits(vrt_g3* g3, float* host_logits, uint32_t n);
 int vrt_g3_generate(vrt_g3* g3, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
                     uint32_t* out_tokens, uint32_t* n_out);
 
+/* The same loop split for callers that overlap or time it: vrt_g3_start resets and uploads
+ * the prompt; vrt_g3_step enqueues n steps (asynchronous, stream-ordered; n_prompt +
+ * max_new - 1 steps in total complete the generation); vrt_g3_collect waits and returns the
+ * generated ids (stopping after EOS) as vrt_g3_generate does. */
+int vrt_g3_start(vrt_g3* g3, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new);
+int vrt_g3_step(vrt_g3* g3, uint32_t n);
+int vrt_g3_collect(vrt_g3* g3, uint32_t* out_tokens, uint32_t* n_out);
+
 /* Teacher-forced run (validation): resets, then step i consumes tokens[i] at position i;
  * steps i >= first_logit_step run the LM head and record their greedy result in out[i]. */
 int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first_logit_step,

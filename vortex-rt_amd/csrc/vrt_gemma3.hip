@@ -410,12 +410,16 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
                 if (h < H) mypart[2u * H + h * hd + i] = acc[h];
         }
     }
-    __threadfence();
+    // one device-scope release per workgroup (after the barrier orders the block's writes),
+    // one acquire in the last workgroup
     __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(&P.st->tickets[0], 1u) == gridDim.x - 1u;
+    if (threadIdx.x == 0) {
+        __threadfence();
+        last = atomicAdd(&P.st->tickets[0], 1u) == gridDim.x - 1u;
+        if (last) __threadfence();
+    }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     // merge: att[h][i] = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c
     for (uint32_t idx = threadIdx.x; idx < H * hd; idx += blockDim.x) {
         const uint32_t h = idx / hd, i = idx % hd;
@@ -644,12 +648,14 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
             P.lm_part[blockIdx.x] = {bvs[0], bis[0]};
         }
     }
-    __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(&P.st->tickets[1], 1u) == gridDim.x - 1u;
+    if (threadIdx.x == 0) {
+        __threadfence();
+        last = atomicAdd(&P.st->tickets[1], 1u) == gridDim.x - 1u;
+        if (last) __threadfence();
+    }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     if (run_lm) {
         bv = -INFINITY;
         bi = 0xffffffffu;
@@ -745,7 +751,9 @@ struct vrt_g3 {
     uint32_t next_pos = 0;
     bool use_graph = true;
     hipGraphExec_t graph = nullptr;
-    bool graph_broken = false;
+    uint32_t gen_prompt = 0;     // generation in flight (vrt_g3_start .. vrt_g3_collect)
+    uint32_t gen_max = 0;
+    uint64_t gen_steps = 0;
 };
 
 static int g3_alloc(vrt_g3* g, size_t bytes, void** out) {
@@ -1078,13 +1086,14 @@ extern "C" int vrt_g3_logits(vrt_g3* g, float* host, uint32_t n) {
     return VRT_OK;
 }
 
-extern "C" int vrt_g3_generate(vrt_g3* g, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
-                               uint32_t* out_tokens, uint32_t* n_out) {
-    VRT_REQUIRE(g && n_out, "vrt_g3_generate: null argument");
-    *n_out = 0;
+extern "C" int vrt_g3_start(vrt_g3* g, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new) {
+    VRT_REQUIRE(g, "vrt_g3_start: null executor");
     g->next_pos = 0;
+    g->gen_prompt = 0;
+    g->gen_max = 0;
+    g->gen_steps = 0;
     if (max_new == 0) return vrt_g3_reset(g);
-    VRT_REQUIRE(prompt && out_tokens, "vrt_g3_generate: null argument");
+    VRT_REQUIRE(prompt, "vrt_g3_start: null prompt");
     if (n_prompt == 0) return set_error(VRT_ERR_INVALID, "Gemma 3 prompt produced no input tokens");
     const uint64_t steps = static_cast<uint64_t>(n_prompt) + max_new - 1u;
     if (steps > g->cfg.context_length) return set_error(VRT_ERR_STATE, "Gemma 3 context length exceeded");
@@ -1093,22 +1102,56 @@ extern "C" int vrt_g3_generate(vrt_g3* g, const uint32_t* prompt, uint32_t n_pro
     hipStream_t s = g->ctx->stream;
     VRT_HIP_CHECK(hipMemcpyAsync(g->P.tokens, prompt, n_prompt * 4u, hipMemcpyHostToDevice, s));
     if (int rc = g3_write_ctl(g, 0, n_prompt - 1u, n_prompt, 0)) return rc;
-    if (int rc = g3_run_steps(g, static_cast<uint32_t>(steps))) return g3_fail_reset(g, rc, vrt_last_error());
-    VRT_HIP_CHECK(hipMemcpyAsync(g->host_res, g->P.results + (n_prompt - 1u), max_new * sizeof(vrt_argmax_result),
+    VRT_HIP_CHECK(hipStreamSynchronize(s));
+    g->gen_prompt = n_prompt;
+    g->gen_max = max_new;
+    return VRT_OK;
+}
+
+extern "C" int vrt_g3_step(vrt_g3* g, uint32_t n) {
+    VRT_REQUIRE(g, "vrt_g3_step: null executor");
+    VRT_REQUIRE(g->gen_max != 0, "vrt_g3_step: no generation started");
+    const uint64_t total = static_cast<uint64_t>(g->gen_prompt) + g->gen_max - 1u;
+    VRT_REQUIRE(g->gen_steps + n <= total, "vrt_g3_step: more steps than the generation needs");
+    if (int rc = g3_run_steps(g, n)) return g3_fail_reset(g, rc, vrt_last_error());
+    g->gen_steps += n;
+    return VRT_OK;
+}
+
+extern "C" int vrt_g3_collect(vrt_g3* g, uint32_t* out_tokens, uint32_t* n_out) {
+    VRT_REQUIRE(g && n_out, "vrt_g3_collect: null argument");
+    *n_out = 0;
+    if (g->gen_max == 0) return VRT_OK;
+    VRT_REQUIRE(out_tokens, "vrt_g3_collect: null output");
+    const uint64_t total = static_cast<uint64_t>(g->gen_prompt) + g->gen_max - 1u;
+    if (g->gen_steps < total)
+        if (int rc = vrt_g3_step(g, static_cast<uint32_t>(total - g->gen_steps))) return rc;
+    hipStream_t s = g->ctx->stream;
+    VRT_HIP_CHECK(hipMemcpyAsync(g->host_res, g->P.results + (g->gen_prompt - 1u), g->gen_max * sizeof(vrt_argmax_result),
                                  hipMemcpyDeviceToHost, s));
     G3State st;
     if (int rc = g3_check_state(g, &st)) return rc;
     uint32_t n = 0;
-    for (uint32_t i = 0; i < max_new; ++i) {
+    for (uint32_t i = 0; i < g->gen_max; ++i) {
         const vrt_argmax_result r = g->host_res[i];
-        if (r.index >= g->cfg.vocab_size || !std::isfinite(r.value))
+        if (r.index >= g->cfg.vocab_size || !std::isfinite(r.value))                  // :1171-1176
             return g3_fail_reset(g, VRT_ERR_NUMERIC, "GPU argmax produced invalid result");
         out_tokens[n++] = r.index;
         if (r.index == g->eos) break;                                                  // :2134-2141
     }
     *n_out = n;
     g->next_pos = st.step;
+    g->gen_max = 0;
     return VRT_OK;
+}
+
+extern "C" int vrt_g3_generate(vrt_g3* g, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                               uint32_t* out_tokens, uint32_t* n_out) {
+    VRT_REQUIRE(g && n_out, "vrt_g3_generate: null argument");
+    *n_out = 0;
+    if (int rc = vrt_g3_start(g, prompt, n_prompt, max_new)) return rc;
+    if (max_new == 0) return VRT_OK;
+    return vrt_g3_collect(g, out_tokens, n_out);
 }
 
 extern "C" int vrt_g3_forced(vrt_g3* g, const uint32_t* tokens, uint32_t n, uint32_t first_logit_step,

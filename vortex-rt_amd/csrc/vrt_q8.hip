@@ -177,10 +177,10 @@ __global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ x, uin
         parts[blockIdx.x] = {sv[0], si[0]};
         __threadfence();
         last = atomicAdd(ticket, 1u) == gridDim.x - 1u;
+        if (last) __threadfence();
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     bv = -INFINITY;
     bi = 0xffffffffu;
     for (uint32_t k = threadIdx.x; k < gridDim.x; k += blockDim.x) {

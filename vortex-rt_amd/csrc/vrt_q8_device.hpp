@@ -105,11 +105,11 @@ __device__ __forceinline__ void q8_load(const uint8_t* blk, const uint8_t* end, 
     r.sh = static_cast<uint32_t>(q & 3u);
     r.sbits = *reinterpret_cast<const uint16_t*>(blk);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r.d[j] = __builtin_nontemporal_load(lb + j);
+    for (int j = 0; j < 8; ++j) r.d[j] = lb[j];
     r.d[8] = 0u;
     if (r.sh) {
         const uint8_t* tail = reinterpret_cast<const uint8_t*>(lb + 8);
-        r.d[8] = (tail + 4 <= end) ? __builtin_nontemporal_load(lb + 8)
+        r.d[8] = (tail + 4 <= end) ? lb[8]
                                    : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tail));
     }
 }

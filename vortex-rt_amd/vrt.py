@@ -86,6 +86,9 @@ SIGNATURES = {
     "vrt_g3_decode": (_I, [_P, _U32, _U32, _U32, C.POINTER(ArgmaxResult), _P]),
     "vrt_g3_logits": (_I, [_P, _P, _U32]),
     "vrt_g3_generate": (_I, [_P, _P, _U32, _U32, _P, C.POINTER(_U32)]),
+    "vrt_g3_start": (_I, [_P, _P, _U32, _U32]),
+    "vrt_g3_step": (_I, [_P, _U32]),
+    "vrt_g3_collect": (_I, [_P, _P, C.POINTER(_U32)]),
     "vrt_g3_forced": (_I, [_P, _P, _U32, _U32, _P]),
     "vrt_g3_set_option": (_I, [_P, _U32, _U32]),
     "vrt_g3_time_lm_head": (_I, [_P, _U32, C.POINTER(_F)]),
@@ -358,6 +361,20 @@ class Gemma3:
         out = np.empty(max(1, max_new), dtype=np.uint32)
         n = C.c_uint32()
         check(lib().vrt_g3_generate(self.h, ptr(pr), pr.size, max_new, ptr(out), C.byref(n)))
+        return out[: n.value].copy()
+
+    def start(self, prompt, max_new: int):
+        pr = np.ascontiguousarray(prompt, dtype=np.uint32)
+        self._gen_max = max_new
+        check(lib().vrt_g3_start(self.h, ptr(pr), pr.size, max_new))
+
+    def step(self, n: int):
+        check(lib().vrt_g3_step(self.h, n))
+
+    def collect(self) -> np.ndarray:
+        out = np.empty(max(1, self._gen_max), dtype=np.uint32)
+        n = C.c_uint32()
+        check(lib().vrt_g3_collect(self.h, ptr(out), C.byref(n)))
         return out[: n.value].copy()
 
     def forced(self, tokens, first_logit_step: int):
