@@ -688,7 +688,9 @@ done:
 int or_g3_decode(or_g3* m, uint32_t token, uint32_t pos, int want_logits,
                  float* hidden_out, float* logits_out, uint32_t* argmax_index, float* argmax_value) {
     int rc = decode_impl(m, token, pos, want_logits, hidden_out, logits_out, argmax_index, argmax_value);
-    if (rc) { /* reset_cache on any exception (src/gemma3.cpp:1878-1881) */
+    /* reset_cache on any exception inside the step's try block (src/gemma3.cpp:1476-1881);
+     * the position checks before it (:1467-1474, rc -1) leave the cache alone */
+    if (rc && rc != -1) {
         for (uint32_t l = 0; l < m->info.block_count; ++l) { m->layers[l].start = 0; m->layers[l].count = 0; }
         m->next_pos = 0;
     }

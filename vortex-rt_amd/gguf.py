@@ -224,8 +224,12 @@ class GgufFile:
         return self.tensor_bytes(name).view(np.float32).copy()
 
     def close(self):
+        """Unmaps the file; arrays still viewing the payload keep the map alive until they go."""
         if self._mm is not None:
-            self._mm.close()
+            try:
+                self._mm.close()
+            except BufferError:
+                pass
             self._mm = None
 
 

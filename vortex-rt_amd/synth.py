@@ -158,11 +158,14 @@ GEMMA3_270M = dict(n_layers=18, d_model=640, n_heads=4, head_dim=256, ffn=2048, 
 def write_gemma3_gguf(path, seed: int = 0, n_layers: int = 18, d_model: int = 640, n_heads: int = 4,
                       head_dim: int = 256, ffn: int = 2048, vocab: int = 262144, context: int = 32768,
                       window: int = 512, eps: float = 1e-6, rope_global: float = 1.0e6,
-                      weight_std: float = 0.02, norm_std: float = 0.1, with_window: bool = True):
+                      weight_std: float = 0.02, norm_std: float = 0.1, with_window: bool = True,
+                      embd_std: float | None = None):
     """A random-init Gemma-3-architecture GGUF carrying every key the reference executor
     requires (src/gemma3.cpp:174-257, :289-313) and the tensor set of :456-505.
     Norm weights are stored as 1 + N(0, norm_std^2): Gemma GGUFs fold the (1 + w)
-    convention into the stored value (src/gemma3.cpp:991-996)."""
+    convention into the stored value (src/gemma3.cpp:991-996). embd_std (default
+    weight_std) sets the tied embedding / LM head alone, so a model whose block
+    projections are all zero (weight_std=0) still has a non-trivial embedding."""
     w = GgufWriter(alignment=32)
     w.add("general.architecture", T_STR, "gemma3")
     w.add("general.alignment", T_U32, 32)
@@ -193,15 +196,15 @@ def write_gemma3_gguf(path, seed: int = 0, n_layers: int = 18, d_model: int = 64
     w.add("tokenizer.ggml.eos_token_id", T_U32, 1)
     w.add("tokenizer.ggml.unknown_token_id", T_U32, 3)
 
-    def q8(name, rows, cols):
+    def q8(name, rows, cols, std=weight_std):
         w.add_tensor(name, [cols, rows], GGML_Q8_0, rows * cols // 32 * 34,
-                     lambda: q8_matrix_chunks(seed, name, rows, cols, weight_std))
+                     lambda: q8_matrix_chunks(seed, name, rows, cols, std))
 
     def f32norm(name, n):
         w.add_tensor(name, [n], GGML_F32, 4 * n,
                      lambda: normal_f32(tensor_seed(seed, name), n, norm_std, 1.0))
 
-    q8("token_embd.weight", vocab, d_model)
+    q8("token_embd.weight", vocab, d_model, weight_std if embd_std is None else embd_std)
     f32norm("output_norm.weight", d_model)
     qw = n_heads * head_dim
     for l in range(n_layers):
