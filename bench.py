@@ -109,6 +109,8 @@ def main():
     ctx = vrt.Context("")
     g = vrt.Gemma3(ctx, args.model)
     cfg = g.config
+    if not g.persistent_available():
+        raise SystemExit("[bench] the persistent decode kernel is unavailable for this shape/device")
     prompt = synth.uniform_ids(0, 8, 2, cfg.vocab_size)
     n_prompt = prompt.size
     print(f"[bench] device {ctx.info.name.decode()} ({ctx.info.arch.decode()}, {ctx.info.compute_units} CUs)",

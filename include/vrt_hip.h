@@ -208,8 +208,28 @@ int vrt_g3_collect(vrt_g3* g3, uint32_t* out_tokens, uint32_t* n_out);
 int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first_logit_step,
                   vrt_argmax_result* out);
 
-/* Executor options. */
-#define VRT_G3_OPT_USE_GRAPH 1      /* 1 (default): replay the captured step graph */
+/* Executor options. The persistent kernel (one cooperative launch runs a batch of steps) is
+ * used when the device and shape support it; otherwise, or with VRT_G3_OPT_PERSISTENT = 0,
+ * each step is the multi-kernel sequence, replayed from a hipGraph unless
+ * VRT_G3_OPT_USE_GRAPH = 0. VRT_G3_OPT_QUERY_PERSISTENT returns VRT_OK when the persistent
+ * kernel is available (value ignored). */
+#define VRT_G3_OPT_USE_GRAPH 1
+#define VRT_G3_OPT_PERSISTENT 2
+#define VRT_G3_OPT_QUERY_PERSISTENT 3
+#define VRT_G3_OPT_TRACE 4          /* 1: timestamp the phases of the first step of each launch */
+
+/* Phase trace of the last persistent launch (tracing tool; no reference counterpart, which
+ * only has CLI wall timers, src/gemma_main.cpp:194-232): out[w * slots + k] is the
+ * s_memrealtime tick (100 MHz) at which workgroup w finished phase k of the launch's first
+ * step: k = 0 step start, 5l + 1 .. 5l + 5 phases A..E of block l, 5L + 1 end of the blocks,
+ * 5L + 2 end of the LM head. Entries of phases a workgroup does not run keep older values. */
+int vrt_g3_read_trace(vrt_g3* g3, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);
+
+/* Raw tagged words {fp32 bits | tag << 32} of a persistent-kernel exchange buffer as the last
+ * launch left them (diagnostics; no reference counterpart): which = 0 q|k|v, 1 attention chunk
+ * partials, 2 attention output projection, 3 gelu(gate)*up, 4 down projection, 5 argmax
+ * partials. *n receives the word count; synchronises the context's stream. */
+int vrt_g3_read_exchange(vrt_g3* g3, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
 
 /* Launches the tied LM head + argmax kernel `iters` times back to back between two

@@ -121,6 +121,7 @@ def test_full_shape_greedy_and_logits(ctx, full_model):
     """Config 2 shapes: 8-token prompt, greedy continuation compared token by token and the
     last step's logits within 1e-3."""
     g = vrt.Gemma3(ctx, full_model)
+    assert g.persistent_available(), "the Gemma-3-270M shape must run on the persistent decode kernel"
     prompt = synth.uniform_ids(0, 8, 2, 262144)
     n_new = 12
     print("[g3] full-shape generate", flush=True)
@@ -141,3 +142,37 @@ def test_full_shape_greedy_and_logits(ctx, full_model):
     assert idx == r["index"]
     m.close()
     g.close()
+
+
+def test_persistent_matches_multikernel(ctx, tiny_model):
+    """The persistent decode kernel and the multi-kernel step agree on tokens; their logits
+    agree within the logit tolerance (the attention split differs between them)."""
+    g = vrt.Gemma3(ctx, tiny_model)
+    assert g.persistent_available(), "persistent decode kernel not available for the test shape"
+    toks = synth.uniform_ids(77, 48, 2, 1000)
+    g.set_persistent(True)
+    a = g.forced(toks, 0)
+    g.set_persistent(False)
+    b = g.forced(toks, 0)
+    assert np.array_equal(a["index"], b["index"])
+    assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"]))
+    g.set_persistent(True)
+    prompt = synth.uniform_ids(3, 6, 2, 1000)
+    p1 = g.generate(prompt, 40)
+    g.set_persistent(False)
+    p2 = g.generate(prompt, 40)
+    g.close()
+    assert np.array_equal(p1, p2)
+
+
+def test_persistent_split_launches(ctx, tiny_model):
+    """A generation split over several persistent launches equals one launch."""
+    g = vrt.Gemma3(ctx, tiny_model)
+    prompt = synth.uniform_ids(9, 7, 2, 1000)
+    whole = g.generate(prompt, 30)
+    g.start(prompt, 30)
+    for n in (3, 1, 10, 7, 15):
+        g.step(n)
+    parts = g.collect()
+    g.close()
+    assert np.array_equal(whole, parts)

@@ -1,0 +1,1369 @@
+// vrt_decode.hip -- persistent Gemma 3 decode kernel for gfx950 (the token loop of
+// src/gemma3.cpp:1462-1882 and :2080-2149, several steps per launch).
+//
+// Why one kernel. A batch-1 step of the Gemma-3-270M shape is ~91 dependent phases (five per
+// block plus the LM head) over small matrices (0.17-2.8 MB each). Separate kernels pay ~1.6 us
+// of dispatch per phase even inside a hipGraph, and a grid barrier built on device-scope
+// atomics costs 5-11 us at 256 workgroups on this part. Here every workgroup (one per CU,
+// launched cooperatively so all are resident) runs the whole step and the phases hand their
+// outputs to each other through "tagged" 8-byte words: {fp32 value, u32 tag} written with one
+// device-coherent store and read with device-coherent loads until the tag matches. A phase's
+// consumer therefore waits for exactly the data it needs, with no separate flag or barrier,
+// and issues its weight loads before it starts waiting, so the HBM fetch overlaps the
+// hand-off latency.
+//
+// Phases of block l (rows are split over workgroups; "all" = every workgroup):
+//   A  all   h = RMSNorm(f_{l-1}, post_ffw) + h (or the scaled embedding row), x = RMSNorm(h,
+//            attn_norm), rows of [Wq | Wk | Wv]                                   (:1511-1541)
+//   B  nch   QK-norm, RoPE, KV append, attention over one chunk of the history: per head the
+//            chunk max m, sum l and the unnormalised sum acc                      (:1557-1696)
+//   C  nc    merge the chunks (att = sum_c e^(m_c-M) acc_c / sum_c e^(m_c-M) l_c), Wo rows
+//   D  all   h = RMSNorm(o, post_attn) + h, x = RMSNorm(h, ffn_norm), gate/up row pairs,
+//            g = gelu_tanh(gate) * up                                             (:1703-1801)
+//   E  ne    Wd rows -> f
+// After the last block every workgroup folds f into h; when the step runs the LM head all of
+// them stream an even share of the tied Q8_0 table (staged through LDS with 16-byte loads),
+// keep a local greedy argmax and publish it; the next step (or workgroup 0 at the end of the
+// launch) reduces the partials with the argmax rule of shaders/argmax.comp:30-43.
+//
+// Every workgroup keeps its own copy of the residual stream h in LDS. All copies are computed
+// by the same code from the same exchanged inputs, so they are bitwise identical and h itself
+// is never exchanged.
+//
+// Buffer reuse is safe without double buffering: a producer can only rewrite an exchange
+// buffer after it has consumed data that every reader of the previous contents produced after
+// reading them (each step ends with all workgroups reading f of the last block).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "vrt_g3_internal.hpp"
+#include "vrt_internal.hpp"
+#include "vrt_q8_device.hpp"
+
+namespace vrt {
+
+typedef unsigned long long u64;
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// Address spaces. Pointers that reach device code through the parameter block are generic,
+// so every access would become a FLAT instruction (slower, and it makes the compiler wait on
+// both the vector-memory and the LDS counters); these casts restore global / constant
+// (scalar-load) addressing.
+#define VRT_AS_GLOBAL __attribute__((address_space(1)))
+#define VRT_AS_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ VRT_AS_GLOBAL T* gp(T* p) { return (VRT_AS_GLOBAL T*)p; }
+template <typename T>
+__device__ __forceinline__ const VRT_AS_GLOBAL T* gp(const T* p) { return (const VRT_AS_GLOBAL T*)p; }
+template <typename T>
+__device__ __forceinline__ const VRT_AS_CONST T* cp(const T* p) { return (const VRT_AS_CONST T*)p; }
+
+constexpr uint32_t kMkThreads = 512;         // 8 waves: two per SIMD
+constexpr uint32_t kMkWaves = kMkThreads / 64;
+constexpr uint32_t kVec = 4;                 // vector elements per thread (vectors <= 2048)
+constexpr uint32_t kSpinLimit = 1u << 21;    // polls before a hand-off is declared lost
+constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
+constexpr uint32_t kLmUnits = 3;             // 16-byte LM-head loads per thread per tile
+constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
+constexpr uint32_t kGrpPerWave = kGrp / kMkWaves;
+constexpr uint32_t kPartRound = 12 * kMkThreads;   // attention partials gathered per wait
+constexpr int kRsrcFlags = 0x00020000;       // raw buffer resource, 32-bit data format
+constexpr int kCoherent = 16;                // buffer-load cache policy: device scope (sc1)
+constexpr uint32_t kMarks = 32;              // sub-phase trace marks
+
+struct MkLayer {
+    const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    const float *attn_norm, *q_norm, *k_norm, *post_attn, *ffn_norm, *post_ffw;
+    float* kc;
+    float* vc;
+    uint32_t slots;
+    uint32_t global;
+};
+
+// Byte offsets of the dynamic LDS carve-up. `u` is phase-local scratch shared by the
+// attention partial sums (B), the gathered chunk partials (C) and the LM-head tile.
+struct MkLds {
+    uint32_t h, xs, la, lb, lc, ls, sq, sc, mw, gu, red, u, total;
+};
+
+constexpr uint32_t kMkLdsBytes = 120u * 1024u;   // static LDS of the persistent kernel
+
+struct MkParams {
+    uint32_t d, H, hd, F, V, L, ctx_len, eos;
+    float eps, emb_scale, attn_scale;
+    uint32_t nwg, nc, ne;          // workgroups: all, phase C, phase E
+    uint32_t chunk_min;            // attention: positions per chunk before splitting further
+    uint32_t lm_rows;              // LM-head rows per workgroup
+    uint32_t lm_tile_rows;         // rows per LDS tile
+    uint32_t trace_slots;          // phase timestamps per workgroup (0: tracing off)
+    MkLds lds;
+    const uint8_t* tok_embd;
+    const uint8_t* arena_end;
+    const float* out_norm;
+    const float *cos_l, *sin_l, *cos_g, *sin_g;
+    u64 *x_qkv, *x_part, *x_o, *x_g, *x_f, *x_am;
+    uint32_t* abort_flag;
+    G3State* st;
+    uint32_t* tokens;
+    vrt_argmax_result* results;
+    float* logits;
+    float* hidden;
+    uint64_t* trace;               // [nwg][trace_slots] s_memrealtime ticks of the first step
+};
+
+constexpr uint32_t kMkMaxLayers = 64;
+
+// The parameter block of the launch in flight, in constant memory: every access is a scalar
+// load through the scalar cache (no pointer chase through global memory on the critical path).
+// One block per device: persistent launches of different executors are serialised by the host.
+__constant__ MkParams g_mk;
+__constant__ MkLayer g_mk_layers[kMkMaxLayers];
+
+__shared__ __align__(16) unsigned char g_mk_lds[kMkLdsBytes];
+
+// ---- tagged exchange -----------------------------------------------------------------------
+
+__device__ __forceinline__ u64 ll_ld(const u64* p) {
+    return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_st(u64* p, uint32_t bits, uint32_t tag) {
+    __hip_atomic_store(gp(p), static_cast<u64>(bits) | (static_cast<u64>(tag) << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_stf(u64* p, float v, uint32_t tag) { ll_st(p, __float_as_uint(v), tag); }
+__device__ __forceinline__ void co_stf(float* p, float v) {
+    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes at byte `off` of a buffer, device-coherent (bypasses a possibly stale local L2).
+__device__ __forceinline__ v4u co_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, kCoherent);
+}
+__device__ __forceinline__ bool mk_aborted() {
+    return __hip_atomic_load(gp(g_mk.abort_flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+__device__ __forceinline__ void mk_abort() {
+    __hip_atomic_store(gp(g_mk.abort_flag), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void mk_flag_min(uint32_t v) {
+    __hip_atomic_fetch_min(gp(&g_mk.st->nonfinite), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls src[i] for i = tid + kMkThreads * k (k < MAXK, i < n) until every tag equals `tag`;
+// the values land in out[k]. Returns 0, or 1 if the wait was abandoned (abort raised).
+// The caller turns the per-thread result into a workgroup decision at its next barrier.
+template <int MAXK>
+__device__ __forceinline__ int ll_wait(const u64* src, uint32_t n, uint32_t tag, float (&out)[MAXK]) {
+    u64 v[MAXK];
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        const uint32_t i = t + static_cast<uint32_t>(k) * kMkThreads;
+        v[k] = ll_ld(src + (i < n ? i : n - 1u));   // branch-free: clamped, ignored past n
+    }
+    int fail = 0;
+    uint32_t spins = 0;
+    for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k)
+            ready &= static_cast<uint32_t>(v[k] >> 32) == tag || t + static_cast<uint32_t>(k) * kMkThreads >= n;
+        if (ready) break;
+        if ((++spins & 63u) == 0u && (spins > kSpinLimit || mk_aborted())) {
+            fail = 1;
+            mk_abort();
+            break;
+        }
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) {
+            const uint32_t i = t + static_cast<uint32_t>(k) * kMkThreads;
+            if (i < n && static_cast<uint32_t>(v[k] >> 32) != tag) v[k] = ll_ld(src + i);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) out[k] = __uint_as_float(static_cast<uint32_t>(v[k]));
+    return fail;
+}
+
+// ll_wait into LDS dst[0..n), then a barrier; false (in every thread) if abandoned.
+template <int MAXK>
+__device__ __forceinline__ bool ll_gather(const u64* src, uint32_t n, uint32_t tag, float* dst) {
+    float v[MAXK];
+    const int fail = ll_wait<MAXK>(src, n, tag, v);
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        const uint32_t i = threadIdx.x + static_cast<uint32_t>(k) * kMkThreads;
+        if (i < n) dst[i] = v[k];
+    }
+    return __syncthreads_or(fail) == 0;
+}
+
+// ---- workgroup reductions (one barrier each) ----------------------------------------------------
+
+struct BlkRed {
+    double* red;   // LDS: [2][kMkWaves] sums, then [2][kMkWaves] flags as doubles
+    uint32_t n;    // calls so far: slots alternate, so a slot is rewritten only two barriers later
+};
+
+// Workgroup sum of v (fixed order: DPP within each wave, then waves 0..7), and the OR of flag.
+__device__ __forceinline__ double blk_sum(BlkRed& R, double v, int& flag) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t slot = (R.n++ & 1u) * kMkWaves;
+    v = wave_red_sum_d(v);
+    const float f = wave_red_max(flag ? 1.0f : 0.0f);
+    if (lane == 0) {
+        R.red[slot + wave] = v;
+        R.red[2u * kMkWaves + slot + wave] = f;
+    }
+    __syncthreads();
+    double s = 0.0, fl = 0.0;
+#pragma unroll
+    for (uint32_t k = 0; k < kMkWaves; ++k) {
+        s += R.red[slot + k];
+        fl += R.red[2u * kMkWaves + slot + k];
+    }
+    flag = fl != 0.0;
+    return s;
+}
+
+// 1.0f / std::sqrt(float(sum_sq / n) + eps) (src/gemma3.cpp:967-983).
+__device__ __forceinline__ float mk_rms_scale(double ss, uint32_t n, float eps) {
+#pragma clang fp contract(off)
+    return 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(n)) + eps);
+}
+
+__device__ __forceinline__ float mk_gelu(float x) {
+#pragma clang fp contract(off)
+    const float kSqrt2OverPi = 0.7978845608028654f;
+    const float kCubic = 0.044715f;
+    const float cubic = x * x * x;
+    return 0.5f * x * (1.0f + tanhf(kSqrt2OverPi * (x + kCubic * cubic)));
+}
+
+// ---- LDS views -----------------------------------------------------------------------------
+
+struct MkSmem {
+    float* h;       // residual stream: element i belongs to thread i % kMkThreads
+    float* xs;      // matvec input
+    LimbLds L;      // LM-head activation limbs
+    float* sq;      // phase B: q | k | v
+    float* sc;      // phase B scores; argmax partials
+    float* mw;      // phase B/C per-head scalars
+    float* gu;      // phase D gate/up values of this workgroup
+    double* red;    // block reductions
+    float* u;       // phase-local scratch
+};
+
+__device__ __forceinline__ MkSmem mk_smem() {
+    unsigned char* smem = g_mk_lds;
+    MkSmem m;
+    m.h = reinterpret_cast<float*>(smem + g_mk.lds.h);
+    m.xs = reinterpret_cast<float*>(smem + g_mk.lds.xs);
+    m.L = LimbLds{reinterpret_cast<int8_t*>(smem + g_mk.lds.la), reinterpret_cast<int8_t*>(smem + g_mk.lds.lb),
+                  reinterpret_cast<int8_t*>(smem + g_mk.lds.lc), reinterpret_cast<float*>(smem + g_mk.lds.ls)};
+    m.sq = reinterpret_cast<float*>(smem + g_mk.lds.sq);
+    m.sc = reinterpret_cast<float*>(smem + g_mk.lds.sc);
+    m.mw = reinterpret_cast<float*>(smem + g_mk.lds.mw);
+    m.gu = reinterpret_cast<float*>(smem + g_mk.lds.gu);
+    m.red = reinterpret_cast<double*>(smem + g_mk.lds.red);
+    m.u = reinterpret_cast<float*>(smem + g_mk.lds.u);
+    return m;
+}
+
+__device__ __forceinline__ void split_range(uint32_t total, uint32_t parts, uint32_t idx, uint32_t& a, uint32_t& b) {
+    a = static_cast<uint32_t>(static_cast<uint64_t>(total) * idx / parts);
+    b = static_cast<uint32_t>(static_cast<uint64_t>(total) * (idx + 1u) / parts);
+}
+
+// Attention split of a history of `hist` positions: number of chunks and chunk length.
+// Chunk c runs on workgroup nwg - 1 - c; every other workgroup produces rows in phases A and
+// D. So every workgroup either produces in A/D or publishes an attention chunk, which is what
+// makes rewriting an exchange buffer safe once its successors' data has arrived.
+__device__ __forceinline__ void attn_split(uint32_t hist, uint32_t chunk_min, uint32_t& nch, uint32_t& clen) {
+    nch = min(kMaxChunks, (hist + chunk_min - 1u) / chunk_min);
+    clen = (hist + nch - 1u) / nch;
+}
+
+__device__ __forceinline__ uint32_t n_chunks(uint32_t slots, uint32_t pos) {
+    uint32_t nch, clen;
+    attn_split(min(pos + 1u, slots), g_mk.chunk_min, nch, clen);
+    return nch;
+}
+
+// Loads this thread's elements i = tid + kMkThreads * k of a static vector (norm weights).
+__device__ __forceinline__ void vec_load(const float* src, uint32_t n, float (&r)[kVec]) {
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = threadIdx.x + k * kMkThreads;
+        r[k] = gp(src)[i < n ? i : n - 1u];   // branch-free: clamped, then ignored past n
+    }
+}
+
+__device__ __forceinline__ double vec_sumsq(const float (&r)[kVec], uint32_t n) {
+    double acc = 0.0;
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k)
+        if (threadIdx.x + k * kMkThreads < n) acc += static_cast<double>(r[k]) * static_cast<double>(r[k]);
+    return acc;
+}
+
+__device__ __forceinline__ int vec_nonfinite(const float (&r)[kVec], uint32_t n) {
+    int bad = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k)
+        if (threadIdx.x + k * kMkThreads < n) bad |= !__builtin_isfinite(r[k]);
+    return bad;
+}
+
+// ---- LM head tiles ---------------------------------------------------------------------------
+
+// One 34-byte block at byte `off` (even) of an LDS tile whose base is 16-byte aligned; up to
+// 4 bytes past the block are read.
+__device__ __forceinline__ void q8_load_lds(const uint8_t* tile, uint32_t off, Q8Raw& r) {
+    const uint32_t sh = (off + 2u) & 3u;
+    const uint32_t* lb = reinterpret_cast<const uint32_t*>(tile + (off + 2u - sh));
+    r.sh = sh;
+    r.sbits = *reinterpret_cast<const uint16_t*>(tile + off);
+#pragma unroll
+    for (int j = 0; j < 9; ++j) r.d[j] = lb[j];
+}
+
+struct LmTile {
+    v4u u[kLmUnits];
+};
+
+// Loads rows [r0, r1) of the LM head (16-byte units of the 16-byte aligned span) into
+// registers. Branch-free: units past the span re-load its last unit. The host only enables
+// this kernel when the table is followed by at least 16 readable bytes of the arena.
+__device__ __forceinline__ void lm_tile_load(uint32_t r0, uint32_t r1, uint64_t row_bytes, LmTile& t,
+                                             uint32_t& pre, uint32_t& n16) {
+    const uintptr_t s = reinterpret_cast<uintptr_t>(g_mk.tok_embd) + static_cast<uint64_t>(r0) * row_bytes;
+    const uintptr_t a0 = s & ~uintptr_t(15);
+    pre = static_cast<uint32_t>(s - a0);
+    const uint64_t nbytes = pre + static_cast<uint64_t>(r1 - r0) * row_bytes;
+    n16 = static_cast<uint32_t>((nbytes + 15u) / 16u);
+#pragma unroll
+    for (uint32_t k = 0; k < kLmUnits; ++k) {
+        const uint32_t j = threadIdx.x + k * kMkThreads;
+        const uintptr_t p = a0 + static_cast<uintptr_t>(j < n16 ? j : n16 - 1u) * 16u;
+        t.u[k] = __builtin_nontemporal_load(reinterpret_cast<const VRT_AS_GLOBAL v4u*>(p));
+    }
+}
+
+__device__ __forceinline__ void lm_tile_store(const LmTile& t, uint32_t n16, uint8_t* lds) {
+#pragma unroll
+    for (uint32_t k = 0; k < kLmUnits; ++k) {
+        const uint32_t j = threadIdx.x + k * kMkThreads;
+        if (j < n16) *reinterpret_cast<v4u*>(lds + 16u * j) = t.u[k];
+    }
+}
+
+// =============================================================================================
+// Phases (each its own function, so every phase gets the whole register budget)
+// =============================================================================================
+
+#define MK_LOCALS                                                                                            \
+    const MkSmem m = mk_smem();                                                                             \
+    const uint32_t w = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;                    \
+    const uint32_t d = g_mk.d, H = g_mk.H, hd = g_mk.hd, F = g_mk.F, L = g_mk.L;                                           \
+    const uint32_t qw = H * hd, nqkv = qw + 2u * hd, half = hd >> 1, part_stride = qw + 2u * H;             \
+    const uint32_t nblk_d = d >> 5, nblk_a = qw >> 5, nblk_f = F >> 5;                                      \
+    const uint64_t rb_d = static_cast<uint64_t>(nblk_d) * 34u, rb_a = static_cast<uint64_t>(nblk_a) * 34u,  \
+                   rb_f = static_cast<uint64_t>(nblk_f) * 34u;                                              \
+    BlkRed R{m.red, 0u};                                                                                     \
+    (void)w; (void)tid; (void)lane; (void)wave; (void)d; (void)H; (void)hd; (void)F; (void)L; (void)qw;     \
+    (void)nqkv; (void)half; (void)part_stride; (void)nblk_d; (void)nblk_a; (void)nblk_f; (void)rb_d;         \
+    (void)rb_a; (void)rb_f; (void)R
+
+// Sub-phase mark k (< kMarks) of the traced block, in the last kMarks trace slots.
+#define MK_MARK(k)                                                                                        \
+    do {                                                                                                  \
+        if (tr && tid == 0u)                                                                              \
+            gp(g_mk.trace)[w * g_mk.trace_slots + g_mk.trace_slots - kMarks + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+
+// Scalar (uniform) copies of a phase's arguments: function arguments arrive in vector
+// registers, which would turn every parameter-block access into a vector load.
+#define MK_UNIFORM(x) x = __builtin_amdgcn_readfirstlane(x)
+
+#define MK_TAGS(l)                                                                                   \
+    const uint32_t tA = tagb + 5u * (l) + 1u, tB = tA + 1u, tC = tA + 2u, tD = tA + 3u, tE = tA + 4u; \
+    (void)tA; (void)tB; (void)tC; (void)tD; (void)tE
+
+// The first workgroup of the attention chunks: chunks run on the last workgroups, away from
+// the O-projection and down-projection workgroups (the first ones).
+__device__ __forceinline__ uint32_t chunk_of(uint32_t w, uint32_t nwg) { return nwg - 1u - w; }
+
+// Phase A: fold f of block l-1 into h, RMSNorm(attn_norm), rows of [Wq | Wk | Wv].
+template <int SD>
+__device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(l);
+    MK_UNIFORM(tagb);
+    MK_UNIFORM(pos);
+    MK_TAGS(l);
+    const MkLayer& Ly = g_mk_layers[l];
+    MK_MARK(0);
+    float wpost[kVec], wattn[kVec], hv[kVec];
+    vec_load(Ly.attn_norm, d, wattn);
+    if (l > 0) vec_load(g_mk_layers[l - 1u].post_ffw, d, wpost);
+    // producers: every workgroup that is not an attention chunk of this block at this position
+    uint32_t v0 = 0, v1 = 0;
+    const uint32_t nprod = g_mk.nwg - n_chunks(Ly.slots, pos);
+    if (w < nprod) split_range(nqkv, nprod, w, v0, v1);
+    const uint8_t *wq = Ly.wq, *wk = Ly.wk, *wv = Ly.wv;
+    auto rowp = [=](uint32_t v) -> const uint8_t* {
+        return v < qw ? wq + static_cast<uint64_t>(v) * rb_d
+                      : (v < qw + hd ? wk + static_cast<uint64_t>(v - qw) * rb_d
+                                     : wv + static_cast<uint64_t>(v - qw - hd) * rb_d);
+    };
+    RowBatch<SD, 1, 1> rb;
+    batch_load<SD, 1, 1>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
+    MK_MARK(1);
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = tid + k * kMkThreads;
+        hv[k] = i < d ? m.h[i] : 0.0f;
+    }
+    if (l > 0) {
+        float f[kVec];
+        int fail = ll_wait<kVec>(g_mk.x_f, d, tagb + 5u * (l - 1u) + 5u, f);
+        MK_MARK(2);
+        const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(f, d), fail), d, g_mk.eps);
+        if (fail) return false;
+#pragma unroll
+        for (uint32_t k = 0; k < kVec; ++k) hv[k] = f[k] * (sc * wpost[k]) + hv[k];   // src/gemma3.cpp:1849-1855
+    }
+    int bad = vec_nonfinite(hv, d);
+    const float sc2 = mk_rms_scale(blk_sum(R, vec_sumsq(hv, d), bad), d, g_mk.eps);
+    if (bad && w == 0 && tid == 0 && l > 0) mk_flag_min(l - 1u);   // :1857-1863
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = tid + k * kMkThreads;
+        if (i < d) {
+            m.h[i] = hv[k];
+            m.xs[i] = hv[k] * sc2 * wattn[k];                                      // :991-996
+        }
+    }
+    __syncthreads();
+    MK_MARK(3);
+    u64* out = g_mk.x_qkv;
+    batch_consume_x<SD, 1, 1>(rb, nblk_d, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tA); });
+    MK_MARK(5);
+    return true;
+}
+
+// Phase B: QK-norm, RoPE, KV append and attention over one chunk of the history; publishes
+// per head the chunk max m, the sum l of exp(s - m) and acc = sum exp(s - m) v.
+__device__ __attribute__((noinline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(l);
+    MK_UNIFORM(tagb);
+    MK_UNIFORM(pos);
+    MK_TAGS(l);
+    const MkLayer& Ly = g_mk_layers[l];
+    const uint32_t hist = min(pos + 1u, Ly.slots);
+    const uint32_t t_first = pos + 1u - hist;
+    uint32_t nch, clen;
+    attn_split(hist, g_mk.chunk_min, nch, clen);
+    const uint32_t c = chunk_of(w, g_mk.nwg);
+    if (c >= nch) return true;
+    MK_MARK(6);
+    const uint32_t c0 = t_first + c * clen;
+    const uint32_t c1 = min(pos + 1u, c0 + clen);
+    const uint32_t dl = lane * 4u;                 // this lane's 4 head dims
+    const bool dlive = dl < hd;
+    // static inputs first: norm weights and this position's RoPE rows
+    float wn[kVec], cs[kVec], sn[kVec];
+    {
+        const VRT_AS_GLOBAL float* ct = gp(Ly.global ? g_mk.cos_g : g_mk.cos_l) + static_cast<uint64_t>(pos) * half;
+        const VRT_AS_GLOBAL float* st = gp(Ly.global ? g_mk.sin_g : g_mk.sin_l) + static_cast<uint64_t>(pos) * half;
+#pragma unroll
+        for (uint32_t k = 0; k < kVec; ++k) {
+            const uint32_t i = tid + k * kMkThreads;          // element of [q heads | k | v]
+            const uint32_t e = i % hd;
+            wn[k] = i < qw ? gp(Ly.q_norm)[e] : (i < qw + hd ? gp(Ly.k_norm)[e] : 1.0f);
+            cs[k] = (i < qw + hd && e < half) ? ct[e] : 0.0f;
+            sn[k] = (i < qw + hd && e < half) ? st[e] : 0.0f;
+        }
+    }
+    // this wave's K/V rows of the first 32-position group, from the cache (device-coherent)
+    const uint32_t kv_bytes = Ly.slots * hd * 4u;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
+    v4u kr[kGrpPerWave], vr[kGrpPerWave];
+    auto load_grp = [&](uint32_t g0, uint32_t g1) {
+#pragma unroll
+        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
+            const uint32_t t = g0 + wave + kMkWaves * i;
+            if (t < g1 && t != pos && dlive) {
+                const uint32_t off = ((t % Ly.slots) * hd + dl) * 4u;
+                kr[i] = co_ld4(rk, off);
+                vr[i] = co_ld4(rv, off);
+            }
+        }
+    };
+    load_grp(c0, min(c1, c0 + kGrp));
+    float qv[kVec];
+    int fail = ll_wait<kVec>(g_mk.x_qkv, nqkv, tA, qv);
+    MK_MARK(7);
+    // QK-norm (src/gemma3.cpp:1045-1104): per head sum of squares, H q heads then k
+    {
+        double hs[9];
+#pragma unroll
+        for (uint32_t h = 0; h < 9u; ++h) hs[h] = 0.0;
+#pragma unroll
+        for (uint32_t k = 0; k < kVec; ++k) {
+            const uint32_t i = tid + k * kMkThreads;
+            const uint32_t h = i / hd;
+#pragma unroll
+            for (uint32_t hh = 0; hh < 9u; ++hh)
+                if (hh == h && i < qw + hd) hs[hh] += static_cast<double>(qv[k]) * static_cast<double>(qv[k]);
+        }
+        double* red = m.red + 4u * kMkWaves;   // [9][waves] past the blk_sum slots
+#pragma unroll
+        for (uint32_t hh = 0; hh < 9u; ++hh) {
+            if (hh <= H) {
+                const double r = wave_red_sum_d(hs[hh]);
+                if (lane == 0) red[hh * kMkWaves + wave] = r;
+            }
+        }
+        if (__syncthreads_or(fail)) return false;
+#pragma unroll
+        for (uint32_t k = 0; k < kVec; ++k) {
+            const uint32_t i = tid + k * kMkThreads;
+            if (i < qw + hd) {
+                const uint32_t h = i / hd;
+                double ss = 0.0;
+#pragma unroll
+                for (uint32_t q = 0; q < kMkWaves; ++q) ss += red[h * kMkWaves + q];
+                qv[k] *= mk_rms_scale(ss, hd, g_mk.eps) * wn[k];
+            }
+            if (i < nqkv) m.sq[i] = qv[k];
+        }
+    }
+    __syncthreads();
+    // RoPE (src/gemma3.cpp:1371-1424): the thread holding element e < half of a q/k head
+    // rotates the pair (e, e + half)
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = tid + k * kMkThreads;
+        if (i < qw + hd && (i % hd) < half) {
+            const float a = m.sq[i], b = m.sq[i + half];
+            m.sq[i] = a * cs[k] - b * sn[k];
+            m.sq[i + half] = b * cs[k] + a * sn[k];
+        }
+    }
+    __syncthreads();
+    MK_MARK(8);
+    const float* sk = m.sq + qw;
+    const float* sv = sk + hd;
+    // KV append by the chunk that holds the current position (src/gemma3.cpp:1590-1600)
+    if (c1 == pos + 1u) {
+        const uint64_t slot = static_cast<uint64_t>(pos % Ly.slots) * hd;
+        for (uint32_t i = tid; i < hd; i += kMkThreads) {
+            co_stf(Ly.kc + slot + i, sk[i]);
+            co_stf(Ly.vc + slot + i, sv[i]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);   // complete before anything this workgroup publishes later
+    }
+    float qr[8][4];
+#pragma unroll
+    for (uint32_t h = 0; h < 8u; ++h)
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) qr[h][e] = (h < H && dlive) ? m.sq[h * hd + dl + e] : 0.0f;
+    // online softmax over 32-position groups; acc is this wave's partial over its positions
+    float acc[8][4];
+    float m_run[8], l_run[8];
+#pragma unroll
+    for (uint32_t h = 0; h < 8u; ++h) {
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.0f;
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) acc[h][e] = 0.0f;
+    }
+    float* sc = m.sc;   // [8][kGrp]: scores, then exp weights
+    for (uint32_t g0 = c0; g0 < c1; g0 += kGrp) {
+        const uint32_t g1 = min(c1, g0 + kGrp);
+        if (g0 != c0) load_grp(g0, g1);
+#pragma unroll
+        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
+            const uint32_t t = g0 + wave + kMkWaves * i;
+            if (t == pos && dlive) {
+                kr[i] = v4u{__float_as_uint(sk[dl]), __float_as_uint(sk[dl + 1]), __float_as_uint(sk[dl + 2]),
+                            __float_as_uint(sk[dl + 3])};
+                vr[i] = v4u{__float_as_uint(sv[dl]), __float_as_uint(sv[dl + 1]), __float_as_uint(sv[dl + 2]),
+                            __float_as_uint(sv[dl + 3])};
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
+            const uint32_t t = g0 + wave + kMkWaves * i;
+            if (t < g1) {   // wave-uniform
+#pragma unroll
+                for (uint32_t h = 0; h < 8u; ++h) {
+                    if (h < H) {
+                        float p = 0.0f;
+                        if (dlive)   // lanes past head_dim hold no key
+#pragma unroll
+                            for (uint32_t e = 0; e < 4u; ++e) p += qr[h][e] * __uint_as_float(kr[i][e]);
+                        p = wave_red_sum(p);
+                        if (lane == 0) sc[h * kGrp + (t - g0)] = p * g_mk.attn_scale;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const uint32_t n = g1 - g0;
+#pragma unroll
+        for (uint32_t h = 0; h < 8u; ++h) {
+            if (h >= H || h % kMkWaves != wave) continue;
+            const float mx = wave_red_max(lane < n ? sc[h * kGrp + lane] : -INFINITY);
+            const float m_new = fmaxf(m_run[h], mx);
+            float e = 0.0f;
+            if (lane < n) {
+                e = expf(sc[h * kGrp + lane] - m_new);
+                sc[h * kGrp + lane] = e;
+            }
+            const float ls = wave_red_sum(e);
+            if (lane == 0) { m.mw[h] = m_new; m.mw[8u + h] = ls; }
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t h = 0; h < 8u; ++h) {
+            if (h < H) {
+                const float m_new = m.mw[h];
+                const float r = m_run[h] == -INFINITY ? 0.0f : expf(m_run[h] - m_new);
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) acc[h][e] *= r;
+                l_run[h] = l_run[h] * r + m.mw[8u + h];
+                m_run[h] = m_new;
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
+            const uint32_t t = g0 + wave + kMkWaves * i;
+            if (t < g1 && dlive) {
+#pragma unroll
+                for (uint32_t h = 0; h < 8u; ++h) {
+                    if (h < H) {
+                        const float pw = sc[h * kGrp + (t - g0)];
+#pragma unroll
+                        for (uint32_t e = 0; e < 4u; ++e) acc[h][e] += pw * __uint_as_float(vr[i][e]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    MK_MARK(9);
+    // sum the waves' partials and publish {acc[H][hd], m[H], l[H]}
+    float* ra = m.u;   // [waves][H * hd]
+    if (dlive) {
+#pragma unroll
+        for (uint32_t h = 0; h < 8u; ++h)
+            if (h < H)
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) ra[wave * qw + h * hd + dl + e] = acc[h][e];
+    }
+    __syncthreads();
+    u64* part = g_mk.x_part + static_cast<uint64_t>(c) * part_stride;
+    for (uint32_t idx = tid; idx < qw; idx += kMkThreads) {
+        float sacc = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < kMkWaves; ++k) sacc += ra[k * qw + idx];
+        ll_stf(part + idx, sacc, tB);
+    }
+    if (tid < H) {
+#pragma unroll
+        for (uint32_t h = 0; h < 8u; ++h) {
+            if (h == tid) {
+                ll_stf(part + qw + h, m_run[h], tB);
+                ll_stf(part + qw + H + h, l_run[h], tB);
+            }
+        }
+    }
+    MK_MARK(10);
+    return true;
+}
+
+// Phase C: merge the chunks (att = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c), Wo rows.
+template <int SA>
+__device__ __attribute__((noinline)) bool mk_phase_c(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(l);
+    MK_UNIFORM(tagb);
+    MK_UNIFORM(pos);
+    MK_TAGS(l);
+    const MkLayer& Ly = g_mk_layers[l];
+    if (w >= g_mk.nc) return true;
+    MK_MARK(11);
+    const uint32_t hist = min(pos + 1u, Ly.slots);
+    uint32_t nch, clen;
+    attn_split(hist, g_mk.chunk_min, nch, clen);
+    uint32_t v0, v1;
+    split_range(d, g_mk.nc, w, v0, v1);
+    const uint8_t* wo = Ly.wo;
+    auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
+    RowBatch<SA, 1, 1> rb;
+    batch_load<SA, 1, 1>(rowp, nblk_a, g_mk.arena_end, v0, v1, wave, rb);
+    float* parts = m.u;
+    const uint32_t ntot = nch * part_stride;
+    for (uint32_t o = 0; o < ntot; o += kPartRound)
+        if (!ll_gather<kPartRound / kMkThreads>(g_mk.x_part + o, min(kPartRound, ntot - o), tB, parts + o)) return false;
+    MK_MARK(12);
+    float* wts = m.mw;   // [8][kMaxChunks] weights, then den [8]
+    if (tid < H) {
+        const uint32_t h = tid;
+        float M = -INFINITY;
+        for (uint32_t q = 0; q < nch; ++q) M = fmaxf(M, parts[q * part_stride + qw + h]);
+        double den = 0.0;
+        for (uint32_t q = 0; q < nch; ++q) {
+            const float e = expf(parts[q * part_stride + qw + h] - M);
+            wts[h * kMaxChunks + q] = e;
+            den += static_cast<double>(e) * static_cast<double>(parts[q * part_stride + qw + H + h]);
+        }
+        wts[8u * kMaxChunks + h] = static_cast<float>(den);
+        if (!(den > 0.0) || !__builtin_isfinite(den)) mk_flag_min(0x40000000u | l);   // :1666-1670
+    }
+    __syncthreads();
+    for (uint32_t idx = tid; idx < qw; idx += kMkThreads) {
+        const uint32_t h = idx / hd;
+        float num = 0.0f;
+        for (uint32_t q = 0; q < nch; ++q) num += wts[h * kMaxChunks + q] * parts[q * part_stride + idx];
+        m.xs[idx] = num / wts[8u * kMaxChunks + h];
+    }
+    __syncthreads();
+    MK_MARK(13);
+    u64* out = g_mk.x_o;
+    batch_consume_x<SA, 1, 1>(rb, nblk_a, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tC); });
+    MK_MARK(14);
+    return true;
+}
+
+// Phase D: h = RMSNorm(o, post_attn) + h, x = RMSNorm(h, ffn_norm), gate/up row pairs,
+// g = gelu_tanh(gate) * up (src/gemma3.cpp:1703-1801, shaders/gelu_mul.comp:23-31).
+template <int SD>
+__device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(l);
+    MK_UNIFORM(tagb);
+    MK_UNIFORM(pos);
+    MK_TAGS(l);
+    const MkLayer& Ly = g_mk_layers[l];
+    MK_MARK(15);
+    float wpa[kVec], wffn[kVec], hv[kVec], o[kVec];
+    vec_load(Ly.post_attn, d, wpa);
+    vec_load(Ly.ffn_norm, d, wffn);
+    uint32_t p0 = 0, p1 = 0;
+    const uint32_t nprod = g_mk.nwg - n_chunks(Ly.slots, pos);
+    if (w < nprod) split_range(F, nprod, w, p0, p1);
+    const uint32_t v0 = 2u * p0, v1 = 2u * p1;
+    const uint8_t *wg = Ly.wg, *wu = Ly.wu;
+    auto rowp = [=](uint32_t v) { return ((v & 1u) ? wu : wg) + static_cast<uint64_t>(v >> 1) * rb_d; };
+    RowBatch<SD, 1, 2> rb;
+    batch_load<SD, 1, 2>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = tid + k * kMkThreads;
+        hv[k] = i < d ? m.h[i] : 0.0f;
+    }
+    int fail = ll_wait<kVec>(g_mk.x_o, d, tC, o);
+    MK_MARK(16);
+    const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(o, d), fail), d, g_mk.eps);
+    if (fail) return false;
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) hv[k] = o[k] * (sc * wpa[k]) + hv[k];      // :1703-1711
+    int none = 0;
+    const float sc2 = mk_rms_scale(blk_sum(R, vec_sumsq(hv, d), none), d, g_mk.eps);
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = tid + k * kMkThreads;
+        if (i < d) {
+            m.h[i] = hv[k];
+            m.xs[i] = hv[k] * sc2 * wffn[k];                                         // :1713-1718
+        }
+    }
+    __syncthreads();
+    MK_MARK(17);
+    float* gu = m.gu;
+    batch_consume_x<SD, 1, 2>(rb, nblk_d, m.xs, [&](uint32_t v, float val) { gu[v - v0] = val; });
+    __syncthreads();
+    MK_MARK(18);
+    u64* out = g_mk.x_g;
+    for (uint32_t r = p0 + tid; r < p1; r += kMkThreads) {
+        const uint32_t j = (r - p0) * 2u;
+        ll_stf(out + r, mk_gelu(gu[j]) * gu[j + 1u], tD);
+    }
+    MK_MARK(19);
+    return true;
+}
+
+// Phase E: down-projection rows -> f.
+template <int SF>
+__device__ __attribute__((noinline)) bool mk_phase_e(uint32_t l, uint32_t tagb, bool tr) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(l);
+    MK_UNIFORM(tagb);
+    MK_TAGS(l);
+    const MkLayer& Ly = g_mk_layers[l];
+    if (w >= g_mk.ne) return true;
+    MK_MARK(20);
+    uint32_t v0, v1;
+    split_range(d, g_mk.ne, w, v0, v1);
+    const uint8_t* wd = Ly.wd;
+    auto rowp = [=](uint32_t v) { return wd + static_cast<uint64_t>(v) * rb_f; };
+    RowBatch<SF, 1, 1> rb;
+    batch_load<SF, 1, 1>(rowp, nblk_f, g_mk.arena_end, v0, v1, wave, rb);
+    if (!ll_gather<kVec>(g_mk.x_g, F, tD, m.xs)) return false;
+    MK_MARK(21);
+    u64* out = g_mk.x_f;
+    batch_consume_x<SF, 1, 1>(rb, nblk_f, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tE); });
+    MK_MARK(22);
+    return true;
+}
+
+// End of the step: fold the last block's f into h, output norm (src/gemma3.cpp:1866-1868);
+// the normed hidden state goes to xs (LM head input) and, from workgroup 0, to g_mk.hidden.
+__device__ __attribute__((noinline)) bool mk_phase_fold(uint32_t tagb) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(tagb);
+    float wpost[kVec], wout[kVec], hv[kVec], f[kVec];
+    vec_load(g_mk_layers[L - 1u].post_ffw, d, wpost);
+    vec_load(g_mk.out_norm, d, wout);
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = tid + k * kMkThreads;
+        hv[k] = i < d ? m.h[i] : 0.0f;
+    }
+    int fail = ll_wait<kVec>(g_mk.x_f, d, tagb + 5u * (L - 1u) + 5u, f);
+    const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(f, d), fail), d, g_mk.eps);
+    if (fail) return false;
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) hv[k] = f[k] * (sc * wpost[k]) + hv[k];
+    int bad = vec_nonfinite(hv, d);
+    const float sc3 = mk_rms_scale(blk_sum(R, vec_sumsq(hv, d), bad), d, g_mk.eps);
+    if (bad && w == 0 && tid == 0) mk_flag_min(L - 1u);
+#pragma unroll
+    for (uint32_t k = 0; k < kVec; ++k) {
+        const uint32_t i = tid + k * kMkThreads;
+        if (i < d) {
+            const float hn = hv[k] * (sc3 * wout[k]);
+            m.h[i] = hv[k];
+            m.xs[i] = hn;
+            if (w == 0) gp(g_mk.hidden)[i] = hn;
+        }
+    }
+    __syncthreads();
+    return true;
+}
+
+// Tied Q8_0 LM head over this workgroup's rows, local greedy argmax published with tag tLM.
+template <int SD>
+__device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tLM, uint32_t want_logits, bool tr) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(tLM);
+    MK_UNIFORM(want_logits);
+    __shared__ float s_v[kMkWaves];
+    __shared__ uint32_t s_i[kMkWaves];
+    const uint32_t r_begin = min(g_mk.V, w * g_mk.lm_rows), r_end = min(g_mk.V, r_begin + g_mk.lm_rows);
+    const uint32_t TR = g_mk.lm_tile_rows;
+    const uint32_t ntiles = (r_end - r_begin + TR - 1u) / TR;
+    // first two tiles in flight before the limbs are built
+    LmTile tl0, tl1;
+    uint32_t pre0 = 0u, pre1 = 0u, n160 = 0u, n161 = 0u;
+    if (ntiles > 0) lm_tile_load(r_begin, min(r_end, r_begin + TR), rb_d, tl0, pre0, n160);
+    if (ntiles > 1) lm_tile_load(r_begin + TR, min(r_end, r_begin + 2u * TR), rb_d, tl1, pre1, n161);
+    MK_MARK(23);
+    build_limbs(m.xs, d, m.L);
+    XLimb xl[1];
+    lane_limbs<SD, 1>(m.L, nblk_d, xl);
+    MK_MARK(24);
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    constexpr uint32_t RPW = 64u / SD;
+    const uint32_t slot = lane / SD, sl = lane % SD;
+    uint8_t* tile = reinterpret_cast<uint8_t*>(m.u);
+    auto consume = [&](uint32_t ti, LmTile& tl, uint32_t& pre, uint32_t& n16) {
+        const uint32_t t0 = r_begin + ti * TR, t1 = min(r_end, t0 + TR);
+        lm_tile_store(tl, n16, tile);
+        const uint32_t pre_cur = pre;
+        __syncthreads();
+        if (ti + 2u < ntiles) {
+            const uint32_t n0 = r_begin + (ti + 2u) * TR;
+            lm_tile_load(n0, min(r_end, n0 + TR), rb_d, tl, pre, n16);
+        }
+        const uint32_t nrows = t1 - t0;
+        for (uint32_t rg = wave * RPW; rg < nrows; rg += kMkWaves * RPW) {   // wave-uniform trip count
+            const uint32_t r = rg + slot;
+            const bool live = r < nrows;
+            float acc = 0.0f;
+            if (live && sl < nblk_d) {
+                Q8Raw raw;
+                q8_load_lds(tile, pre_cur + r * static_cast<uint32_t>(rb_d) + 34u * sl, raw);
+                acc = q8_dot(raw, xl[0]);
+            }
+            float tot;
+            if constexpr (SD == 64) {
+                const float hsum = slot_sum<32>(acc);
+                tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 0)) +
+                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 32));
+            } else {
+                tot = slot_sum<SD>(acc);
+            }
+            if (live && sl == 0u) {
+                const uint32_t v = t0 + r;
+                if (want_logits) gp(g_mk.logits)[v] = tot;
+                if (am_better(tot, v, bv, bi)) { bv = tot; bi = v; }
+            }
+        }
+        __syncthreads();
+    };
+    for (uint32_t ti = 0; ti < ntiles; ti += 2u) {
+        consume(ti, tl0, pre0, n160);
+        if (ti == 0u) MK_MARK(25);
+        if (ti + 1u < ntiles) consume(ti + 1u, tl1, pre1, n161);
+    }
+    MK_MARK(26);
+    wave_argmax(bv, bi);
+    if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (uint32_t k = 1; k < kMkWaves; ++k)
+            if (am_better(s_v[k], s_i[k], s_v[0], s_i[0])) { s_v[0] = s_v[k]; s_i[0] = s_i[k]; }
+        ll_stf(g_mk.x_am + 2u * w, s_v[0], tLM);
+        ll_st(g_mk.x_am + 2u * w + 1u, s_i[0], tLM);
+    }
+    __syncthreads();
+    return true;
+}
+
+// Reduces the argmax partials tagged `tag` (every workgroup that calls it gets the same result).
+__device__ __attribute__((noinline)) bool mk_reduce_argmax(uint32_t tag, uint32_t& idx, float& val) {
+    MK_LOCALS;
+    MK_UNIFORM(tag);
+    __shared__ float s_v[kMkWaves];
+    __shared__ uint32_t s_i[kMkWaves];
+    float* buf = m.sc;   // 2 * nwg floats
+    const bool good = ll_gather<2>(g_mk.x_am, 2u * g_mk.nwg, tag, buf);
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t k = tid; k < g_mk.nwg; k += kMkThreads) {
+        const float v = buf[2u * k];
+        const uint32_t i = __float_as_uint(buf[2u * k + 1u]);
+        if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    wave_argmax(bv, bi);
+    if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
+    __syncthreads();
+    bv = s_v[0];
+    bi = s_i[0];
+    for (uint32_t k = 1; k < kMkWaves; ++k)
+        if (am_better(s_v[k], s_i[k], bv, bi)) { bv = s_v[k]; bi = s_i[k]; }
+    __syncthreads();
+    idx = bi;
+    val = bv;
+    return good;
+}
+
+// The step embedding: dequantised row * sqrt(d) (src/gemma3.cpp:1106-1136), this thread's
+// elements of h.
+__device__ __attribute__((noinline)) void mk_embed(uint32_t token) {
+#pragma clang fp contract(off)
+    MK_LOCALS;
+    MK_UNIFORM(token);
+    const VRT_AS_GLOBAL uint8_t* row = gp(g_mk.tok_embd) + static_cast<uint64_t>(token) * rb_d;
+    for (uint32_t i = tid; i < d; i += kMkThreads) {
+        const VRT_AS_GLOBAL uint8_t* b = row + (i >> 5) * 34u;
+        const float sc = half_bits_to_float(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
+        m.h[i] = (sc * static_cast<float>(static_cast<int8_t>(b[2 + (i & 31u)]))) * g_mk.emb_scale;
+    }
+}
+
+template <int SD, int SA, int SF>
+__global__ void __launch_bounds__(kMkThreads, 1)
+k_decode(uint32_t nsteps, uint32_t tag0) {
+    const uint32_t w = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t L = g_mk.L;
+    const uint32_t nph = 5u * L + 1u;   // tags per step
+
+    // step state (written by the host or the previous launch before this one started)
+    const uint32_t step0 = gp(g_mk.st)->step;
+    uint32_t stop = gp(g_mk.st)->stop;
+    const uint32_t lm_from = gp(g_mk.st)->lm_from;
+    const uint32_t feed_until = gp(g_mk.st)->feed_until;
+    const uint32_t want_logits = gp(g_mk.st)->want_logits;
+
+    uint32_t prev_lm_tag = 0;     // tag of the previous step's argmax partials (0: none)
+    uint32_t s = step0;
+    bool ok = true;
+#define MK_TRACE(k)                                                                                    \
+    do {                                                                                               \
+        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u)                                              \
+            gp(g_mk.trace)[w * g_mk.trace_slots + (k)] = __builtin_amdgcn_s_memrealtime();                       \
+    } while (0)
+
+    for (uint32_t si = 0; si < nsteps && ok; ++si, ++s) {
+        if (stop || s >= g_mk.ctx_len) break;
+        const uint32_t tagb = tag0 + si * nph;
+
+        // ---- token of this step ----
+        uint32_t token;
+        if (prev_lm_tag != 0u) {
+            uint32_t idx;
+            float val;
+            ok = mk_reduce_argmax(prev_lm_tag, idx, val);
+            if (!ok) break;
+            if (w == 0 && tid == 0) { VRT_AS_GLOBAL vrt_argmax_result* r = gp(g_mk.results) + (s - 1u); r->index = idx; r->value = val; }
+            if (s >= feed_until) {
+                token = idx < g_mk.V ? idx : 0u;
+                if (w == 0 && tid == 0) gp(g_mk.tokens)[s] = token;
+                if (idx == g_mk.eos) {   // generation ends after EOS (src/gemma3.cpp:2134-2141)
+                    stop = 1u;
+                    break;
+                }
+            } else {
+                token = gp(g_mk.tokens)[s];
+            }
+        } else {
+            token = gp(g_mk.tokens)[s];
+        }
+        prev_lm_tag = 0u;
+        MK_TRACE(0u);
+        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u)   // shader-clock ticks: clock = d(memtime) / d(realtime)
+            gp(g_mk.trace)[w * g_mk.trace_slots + g_mk.trace_slots - 2u] = __builtin_amdgcn_s_memtime();
+        mk_embed(token);
+
+        for (uint32_t l = 0; l < L && ok; ++l) {
+            const bool tr = g_mk.trace_slots != 0u && si == 0u && l == 1u;   // sub-phase marks of block 1
+            ok = mk_phase_a<SD>(l, s, tagb, tr);
+            MK_TRACE(5u * l + 1u);
+            ok = ok && mk_phase_b(l, s, tagb, tr);
+            MK_TRACE(5u * l + 2u);
+            ok = ok && mk_phase_c<SA>(l, s, tagb, tr);
+            MK_TRACE(5u * l + 3u);
+            ok = ok && mk_phase_d<SD>(l, s, tagb, tr);
+            MK_TRACE(5u * l + 4u);
+            ok = ok && mk_phase_e<SF>(l, tagb, tr);
+            MK_TRACE(5u * l + 5u);
+        }
+        ok = ok && mk_phase_fold(tagb);
+        if (!ok) break;
+        MK_TRACE(5u * L + 1u);
+        if (s >= lm_from) {   // LM head + local argmax (src/gemma3.cpp:1138-1185)
+            ok = mk_phase_lm<SD>(tagb + nph, want_logits, g_mk.trace_slots != 0u && si == 0u);
+            prev_lm_tag = tagb + nph;
+        }
+        MK_TRACE(5u * L + 2u);
+        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u)
+            gp(g_mk.trace)[w * g_mk.trace_slots + g_mk.trace_slots - 1u] = __builtin_amdgcn_s_memtime();
+    }
+#undef MK_TRACE
+
+    // ---- end of launch: workgroup 0 records the last step's result and the step state ----
+    if (w == 0) {
+        if (ok && prev_lm_tag != 0u) {
+            uint32_t idx;
+            float val;
+            ok = mk_reduce_argmax(prev_lm_tag, idx, val);
+            if (ok && tid == 0) {
+                { VRT_AS_GLOBAL vrt_argmax_result* r = gp(g_mk.results) + (s - 1u); r->index = idx; r->value = val; }
+                if (s >= feed_until) {
+                    gp(g_mk.tokens)[s] = idx < g_mk.V ? idx : 0u;
+                    if (idx == g_mk.eos) stop = 1u;
+                }
+            }
+        }
+        if (tid == 0) {
+            gp(g_mk.st)->step = s;
+            gp(g_mk.st)->stop = stop;
+            if (!ok) mk_flag_min(0x20000000u);
+        }
+    }
+}
+
+// =============================================================================================
+// Host side
+// =============================================================================================
+
+struct MkState {
+    MkParams P{};
+    std::vector<MkLayer> layers;   // host image of g_mk_layers
+    uint64_t version = 1;          // bumped whenever P changes
+    const void* fn = nullptr;
+    size_t lds_bytes = 0;
+    uint32_t grid = 0;
+    uint32_t trace_slots = 0;      // slots per workgroup when tracing is enabled
+    std::vector<void*> allocs;
+};
+
+// Who last wrote g_mk / g_mk_layers on a device, and the event after its last launch.
+constexpr int kMaxDevices = 64;
+struct MkDeviceSlot {
+    std::mutex mu;
+    const MkState* owner = nullptr;
+    uint64_t version = 0;
+    hipEvent_t last = nullptr;
+    hipStream_t last_stream = nullptr;
+};
+// Never destroyed: executors released during process exit may still lock it.
+static MkDeviceSlot* device_slots() {
+    static MkDeviceSlot* s = new MkDeviceSlot[kMaxDevices];
+    return s;
+}
+
+template <int SD, int SA, int SF>
+static const void* mk_fn() { return reinterpret_cast<const void*>(&k_decode<SD, SA, SF>); }
+
+static const void* mk_pick(int sd, int sa, int sf) {
+#define VRT_MK(a, b, c) if (sd == a && sa == b && sf == c) return mk_fn<a, b, c>();
+    VRT_MK(32, 32, 64)   // Gemma-3-270M: d 640, 4 x 256 heads, FFN 2048
+    VRT_MK(4, 4, 8)      // d 128, 2 x 64 heads, FFN 256 (test shape)
+    VRT_MK(32, 64, 64)
+    VRT_MK(16, 16, 32)
+    VRT_MK(8, 8, 16)
+#undef VRT_MK
+    return nullptr;
+}
+
+static int mk_alloc(MkState* mk, size_t bytes, void** out) {
+    void* p = nullptr;
+    VRT_HIP_CHECK(hipMalloc(&p, bytes + 256));
+    mk->allocs.push_back(p);
+    VRT_HIP_CHECK(hipMemset(p, 0, bytes + 256));
+    *out = p;
+    return VRT_OK;
+}
+
+void mk_destroy(vrt_g3* g) {
+    if (!g || !g->mk) return;
+    {
+        MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
+        std::lock_guard<std::mutex> lock(ds.mu);
+        if (ds.owner == g->mk) ds.owner = nullptr;
+    }
+    for (void* p : g->mk->allocs) (void)hipFree(p);
+    delete g->mk;
+    g->mk = nullptr;
+}
+
+int mk_setup(vrt_g3* g) {
+    const vrt_g3_config& c = g->cfg;
+    const uint32_t d = c.embedding_length, H = c.head_count, hd = c.head_dim, F = c.feed_forward_length;
+    const uint32_t qw = H * hd;
+    if (!g->use_persistent) return VRT_OK;
+    if (hd % 64u != 0u || hd > 256u || H > 8u || d > 2048u || F > 2048u || qw > 2048u) return VRT_OK;
+    if (c.block_count > kMkMaxLayers) return VRT_OK;
+    // branch-free block loads need even block counts (no block reads past its matrix), and the
+    // LM-head tile loads need 16 readable bytes after the table
+    if ((d / 32u) % 2u != 0u || (qw / 32u) % 2u != 0u || (F / 32u) % 2u != 0u) return VRT_OK;
+    if (static_cast<uint64_t>(g->P.tok_embd - (g->P.arena_end - g->arena_bytes)) +
+            static_cast<uint64_t>(c.vocab_size) * (d / 32u) * 34u + 16u > g->arena_bytes)
+        return VRT_OK;
+    MvShape sd, sa, sf;
+    if (!mv_shape(d, &sd) || !mv_shape(qw, &sa) || !mv_shape(F, &sf) || sd.NB != 1 || sa.NB != 1 || sf.NB != 1) return VRT_OK;
+    const void* fn = mk_pick(sd.S, sa.S, sf.S);
+    if (!fn) return VRT_OK;
+    int coop = 0;
+    VRT_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, g->ctx->device));
+    if (!coop) return VRT_OK;
+
+    auto* mk = new (std::nothrow) MkState();
+    VRT_REQUIRE(mk != nullptr, "out of memory");
+    g->mk = mk;
+    MkParams& P = mk->P;
+    const uint32_t nwg = g->ctx->info.compute_units;
+    const uint32_t cap_d = kMkWaves * (64u / static_cast<uint32_t>(sd.S));
+    const uint32_t cap_a = kMkWaves * (64u / static_cast<uint32_t>(sa.S));
+    const uint32_t cap_f = kMkWaves * (64u / static_cast<uint32_t>(sf.S));
+    const uint32_t nqkv = qw + 2u * hd;
+    // every workgroup must cover its share of the all-workgroup phases in one batch
+    const uint32_t nprod = nwg - kMaxChunks;
+    if (nwg < 2u * kMaxChunks || nwg > 512u || (nqkv + nprod - 1u) / nprod > cap_d ||
+        2u * ((F + nprod - 1u) / nprod) > 2u * cap_d || nqkv > kVec * kMkThreads) {
+        mk_destroy(g);
+        return VRT_OK;
+    }
+    P.d = d; P.H = H; P.hd = hd; P.F = F; P.V = c.vocab_size; P.L = c.block_count; P.ctx_len = c.context_length;
+    P.eos = g->P.eos;
+    P.eps = g->P.eps; P.emb_scale = g->P.emb_scale; P.attn_scale = g->P.attn_scale;
+    P.nwg = nwg;
+    P.nc = std::min(nwg, (d + cap_a - 1u) / cap_a);
+    P.ne = std::min(nwg, (d + cap_f - 1u) / cap_f);
+    if ((d + P.nc - 1u) / P.nc > cap_a || (d + P.ne - 1u) / P.ne > cap_f) { mk_destroy(g); return VRT_OK; }
+    P.chunk_min = 32u;
+    P.lm_rows = (c.vocab_size + nwg - 1u) / nwg;
+    const uint64_t rb = static_cast<uint64_t>(d / 32u) * 34u;
+    P.lm_tile_rows = static_cast<uint32_t>(std::min<uint64_t>(P.lm_rows, (kLmUnits * kMkThreads * 16u - 16u) / rb));
+    if (P.lm_tile_rows == 0u) { mk_destroy(g); return VRT_OK; }
+    uint32_t slots_max = 1;
+    for (const auto& Ly : g->layers) slots_max = std::max(slots_max, Ly.slots);
+    (void)slots_max;
+
+    // LDS layout
+    const uint32_t kmax = std::max(std::max(d, qw), F);
+    uint32_t off = 0;
+    auto take = [&](uint32_t bytes) { const uint32_t o = off; off += (bytes + 15u) & ~15u; return o; };
+    P.lds.h = take(d * 4u);
+    P.lds.xs = take(kmax * 4u);
+    P.lds.la = take(d);
+    P.lds.lb = take(d);
+    P.lds.lc = take(d);
+    P.lds.ls = take(d / 32u * 4u);
+    P.lds.sq = take((H + 2u) * hd * 4u);
+    P.lds.sc = take(std::max(8u * kGrp, 2u * nwg) * 4u);
+    P.lds.mw = take((8u * kMaxChunks + 16u) * 4u);
+    P.lds.gu = take(2u * ((F + nprod - 1u) / nprod + 1u) * 4u);
+    P.lds.red = take((4u + 9u) * kMkWaves * 8u);
+    P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + 2u * H)) * 4u, kLmUnits * kMkThreads * 16u + 16u));
+    P.lds.total = off;
+    mk->lds_bytes = off;
+    if (off > kMkLdsBytes) { mk_destroy(g); return VRT_OK; }
+
+    // exchange buffers
+    void* p;
+    if (int rc = mk_alloc(mk, nqkv * 8u, &p)) return rc;
+    P.x_qkv = static_cast<u64*>(p);
+    if (int rc = mk_alloc(mk, static_cast<size_t>(kMaxChunks) * (qw + 2u * H) * 8u, &p)) return rc;
+    P.x_part = static_cast<u64*>(p);
+    if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
+    P.x_o = static_cast<u64*>(p);
+    if (int rc = mk_alloc(mk, F * 8u, &p)) return rc;
+    P.x_g = static_cast<u64*>(p);
+    if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
+    P.x_f = static_cast<u64*>(p);
+    if (int rc = mk_alloc(mk, 2u * nwg * 8u, &p)) return rc;
+    P.x_am = static_cast<u64*>(p);
+    if (int rc = mk_alloc(mk, 64, &p)) return rc;
+    P.abort_flag = static_cast<uint32_t*>(p);
+    mk->trace_slots = 5u * c.block_count + 3u + kMarks;
+    if (int rc = mk_alloc(mk, static_cast<size_t>(nwg) * mk->trace_slots * 8u, &p)) return rc;
+    P.trace = static_cast<uint64_t*>(p);
+    P.trace_slots = 0u;
+    std::vector<MkLayer> hl(c.block_count);
+    for (uint32_t l = 0; l < c.block_count; ++l) {
+        const LayerParams& s = g->layers[l];
+        hl[l] = MkLayer{s.wq, s.wk, s.wv, s.wo, s.wg, s.wu, s.wd, s.attn_norm, s.q_norm, s.k_norm, s.post_attn,
+                        s.ffn_norm, s.post_ffw, s.kc, s.vc, s.slots, s.global};
+    }
+    mk->layers = hl;
+    P.tok_embd = g->P.tok_embd;
+    P.arena_end = g->P.arena_end;
+    P.out_norm = g->out_norm_dev;
+    P.cos_l = g->P.cos_l; P.sin_l = g->P.sin_l; P.cos_g = g->P.cos_g; P.sin_g = g->P.sin_g;
+    P.st = g->P.st;
+    P.tokens = g->P.tokens;
+    P.results = g->P.results;
+    P.logits = g->P.logits;
+    P.hidden = g->P.hidden;
+
+    int per_cu = 0;
+    VRT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kMkThreads, 0));
+    if (per_cu < 1) { mk_destroy(g); return VRT_OK; }
+    mk->fn = fn;
+    mk->grid = nwg;
+    g->mk_tag = 1u;
+    return VRT_OK;
+}
+
+int mk_set_trace(vrt_g3* g, bool on) {
+    VRT_REQUIRE(g->mk, "persistent decode kernel unavailable");
+    g->mk->P.trace_slots = on ? g->mk->trace_slots : 0u;
+    ++g->mk->version;
+    return VRT_OK;
+}
+
+int mk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots) {
+    VRT_REQUIRE(g->mk, "persistent decode kernel unavailable");
+    const uint64_t n = static_cast<uint64_t>(g->mk->grid) * g->mk->trace_slots;
+    *nwg = g->mk->grid;
+    *slots = g->mk->trace_slots;
+    VRT_REQUIRE(cap >= n, "trace buffer too small: %llu entries needed", static_cast<unsigned long long>(n));
+    VRT_HIP_CHECK(hipMemcpyAsync(out, g->mk->P.trace, n * 8u, hipMemcpyDeviceToHost, g->ctx->stream));
+    VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+    return VRT_OK;
+}
+
+int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n) {
+    VRT_REQUIRE(g->mk, "persistent decode kernel unavailable");
+    const MkParams& P = g->mk->P;
+    const uint32_t qw = P.H * P.hd;
+    const u64* src = nullptr;
+    uint64_t cnt = 0;
+    switch (which) {
+    case 0: src = P.x_qkv; cnt = qw + 2u * P.hd; break;
+    case 1: src = P.x_part; cnt = static_cast<uint64_t>(kMaxChunks) * (qw + 2u * P.H); break;
+    case 2: src = P.x_o; cnt = P.d; break;
+    case 3: src = P.x_g; cnt = P.F; break;
+    case 4: src = P.x_f; cnt = P.d; break;
+    case 5: src = P.x_am; cnt = 2u * P.nwg; break;
+    default: return set_error(VRT_ERR_INVALID, "unknown exchange buffer %u", which);
+    }
+    *n = cnt;
+    VRT_REQUIRE(cap >= cnt, "exchange buffer needs %llu words", static_cast<unsigned long long>(cnt));
+    VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+    VRT_HIP_CHECK(hipMemcpy(out, src, cnt * 8u, hipMemcpyDeviceToHost));
+    return VRT_OK;
+}
+
+int mk_clear_abort(vrt_g3* g) {
+    if (!g->mk) return VRT_OK;
+    VRT_HIP_CHECK(hipMemsetAsync(g->mk->P.abort_flag, 0, 4, g->ctx->stream));
+    VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+    return VRT_OK;
+}
+
+int mk_run(vrt_g3* g, uint32_t nsteps) {
+    MkState* mk = g->mk;
+    if (nsteps == 0) return VRT_OK;
+    const uint32_t nph = 5u * g->cfg.block_count + 1u;
+    // tags only grow; on wrap clear every exchange buffer and start again
+    if (static_cast<uint64_t>(g->mk_tag) + static_cast<uint64_t>(nsteps + 1u) * nph >= 0xfff00000ull) {
+        VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+        const uint32_t d = g->cfg.embedding_length, F = g->cfg.feed_forward_length;
+        const uint32_t qw = g->cfg.head_count * g->cfg.head_dim;
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_qkv, 0, (qw + 2u * g->cfg.head_dim) * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_part, 0, static_cast<size_t>(kMaxChunks) * (qw + 2u * g->cfg.head_count) * 8u,
+                                     g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_o, 0, d * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_g, 0, F * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_f, 0, d * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_am, 0, 2u * mk->grid * 8u, g->ctx->stream));
+        g->mk_tag = 1u;
+    }
+    uint32_t tag0 = g->mk_tag;
+    hipStream_t stream = g->ctx->stream;
+    MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    // the parameter block is one per device: order this launch after any other executor's
+    if (ds.last && ds.last_stream != stream) VRT_HIP_CHECK(hipStreamWaitEvent(stream, ds.last, 0));
+    if (ds.owner != mk || ds.version != mk->version) {
+        VRT_HIP_CHECK(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_mk), &mk->P, sizeof(MkParams), 0, hipMemcpyHostToDevice, stream));
+        VRT_HIP_CHECK(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_mk_layers), mk->layers.data(), mk->layers.size() * sizeof(MkLayer), 0,
+                                             hipMemcpyHostToDevice, stream));
+        ds.owner = mk;
+        ds.version = mk->version;
+    }
+    void* args[] = {&nsteps, &tag0};
+    VRT_HIP_CHECK(hipLaunchCooperativeKernel(mk->fn, dim3(mk->grid), dim3(kMkThreads), args, 0, stream));
+    if (!ds.last) VRT_HIP_CHECK(hipEventCreateWithFlags(&ds.last, hipEventDisableTiming));
+    VRT_HIP_CHECK(hipEventRecord(ds.last, stream));
+    ds.last_stream = stream;
+    g->mk_tag += nsteps * nph;
+    return VRT_OK;
+}
+
+}  // namespace vrt

@@ -1,0 +1,112 @@
+// vrt_g3_internal.hpp -- Gemma 3 executor state shared by the multi-kernel step
+// (vrt_gemma3.hip) and the persistent decode kernel (vrt_decode.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "vrt_hip.h"
+#include "vrt_internal.hpp"
+
+namespace vrt {
+
+struct G3State {
+    uint32_t step;         // position of the next step (== steps since reset)
+    uint32_t stop;         // EOS generated: later steps do nothing
+    uint32_t lm_from;      // steps >= lm_from run the LM head
+    uint32_t feed_until;   // tokens[s+1] comes from the host when s+1 < feed_until
+    uint32_t want_logits;  // LM head also writes the logits
+    uint32_t nonfinite;    // first block whose output hidden state was non-finite (~0u: none)
+    uint32_t pad[2];
+    uint32_t tickets[8];   // last-workgroup counters (self-resetting)
+};
+
+struct LmPartial {
+    float value;
+    uint32_t index;
+};
+
+struct G3Params {
+    uint32_t d, H, hd, F, V, L, ctx_len, eos;
+    float eps, emb_scale, attn_scale;
+    uint32_t pad0;
+    const uint8_t* arena_end;
+    const uint8_t* tok_embd;
+    G3State* st;
+    uint32_t* tokens;
+    vrt_argmax_result* results;
+    float* hres;
+    float* hmid;
+    float* qkv;
+    float* att;
+    float* part;
+    float* o;
+    float* g;
+    float* f;
+    float* hidden;
+    float* logits;
+    LmPartial* lm_part;
+    const float* cos_l;
+    const float* sin_l;
+    const float* cos_g;
+    const float* sin_g;
+};
+
+struct LayerParams {
+    const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    const float *attn_norm, *q_norm, *k_norm, *post_attn, *ffn_norm, *post_ffw;
+    float* kc;
+    float* vc;
+    uint32_t slots;       // KV slots: window for local layers, context_length otherwise
+    uint32_t global;
+    uint32_t attn_grid;   // workgroups of k_attn
+    uint32_t chunk_max;   // max positions per attention workgroup
+};
+
+struct LaunchDesc {
+    const void* fn;
+    uint32_t grid;
+    size_t smem;
+};
+
+struct MkState;   // persistent decode kernel: exchange buffers and launch shape (vrt_decode.hip)
+
+}  // namespace vrt
+
+struct vrt_g3 {
+    vrt_ctx* ctx = nullptr;
+    vrt_g3_config cfg{};
+    uint32_t eos = 1;
+    uint64_t arena_bytes = 0;
+    vrt::G3Params P{};
+    std::vector<vrt::LayerParams> layers;
+    vrt::LaunchDesc ld_qkv{}, ld_o{}, ld_gateup{}, ld_down{}, ld_lm{};
+    uint32_t lm_rows_per_wg = 0;
+    const float* out_norm_dev = nullptr;
+    std::vector<void*> allocs;   // device allocations owned by the executor
+    vrt::G3State* host_ctl = nullptr; // pinned control block
+    vrt_argmax_result* host_res = nullptr;
+    uint32_t next_pos = 0;
+    bool use_graph = true;
+    bool use_persistent = true;  // one cooperative launch per batch of steps (vrt_decode.hip)
+    vrt::MkState* mk = nullptr;
+    uint32_t mk_tag = 1;         // first exchange tag of the next persistent launch
+    hipGraphExec_t graph = nullptr;
+    uint32_t gen_prompt = 0;     // generation in flight (vrt_g3_start .. vrt_g3_collect)
+    uint32_t gen_max = 0;
+    uint64_t gen_steps = 0;
+};
+
+namespace vrt {
+// Persistent decode kernel (vrt_decode.hip). mk_setup returns VRT_OK and leaves g->mk null
+// when the configuration or device does not support it (the multi-kernel step is used).
+int mk_setup(vrt_g3* g);
+int mk_run(vrt_g3* g, uint32_t nsteps);
+void mk_destroy(vrt_g3* g);
+int mk_clear_abort(vrt_g3* g);
+int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
+int mk_set_trace(vrt_g3* g, bool on);
+int mk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);
+}  // namespace vrt

@@ -26,63 +26,11 @@
 #include <new>
 #include <vector>
 
+#include "vrt_g3_internal.hpp"
 #include "vrt_internal.hpp"
 #include "vrt_q8_device.hpp"
 
 namespace vrt {
-
-struct G3State {
-    uint32_t step;         // position of the next step (== steps since reset)
-    uint32_t stop;         // EOS generated: later steps do nothing
-    uint32_t lm_from;      // steps >= lm_from run the LM head
-    uint32_t feed_until;   // tokens[s+1] comes from the host when s+1 < feed_until
-    uint32_t want_logits;  // LM head also writes the logits
-    uint32_t nonfinite;    // first block whose output hidden state was non-finite (~0u: none)
-    uint32_t pad[2];
-    uint32_t tickets[8];   // last-workgroup counters (self-resetting)
-};
-
-struct LmPartial {
-    float value;
-    uint32_t index;
-};
-
-struct G3Params {
-    uint32_t d, H, hd, F, V, L, ctx_len, eos;
-    float eps, emb_scale, attn_scale;
-    uint32_t pad0;
-    const uint8_t* arena_end;
-    const uint8_t* tok_embd;
-    G3State* st;
-    uint32_t* tokens;
-    vrt_argmax_result* results;
-    float* hres;
-    float* hmid;
-    float* qkv;
-    float* att;
-    float* part;
-    float* o;
-    float* g;
-    float* f;
-    float* hidden;
-    float* logits;
-    LmPartial* lm_part;
-    const float* cos_l;
-    const float* sin_l;
-    const float* cos_g;
-    const float* sin_g;
-};
-
-struct LayerParams {
-    const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
-    const float *attn_norm, *q_norm, *k_norm, *post_attn, *ffn_norm, *post_ffw;
-    float* kc;
-    float* vc;
-    uint32_t slots;       // KV slots: window for local layers, context_length otherwise
-    uint32_t global;
-    uint32_t attn_grid;   // workgroups of k_attn
-    uint32_t chunk_max;   // max positions per attention workgroup
-};
 
 constexpr int kThreads = 256;
 constexpr int kMaxE = 8;  // vector elements per thread in prologues: d, H*hd, F <= 2048
@@ -145,71 +93,6 @@ __device__ __forceinline__ MvSmem mv_smem(uint32_t K) {
 static size_t mv_smem_bytes(uint32_t K, uint32_t extra_floats) {
     return static_cast<size_t>(K) * 4 + static_cast<size_t>(K) * 3 + ((K / 32u) * 4u + 15u) / 16u * 16u +
            static_cast<size_t>(extra_floats) * 4 + 16;
-}
-
-// ---- batched row streaming (prefetch, then consume) ------------------------------------------
-
-template <int S, int NB, int U>
-struct RowBatch {
-    Q8Raw raw[U][NB];
-    uint32_t vrow[U];
-    bool live[U];
-};
-
-// rowp(v) returns the first byte of virtual row v.
-template <int S, int NB, int U, typename RowFn>
-__device__ __forceinline__ void batch_load(RowFn&& rowp, uint32_t nblk, const uint8_t* w_end, uint32_t v_begin,
-                                           uint32_t v_end, uint32_t g0, RowBatch<S, NB, U>& rb) {
-    constexpr uint32_t RPW = 64u / S;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t slot = lane / S, sl = lane % S;
-    const uint32_t nwaves = blockDim.x >> 6;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const uint32_t g = g0 + static_cast<uint32_t>(u) * nwaves;
-        rb.vrow[u] = v_begin + g * RPW + slot;
-        rb.live[u] = rb.vrow[u] < v_end;
-        const uint8_t* rp = rb.live[u] ? rowp(rb.vrow[u]) : nullptr;
-#pragma unroll
-        for (int n = 0; n < NB; ++n) {
-            const uint32_t b = sl + static_cast<uint32_t>(n) * S;
-            if (rb.live[u] && b < nblk) q8_load(rp + 34u * b, w_end, rb.raw[u][n]);
-        }
-    }
-}
-
-template <int S, int NB, int U, typename Sink>
-__device__ __forceinline__ void batch_consume(const RowBatch<S, NB, U>& rb, uint32_t nblk, const XLimb (&xl)[NB],
-                                              Sink&& sink) {
-    const uint32_t sl = (threadIdx.x & 63u) % S;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int n = 0; n < NB; ++n) {
-            const uint32_t b = sl + static_cast<uint32_t>(n) * S;
-            if (rb.live[u] && b < nblk) acc += q8_dot(rb.raw[u][n], xl[n]);
-        }
-        float tot;
-        if constexpr (S == 64) {
-            const float h = slot_sum<32>(acc);
-            tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 0)) +
-                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 32));
-        } else {
-            tot = slot_sum<S>(acc);
-        }
-        if (rb.live[u] && sl == 0u) sink(rb.vrow[u], tot);
-    }
-}
-
-template <int S, int NB>
-__device__ __forceinline__ void lane_limbs(const LimbLds& L, uint32_t nblk, XLimb (&xl)[NB]) {
-    const uint32_t sl = (threadIdx.x & 63u) % S;
-#pragma unroll
-    for (int n = 0; n < NB; ++n) {
-        const uint32_t b = sl + static_cast<uint32_t>(n) * S;
-        if (b < nblk) load_limb(L, b, xl[n]);
-    }
 }
 
 __device__ __forceinline__ void flag_nonfinite(const float (&h)[kMaxE], uint32_t n, G3State* st, uint32_t block,
@@ -694,11 +577,7 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
 
 enum KernelKind { KQKV, KO, KGATEUP, KDOWN, KLM };
 
-struct LaunchDesc {
-    const void* fn;
-    uint32_t grid;
-    size_t smem;
-};
+
 
 template <int S, int NB>
 static LaunchDesc pick(KernelKind kind, uint32_t rows, uint32_t K, uint32_t extra_per_wg) {
@@ -735,26 +614,6 @@ using namespace vrt;
 // =======================================================================================
 // Host side
 // =======================================================================================
-
-struct vrt_g3 {
-    vrt_ctx* ctx = nullptr;
-    vrt_g3_config cfg{};
-    uint32_t eos = 1;
-    G3Params P{};
-    std::vector<LayerParams> layers;
-    LaunchDesc ld_qkv{}, ld_o{}, ld_gateup{}, ld_down{}, ld_lm{};
-    uint32_t lm_rows_per_wg = 0;
-    const float* out_norm_dev = nullptr;
-    std::vector<void*> allocs;   // device allocations owned by the executor
-    G3State* host_ctl = nullptr; // pinned control block
-    vrt_argmax_result* host_res = nullptr;
-    uint32_t next_pos = 0;
-    bool use_graph = true;
-    hipGraphExec_t graph = nullptr;
-    uint32_t gen_prompt = 0;     // generation in flight (vrt_g3_start .. vrt_g3_collect)
-    uint32_t gen_max = 0;
-    uint64_t gen_steps = 0;
-};
 
 static int g3_alloc(vrt_g3* g, size_t bytes, void** out) {
     void* p = nullptr;
@@ -820,6 +679,7 @@ static int g3_capture(vrt_g3* g) {
 
 static int g3_run_steps(vrt_g3* g, uint32_t n) {
     hipStream_t s = g->ctx->stream;
+    if (g->mk && g->use_persistent) return mk_run(g, n);
     for (uint32_t i = 0; i < n; ++i) {
         if (g->use_graph) {
             if (!g->graph) { if (int rc = g3_capture(g)) return rc; }
@@ -858,9 +718,18 @@ static int g3_check_state(vrt_g3* g, G3State* out) {
     *out = *g->host_ctl;
     if (out->nonfinite != 0xffffffffu) {
         char msg[128];
-        if (out->nonfinite & 0x40000000u) std::snprintf(msg, sizeof msg, "Gemma 3 attention softmax failed");
-        else std::snprintf(msg, sizeof msg, "Non-finite value after Gemma 3 block %u", out->nonfinite);
-        return g3_fail_reset(g, VRT_ERR_NUMERIC, msg);
+        int code = VRT_ERR_NUMERIC;
+        if (out->nonfinite & 0x40000000u) {
+            std::snprintf(msg, sizeof msg, "Gemma 3 attention softmax failed");
+        } else if (out->nonfinite == 0x20000000u) {
+            // a persistent-kernel hand-off timed out; clear its abort flag for the next launch
+            std::snprintf(msg, sizeof msg, "Gemma 3 decode: device hand-off timed out");
+            if (int rc = mk_clear_abort(g)) return rc;
+            code = VRT_ERR_HIP;
+        } else {
+            std::snprintf(msg, sizeof msg, "Non-finite value after Gemma 3 block %u", out->nonfinite);
+        }
+        return g3_fail_reset(g, code, msg);
     }
     return VRT_OK;
 }
@@ -913,6 +782,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
     P.emb_scale = std::sqrt(static_cast<float>(d));                         // :259-264
     P.attn_scale = 1.0f / std::sqrt(static_cast<float>(hd));                // :265-269
     P.arena_end = arena + desc->arena_bytes;
+    g->arena_bytes = desc->arena_bytes;
     P.tok_embd = arena + desc->token_embd;
 
     void* p;
@@ -1020,6 +890,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
         if (e != hipSuccess) return fail(set_error(VRT_ERR_HIP, "hipHostMalloc failed: %s", hipGetErrorString(e)));
     }
     if (int rc = g3_write_ctl(g, 0, 0xffffffffu, 0xffffffffu, 0)) return fail(rc);
+    if (int rc = mk_setup(g)) return fail(rc);
     VRT_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     *out = g;
     return VRT_OK;
@@ -1030,6 +901,7 @@ extern "C" int vrt_g3_destroy(vrt_g3* g) {
     (void)hipSetDevice(g->ctx->device);
     (void)hipStreamSynchronize(g->ctx->stream);
     if (g->graph) (void)hipGraphExecDestroy(g->graph);
+    mk_destroy(g);
     for (void* p : g->allocs) (void)hipFree(p);
     if (g->host_ctl) (void)hipHostFree(g->host_ctl);
     if (g->host_res) (void)hipHostFree(g->host_res);
@@ -1049,6 +921,9 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
     VRT_REQUIRE(g, "vrt_g3_set_option: null executor");
     switch (option) {
     case VRT_G3_OPT_USE_GRAPH: g->use_graph = value != 0; return VRT_OK;
+    case VRT_G3_OPT_PERSISTENT: g->use_persistent = value != 0; return VRT_OK;
+    case VRT_G3_OPT_QUERY_PERSISTENT: return g->mk ? VRT_OK : set_error(VRT_ERR_STATE, "persistent decode kernel unavailable");
+    case VRT_G3_OPT_TRACE: return mk_set_trace(g, value != 0);
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
     }
 }
@@ -1170,6 +1045,16 @@ extern "C" int vrt_g3_forced(vrt_g3* g, const uint32_t* tokens, uint32_t n, uint
     if (int rc = g3_check_state(g, &st)) return rc;
     g->next_pos = n;
     return VRT_OK;
+}
+
+extern "C" int vrt_g3_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n) {
+    VRT_REQUIRE(g && out && n, "vrt_g3_read_exchange: null argument");
+    return mk_read_exchange(g, which, out, cap, n);
+}
+
+extern "C" int vrt_g3_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots) {
+    VRT_REQUIRE(g && out && nwg && slots, "vrt_g3_read_trace: null argument");
+    return mk_read_trace(g, out, cap, nwg, slots);
 }
 
 extern "C" int vrt_g3_time_lm_head(vrt_g3* g, uint32_t iters, float* mean_us) {

@@ -56,6 +56,61 @@ __device__ __forceinline__ float wave_sum(float v) {
            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
+// Full-wave reductions on the DPP path (no LDS round trips): rows of 16 lanes first, then
+// row_bcast15 / row_bcast31 fold the rows into lane 63, which is read back uniformly.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_or_zero(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_red_sum(float v) {
+    v = slot_sum<16>(v);                        // every lane: its row's total
+    v += dpp_or_zero<0x142, 0xa>(v);            // row_bcast:15 into rows 1 and 3
+    v += dpp_or_zero<0x143, 0xc>(v);            // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_red_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    // lanes outside the row mask keep their own value (old = v): max is unchanged
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_d(double v, bool zero_fill) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = static_cast<int>(b), hi = static_cast<int>(b >> 32);
+    const int olo = zero_fill ? 0 : lo, ohi = zero_fill ? 0 : hi;
+    const int rlo = __builtin_amdgcn_update_dpp(olo, lo, CTRL, ROW_MASK, 0xf, false);
+    const int rhi = __builtin_amdgcn_update_dpp(ohi, hi, CTRL, ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, (static_cast<long long>(rhi) << 32) | static_cast<unsigned int>(rlo));
+}
+
+// Full-wave double sum (uniform result). The order of the adds is fixed, so every workgroup
+// reducing the same values gets the same bits.
+__device__ __forceinline__ double wave_red_sum_d(double v) {
+    v += dpp_d<0xB1, 0xf>(v, false);
+    v += dpp_d<0x4E, 0xf>(v, false);
+    v += dpp_d<0x141, 0xf>(v, false);
+    v += dpp_d<0x140, 0xf>(v, false);
+    v += dpp_d<0x142, 0xa>(v, true);
+    v += dpp_d<0x143, 0xc>(v, true);
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_readlane(static_cast<int>(b), 63);
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), 63);
+    return __builtin_bit_cast(double, (static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+
 __device__ __forceinline__ double wave_sum_f64(double v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
     return v;
@@ -99,18 +154,20 @@ struct Q8Raw {
 // blk: start of a 34-byte block (2-byte aligned); end: one past the last readable byte.
 // Reads stay inside [blk, blk + 34) except for up to 2 bytes past the block, which are
 // read only when they lie before `end`.
+// Weights always live in global memory: global (not FLAT) loads.
 __device__ __forceinline__ void q8_load(const uint8_t* blk, const uint8_t* end, Q8Raw& r) {
+    typedef const __attribute__((address_space(1))) uint32_t* gu32;
+    typedef const __attribute__((address_space(1))) uint16_t* gu16;
     const uintptr_t q = reinterpret_cast<uintptr_t>(blk) + 2u;
-    const uint32_t* lb = reinterpret_cast<const uint32_t*>(q & ~uintptr_t(3));
+    const gu32 lb = reinterpret_cast<gu32>(q & ~uintptr_t(3));
     r.sh = static_cast<uint32_t>(q & 3u);
-    r.sbits = *reinterpret_cast<const uint16_t*>(blk);
+    r.sbits = *(gu16)(blk);
 #pragma unroll
     for (int j = 0; j < 8; ++j) r.d[j] = lb[j];
     r.d[8] = 0u;
     if (r.sh) {
-        const uint8_t* tail = reinterpret_cast<const uint8_t*>(lb + 8);
-        r.d[8] = (tail + 4 <= end) ? lb[8]
-                                   : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tail));
+        const uintptr_t tail = (q & ~uintptr_t(3)) + 32u;
+        r.d[8] = (tail + 4 <= reinterpret_cast<uintptr_t>(end)) ? lb[8] : static_cast<uint32_t>(*reinterpret_cast<gu16>(tail));
     }
 }
 
@@ -197,6 +254,22 @@ __device__ __forceinline__ float q8_dot(const Q8Raw& r, const XLimb& x) {
     const float t = fmaf(static_cast<float>(Cc), 1.0f / 64516.0f,
                          fmaf(static_cast<float>(B), 1.0f / 254.0f, static_cast<float>(A)));
     return half_bits_to_float(r.sbits) * x.s * t;
+}
+
+// One block's contribution against fp32 activations x[0..31] (LDS, 16-byte aligned): the 32
+// int8 products summed in k order, then scaled: d_w * sum_k q_k x_k.
+__device__ __forceinline__ float q8_dot_x(const Q8Raw& r, const float* x) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = static_cast<int>(__builtin_amdgcn_alignbyte(r.d[j + 1], r.d[j], r.sh));
+        const float4 xv = *reinterpret_cast<const float4*>(x + 4 * j);
+        acc = fmaf(static_cast<float>((q << 24) >> 24), xv.x, acc);
+        acc = fmaf(static_cast<float>((q << 16) >> 24), xv.y, acc);
+        acc = fmaf(static_cast<float>((q << 8) >> 24), xv.z, acc);
+        acc = fmaf(static_cast<float>(q >> 24), xv.w, acc);
+    }
+    return half_bits_to_float(r.sbits) * acc;
 }
 
 // ---- row streaming ----------------------------------------------------------------------
@@ -291,5 +364,96 @@ __device__ __forceinline__ void stream_rows(const RowSpace& rs, uint64_t row_byt
         }
     }
 }
+
+// ---- batched row streaming (prefetch, then consume) ------------------------------------------
+
+template <int S, int NB, int U>
+struct RowBatch {
+    Q8Raw raw[U][NB];
+    uint32_t vrow[U];
+    bool live[U];
+};
+
+// rowp(v) returns the first byte of virtual row v.
+template <int S, int NB, int U, typename RowFn>
+__device__ __forceinline__ void batch_load(RowFn&& rowp, uint32_t nblk, const uint8_t* w_end, uint32_t v_begin,
+                                           uint32_t v_end, uint32_t g0, RowBatch<S, NB, U>& rb) {
+    constexpr uint32_t RPW = 64u / S;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t slot = lane / S, sl = lane % S;
+    const uint32_t nwaves = blockDim.x >> 6;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t g = g0 + static_cast<uint32_t>(u) * nwaves;
+        rb.vrow[u] = v_begin + g * RPW + slot;
+        rb.live[u] = rb.vrow[u] < v_end;
+        const uint8_t* rp = rb.live[u] ? rowp(rb.vrow[u]) : nullptr;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+            if (rb.live[u] && b < nblk) q8_load(rp + 34u * b, w_end, rb.raw[u][n]);
+        }
+    }
+}
+
+template <int S, int NB, int U, typename Sink>
+__device__ __forceinline__ void batch_consume(const RowBatch<S, NB, U>& rb, uint32_t nblk, const XLimb (&xl)[NB],
+                                              Sink&& sink) {
+    const uint32_t sl = (threadIdx.x & 63u) % S;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+            if (rb.live[u] && b < nblk) acc += q8_dot(rb.raw[u][n], xl[n]);
+        }
+        float tot;
+        if constexpr (S == 64) {
+            const float h = slot_sum<32>(acc);
+            tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 0)) +
+                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 32));
+        } else {
+            tot = slot_sum<S>(acc);
+        }
+        if (rb.live[u] && sl == 0u) sink(rb.vrow[u], tot);
+    }
+}
+
+// As batch_consume, against fp32 activations xs[0..K) in LDS (q8_dot_x per block).
+template <int S, int NB, int U, typename Sink>
+__device__ __forceinline__ void batch_consume_x(const RowBatch<S, NB, U>& rb, uint32_t nblk, const float* xs,
+                                                Sink&& sink) {
+    const uint32_t sl = (threadIdx.x & 63u) % S;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+            if (rb.live[u] && b < nblk) acc += q8_dot_x(rb.raw[u][n], xs + 32u * b);
+        }
+        float tot;
+        if constexpr (S == 64) {
+            const float h = slot_sum<32>(acc);
+            tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 0)) +
+                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h), 32));
+        } else {
+            tot = slot_sum<S>(acc);
+        }
+        if (rb.live[u] && sl == 0u) sink(rb.vrow[u], tot);
+    }
+}
+
+template <int S, int NB>
+__device__ __forceinline__ void lane_limbs(const LimbLds& L, uint32_t nblk, XLimb (&xl)[NB]) {
+    const uint32_t sl = (threadIdx.x & 63u) % S;
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+        if (b < nblk) load_limb(L, b, xl[n]);
+    }
+}
+
 
 }  // namespace vrt

@@ -16,6 +16,9 @@ LIB_PATH = os.path.join(PKG, "_build", "libvrt_hip.so")
 VRT_OK, VRT_ERR_INVALID, VRT_ERR_HIP, VRT_ERR_STATE, VRT_ERR_NUMERIC = 0, 1, 2, 3, 4
 MEM_DEVICE, MEM_HOST = 0, 1
 OPT_USE_GRAPH = 1
+OPT_PERSISTENT = 2
+OPT_QUERY_PERSISTENT = 3
+OPT_TRACE = 4
 
 
 class VrtError(RuntimeError):
@@ -92,6 +95,8 @@ SIGNATURES = {
     "vrt_g3_forced": (_I, [_P, _P, _U32, _U32, _P]),
     "vrt_g3_set_option": (_I, [_P, _U32, _U32]),
     "vrt_g3_time_lm_head": (_I, [_P, _U32, C.POINTER(_F)]),
+    "vrt_g3_read_trace": (_I, [_P, _P, _U64, C.POINTER(_U32), C.POINTER(_U32)]),
+    "vrt_g3_read_exchange": (_I, [_P, _U32, _P, _U64, C.POINTER(_U64)]),
 }
 
 _lib = None
@@ -341,6 +346,31 @@ class Gemma3:
 
     def set_graph(self, on: bool):
         check(lib().vrt_g3_set_option(self.h, OPT_USE_GRAPH, 1 if on else 0))
+
+    def set_persistent(self, on: bool):
+        """Persistent decode kernel (default when available) or the multi-kernel step."""
+        check(lib().vrt_g3_set_option(self.h, OPT_PERSISTENT, 1 if on else 0))
+
+    def set_trace(self, on: bool):
+        check(lib().vrt_g3_set_option(self.h, OPT_TRACE, 1 if on else 0))
+
+    def read_trace(self) -> np.ndarray:
+        """[nwg, slots] s_memrealtime ticks (100 MHz) of the last persistent launch's first step."""
+        nwg, slots = C.c_uint32(), C.c_uint32()
+        buf = np.zeros(1 << 20, dtype=np.uint64)
+        check(lib().vrt_g3_read_trace(self.h, ptr(buf), buf.size, C.byref(nwg), C.byref(slots)))
+        return buf[: nwg.value * slots.value].reshape(nwg.value, slots.value).copy()
+
+    def read_exchange(self, which: int):
+        """(values, tags) of a persistent-kernel exchange buffer (0 qkv, 1 partials, 2 o, 3 g, 4 f, 5 argmax)."""
+        buf = np.zeros(1 << 20, dtype=np.uint64)
+        n = C.c_uint64()
+        check(lib().vrt_g3_read_exchange(self.h, which, ptr(buf), buf.size, C.byref(n)))
+        w = buf[: n.value]
+        return (w & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32), (w >> np.uint64(32)).astype(np.uint32)
+
+    def persistent_available(self) -> bool:
+        return lib().vrt_g3_set_option(self.h, OPT_QUERY_PERSISTENT, 0) == VRT_OK
 
     def reset(self):
         check(lib().vrt_g3_reset(self.h))
