@@ -8,6 +8,11 @@ of uniform ids in [2, 262144) from seed 0, then greedy decode with an fp32 KV ca
 prompt is prefilled first (untimed); --steps decode steps at positions 8, 9, ... are timed
 with hipEvents on the library's stream. Inputs are resident in HBM before timing.
 
+The whole decode loop is one kernel, k_decode: a cooperative launch with one workgroup per CU
+that runs every block, the LM head and argmax for each of the launch's steps. The timed region
+is exactly one k_decode launch of --steps steps, so the roofline's launch duration is the
+event-timed region itself.
+
 Algorithmic bytes per step at position p: every Q8_0 weight byte, the fp32 norm weights, one
 embedding row, plus the fp32 KV rows attention reads (min(p+1, window) positions for local
 blocks, p+1 for global ones), each counted once.
@@ -42,18 +47,48 @@ def step_bytes(cfg, pos: int) -> int:
     return total
 
 
-def lm_head_bytes(cfg) -> int:
-    return cfg.vocab_size * (cfg.embedding_length // 32) * 34
-
-
-def load_traffic():
-    """HBM bytes per LM-head launch from the committed rocprofv3 PMC summary, if present."""
-    p = os.path.join(REPO, "profiles", "lm_head_pmc.json")
+def load_traffic(steps: int):
+    """HBM bytes per k_decode launch of `steps` steps, from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE per decode step, calibrated against a copy of known size)."""
+    p = os.path.join(REPO, "profiles", "decode_gemma3_270m_pmc.json")
     try:
         with open(p) as fp:
-            return json.load(fp).get("traffic_bytes_per_launch")
-    except (OSError, ValueError):
+            per_step = json.load(fp)["hbm_bytes_per_step"]
+    except (OSError, ValueError, KeyError):
         return None
+    return int(per_step * steps)
+
+
+def phase_split(g, prompt, cfg, steps: int = 24):
+    """Per-phase time of one decode step from the kernel's own clock marks: each phase's end is
+    the latest workgroup's end timestamp (s_memrealtime, 100 MHz). Median over blocks 1..L-1."""
+    g.set_trace(True)
+    g.start(prompt, steps + 1)
+    g.step(len(prompt))
+    g.step(steps)            # the traced step is the first of this launch
+    tr = g.read_trace().astype(np.int64)
+    g.collect()
+    g.set_trace(False)
+    L = cfg.block_count
+    mx = tr[:, : 5 * L + 3].max(axis=0) * 10.0 / 1000.0        # us
+    out = {}
+    for k, p in enumerate("ABCDE"):
+        out[p] = float(np.median([mx[1 + 5 * l + k] - mx[5 * l + k] for l in range(1, L)]))
+    out["lm_head"] = float(mx[5 * L + 2] - mx[5 * L + 1])
+    out["step"] = float(mx[5 * L + 2] - mx[0])
+    return {k: round(v, 2) for k, v in out.items()}
+
+
+def copy_calibration(nbytes: int = 1 << 30):
+    """A plain device copy of known size for scaling the PMC counters (FETCH_SIZE / WRITE_SIZE
+    of this dispatch against nbytes read and nbytes written)."""
+    import torch
+    a = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes}))
 
 
 def cpu_baseline(path, prompt, target_s: float = 12.0):
@@ -90,8 +125,14 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-phases", action="store_true", help="skip the traced per-phase split")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the batch-1 token loop is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
@@ -142,10 +183,7 @@ def main():
     total_bytes = sum(step_bytes(cfg, n_prompt + i) for i in range(args.steps))
     gbps = total_bytes / (ms / 1e3) / 1e9
 
-    # dominant kernel: tied LM head + argmax, timed alone with events on the same stream
-    lm_us = g.time_lm_head(50)
-    lm_bytes = lm_head_bytes(cfg)
-    lm_gbps = lm_bytes / (lm_us * 1e-6) / 1e9
+    phases = None if args.no_phases else phase_split(g, prompt, cfg)
 
     out = {
         "metric": METRIC,
@@ -169,19 +207,20 @@ def main():
             "parallelism": "single GPU",
         },
         "hbm_gbps": round(gbps, 1),
-        "step_roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "bytes_per_step_mean": int(total_bytes / args.steps),
         "roofline": {
-            "kernel": "k_lm (tied 262144x640 Q8_0 LM head fused with greedy argmax)",
+            "kernel": f"k_decode (persistent: {cfg.block_count} blocks + tied LM head + argmax per step, "
+                      f"{args.steps} steps per launch)",
             "bound": "hbm",
-            "achieved": round(lm_gbps, 1),
+            "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(lm_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": load_traffic(),
-            "mean_launch_us": round(lm_us, 3),
-            "algorithmic_bytes_per_launch": lm_bytes,
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": load_traffic(args.steps),
+            "mean_launch_us": round(ms * 1e3, 1),
+            "algorithmic_bytes_per_launch": total_bytes,
         },
+        "phase_us_per_step": phases,
         "cpu_baseline": None,
     }
     g.close()

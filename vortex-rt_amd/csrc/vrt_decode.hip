@@ -50,6 +50,7 @@ namespace vrt {
 
 typedef unsigned long long u64;
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 // Address spaces. Pointers that reach device code through the parameter block are generic,
 // so every access would become a FLAT instruction (slower, and it makes the compiler wait on
@@ -69,6 +70,7 @@ constexpr uint32_t kMkWaves = kMkThreads / 64;
 constexpr uint32_t kVec = 4;                 // vector elements per thread (vectors <= 2048)
 constexpr uint32_t kSpinLimit = 1u << 21;    // polls before a hand-off is declared lost
 constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
+constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x query heads) per block
 constexpr uint32_t kLmUnits = 3;             // 16-byte LM-head loads per thread per tile
 constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
 constexpr uint32_t kGrpPerWave = kGrp / kMkWaves;
@@ -99,6 +101,7 @@ struct MkParams {
     float eps, emb_scale, attn_scale;
     uint32_t nwg, nc, ne;          // workgroups: all, phase C, phase E
     uint32_t chunk_min;            // attention: positions per chunk before splitting further
+    uint32_t max_chunks;           // attention: chunks per block (H * max_chunks <= kMaxBUnits)
     uint32_t lm_rows;              // LM-head rows per workgroup
     uint32_t lm_tile_rows;         // rows per LDS tile
     uint32_t trace_slots;          // phase timestamps per workgroup (0: tracing off)
@@ -157,36 +160,70 @@ __device__ __forceinline__ void mk_flag_min(uint32_t v) {
 // Polls src[i] for i = tid + kMkThreads * k (k < MAXK, i < n) until every tag equals `tag`;
 // the values land in out[k]. Returns 0, or 1 if the wait was abandoned (abort raised).
 // The caller turns the per-thread result into a workgroup decision at its next barrier.
+// The polls are device-coherent (sc1) buffer loads over [src, src + n): one VGPR offset for
+// all k (a constant SGPR offset each), and a load past n returns 0 without touching memory.
+// Each round re-issues every load, then waits once, so a round's loads are in flight
+// together; the compiler barrier keeps the loads inside the loop.
 template <int MAXK>
 __device__ __forceinline__ int ll_wait(const u64* src, uint32_t n, uint32_t tag, float (&out)[MAXK]) {
-    u64 v[MAXK];
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(src), 0, static_cast<int>(n * 8u), kRsrcFlags);
     const uint32_t t = threadIdx.x;
+    const int voff = static_cast<int>(t * 8u);
+    v2u v[MAXK];
 #pragma unroll
-    for (int k = 0; k < MAXK; ++k) {
-        const uint32_t i = t + static_cast<uint32_t>(k) * kMkThreads;
-        v[k] = ll_ld(src + (i < n ? i : n - 1u));   // branch-free: clamped, ignored past n
-    }
+    for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b64(r, voff, k * kMkThreads * 8, kCoherent);
     int fail = 0;
     uint32_t spins = 0;
     for (;;) {
         bool ready = true;
 #pragma unroll
-        for (int k = 0; k < MAXK; ++k)
-            ready &= static_cast<uint32_t>(v[k] >> 32) == tag || t + static_cast<uint32_t>(k) * kMkThreads >= n;
+        for (int k = 0; k < MAXK; ++k) ready &= v[k].y == tag || t + static_cast<uint32_t>(k) * kMkThreads >= n;
         if (ready) break;
         if ((++spins & 63u) == 0u && (spins > kSpinLimit || mk_aborted())) {
             fail = 1;
             mk_abort();
             break;
         }
+        __asm__ volatile("" ::: "memory");
 #pragma unroll
-        for (int k = 0; k < MAXK; ++k) {
-            const uint32_t i = t + static_cast<uint32_t>(k) * kMkThreads;
-            if (i < n && static_cast<uint32_t>(v[k] >> 32) != tag) v[k] = ll_ld(src + i);
-        }
+        for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b64(r, voff, k * kMkThreads * 8, kCoherent);
     }
 #pragma unroll
-    for (int k = 0; k < MAXK; ++k) out[k] = __uint_as_float(static_cast<uint32_t>(v[k]));
+    for (int k = 0; k < MAXK; ++k) out[k] = __uint_as_float(v[k].x);
+    return fail;
+}
+
+// As ll_wait, for this thread's elements j = tid + kMkThreads * k (j < nj) at arbitrary
+// word indices idx[k] of src[0..n).
+template <int MAXK>
+__device__ __forceinline__ int ll_wait_at(const u64* src, uint32_t n, const uint32_t (&idx)[MAXK], uint32_t nj,
+                                          uint32_t tag, float (&out)[MAXK]) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(src), 0, static_cast<int>(n * 8u), kRsrcFlags);
+    const uint32_t t = threadIdx.x;
+    v2u v[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(idx[k] * 8u), 0, kCoherent);
+    int fail = 0;
+    uint32_t spins = 0;
+    for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) ready &= v[k].y == tag || t + static_cast<uint32_t>(k) * kMkThreads >= nj;
+        if (ready) break;
+        if ((++spins & 63u) == 0u && (spins > kSpinLimit || mk_aborted())) {
+            fail = 1;
+            mk_abort();
+            break;
+        }
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k)
+            v[k] = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(idx[k] * 8u), 0, kCoherent);
+    }
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) out[k] = __uint_as_float(v[k].x);
     return fail;
 }
 
@@ -284,15 +321,17 @@ __device__ __forceinline__ void split_range(uint32_t total, uint32_t parts, uint
 // Chunk c runs on workgroup nwg - 1 - c; every other workgroup produces rows in phases A and
 // D. So every workgroup either produces in A/D or publishes an attention chunk, which is what
 // makes rewriting an exchange buffer safe once its successors' data has arrived.
-__device__ __forceinline__ void attn_split(uint32_t hist, uint32_t chunk_min, uint32_t& nch, uint32_t& clen) {
-    nch = min(kMaxChunks, (hist + chunk_min - 1u) / chunk_min);
+__device__ __forceinline__ void attn_split(uint32_t hist, uint32_t max_chunks, uint32_t chunk_min, uint32_t& nch,
+                                           uint32_t& clen) {
+    nch = min(max_chunks, (hist + chunk_min - 1u) / chunk_min);
     clen = (hist + nch - 1u) / nch;
 }
 
-__device__ __forceinline__ uint32_t n_chunks(uint32_t slots, uint32_t pos) {
+// Attention workgroups of a block at a position: one per (chunk, query head).
+__device__ __forceinline__ uint32_t n_bunits(uint32_t slots, uint32_t pos) {
     uint32_t nch, clen;
-    attn_split(min(pos + 1u, slots), g_mk.chunk_min, nch, clen);
-    return nch;
+    attn_split(min(pos + 1u, slots), g_mk.max_chunks, g_mk.chunk_min, nch, clen);
+    return nch * g_mk.H;
 }
 
 // Loads this thread's elements i = tid + kMkThreads * k of a static vector (norm weights).
@@ -395,9 +434,9 @@ __device__ __forceinline__ void lm_tile_store(const LmTile& t, uint32_t n16, uin
     const uint32_t tA = tagb + 5u * (l) + 1u, tB = tA + 1u, tC = tA + 2u, tD = tA + 3u, tE = tA + 4u; \
     (void)tA; (void)tB; (void)tC; (void)tD; (void)tE
 
-// The first workgroup of the attention chunks: chunks run on the last workgroups, away from
-// the O-projection and down-projection workgroups (the first ones).
-__device__ __forceinline__ uint32_t chunk_of(uint32_t w, uint32_t nwg) { return nwg - 1u - w; }
+// Attention unit of workgroup w: units run on the last workgroups, away from the O-projection
+// and down-projection workgroups (the first ones).
+__device__ __forceinline__ uint32_t bunit_of(uint32_t w, uint32_t nwg) { return nwg - 1u - w; }
 
 // Phase A: fold f of block l-1 into h, RMSNorm(attn_norm), rows of [Wq | Wk | Wv].
 template <int SD>
@@ -415,7 +454,7 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     if (l > 0) vec_load(g_mk_layers[l - 1u].post_ffw, d, wpost);
     // producers: every workgroup that is not an attention chunk of this block at this position
     uint32_t v0 = 0, v1 = 0;
-    const uint32_t nprod = g_mk.nwg - n_chunks(Ly.slots, pos);
+    const uint32_t nprod = g_mk.nwg - n_bunits(Ly.slots, pos);
     if (w < nprod) split_range(nqkv, nprod, w, v0, v1);
     const uint8_t *wq = Ly.wq, *wk = Ly.wk, *wv = Ly.wv;
     auto rowp = [=](uint32_t v) -> const uint8_t* {
@@ -459,8 +498,11 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     return true;
 }
 
-// Phase B: QK-norm, RoPE, KV append and attention over one chunk of the history; publishes
-// per head the chunk max m, the sum l of exp(s - m) and acc = sum exp(s - m) v.
+// Phase B: one workgroup per (chunk c, query head h). QK-norm and RoPE of q_h and k
+// (src/gemma3.cpp:1045-1104, :1371-1424), the KV append by head 0 of the chunk holding the
+// current position (:1590-1600), then online softmax attention of q_h over the chunk's
+// positions (:1602-1696). Publishes the unnormalised partial {acc[hd], m, l} of (c, h).
+// Waves take positions t = g0 + wave + 8i of each 32-position group; lane owns 4 head dims.
 __device__ __attribute__((noinline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
@@ -472,127 +514,119 @@ __device__ __attribute__((noinline)) bool mk_phase_b(uint32_t l, uint32_t pos, u
     const uint32_t hist = min(pos + 1u, Ly.slots);
     const uint32_t t_first = pos + 1u - hist;
     uint32_t nch, clen;
-    attn_split(hist, g_mk.chunk_min, nch, clen);
-    const uint32_t c = chunk_of(w, g_mk.nwg);
-    if (c >= nch) return true;
+    attn_split(hist, g_mk.max_chunks, g_mk.chunk_min, nch, clen);
+    const uint32_t u = bunit_of(w, g_mk.nwg);   // caller guarantees u < H * nch
+    const uint32_t c = u / H, h = u % H;
     MK_MARK(6);
     const uint32_t c0 = t_first + c * clen;
     const uint32_t c1 = min(pos + 1u, c0 + clen);
     const uint32_t dl = lane * 4u;                 // this lane's 4 head dims
     const bool dlive = dl < hd;
-    // static inputs first: norm weights and this position's RoPE rows
-    float wn[kVec], cs[kVec], sn[kVec];
+    // this thread's gathered elements j = tid, tid + 512 of [q_h | k | v] (3 hd values)
+    const uint32_t nj = 3u * hd;
+    float wn[2], cs[2], sn[2];
+    uint32_t src[2];
     {
         const VRT_AS_GLOBAL float* ct = gp(Ly.global ? g_mk.cos_g : g_mk.cos_l) + static_cast<uint64_t>(pos) * half;
         const VRT_AS_GLOBAL float* st = gp(Ly.global ? g_mk.sin_g : g_mk.sin_l) + static_cast<uint64_t>(pos) * half;
 #pragma unroll
-        for (uint32_t k = 0; k < kVec; ++k) {
-            const uint32_t i = tid + k * kMkThreads;          // element of [q heads | k | v]
-            const uint32_t e = i % hd;
-            wn[k] = i < qw ? gp(Ly.q_norm)[e] : (i < qw + hd ? gp(Ly.k_norm)[e] : 1.0f);
-            cs[k] = (i < qw + hd && e < half) ? ct[e] : 0.0f;
-            sn[k] = (i < qw + hd && e < half) ? st[e] : 0.0f;
+        for (uint32_t k = 0; k < 2u; ++k) {
+            const uint32_t j = tid + k * kMkThreads;
+            const uint32_t e = j % hd;
+            src[k] = j < hd ? h * hd + j : qw - hd + j;
+            wn[k] = j < hd ? gp(Ly.q_norm)[e] : (j < 2u * hd ? gp(Ly.k_norm)[e] : 1.0f);
+            cs[k] = (j < 2u * hd && e < half) ? ct[e] : 0.0f;
+            sn[k] = (j < 2u * hd && e < half) ? st[e] : 0.0f;
         }
     }
-    // this wave's K/V rows of the first 32-position group, from the cache (device-coherent)
+    // this wave's K/V rows of the first group, from the cache (device-coherent)
     const uint32_t kv_bytes = Ly.slots * hd * 4u;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
     v4u kr[kGrpPerWave], vr[kGrpPerWave];
-    auto load_grp = [&](uint32_t g0, uint32_t g1) {
+#pragma unroll
+    for (uint32_t i = 0; i < kGrpPerWave; ++i) kr[i] = vr[i] = v4u{0u, 0u, 0u, 0u};
+    auto kv_off = [&](uint32_t t) { return ((t % Ly.slots) * hd + dl) * 4u; };
+    auto cached = [&](uint32_t t, uint32_t g1) { return t < g1 && t != pos && dlive; };
+    {
+        const uint32_t g1 = min(c1, c0 + kGrp);
 #pragma unroll
         for (uint32_t i = 0; i < kGrpPerWave; ++i) {
-            const uint32_t t = g0 + wave + kMkWaves * i;
-            if (t < g1 && t != pos && dlive) {
-                const uint32_t off = ((t % Ly.slots) * hd + dl) * 4u;
-                kr[i] = co_ld4(rk, off);
-                vr[i] = co_ld4(rv, off);
+            const uint32_t t = c0 + wave + kMkWaves * i;
+            if (cached(t, g1)) {
+                kr[i] = co_ld4(rk, kv_off(t));
+                vr[i] = co_ld4(rv, kv_off(t));
             }
         }
-    };
-    load_grp(c0, min(c1, c0 + kGrp));
-    float qv[kVec];
-    int fail = ll_wait<kVec>(g_mk.x_qkv, nqkv, tA, qv);
+    }
+    float qv[2];
+    int fail = ll_wait_at<2>(g_mk.x_qkv, nqkv, src, nj, tA, qv);
     MK_MARK(7);
-    // QK-norm (src/gemma3.cpp:1045-1104): per head sum of squares, H q heads then k
+    // QK-norm: sums of squares of q_h (j < hd) and k (hd <= j < 2hd), one barrier
     {
-        double hs[9];
+        double sq_q = 0.0, sq_k = 0.0;
 #pragma unroll
-        for (uint32_t h = 0; h < 9u; ++h) hs[h] = 0.0;
-#pragma unroll
-        for (uint32_t k = 0; k < kVec; ++k) {
-            const uint32_t i = tid + k * kMkThreads;
-            const uint32_t h = i / hd;
-#pragma unroll
-            for (uint32_t hh = 0; hh < 9u; ++hh)
-                if (hh == h && i < qw + hd) hs[hh] += static_cast<double>(qv[k]) * static_cast<double>(qv[k]);
+        for (uint32_t k = 0; k < 2u; ++k) {
+            const uint32_t j = tid + k * kMkThreads;
+            const double x2 = static_cast<double>(qv[k]) * static_cast<double>(qv[k]);
+            if (j < hd) sq_q += x2;
+            else if (j < 2u * hd) sq_k += x2;
         }
-        double* red = m.red + 4u * kMkWaves;   // [9][waves] past the blk_sum slots
-#pragma unroll
-        for (uint32_t hh = 0; hh < 9u; ++hh) {
-            if (hh <= H) {
-                const double r = wave_red_sum_d(hs[hh]);
-                if (lane == 0) red[hh * kMkWaves + wave] = r;
-            }
+        sq_q = wave_red_sum_d(sq_q);
+        sq_k = wave_red_sum_d(sq_k);
+        double* red = m.red + 4u * kMkWaves;   // [2][waves] past the blk_sum slots
+        if (lane == 0) {
+            red[wave] = sq_q;
+            red[kMkWaves + wave] = sq_k;
         }
         if (__syncthreads_or(fail)) return false;
+        double ssq = 0.0, ssk = 0.0;
 #pragma unroll
-        for (uint32_t k = 0; k < kVec; ++k) {
-            const uint32_t i = tid + k * kMkThreads;
-            if (i < qw + hd) {
-                const uint32_t h = i / hd;
-                double ss = 0.0;
+        for (uint32_t q = 0; q < kMkWaves; ++q) {
+            ssq += red[q];
+            ssk += red[kMkWaves + q];
+        }
+        const float scq = mk_rms_scale(ssq, hd, g_mk.eps), sck = mk_rms_scale(ssk, hd, g_mk.eps);
 #pragma unroll
-                for (uint32_t q = 0; q < kMkWaves; ++q) ss += red[h * kMkWaves + q];
-                qv[k] *= mk_rms_scale(ss, hd, g_mk.eps) * wn[k];
-            }
-            if (i < nqkv) m.sq[i] = qv[k];
+        for (uint32_t k = 0; k < 2u; ++k) {
+            const uint32_t j = tid + k * kMkThreads;
+            if (j < nj) m.sq[j] = j < hd ? qv[k] * scq * wn[k] : (j < 2u * hd ? qv[k] * sck * wn[k] : qv[k]);
         }
     }
     __syncthreads();
-    // RoPE (src/gemma3.cpp:1371-1424): the thread holding element e < half of a q/k head
-    // rotates the pair (e, e + half)
+    // RoPE: the thread holding element e < half of q_h or k rotates the pair (e, e + half)
 #pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = tid + k * kMkThreads;
-        if (i < qw + hd && (i % hd) < half) {
-            const float a = m.sq[i], b = m.sq[i + half];
-            m.sq[i] = a * cs[k] - b * sn[k];
-            m.sq[i + half] = b * cs[k] + a * sn[k];
+    for (uint32_t k = 0; k < 2u; ++k) {
+        const uint32_t j = tid + k * kMkThreads;
+        if (j < 2u * hd && (j % hd) < half) {
+            const float a = m.sq[j], b = m.sq[j + half];
+            m.sq[j] = a * cs[k] - b * sn[k];
+            m.sq[j + half] = b * cs[k] + a * sn[k];
         }
     }
     __syncthreads();
     MK_MARK(8);
-    const float* sk = m.sq + qw;
+    const float* sk = m.sq + hd;
     const float* sv = sk + hd;
-    // KV append by the chunk that holds the current position (src/gemma3.cpp:1590-1600)
-    if (c1 == pos + 1u) {
+    // KV append by head 0 of the chunk that holds the current position; the other heads use
+    // their own copy of the new row
+    if (h == 0u && c1 == pos + 1u) {
         const uint64_t slot = static_cast<uint64_t>(pos % Ly.slots) * hd;
         for (uint32_t i = tid; i < hd; i += kMkThreads) {
             co_stf(Ly.kc + slot + i, sk[i]);
             co_stf(Ly.vc + slot + i, sv[i]);
         }
-        __builtin_amdgcn_s_waitcnt(0);   // complete before anything this workgroup publishes later
+        __builtin_amdgcn_s_waitcnt(0);   // complete before this workgroup publishes its partial
     }
-    float qr[8][4];
+    float qr[4];
 #pragma unroll
-    for (uint32_t h = 0; h < 8u; ++h)
-#pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) qr[h][e] = (h < H && dlive) ? m.sq[h * hd + dl + e] : 0.0f;
-    // online softmax over 32-position groups; acc is this wave's partial over its positions
-    float acc[8][4];
-    float m_run[8], l_run[8];
-#pragma unroll
-    for (uint32_t h = 0; h < 8u; ++h) {
-        m_run[h] = -INFINITY;
-        l_run[h] = 0.0f;
-#pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) acc[h][e] = 0.0f;
-    }
-    float* sc = m.sc;   // [8][kGrp]: scores, then exp weights
+    for (uint32_t e = 0; e < 4u; ++e) qr[e] = dlive ? m.sq[dl + e] : 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    float* sc = m.sc;   // [kGrp]: scores, then exp weights
     for (uint32_t g0 = c0; g0 < c1; g0 += kGrp) {
         const uint32_t g1 = min(c1, g0 + kGrp);
-        if (g0 != c0) load_grp(g0, g1);
+        const uint32_t n = g1 - g0;
 #pragma unroll
         for (uint32_t i = 0; i < kGrpPerWave; ++i) {
             const uint32_t t = g0 + wave + kMkWaves * i;
@@ -607,96 +641,91 @@ __device__ __attribute__((noinline)) bool mk_phase_b(uint32_t l, uint32_t pos, u
         for (uint32_t i = 0; i < kGrpPerWave; ++i) {
             const uint32_t t = g0 + wave + kMkWaves * i;
             if (t < g1) {   // wave-uniform
+                float p = 0.0f;
+                if (dlive)   // lanes past head_dim hold no key
 #pragma unroll
-                for (uint32_t h = 0; h < 8u; ++h) {
-                    if (h < H) {
-                        float p = 0.0f;
-                        if (dlive)   // lanes past head_dim hold no key
-#pragma unroll
-                            for (uint32_t e = 0; e < 4u; ++e) p += qr[h][e] * __uint_as_float(kr[i][e]);
-                        p = wave_red_sum(p);
-                        if (lane == 0) sc[h * kGrp + (t - g0)] = p * g_mk.attn_scale;
-                    }
-                }
+                    for (uint32_t e = 0; e < 4u; ++e) p += qr[e] * __uint_as_float(kr[i][e]);
+                p = wave_red_sum(p);
+                if (lane == 0) sc[t - g0] = p * g_mk.attn_scale;
             }
         }
-        __syncthreads();
-        const uint32_t n = g1 - g0;
+        // the next group's keys load while this group's softmax and values run
+        const uint32_t n0 = g0 + kGrp, n1 = min(c1, n0 + kGrp);
 #pragma unroll
-        for (uint32_t h = 0; h < 8u; ++h) {
-            if (h >= H || h % kMkWaves != wave) continue;
-            const float mx = wave_red_max(lane < n ? sc[h * kGrp + lane] : -INFINITY);
-            const float m_new = fmaxf(m_run[h], mx);
+        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
+            const uint32_t t = n0 + wave + kMkWaves * i;
+            if (cached(t, n1)) kr[i] = co_ld4(rk, kv_off(t));
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float mx = wave_red_max(lane < n ? sc[lane] : -INFINITY);
+            const float m_new = fmaxf(m_run, mx);
             float e = 0.0f;
             if (lane < n) {
-                e = expf(sc[h * kGrp + lane] - m_new);
-                sc[h * kGrp + lane] = e;
+                e = expf(sc[lane] - m_new);
+                sc[lane] = e;
             }
             const float ls = wave_red_sum(e);
-            if (lane == 0) { m.mw[h] = m_new; m.mw[8u + h] = ls; }
+            if (lane == 0) { m.mw[0] = m_new; m.mw[1] = ls; }
         }
         __syncthreads();
+        {
+            const float m_new = m.mw[0];
+            const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
 #pragma unroll
-        for (uint32_t h = 0; h < 8u; ++h) {
-            if (h < H) {
-                const float m_new = m.mw[h];
-                const float r = m_run[h] == -INFINITY ? 0.0f : expf(m_run[h] - m_new);
-#pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) acc[h][e] *= r;
-                l_run[h] = l_run[h] * r + m.mw[8u + h];
-                m_run[h] = m_new;
-            }
+            for (uint32_t e = 0; e < 4u; ++e) acc[e] *= r;
+            l_run = l_run * r + m.mw[1];
+            m_run = m_new;
         }
 #pragma unroll
         for (uint32_t i = 0; i < kGrpPerWave; ++i) {
             const uint32_t t = g0 + wave + kMkWaves * i;
             if (t < g1 && dlive) {
+                const float pw = sc[t - g0];
 #pragma unroll
-                for (uint32_t h = 0; h < 8u; ++h) {
-                    if (h < H) {
-                        const float pw = sc[h * kGrp + (t - g0)];
-#pragma unroll
-                        for (uint32_t e = 0; e < 4u; ++e) acc[h][e] += pw * __uint_as_float(vr[i][e]);
-                    }
-                }
+                for (uint32_t e = 0; e < 4u; ++e) acc[e] += pw * __uint_as_float(vr[i][e]);
             }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
+            const uint32_t t = n0 + wave + kMkWaves * i;
+            if (cached(t, n1)) vr[i] = co_ld4(rv, kv_off(t));
         }
         __syncthreads();
     }
     MK_MARK(9);
-    // sum the waves' partials and publish {acc[H][hd], m[H], l[H]}
-    float* ra = m.u;   // [waves][H * hd]
+    // sum the waves' partials and publish {acc[hd] of head h, m, l}
+    float* ra = m.u;   // [waves][hd]
     if (dlive) {
 #pragma unroll
-        for (uint32_t h = 0; h < 8u; ++h)
-            if (h < H)
-#pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) ra[wave * qw + h * hd + dl + e] = acc[h][e];
+        for (uint32_t e = 0; e < 4u; ++e) ra[wave * hd + dl + e] = acc[e];
     }
     __syncthreads();
     u64* part = g_mk.x_part + static_cast<uint64_t>(c) * part_stride;
-    for (uint32_t idx = tid; idx < qw; idx += kMkThreads) {
+    for (uint32_t j = tid; j < hd; j += kMkThreads) {
         float sacc = 0.0f;
 #pragma unroll
-        for (uint32_t k = 0; k < kMkWaves; ++k) sacc += ra[k * qw + idx];
-        ll_stf(part + idx, sacc, tB);
+        for (uint32_t k = 0; k < kMkWaves; ++k) sacc += ra[k * hd + j];
+        ll_stf(part + h * hd + j, sacc, tB);
     }
-    if (tid < H) {
-#pragma unroll
-        for (uint32_t h = 0; h < 8u; ++h) {
-            if (h == tid) {
-                ll_stf(part + qw + h, m_run[h], tB);
-                ll_stf(part + qw + H + h, l_run[h], tB);
-            }
-        }
+    if (tid == 0) {
+        ll_stf(part + qw + h, m_run, tB);
+        ll_stf(part + qw + H + h, l_run, tB);
     }
     MK_MARK(10);
     return true;
 }
 
+// Whether this workgroup runs an attention unit of block l at position pos.
+__device__ __forceinline__ bool mk_in_b(uint32_t l, uint32_t pos) {
+    return bunit_of(blockIdx.x, g_mk.nwg) < n_bunits(g_mk_layers[l].slots, pos);
+}
+
 // Phase C: merge the chunks (att = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c), Wo rows.
+// Inlined into the kernel: its gather keeps many loads in flight, and as a call it would save
+// and restore callee-saved registers through scratch in every block.
 template <int SA>
-__device__ __attribute__((noinline)) bool mk_phase_c(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
+__device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
     MK_UNIFORM(l);
@@ -708,7 +737,7 @@ __device__ __attribute__((noinline)) bool mk_phase_c(uint32_t l, uint32_t pos, u
     MK_MARK(11);
     const uint32_t hist = min(pos + 1u, Ly.slots);
     uint32_t nch, clen;
-    attn_split(hist, g_mk.chunk_min, nch, clen);
+    attn_split(hist, g_mk.max_chunks, g_mk.chunk_min, nch, clen);
     uint32_t v0, v1;
     split_range(d, g_mk.nc, w, v0, v1);
     const uint8_t* wo = Ly.wo;
@@ -765,7 +794,7 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     vec_load(Ly.post_attn, d, wpa);
     vec_load(Ly.ffn_norm, d, wffn);
     uint32_t p0 = 0, p1 = 0;
-    const uint32_t nprod = g_mk.nwg - n_chunks(Ly.slots, pos);
+    const uint32_t nprod = g_mk.nwg - n_bunits(Ly.slots, pos);
     if (w < nprod) split_range(F, nprod, w, p0, p1);
     const uint32_t v0 = 2u * p0, v1 = 2u * p1;
     const uint8_t *wg = Ly.wg, *wu = Ly.wu;
@@ -951,7 +980,14 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tLM, uint32_t wan
 }
 
 // Reduces the argmax partials tagged `tag` (every workgroup that calls it gets the same result).
-__device__ __attribute__((noinline)) bool mk_reduce_argmax(uint32_t tag, uint32_t& idx, float& val) {
+struct MkArg {
+    uint32_t idx;
+    float val;
+    bool ok;
+};
+
+// Returned by value (in registers): reference out-parameters would go through scratch.
+__device__ __attribute__((noinline)) MkArg mk_reduce_argmax(uint32_t tag) {
     MK_LOCALS;
     MK_UNIFORM(tag);
     __shared__ float s_v[kMkWaves];
@@ -973,9 +1009,7 @@ __device__ __attribute__((noinline)) bool mk_reduce_argmax(uint32_t tag, uint32_
     for (uint32_t k = 1; k < kMkWaves; ++k)
         if (am_better(s_v[k], s_i[k], bv, bi)) { bv = s_v[k]; bi = s_i[k]; }
     __syncthreads();
-    idx = bi;
-    val = bv;
-    return good;
+    return MkArg{bi, bv, good};
 }
 
 // The step embedding: dequantised row * sqrt(d) (src/gemma3.cpp:1106-1136), this thread's
@@ -1023,10 +1057,11 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
         // ---- token of this step ----
         uint32_t token;
         if (prev_lm_tag != 0u) {
-            uint32_t idx;
-            float val;
-            ok = mk_reduce_argmax(prev_lm_tag, idx, val);
+            const MkArg a = mk_reduce_argmax(prev_lm_tag);
+            ok = a.ok;
             if (!ok) break;
+            const uint32_t idx = a.idx;
+            const float val = a.val;
             if (w == 0 && tid == 0) { VRT_AS_GLOBAL vrt_argmax_result* r = gp(g_mk.results) + (s - 1u); r->index = idx; r->value = val; }
             if (s >= feed_until) {
                 token = idx < g_mk.V ? idx : 0u;
@@ -1051,13 +1086,15 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             const bool tr = g_mk.trace_slots != 0u && si == 0u && l == 1u;   // sub-phase marks of block 1
             ok = mk_phase_a<SD>(l, s, tagb, tr);
             MK_TRACE(5u * l + 1u);
-            ok = ok && mk_phase_b(l, s, tagb, tr);
+            // B, C and E run on a subset of the workgroups; the others skip the call (and its
+            // register save/restore through scratch) entirely
+            ok = ok && (!mk_in_b(l, s) || mk_phase_b(l, s, tagb, tr));
             MK_TRACE(5u * l + 2u);
-            ok = ok && mk_phase_c<SA>(l, s, tagb, tr);
+            ok = ok && (w >= g_mk.nc || mk_phase_c<SA>(l, s, tagb, tr));
             MK_TRACE(5u * l + 3u);
             ok = ok && mk_phase_d<SD>(l, s, tagb, tr);
             MK_TRACE(5u * l + 4u);
-            ok = ok && mk_phase_e<SF>(l, tagb, tr);
+            ok = ok && (w >= g_mk.ne || mk_phase_e<SF>(l, tagb, tr));
             MK_TRACE(5u * l + 5u);
         }
         ok = ok && mk_phase_fold(tagb);
@@ -1076,9 +1113,10 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
     // ---- end of launch: workgroup 0 records the last step's result and the step state ----
     if (w == 0) {
         if (ok && prev_lm_tag != 0u) {
-            uint32_t idx;
-            float val;
-            ok = mk_reduce_argmax(prev_lm_tag, idx, val);
+            const MkArg a = mk_reduce_argmax(prev_lm_tag);
+            ok = a.ok;
+            const uint32_t idx = a.idx;
+            const float val = a.val;
             if (ok && tid == 0) {
                 { VRT_AS_GLOBAL vrt_argmax_result* r = gp(g_mk.results) + (s - 1u); r->index = idx; r->value = val; }
                 if (s >= feed_until) {
@@ -1191,8 +1229,9 @@ int mk_setup(vrt_g3* g) {
     const uint32_t cap_f = kMkWaves * (64u / static_cast<uint32_t>(sf.S));
     const uint32_t nqkv = qw + 2u * hd;
     // every workgroup must cover its share of the all-workgroup phases in one batch
-    const uint32_t nprod = nwg - kMaxChunks;
-    if (nwg < 2u * kMaxChunks || nwg > 512u || (nqkv + nprod - 1u) / nprod > cap_d ||
+    const uint32_t max_chunks = std::min(kMaxChunks, kMaxBUnits / H);
+    const uint32_t nprod = nwg - H * max_chunks;
+    if (nwg < 2u * H * max_chunks || nwg > 512u || 3u * hd > 2u * kMkThreads || (nqkv + nprod - 1u) / nprod > cap_d ||
         2u * ((F + nprod - 1u) / nprod) > 2u * cap_d || nqkv > kVec * kMkThreads) {
         mk_destroy(g);
         return VRT_OK;
@@ -1205,6 +1244,7 @@ int mk_setup(vrt_g3* g) {
     P.ne = std::min(nwg, (d + cap_f - 1u) / cap_f);
     if ((d + P.nc - 1u) / P.nc > cap_a || (d + P.ne - 1u) / P.ne > cap_f) { mk_destroy(g); return VRT_OK; }
     P.chunk_min = 32u;
+    P.max_chunks = max_chunks;
     P.lm_rows = (c.vocab_size + nwg - 1u) / nwg;
     const uint64_t rb = static_cast<uint64_t>(d / 32u) * 34u;
     P.lm_tile_rows = static_cast<uint32_t>(std::min<uint64_t>(P.lm_rows, (kLmUnits * kMkThreads * 16u - 16u) / rb));
