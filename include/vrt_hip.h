@@ -4,8 +4,8 @@
  * nonzero status whose message is available from vrt_last_error() on the calling thread.
  *
  * Each declaration names the reference interface it replaces. The reference exposes a
- * C++ class API (namespace vortexrt) over Vulkan; the headers under include/vortexrt keep that C++
- * surface and is implemented on top of these functions (libvortexrt.so).
+ * C++ class API (namespace vortexrt) over Vulkan; the headers under include/vortexrt keep that
+ * C++ surface, implemented on top of these functions in libvortexrt.so.
  *
  * Conventions
  *  - Device pointers come from vrt_alloc (or any HIP allocation on the context's device).

@@ -199,3 +199,51 @@ def test_abi_library_exports_declared_symbols():
     nm = subprocess.run(["nm", "-D", "--defined-only", vrt.LIB_PATH], capture_output=True, text=True).stdout
     exported = {l.split()[-1] for l in nm.splitlines() if " T " in l}
     assert exported == set(syms), f"unexpected exports: {sorted(exported - set(syms))}"
+
+
+# ---- C++ surface (vortexrt::GgufFile) -------------------------------------------------------
+
+CPP_BIN = os.path.join(REPO, "tests", "cpp", "_build")
+
+
+def _cpp(name):
+    exe = os.path.join(CPP_BIN, name)
+    if not os.path.exists(exe):
+        pytest.skip(f"{name} not built (vortex-rt_amd/build.py)")
+    return exe
+
+
+def test_cpp_gguf_reader_matches(tmp_path):
+    """The C++ GgufFile reads our writer's file like gguf.py does, and its Q8_0 row dequant
+    equals the oracle's bit for bit."""
+    import json
+    p = str(tmp_path / "tiny.gguf")
+    synth.write_gemma3_gguf(p, seed=4, **synth.TINY)
+    out = subprocess.run([_cpp("gguf_test"), p, "token_embd.weight", "999", "blk.2.ffn_down.weight", "5"],
+                         capture_output=True, text=True, check=True).stdout
+    got = json.loads(out)
+    f = gguf.GgufFile.open(p)
+    assert got["version"] == f.version and got["data_offset"] == f.data_offset and got["alignment"] == f.alignment
+    assert got["arch"] == "gemma3" and len(got["tensors"]) == len(f.tensors)
+    for name, t in f.tensors.items():
+        typ, off, nbytes, *dims = got["tensors"][name]
+        assert (typ, off, nbytes, dims) == (t.type, t.offset, t.nbytes(), t.dims)
+    for (name, r), row in zip((("token_embd.weight", 999), ("blk.2.ffn_down.weight", 5)), got["rows"]):
+        t = f.tensors[name]
+        nb = t.dims[0] // 32
+        blk = f.tensor_bytes(name)[r * nb * 34:(r + 1) * nb * 34]
+        assert np.array_equal(np.array(row, dtype=np.float32), oracle.dequant(blk))
+    f.close()
+
+
+def test_cpp_gguf_reader_rejects_corruption(tmp_path):
+    p = str(tmp_path / "tiny.gguf")
+    synth.write_gemma3_gguf(p, seed=1, **synth.TINY)
+    raw = open(p, "rb").read()
+    for name, data, pat in (("magic", b"XXXX" + raw[4:], "Invalid GGUF magic"),
+                            ("version", raw[:4] + (9).to_bytes(4, "little") + raw[8:], "Unsupported GGUF version"),
+                            ("trunc", raw[:200], "end of GGUF file")):
+        q = str(tmp_path / f"{name}.gguf")
+        open(q, "wb").write(data)
+        r = subprocess.run([_cpp("gguf_test"), q], capture_output=True, text=True)
+        assert r.returncode == 1 and pat in r.stdout, (name, r.stdout)

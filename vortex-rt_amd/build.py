@@ -71,9 +71,31 @@ def build_cpp() -> str:
     return LIB_CPP
 
 
+CPP_TESTS = os.path.join(REPO, "tests", "cpp")
+
+
+def build_cpp_tests(jobs: int = 8) -> list:
+    """The C++ test programs of tests/cpp against libvortexrt.so, into tests/cpp/_build."""
+    srcs = sorted(glob.glob(os.path.join(CPP_TESTS, "*.cpp")))
+    out_dir = os.path.join(CPP_TESTS, "_build")
+    os.makedirs(out_dir, exist_ok=True)
+    rpath = "-Wl,-rpath,$ORIGIN/../../../vortex-rt_amd/_build"
+
+    def one(src):
+        exe = os.path.join(out_dir, os.path.basename(src)[:-4])
+        _run(["g++"] + CXX_FLAGS + ["-I" + CPP_TESTS, "-o", exe + ".tmp", src, "-L" + OUT, "-lvortexrt", "-lvrt_hip",
+                                    rpath])
+        os.replace(exe + ".tmp", exe)
+        return exe
+
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        return list(ex.map(one, srcs))
+
+
 def build_all(jobs: int = 8):
     build_hip(jobs)
     build_cpp()
+    build_cpp_tests(jobs)
 
 
 if __name__ == "__main__":
