@@ -79,6 +79,34 @@ def phase_split(g, prompt, cfg, steps: int = 24):
     return {k: round(v, 2) for k, v in out.items()}
 
 
+def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256):
+    """The long-context workload: an n_prompt-token prompt of uniform ids (seed 1) prefilled
+    untimed, then `steps` greedy decode steps timed with events (positions n_prompt..)."""
+    prompt = synth_ids(1, n_prompt, cfg.vocab_size)
+    g.start(prompt, steps + 1)
+    g.step(n_prompt)
+    ctx.sync()
+    ev0, ev1 = ctx.event(), ctx.event()
+    ctx.record(ev0)
+    g.step(steps)
+    ctx.record(ev1)
+    ms = ctx.elapsed_ms(ev0, ev1)
+    ctx.sync()
+    g.collect()
+    total = sum(step_bytes(cfg, n_prompt + i) for i in range(steps))
+    gbps = total / (ms / 1e3) / 1e9
+    return {"workload": f"{n_prompt}-token prompt (untimed prefill), {steps} timed greedy decode steps at positions "
+                        f"{n_prompt}..{n_prompt + steps - 1}",
+            "tokens_per_s": round(steps / (ms / 1e3), 2), "ms_per_step": round(ms / steps, 5),
+            "bytes_per_step_mean": int(total / steps), "hbm_gbps": round(gbps, 1),
+            "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
+def synth_ids(seed: int, n: int, vocab: int):
+    import synth
+    return synth.uniform_ids(seed, n, 2, vocab)
+
+
 def copy_calibration(nbytes: int = 1 << 30):
     """A plain device copy of known size for scaling the PMC counters (FETCH_SIZE / WRITE_SIZE
     of this dispatch against nbytes read and nbytes written)."""
@@ -126,6 +154,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-phases", action="store_true", help="skip the traced per-phase split")
+    ap.add_argument("--no-long", action="store_true", help="skip the 8192-token long-context measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
@@ -184,6 +213,7 @@ def main():
     gbps = total_bytes / (ms / 1e3) / 1e9
 
     phases = None if args.no_phases else phase_split(g, prompt, cfg)
+    longctx = None if args.no_long else long_context(ctx, g, cfg)
 
     out = {
         "metric": METRIC,
@@ -221,6 +251,7 @@ def main():
             "algorithmic_bytes_per_launch": total_bytes,
         },
         "phase_us_per_step": phases,
+        "long_context": longctx,
         "cpu_baseline": None,
     }
     g.close()

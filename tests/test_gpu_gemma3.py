@@ -176,3 +176,50 @@ def test_persistent_split_launches(ctx, tiny_model):
     parts = g.collect()
     g.close()
     assert np.array_equal(whole, parts)
+
+
+MEDIUM = dict(n_layers=6, d_model=512, n_heads=4, head_dim=128, ffn=1024, vocab=2000, context=2048, window=64)
+
+
+def test_long_history_chunked_attention(ctx, model_dir):
+    """Histories far past one chunk: the global block attends over 700 positions (16 chunks of
+    44, several 32-position groups each; the merge gathers its partials in two rounds), the
+    local ones over their 64-position window. Teacher-forced tokens and logits of the last
+    steps against the oracle."""
+    path = os.path.join(str(model_dir), "medium.gguf")
+    if not os.path.exists(path):
+        synth.write_gemma3_gguf(path, seed=21, **MEDIUM)
+    toks = synth.uniform_ids(5, 700, 2, MEDIUM["vocab"])
+    first = toks.size - 6
+    g = vrt.Gemma3(ctx, path)
+    try:
+        assert g.persistent_available()
+        print("[g3] medium model, 700 forced steps", flush=True)
+        got = g.forced(toks, first)
+    finally:
+        g.close()
+    ref = _oracle_forced(path, toks, first)
+    for i in range(first, toks.size):
+        assert got["index"][i] == ref[i]["index"], f"step {i}"
+        assert abs(got["value"][i] - ref[i]["value"]) <= LOGIT_TOL * np.max(np.abs(ref[i]["logits"]))
+
+
+def test_long_context_full_shape(ctx, full_model):
+    """Config 3 shape: an 8192-token prompt, then greedy steps, on the persistent kernel and on
+    the multi-kernel step (an independent attention implementation): the same greedy tokens and
+    argmax logits within the tolerance. Global blocks attend over up to 8200 positions."""
+    g = vrt.Gemma3(ctx, full_model)
+    toks = synth.uniform_ids(1, 8200, 2, 262144)
+    first = 8192 - 1
+    try:
+        print("[g3] 8200 forced steps, persistent", flush=True)
+        g.set_persistent(True)
+        a = g.forced(toks, first)
+        print("[g3] 8200 forced steps, multi-kernel", flush=True)
+        g.set_persistent(False)
+        b = g.forced(toks, first)
+    finally:
+        g.close()
+    assert np.array_equal(a["index"][first:], b["index"][first:])
+    scale = np.max(np.abs(b["value"][first:]))
+    assert np.max(np.abs(a["value"][first:] - b["value"][first:])) <= LOGIT_TOL * scale

@@ -6,6 +6,7 @@ fallback path. Device memory is owned by DeviceBuffer objects (vrt_alloc / vrt_f
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 import os
 
 import numpy as np
@@ -141,9 +142,12 @@ class Context:
         info = DeviceInfo()
         check(lib().vrt_ctx_info(self.h, C.byref(info)))
         self.info = info
+        self._children = weakref.WeakSet()   # executors and buffers: released before the context
 
     def close(self):
         if getattr(self, "h", None):
+            for c in list(getattr(self, "_children", ())):
+                c.close()
             lib().vrt_ctx_destroy(self.h)
             self.h = None
 
@@ -185,6 +189,7 @@ class DeviceBuffer:
         p = C.c_void_p()
         check(lib().vrt_alloc(ctx.h, self.nbytes, kind, C.byref(p)))
         self.ptr = p.value
+        ctx._children.add(self)
 
     def write(self, arr: np.ndarray, offset: int = 0):
         arr = np.ascontiguousarray(arr)
@@ -197,8 +202,11 @@ class DeviceBuffer:
         check(lib().vrt_memcpy(self.ctx.h, ptr(out), self.ptr + offset, out.nbytes))
         return out
 
+    def close(self):
+        self.free()
+
     def free(self):
-        if self.ptr:
+        if getattr(self, "ptr", None):
             lib().vrt_free(self.ctx.h, self.ptr)
             self.ptr = None
 
@@ -331,6 +339,7 @@ class Gemma3:
         h = C.c_void_p()
         check(lib().vrt_g3_create(ctx.h, C.byref(desc), C.byref(h)))
         self.h = h.value
+        ctx._children.add(self)
         self._keep.clear()
 
     def close(self):
