@@ -102,6 +102,47 @@ def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256):
             "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
+def prefill_flops(cfg, T: int) -> int:
+    """Algorithmic FLOPs of a T-token prefill: every projection as a GEMM over T rows, causal
+    attention (QK and PV over the keys each position sees), and the last row's LM head."""
+    d, H, hd, F, V, L = (cfg.embedding_length, cfg.head_count, cfg.head_dim, cfg.feed_forward_length,
+                         cfg.vocab_size, cfg.block_count)
+    params = (H * hd + 2 * hd) * d + d * H * hd + 2 * F * d + d * F
+    total = 2 * T * params * L + 2 * V * d
+    for l in range(L):
+        glob = (l + 1) % 6 == 0
+        w = T if (glob or cfg.sliding_window == 0) else cfg.sliding_window
+        keys = sum(min(t + 1, w) for t in range(T))
+        total += 2 * 2 * H * hd * keys
+    return total
+
+
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_bench(ctx, g, cfg, T: int = 512, reps: int = 5):
+    """The batched prefill workload: T uniform prompt ids (seed 4) in one vrt_g3_prefill call,
+    timed with events over `reps` calls after a warm-up call."""
+    prompt = synth_ids(4, T, cfg.vocab_size)
+    g.prefill(prompt, top_k=1)
+    ctx.sync()
+    ev0, ev1 = ctx.event(), ctx.event()
+    ctx.record(ev0)
+    for _ in range(reps):
+        g.prefill(prompt, top_k=1)
+    ctx.record(ev1)
+    ctx.sync()
+    ms = ctx.elapsed_ms(ev0, ev1) / reps
+    flops = prefill_flops(cfg, T)
+    tflops = flops / (ms / 1e3) / 1e12
+    return {"workload": f"{T}-token prompt, one batched prefill (MFMA Q8_0 GEMMs, causal attention, last-row LM head)",
+            "tokens_per_s": round(T / (ms / 1e3), 1), "ms": round(ms, 4), "gflop": round(flops / 1e9, 2),
+            "tflops": round(tflops, 2), "mfma_peak_tflops": MFMA_F16_PEAK_TFLOPS,
+            "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "note": "projection GEMMs issue two f16 MFMAs per product (activation hi + lo parts); utilisation "
+                    "counts the algorithmic FLOPs only"}
+
+
 def synth_ids(seed: int, n: int, vocab: int):
     import synth
     return synth.uniform_ids(seed, n, 2, vocab)
@@ -155,6 +196,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-phases", action="store_true", help="skip the traced per-phase split")
     ap.add_argument("--no-long", action="store_true", help="skip the 8192-token long-context measurement")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token batched prefill measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
@@ -214,6 +256,7 @@ def main():
 
     phases = None if args.no_phases else phase_split(g, prompt, cfg)
     longctx = None if args.no_long else long_context(ctx, g, cfg)
+    prefill = None if args.no_prefill else prefill_bench(ctx, g, cfg)
 
     out = {
         "metric": METRIC,
@@ -252,6 +295,7 @@ def main():
         },
         "phase_us_per_step": phases,
         "long_context": longctx,
+        "prefill": prefill,
         "cpu_baseline": None,
     }
     g.close()

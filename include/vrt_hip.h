@@ -186,6 +186,17 @@ int vrt_g3_reset(vrt_g3* g3);
 int vrt_g3_decode(vrt_g3* g3, uint32_t token, uint32_t position, uint32_t top_k,
                   vrt_argmax_result* out, float* hidden_out);
 
+/* Batched prompt prefill (the prompt loop of src/gemma3.cpp:2099-2111 in one pass; the
+ * reference has no batched path): resets the cache, then runs positions 0..n-1 with every
+ * projection as a Q8_0 x activation GEMM on MFMA and causal local/global attention; the last
+ * position runs the LM head as vrt_g3_decode would with top_k (0 skips it, 1 is the fused
+ * argmax into *out, > 1 keeps the logits for vrt_g3_logits). hidden_out (embedding_length
+ * floats, host) may be NULL. Decoding continues at position n. Prompts longer than the
+ * batched workspace (min(context_length, 2048) positions) or shapes it does not cover run as
+ * serial decode steps. On any error the KV cache is reset. */
+int vrt_g3_prefill(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t top_k, vrt_argmax_result* out,
+                   float* hidden_out);
+
 /* Logits of the last step that ran the LM head with top_k > 1 (host copy, n floats). */
 int vrt_g3_logits(vrt_g3* g3, float* host_logits, uint32_t n);
 

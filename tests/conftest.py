@@ -49,3 +49,14 @@ def tiny_model_nowindow(model_dir):
     import synth
     kw = dict(synth.TINY)
     return _tiny(model_dir, "tiny_nowin.gguf", seed=12, with_window=False, **kw)
+
+
+@pytest.fixture(scope="session")
+def full_model(model_dir):
+    """Gemma-3-270M shape: 18 blocks, d 640, 4 heads x 256, FFN 2048, vocab 262144, seed 0."""
+    import synth
+    path = os.path.join(str(model_dir), "gemma3_270m_seed0.gguf")
+    if not os.path.exists(path):
+        print("[g3] writing Gemma-3-270M-shape model", flush=True)
+        synth.write_gemma3_gguf(path, seed=0, **synth.GEMMA3_270M)
+    return path

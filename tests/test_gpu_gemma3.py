@@ -108,15 +108,6 @@ def test_decode_errors_reset(ctx, tiny_g3):
         tiny_g3.generate(np.arange(2, 200, dtype=np.uint32), 100)
 
 
-@pytest.fixture(scope="module")
-def full_model(model_dir):
-    path = os.path.join(str(model_dir), "gemma3_270m_seed0.gguf")
-    if not os.path.exists(path):
-        print("[g3] writing Gemma-3-270M-shape model", flush=True)
-        synth.write_gemma3_gguf(path, seed=0, **synth.GEMMA3_270M)
-    return path
-
-
 def test_full_shape_greedy_and_logits(ctx, full_model):
     """Config 2 shapes: 8-token prompt, greedy continuation compared token by token and the
     last step's logits within 1e-3."""

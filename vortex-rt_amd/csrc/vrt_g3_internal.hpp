@@ -73,6 +73,16 @@ struct LaunchDesc {
 
 struct MkState;   // persistent decode kernel: exchange buffers and launch shape (vrt_decode.hip)
 
+// Batched prefill workspace (vrt_prefill.hip); max_t == 0: prefill unavailable for the shape.
+struct PfState {
+    uint32_t max_t = 0;     // prompt positions per call
+    float* h = nullptr;     // [max_t][d] residual stream
+    float* x = nullptr;     // [max_t][d] sublayer outputs (O projection, down projection)
+    void* ahi = nullptr;    // [max_t][max(d, H*hd, F)] GEMM input, f16 high part
+    void* alo = nullptr;    //   ... and low part
+    float* big = nullptr;   // [max_t][max(H*hd + 2*hd, 2F)] q|k|v rows, then gate|up rows
+};
+
 }  // namespace vrt
 
 struct vrt_g3 {
@@ -94,6 +104,7 @@ struct vrt_g3 {
     vrt::MkState* mk = nullptr;
     uint32_t mk_tag = 1;         // first exchange tag of the next persistent launch
     hipGraphExec_t graph = nullptr;
+    vrt::PfState pf;             // batched prefill (vrt_prefill.hip)
     uint32_t gen_prompt = 0;     // generation in flight (vrt_g3_start .. vrt_g3_collect)
     uint32_t gen_max = 0;
     uint64_t gen_steps = 0;
@@ -108,5 +119,11 @@ void mk_destroy(vrt_g3* g);
 int mk_clear_abort(vrt_g3* g);
 int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int mk_set_trace(vrt_g3* g, bool on);
+// Batched prefill (vrt_prefill.hip): workspace for up to max_t positions, and one prefill of T
+// positions from position 0 whose last position runs g3_enqueue_lm.
+int pf_setup(vrt_g3* g, uint32_t max_t);
+int pf_run(vrt_g3* g, uint32_t T);
+// Final residual + output norm + LM head + argmax of the current step (vrt_gemma3.hip).
+int g3_enqueue_lm(vrt_g3* g, hipStream_t s);
 int mk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);
 }  // namespace vrt

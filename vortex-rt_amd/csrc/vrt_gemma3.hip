@@ -32,6 +32,8 @@
 
 namespace vrt {
 
+constexpr uint32_t kPrefillMax = 2048;   // positions of one batched prefill
+
 constexpr int kThreads = 256;
 constexpr int kMaxE = 8;  // vector elements per thread in prologues: d, H*hd, F <= 2048
 
@@ -656,7 +658,13 @@ static int g3_enqueue_step(vrt_g3* g, hipStream_t stream) {
             VRT_HIP_CHECK(hipLaunchKernel(g->ld_down.fn, dim3(g->ld_down.grid), dim3(kThreads), args, g->ld_down.smem, stream));
         }
     }
-    const float* last_post = g->layers[L - 1].post_ffw;
+    return g3_enqueue_lm(g, stream);
+}
+
+// Final residual (P.f normed by the last block's post-FFW norm, plus P.hmid), output norm and
+// the LM head + argmax of the step in G3State::step.
+int vrt::g3_enqueue_lm(vrt_g3* g, hipStream_t stream) {
+    const float* last_post = g->layers[g->cfg.block_count - 1].post_ffw;
     uint32_t mode = 0;
     void* args[] = {&g->P, &last_post, &g->out_norm_dev, &g->lm_rows_per_wg, &mode};
     VRT_HIP_CHECK(hipLaunchKernel(g->ld_lm.fn, dim3(g->ld_lm.grid), dim3(kThreads), args, g->ld_lm.smem, stream));
@@ -891,6 +899,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
     }
     if (int rc = g3_write_ctl(g, 0, 0xffffffffu, 0xffffffffu, 0)) return fail(rc);
     if (int rc = mk_setup(g)) return fail(rc);
+    if (int rc = pf_setup(g, std::min(c.context_length, kPrefillMax))) return fail(rc);
     VRT_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     *out = g;
     return VRT_OK;
@@ -950,6 +959,40 @@ extern "C" int vrt_g3_decode(vrt_g3* g, uint32_t token, uint32_t position, uint3
         if (out) *out = r;
     }
     g->next_pos = position + 1u;
+    return VRT_OK;
+}
+
+extern "C" int vrt_g3_prefill(vrt_g3* g, const uint32_t* tokens, uint32_t n, uint32_t top_k, vrt_argmax_result* out,
+                              float* hidden_out) {
+    VRT_REQUIRE(g && tokens, "vrt_g3_prefill: null argument");
+    if (n == 0) return set_error(VRT_ERR_INVALID, "Gemma 3 prompt produced no input tokens");
+    if (n > g->cfg.context_length) return set_error(VRT_ERR_STATE, "Gemma 3 context length exceeded");
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= g->cfg.vocab_size) return g3_fail_reset(g, VRT_ERR_INVALID, "Token id is outside Gemma 3 vocabulary");
+    if (g->pf.max_t == 0u || n > g->pf.max_t) {   // serial decode steps (src/gemma3.cpp:2099-2111)
+        g->next_pos = 0;
+        for (uint32_t i = 0; i < n; ++i)
+            if (int rc = vrt_g3_decode(g, tokens[i], i, i + 1u == n ? top_k : 0u, out, i + 1u == n ? hidden_out : nullptr))
+                return rc;
+        return VRT_OK;
+    }
+    hipStream_t s = g->ctx->stream;
+    g->next_pos = 0;
+    VRT_HIP_CHECK(hipMemcpyAsync(g->P.tokens, tokens, n * 4u, hipMemcpyHostToDevice, s));
+    if (int rc = g3_write_ctl(g, n - 1u, top_k ? n - 1u : 0xffffffffu, 0xffffffffu, top_k > 1 ? 1u : 0u)) return rc;
+    if (int rc = pf_run(g, n)) return g3_fail_reset(g, rc, vrt_last_error());
+    if (hidden_out)
+        VRT_HIP_CHECK(hipMemcpyAsync(hidden_out, g->P.hidden, g->cfg.embedding_length * 4u, hipMemcpyDeviceToHost, s));
+    VRT_HIP_CHECK(hipMemcpyAsync(g->host_res, g->P.results + (n - 1u), sizeof(vrt_argmax_result), hipMemcpyDeviceToHost, s));
+    G3State st;
+    if (int rc = g3_check_state(g, &st)) return rc;
+    if (top_k) {
+        const vrt_argmax_result r = g->host_res[0];
+        if (r.index >= g->cfg.vocab_size || !std::isfinite(r.value))  // :1171-1176
+            return g3_fail_reset(g, VRT_ERR_NUMERIC, "GPU argmax produced invalid result");
+        if (out) *out = r;
+    }
+    g->next_pos = n;
     return VRT_OK;
 }
 

@@ -88,6 +88,7 @@ SIGNATURES = {
     "vrt_g3_destroy": (_I, [_P]),
     "vrt_g3_reset": (_I, [_P]),
     "vrt_g3_decode": (_I, [_P, _U32, _U32, _U32, C.POINTER(ArgmaxResult), _P]),
+    "vrt_g3_prefill": (_I, [_P, _P, _U32, _U32, C.POINTER(ArgmaxResult), _P]),
     "vrt_g3_logits": (_I, [_P, _P, _U32]),
     "vrt_g3_generate": (_I, [_P, _P, _U32, _U32, _P, C.POINTER(_U32)]),
     "vrt_g3_start": (_I, [_P, _P, _U32, _U32]),
@@ -388,6 +389,14 @@ class Gemma3:
         r = ArgmaxResult()
         hbuf = np.empty(self.config.embedding_length, dtype=np.float32) if hidden else None
         check(lib().vrt_g3_decode(self.h, token, pos, top_k, C.byref(r), ptr(hbuf)))
+        return (int(r.index), float(r.value)), hbuf
+
+    def prefill(self, tokens, top_k: int = 1, hidden: bool = False):
+        """Batched prefill of positions 0..n-1; returns ((index, value), hidden or None)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        r = ArgmaxResult()
+        hbuf = np.empty(self.config.embedding_length, dtype=np.float32) if hidden else None
+        check(lib().vrt_g3_prefill(self.h, ptr(t), t.size, top_k, C.byref(r), ptr(hbuf)))
         return (int(r.index), float(r.value)), hbuf
 
     def logits(self) -> np.ndarray:
