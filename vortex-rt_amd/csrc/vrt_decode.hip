@@ -471,6 +471,7 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
         int fail = ll_wait<kVec>(g_mk.x_f, d, tagb + 5u * (l - 1u) + 5u, f);
         MK_MARK(2);
         const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(f, d), fail), d, g_mk.eps);
+        MK_MARK(4);   // every wave has its inputs
         if (fail) return false;
 #pragma unroll
         for (uint32_t k = 0; k < kVec; ++k) hv[k] = f[k] * (sc * wpost[k]) + hv[k];   // src/gemma3.cpp:1849-1855
@@ -576,6 +577,7 @@ __device__ __attribute__((noinline)) bool mk_phase_b(uint32_t l, uint32_t pos, u
             red[kMkWaves + wave] = sq_k;
         }
         if (__syncthreads_or(fail)) return false;
+        MK_MARK(27);   // every wave has its inputs
         double ssq = 0.0, ssk = 0.0;
 #pragma unroll
         for (uint32_t q = 0; q < kMkWaves; ++q) {
@@ -805,6 +807,7 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     int fail = ll_wait<kVec>(g_mk.x_o, d, tC, o);
     MK_MARK(16);
     const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(o, d), fail), d, g_mk.eps);
+    MK_MARK(28);   // every wave has its inputs
     if (fail) return false;
 #pragma unroll
     for (uint32_t k = 0; k < kVec; ++k) hv[k] = o[k] * (sc * wpa[k]) + hv[k];      // :1703-1711

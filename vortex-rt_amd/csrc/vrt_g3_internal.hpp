@@ -81,6 +81,10 @@ struct PfState {
     void* ahi = nullptr;    // [max_t][max(d, H*hd, F)] GEMM input, f16 high part
     void* alo = nullptr;    //   ... and low part
     float* big = nullptr;   // [max_t][max(H*hd + 2*hd, 2F)] q|k|v rows, then gate|up rows
+    float* s = nullptr;     // [H][max_t][Tp] attention scores (Tp: max_t rounded up to 64)
+    void* phi = nullptr;    // [H][max_t][Tp] attention probabilities, f16 high part
+    void* plo = nullptr;    //   ... and low part
+    float* vt = nullptr;    // [hd][Tp] V transposed
 };
 
 }  // namespace vrt

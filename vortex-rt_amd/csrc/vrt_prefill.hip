@@ -27,9 +27,7 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kPfThreads = 256;
-constexpr uint32_t kPfTile = 64;     // GEMM tile (rows and columns) of one workgroup
-constexpr uint32_t kPfQT = 32;       // attention: queries per workgroup
-constexpr uint32_t kPfKT = 32;       // attention: keys per LDS tile
+constexpr uint32_t kPfTile = 64;     // attention score rows are padded to a multiple of this
 
 // ---- row kernels ---------------------------------------------------------------------------
 
@@ -133,103 +131,275 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_gelu(const float* gu, uint32_
     }
 }
 
-// ---- Q8_0 x activation GEMM on MFMA ----------------------------------------------------------
+// ---- GEMM on MFMA: Q8_0 weights or fp32 rows as B ---------------------------------------------
 
 struct PfGemm {
-    const _Float16* ahi;     // [M][K] row-major
+    const _Float16* ahi;     // A [M][K] (row stride lda), f16 high and low parts
     const _Float16* alo;
-    const uint8_t* w[3];     // Q8_0 matrices concatenated along N (rows[i] rows each)
+    uint32_t lda;
+    uint64_t a_bs;           // A offset (elements) per batch index blockIdx.z
+    const uint8_t* w[3];     // B as Q8_0 matrices concatenated along N (rows[i] rows each), or
     uint32_t rows[3];
     uint32_t nseg;
+    const uint8_t* w_end;    //   one past the arena
+    const float* b;          // B as fp32 rows: B[n][k] = b[n * ldb + k] (+ b_bs per batch)
+    uint32_t ldb;
+    uint64_t b_bs;
+    float* c;                // C [M][N] fp32 (row stride ldc), or
+    _Float16* chi;           //   C as f16 high and low parts
+    _Float16* clo;
+    uint32_t ldc;
+    uint64_t c_bs;
     uint32_t M, N, K;
-    float* c;                // [M][N] row-major
-    const uint8_t* w_end;    // one past the arena
+    uint32_t window;         // causal modes: keys older than window positions are skipped (0: none)
 };
 
-// Workgroup tile 64 x 64, four waves of 32 x 32 (v_mfma_f32_32x32x16_f16). Lane l of a wave:
-// A operand rows m = l % 32, k = 8 * (l / 32) + 0..7 of each 16-wide k step; B operand
-// column n = l % 32 (a weight row), same k; accumulator element r at row
-// 8 * (r / 4) + 4 * (l / 32) + r % 4, column l % 32 -- so the column's block scale is the
-// lane's own. The next block's operands load while the current block's MFMAs run.
+// One 32 x 32 tile of C per workgroup (v_mfma_f32_32x32x16_f16); the four waves split the
+// K blocks (wave w takes blocks w, w + 4, ...) and their partial tiles are summed through LDS
+// in wave order (deterministic). Lane l of a wave: A operand row m = l % 32, k = 8 * (l / 32)
+// + 0..7 of each 16-wide k step; B operand column n = l % 32, same k; accumulator element r at
+// row 8 * (r / 4) + 4 * (l / 32) + r % 4, column l % 32. Q8 B: per 32-wide block, two f16 MFMA
+// chains (A hi, A lo) against the exact quants, scaled by the column's block scale (the lane's
+// own) in fp32. fp32 B: split into f16 hi + lo in registers, three products (hi hi, lo hi,
+// hi lo) per k step. Each wave's next block loads while its current block's MFMAs run.
+constexpr int kGemmB32 = 1;       // B is fp32 rows (otherwise Q8_0)
+constexpr int kGemmCausalS = 2;   // S = Q K^T: skip key tiles no query of the row tile sees
+constexpr int kGemmCausalO = 4;   // O = P V: the K (key) range ends after the row tile's last query
+constexpr int kGemmOut16 = 8;     // C as f16 hi/lo
+constexpr uint32_t kPfGT = 32;    // GEMM tile (rows and columns)
+constexpr uint32_t kPfDepth = 3;  // K blocks in flight per wave
+template <int MODE>
 __global__ void __launch_bounds__(kPfThreads) k_pf_gemm(PfGemm G) {
+    constexpr bool BF32 = (MODE & kGemmB32) != 0, OUT16 = (MODE & kGemmOut16) != 0;
+    __shared__ float red[3][16][64];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t kh = lane >> 5, l32 = lane & 31u;
-    const uint32_t m = blockIdx.y * kPfTile + (wave >> 1) * 32u + l32;
-    const uint32_t n = blockIdx.x * kPfTile + (wave & 1u) * 32u + l32;
-    const bool mlive = m < G.M, nlive = n < G.N;
-    const uint32_t nblk = G.K >> 5;
-    const uint64_t row_bytes = static_cast<uint64_t>(nblk) * 34u;
-    // this lane's weight row
-    const uint8_t* wrow = G.w[0];
-    {
-        uint32_t r = nlive ? n : 0u, s = 0;
-        while (s + 1u < G.nseg && r >= G.rows[s]) r -= G.rows[s++];
-        wrow = G.w[s] + static_cast<uint64_t>(r) * row_bytes;
+    const uint32_t m0 = blockIdx.y * kPfGT, n0 = blockIdx.x * kPfGT;
+    uint32_t k_lo = 0, k_hi = G.K;
+    if constexpr ((MODE & (kGemmCausalS | kGemmCausalO)) != 0) {
+        const uint32_t q_last = min(G.M, m0 + kPfGT) - 1u;
+        const uint32_t k_old = (G.window != 0u && m0 + 1u > G.window) ? m0 + 1u - G.window : 0u;
+        if constexpr ((MODE & kGemmCausalS) != 0) {
+            if (n0 > q_last || n0 + kPfGT <= k_old) return;   // uniform over the workgroup
+        } else {
+            k_lo = (k_old / 32u) * 32u;
+            k_hi = min(G.K, ((q_last + 32u) / 32u) * 32u);
+        }
     }
-    const uint64_t arow = static_cast<uint64_t>(mlive ? m : 0u) * G.K + 8u * kh;
+    const uint32_t m = m0 + l32, n = n0 + l32;
+    const bool mlive = m < G.M, nlive = n < G.N;
+    const uint64_t zb = blockIdx.z;
     typedef const __attribute__((address_space(1))) half8* gh8;
-    const uintptr_t ahi_base = reinterpret_cast<uintptr_t>(G.ahi), alo_base = reinterpret_cast<uintptr_t>(G.alo);
-    auto load_a = [&](uint32_t b, half8 (&hi)[2], half8 (&lo)[2]) {
+    typedef const __attribute__((address_space(1))) f4* gf4;
+    const uintptr_t ahi_base = reinterpret_cast<uintptr_t>(G.ahi + zb * G.a_bs);
+    const uintptr_t alo_base = reinterpret_cast<uintptr_t>(G.alo + zb * G.a_bs);
+    const uint64_t arow = static_cast<uint64_t>(mlive ? m : 0u) * G.lda + 8u * kh;
+    auto load_a = [&](uint32_t k0, half8 (&hi)[2], half8 (&lo)[2]) {
 #pragma unroll
         for (uint32_t ks = 0; ks < 2; ++ks) {
-            const uint64_t o = (arow + 32u * b + 16u * ks) * 2u;
+            const uint64_t o = (arow + k0 + 16u * ks) * 2u;
             hi[ks] = *reinterpret_cast<gh8>(ahi_base + o);
             lo[ks] = *reinterpret_cast<gh8>(alo_base + o);
         }
     };
-    auto to_half8 = [&](const Q8Raw& r, uint32_t j0) {
-        half8 v;
-        const uint32_t d0 = __builtin_amdgcn_alignbyte(r.d[j0 + 1], r.d[j0], r.sh);
-        const uint32_t d1 = __builtin_amdgcn_alignbyte(r.d[j0 + 2], r.d[j0 + 1], r.sh);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[j] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(d0 >> (8 * j))));
-            v[4 + j] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(d1 >> (8 * j))));
-        }
-        return v;
-    };
     float16v acc = {};
-    half8 ahi[2], alo[2], nhi[2], nlo[2];
-    Q8Raw raw, nraw;
-    load_a(0, ahi, alo);
-    q8_load(wrow, G.w_end, raw);
-    for (uint32_t b = 0; b < nblk; ++b) {
-        if (b + 1u < nblk) {
-            load_a(b + 1u, nhi, nlo);
-            q8_load(wrow + 34u * (b + 1u), G.w_end, nraw);
+    const uint32_t b_lo = k_lo / 32u, b_hi = k_hi / 32u;   // this wave: blocks b_lo + wave + 4i
+    if constexpr (!BF32) {
+        const uint64_t row_bytes = static_cast<uint64_t>(G.K >> 5) * 34u;
+        const uint8_t* wrow = G.w[0];   // the lane's weight row (segments unrolled: no indexed struct)
+        {
+            uint32_t r = nlive ? n : 0u;
+            if (G.nseg > 1u && r >= G.rows[0]) {
+                r -= G.rows[0];
+                wrow = G.w[1];
+                if (G.nseg > 2u && r >= G.rows[1]) {
+                    r -= G.rows[1];
+                    wrow = G.w[2];
+                }
+            }
+            wrow += static_cast<uint64_t>(r) * row_bytes;
         }
-        const half8 w0 = to_half8(raw, 2u * kh), w1 = to_half8(raw, 4u + 2u * kh);
-        float16v p1 = {}, p2 = {};
-        p1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[0], w0, p1, 0, 0, 0);
-        p2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[0], w0, p2, 0, 0, 0);
-        p1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[1], w1, p1, 0, 0, 0);
-        p2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[1], w1, p2, 0, 0, 0);
-        const float s = half_bits_to_float(raw.sbits);
+        // quants 16 ks + 8 kh .. + 7 of a block as f16 (constant register indices, selected by kh)
+        auto to_half8 = [&](const Q8Raw& r, uint32_t ks) {
+            half8 v;
+            const uint32_t j = 4u * ks;
+            const uint32_t a0 = __builtin_amdgcn_alignbyte(r.d[j + 1], r.d[j], r.sh);
+            const uint32_t a1 = __builtin_amdgcn_alignbyte(r.d[j + 2], r.d[j + 1], r.sh);
+            const uint32_t a2 = __builtin_amdgcn_alignbyte(r.d[j + 3], r.d[j + 2], r.sh);
+            const uint32_t a3 = __builtin_amdgcn_alignbyte(r.d[j + 4], r.d[j + 3], r.sh);
+            const uint32_t d0 = kh ? a2 : a0, d1 = kh ? a3 : a1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += s * (p1[r] + p2[r]);
-        if (b + 1u < nblk) {
-            ahi[0] = nhi[0]; ahi[1] = nhi[1]; alo[0] = nlo[0]; alo[1] = nlo[1];
-            raw = nraw;
+            for (int i = 0; i < 4; ++i) {
+                v[i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(d0 >> (8 * i))));
+                v[4 + i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(d1 >> (8 * i))));
+            }
+            return v;
+        };
+        // a ring of kPfDepth blocks in flight per wave (static register sets)
+        half8 ah[kPfDepth][2], al[kPfDepth][2];
+        Q8Raw rw[kPfDepth];
+        const uint32_t b0 = b_lo + wave;
+#pragma unroll
+        for (uint32_t i = 0; i < kPfDepth; ++i) {
+            const uint32_t bb = b0 + 4u * i;
+            if (bb < b_hi) {
+                load_a(32u * bb, ah[i], al[i]);
+                q8_load(wrow + 34u * bb, G.w_end, rw[i]);
+            }
+        }
+        for (uint32_t base = b0; base < b_hi; base += 4u * kPfDepth) {
+#pragma unroll
+            for (uint32_t i = 0; i < kPfDepth; ++i) {
+                const uint32_t bb = base + 4u * i;
+                if (bb < b_hi) {
+                    const half8 w0 = to_half8(rw[i], 0u), w1 = to_half8(rw[i], 1u);
+                    float16v p1 = {}, p2 = {};
+                    p1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], w0, p1, 0, 0, 0);
+                    p2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], w0, p2, 0, 0, 0);
+                    p1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], w1, p1, 0, 0, 0);
+                    p2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], w1, p2, 0, 0, 0);
+                    const float sc = half_bits_to_float(rw[i].sbits);
+                    const uint32_t nb = bb + 4u * kPfDepth;
+                    if (nb < b_hi) {
+                        load_a(32u * nb, ah[i], al[i]);
+                        q8_load(wrow + 34u * nb, G.w_end, rw[i]);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[r] += sc * (p1[r] + p2[r]);
+                }
+            }
+        }
+    } else {
+        const uintptr_t b_base = reinterpret_cast<uintptr_t>(G.b + zb * G.b_bs) +
+                                 (static_cast<uint64_t>(nlive ? n : 0u) * G.ldb + 8u * kh) * 4u;
+        auto load_b = [&](uint32_t k0, f4 (&v)[4]) {   // k step 0: v[0], v[1]; k step 1: v[2], v[3]
+#pragma unroll
+            for (uint32_t ks = 0; ks < 2; ++ks) {
+                v[2 * ks] = *reinterpret_cast<gf4>(b_base + (k0 + 16u * ks) * 4u);
+                v[2 * ks + 1] = *reinterpret_cast<gf4>(b_base + (k0 + 16u * ks + 4u) * 4u);
+            }
+        };
+        half8 ah[kPfDepth][2], al[kPfDepth][2];
+        f4 bv[kPfDepth][4];
+        const uint32_t b0 = b_lo + wave;
+#pragma unroll
+        for (uint32_t i = 0; i < kPfDepth; ++i) {
+            const uint32_t bb = b0 + 4u * i;
+            if (bb < b_hi) {
+                load_a(32u * bb, ah[i], al[i]);
+                load_b(32u * bb, bv[i]);
+            }
+        }
+        for (uint32_t base = b0; base < b_hi; base += 4u * kPfDepth) {
+#pragma unroll
+            for (uint32_t i = 0; i < kPfDepth; ++i) {
+                const uint32_t bb = base + 4u * i;
+                if (bb < b_hi) {
+                    half8 bh[2], bl[2], xh[2], xl[2];
+#pragma unroll
+                    for (uint32_t ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float x0 = bv[i][2 * ks][j], x1 = bv[i][2 * ks + 1][j];
+                            const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
+                            bh[ks][j] = h0;
+                            bh[ks][4 + j] = h1;
+                            bl[ks][j] = static_cast<_Float16>(x0 - static_cast<float>(h0));
+                            bl[ks][4 + j] = static_cast<_Float16>(x1 - static_cast<float>(h1));
+                        }
+                        xh[ks] = ah[i][ks];
+                        xl[ks] = al[i][ks];
+                    }
+                    const uint32_t nb = bb + 4u * kPfDepth;
+                    if (nb < b_hi) {
+                        load_a(32u * nb, ah[i], al[i]);
+                        load_b(32u * nb, bv[i]);
+                    }
+#pragma unroll
+                    for (uint32_t ks = 0; ks < 2; ++ks) {
+                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh[ks], bh[ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl[ks], bh[ks], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh[ks], bl[ks], acc, 0, 0, 0);
+                    }
+                }
+            }
         }
     }
-    if (!nlive) return;
-    const uint32_t mb = blockIdx.y * kPfTile + (wave >> 1) * 32u;
+    // sum the four waves' partial tiles in wave order
+    if (wave != 0u) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave - 1u][r][lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave != 0u || !nlive) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const uint32_t row = mb + 8u * (r / 4) + 4u * kh + (r % 4);
-        if (row < G.M) G.c[static_cast<uint64_t>(row) * G.N + n] = acc[r];
+        const uint32_t row = m0 + 8u * (r / 4) + 4u * kh + (r % 4);
+        if (row < G.M) {
+            const uint64_t o = zb * G.c_bs + static_cast<uint64_t>(row) * G.ldc + n;
+            if constexpr (OUT16) pf_split(acc[r], G.chi + o, G.clo + o);
+            else G.c[o] = acc[r];
+        }
+    }
+}
+
+// Masked softmax of score row (head z, query t): keys j of [max(0, t + 1 - window), t]
+// (window 0: all j <= t), p_j = exp(scale * s_j - max) / sum, the sum in double
+// (src/gemma3.cpp:1602-1696); p as f16 hi/lo over the row's first ceil((t + 1) / 64) * 64
+// columns, zero outside the range (the O = P V GEMM reads up to there).
+__global__ void __launch_bounds__(kPfThreads) k_pf_softmax(const float* S, uint32_t T, uint32_t Tp, float scale,
+                                                           uint32_t window, _Float16* phi, _Float16* plo) {
+#pragma clang fp contract(off)
+    __shared__ double redd[4];
+    __shared__ float redf[4];
+    const uint32_t t = blockIdx.x, z = blockIdx.y;
+    const uint64_t row = (static_cast<uint64_t>(z) * T + t) * Tp;   // rows of Tp columns
+    const uint32_t j0 = (window != 0u && t + 1u > window) ? t + 1u - window : 0u;
+    const uint32_t jend = min(Tp, ((t + kPfTile) / kPfTile) * kPfTile);
+    float mx = -INFINITY;
+    for (uint32_t j = j0 + threadIdx.x; j <= t; j += kPfThreads) mx = fmaxf(mx, S[row + j] * scale);
+    mx = wave_red_max(mx);
+    if ((threadIdx.x & 63u) == 0u) redf[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+    double den = 0.0;
+    for (uint32_t j = j0 + threadIdx.x; j <= t; j += kPfThreads) den += static_cast<double>(expf(S[row + j] * scale - mx));
+    const float inv_den = static_cast<float>(1.0 / pf_sum(den, redd));
+    for (uint32_t j = threadIdx.x; j < jend; j += kPfThreads) {
+        const float p = (j >= j0 && j <= t) ? expf(S[row + j] * scale - mx) * inv_den : 0.0f;
+        pf_split(p, phi + row + j, plo + row + j);
+    }
+}
+
+// V^T of one block: vt[d][t] = v_t[d] for the rows t < T of qkv, zero for T <= t < Tp.
+__global__ void __launch_bounds__(kPfThreads) k_pf_vt(const float* qkv, uint32_t T, uint32_t Tp, uint32_t nqkv,
+                                                      uint32_t voff, float* vt) {
+    __shared__ float tile[32][33];
+    const uint32_t t0 = blockIdx.x * 32u, d0 = blockIdx.y * 32u;
+    const uint32_t tx = threadIdx.x & 31u, ty = threadIdx.x >> 5;   // 32 x 8
+    for (uint32_t r = ty; r < 32u; r += 8u) {
+        const uint32_t t = t0 + r;
+        tile[r][tx] = t < T ? qkv[static_cast<uint64_t>(t) * nqkv + voff + d0 + tx] : 0.0f;
+    }
+    __syncthreads();
+    for (uint32_t r = ty; r < 32u; r += 8u) {
+        const uint32_t t = t0 + tx;
+        if (t < Tp) vt[static_cast<uint64_t>(d0 + r) * Tp + t] = tile[tx][r];
     }
 }
 
 // ---- QK-norm, RoPE, KV cache ------------------------------------------------------------
 
 // Row t of qkv = [q (H heads x hd) | k (hd) | v (hd)]: QK-norm per head (src/gemma3.cpp:
-// 1045-1104), NeoX RoPE at position t (:1371-1424), in place; then k and v go to the KV
-// cache slot t % slots when position t is still in the window after the prompt (the serial
-// loop's eviction leaves exactly those, :1590-1600).
+// 1045-1104), NeoX RoPE at position t (:1371-1424), in place (q also as f16 hi/lo rows of
+// qhi/qlo); then k and v go to the KV cache slot t % slots when position t is still in the
+// window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600).
 __global__ void __launch_bounds__(kPfThreads) k_pf_qk(float* qkv, uint32_t T, uint32_t H, uint32_t hd, const float* q_norm,
                                                       const float* k_norm, const float* cos_t, const float* sin_t,
-                                                      float eps, float* kc, float* vc, uint32_t slots) {
+                                                      float eps, float* kc, float* vc, uint32_t slots, _Float16* qhi,
+                                                      _Float16* qlo) {
 #pragma clang fp contract(off)
     __shared__ double red[4];
     __shared__ float xs[256];
@@ -249,7 +419,12 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_qk(float* qkv, uint32_t T, ui
             const uint32_t e = i < half ? i : i - half;
             const float c = cos_t[static_cast<uint64_t>(t) * half + e], s = sin_t[static_cast<uint64_t>(t) * half + e];
             const float a = xs[e], b = xs[e + half];
-            x[i] = i < half ? a * c - b * s : b * c + a * s;
+            const float y2 = i < half ? a * c - b * s : b * c + a * s;
+            x[i] = y2;
+            if (hh < H) {   // the query as the attention GEMM's A operand, [T][H * hd]
+                const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
+                pf_split(y2, qhi + o, qlo + o);
+            }
         }
         __syncthreads();
     }
@@ -260,182 +435,39 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_qk(float* qkv, uint32_t T, ui
     }
 }
 
-// ---- causal attention -----------------------------------------------------------------------
-
-// One workgroup per (32 queries, head h). Key tiles of 32 in LDS; each thread scores one query
-// against 4 keys, then owns hd/8 output dims of its query (online softmax, fp32). Keys j of
-// query t: j <= t and t - j < window (window = slots of a local block). Output as f16 hi/lo
-// att[t][h * hd + e]. Each tile's K and V rows are fetched into registers (float4 loads, all
-// in flight together) while the previous tile is being used, then stored to LDS; LDS rows
-// are padded by 4 floats against bank conflicts.
-template <uint32_t HD>
-__global__ void __launch_bounds__(kPfThreads) k_pf_attn(const float* qkv, uint32_t T, uint32_t H, uint32_t window,
-                                                        float scale, _Float16* ahi, _Float16* alo) {
-    constexpr uint32_t LD = HD + 4u;
-    constexpr uint32_t DPT = HD / 8u;                        // output dims per thread
-    constexpr uint32_t NV = kPfKT * HD / 4u / kPfThreads;    // f4 of a K (or V) tile per thread
-    static_assert(NV >= 1u && NV * 4u * kPfThreads == kPfKT * HD, "tile shape");
-    extern __shared__ float sm[];
-    float* Qs = sm;                      // [QT][LD]
-    float* Ks = Qs + kPfQT * LD;         // [KT][LD]
-    float* Vs = Ks + kPfKT * LD;         // [KT][LD]
-    float* Ps = Vs + kPfKT * LD;         // [QT][KT + 1]
-    const uint32_t t0 = blockIdx.x * kPfQT, h = blockIdx.y;
-    const uint32_t nq = min(kPfQT, T - t0);
-    const uint32_t nqkv = (H + 2u) * HD;
-    const uint32_t tid = threadIdx.x;
-    const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t i = 0; i < kPfQT * HD / 4u / kPfThreads; ++i) {
-        const uint32_t idx = tid + i * kPfThreads, q = idx / (HD / 4u), e = 4u * (idx % (HD / 4u));
-        *reinterpret_cast<f4*>(Qs + q * LD + e) =
-            q < nq ? *reinterpret_cast<const f4*>(qkv + static_cast<uint64_t>(t0 + q) * nqkv + h * HD + e) : zero4;
-    }
-    const uint32_t qi = tid >> 3, kg = tid & 7u;   // query of this thread, its key group / dim group
-    const uint32_t t = t0 + qi;
-    float acc[DPT];
-#pragma unroll
-    for (uint32_t j = 0; j < DPT; ++j) acc[j] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-    const uint32_t k_first = (window != 0u && t0 + 1u > window) ? t0 + 1u - window : 0u;
-    const uint32_t k_end = t0 + nq;
-    f4 kreg[NV], vreg[NV];
-    const uint32_t kb0 = k_first - (k_first % kPfKT);
-    // this thread's f4 of each tile: row k = i * (KT / NV) + tid / (HD / 4), column
-    // e = 4 * (tid % (HD / 4)); rows past k_end load as zero (clamped address, masked value)
-    const uint32_t frow = tid / (HD / 4u), fcol = 4u * (tid % (HD / 4u));
-#pragma unroll
-    for (uint32_t i = 0; i < NV; ++i) {
-        const uint32_t k = i * (kPfKT / NV) + frow;
-        const bool live = kb0 + k < k_end;
-        const float* row = qkv + static_cast<uint64_t>(live ? kb0 + k : 0u) * nqkv + fcol;
-        const f4 kv = *reinterpret_cast<const f4*>(row + H * HD);
-        const f4 vv = *reinterpret_cast<const f4*>(row + (H + 1u) * HD);
-        kreg[i] = live ? kv : zero4;
-        vreg[i] = live ? vv : zero4;
-    }
-    for (uint32_t kb = kb0; kb < k_end; kb += kPfKT) {
-        __syncthreads();   // the previous tile's LDS is no longer read
-#pragma unroll
-        for (uint32_t i = 0; i < NV; ++i) {
-            const uint32_t k = i * (kPfKT / NV) + frow;
-            *reinterpret_cast<f4*>(Ks + k * LD + fcol) = kreg[i];
-            *reinterpret_cast<f4*>(Vs + k * LD + fcol) = vreg[i];
-        }
-        __syncthreads();
-        const uint32_t kn = kb + kPfKT;   // the next tile is in flight while this one is used
-#pragma unroll
-        for (uint32_t i = 0; i < NV; ++i) {
-            const uint32_t k = i * (kPfKT / NV) + frow;
-            const bool live = kn + k < k_end;
-            const float* row = qkv + static_cast<uint64_t>(live ? kn + k : 0u) * nqkv + fcol;
-            const f4 kv = *reinterpret_cast<const f4*>(row + H * HD);
-            const f4 vv = *reinterpret_cast<const f4*>(row + (H + 1u) * HD);
-            kreg[i] = live ? kv : zero4;
-            vreg[i] = live ? vv : zero4;
-        }
-        // scores of query qi against keys kb + 4 kg .. + 3
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-        for (uint32_t e = 0; e < HD; e += 4u) {
-            const f4 qv = *reinterpret_cast<const f4*>(Qs + qi * LD + e);
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                const f4 kv = *reinterpret_cast<const f4*>(Ks + (4u * kg + j) * LD + e);
-                s[j] = fmaf(qv.x, kv.x, s[j]);
-                s[j] = fmaf(qv.y, kv.y, s[j]);
-                s[j] = fmaf(qv.z, kv.z, s[j]);
-                s[j] = fmaf(qv.w, kv.w, s[j]);
-            }
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            const uint32_t k = kb + 4u * kg + j;
-            const bool ok = qi < nq && k <= t && (window == 0u || t - k < window);
-            s[j] = ok ? s[j] * scale : -INFINITY;
-            mx = fmaxf(mx, s[j]);
-        }
-        // row max / sum over the 8 threads of query qi (adjacent lanes)
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        mx = fmaxf(mx, __shfl_xor(mx, 4));
-        const float m_new = fmaxf(m_run, mx);
-        float ls = 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            const float p = s[j] == -INFINITY ? 0.0f : expf(s[j] - m_new);
-            Ps[qi * (kPfKT + 1u) + 4u * kg + j] = p;
-            ls += p;
-        }
-        ls += __shfl_xor(ls, 1);
-        ls += __shfl_xor(ls, 2);
-        ls += __shfl_xor(ls, 4);
-        const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-        l_run = l_run * r + ls;
-        m_run = m_new;
-        __syncthreads();
-        // acc = acc * r + sum_k p_k v_k over this thread's dims e = 4 kg + 32 j' (+0..3)
-#pragma unroll
-        for (uint32_t j = 0; j < DPT; ++j) acc[j] *= r;
-#pragma unroll 4
-        for (uint32_t k = 0; k < kPfKT; ++k) {
-            const float p = Ps[qi * (kPfKT + 1u) + k];
-#pragma unroll
-            for (uint32_t j = 0; j < DPT / 4u; ++j) {
-                const f4 vv = *reinterpret_cast<const f4*>(Vs + k * LD + 4u * kg + 32u * j);
-                acc[4 * j + 0] = fmaf(p, vv.x, acc[4 * j + 0]);
-                acc[4 * j + 1] = fmaf(p, vv.y, acc[4 * j + 1]);
-                acc[4 * j + 2] = fmaf(p, vv.z, acc[4 * j + 2]);
-                acc[4 * j + 3] = fmaf(p, vv.w, acc[4 * j + 3]);
-            }
-        }
-    }
-    if (qi >= nq) return;
-    const float inv = 1.0f / l_run;
-    const uint64_t o = static_cast<uint64_t>(t) * H * HD + h * HD;
-#pragma unroll
-    for (uint32_t j = 0; j < DPT / 4u; ++j)
-#pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-            const uint32_t e = 4u * kg + 32u * j + c;
-            pf_split(acc[4 * j + c] * inv, ahi + o + e, alo + o + e);
-        }
-}
-
 // ---- host side --------------------------------------------------------------------------
 
+template <int MODE>
+static int pf_launch(const PfGemm& G, uint32_t batch, hipStream_t s) {
+    const dim3 grid((G.N + kPfGT - 1u) / kPfGT, (G.M + kPfGT - 1u) / kPfGT, batch);
+    PfGemm arg = G;
+    void* args[] = {&arg};
+    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_gemm<MODE>), grid, dim3(kPfThreads), args, 0, s));
+    return VRT_OK;
+}
+
+// C[M][N] = A[M][K] (f16 hi/lo) x W^T, W = Q8_0 matrices concatenated along N.
 static int pf_gemm(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t M, uint32_t K,
                    std::initializer_list<std::pair<const uint8_t*, uint32_t>> segs, float* c, hipStream_t s) {
     PfGemm G{};
     G.ahi = ahi;
     G.alo = alo;
-    G.nseg = 0;
-    G.N = 0;
+    G.lda = K;
     for (const auto& sg : segs) {
         G.w[G.nseg] = sg.first;
         G.rows[G.nseg++] = sg.second;
         G.N += sg.second;
     }
+    G.w_end = g->P.arena_end;
+    G.c = c;
+    G.ldc = G.N;
     G.M = M;
     G.K = K;
-    G.c = c;
-    G.w_end = g->P.arena_end;
     if (K % 32u != 0u || G.N % 32u != 0u) return set_error(VRT_ERR_INVALID, "prefill GEMM shape not supported");
-    dim3 grid((G.N + kPfTile - 1u) / kPfTile, (M + kPfTile - 1u) / kPfTile);
-    void* args[] = {&G};
-    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_gemm), grid, dim3(kPfThreads), args, 0, s));
-    return VRT_OK;
+    return pf_launch<0>(G, 1, s);
 }
 
-static const void* pf_attn_fn(uint32_t hd) {
-    return hd == 256u ? reinterpret_cast<const void*>(&k_pf_attn<256>)
-         : hd == 128u ? reinterpret_cast<const void*>(&k_pf_attn<128>)
-                      : reinterpret_cast<const void*>(&k_pf_attn<64>);
-}
-
-static size_t pf_attn_smem(uint32_t hd) {
-    return ((kPfQT + 2u * kPfKT) * (hd + 4u) + kPfQT * (kPfKT + 1u)) * 4u;
-}
+static uint32_t pf_pad(uint32_t T) { return (T + kPfTile - 1u) / kPfTile * kPfTile; }
 
 int pf_setup(vrt_g3* g, uint32_t max_t) {
     const uint32_t d = g->cfg.embedding_length, H = g->cfg.head_count, hd = g->cfg.head_dim;
@@ -443,9 +475,8 @@ int pf_setup(vrt_g3* g, uint32_t max_t) {
     const uint32_t kmax = std::max(std::max(d, qw), F);
     PfState& p = g->pf;
     p.max_t = 0;
-    if (d > 8u * kPfThreads || hd > 256u || (hd != 64u && hd != 128u && hd != 256u) || d % 32u || qw % 32u ||
-        F % 32u || nqkv % 32u)
-        return VRT_OK;   // prefill unavailable for this shape: vrt_g3_prefill falls back to decode steps
+    if (d > 8u * kPfThreads || hd > 256u || hd % 32u || d % 32u || qw % 32u || F % 32u || nqkv % 32u) return VRT_OK;
+    const uint64_t tp = pf_pad(max_t);
     auto take = [&](size_t bytes, void** out) -> int {
         VRT_HIP_CHECK(hipMalloc(out, bytes + 256u));
         g->allocs.push_back(*out);
@@ -462,9 +493,78 @@ int pf_setup(vrt_g3* g, uint32_t max_t) {
     p.alo = q;
     if (int rc = take(static_cast<size_t>(max_t) * std::max(nqkv, 2u * F) * 4u, &q)) return rc;
     p.big = static_cast<float*>(q);
-    VRT_HIP_CHECK(hipFuncSetAttribute(pf_attn_fn(hd), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      static_cast<int>(pf_attn_smem(hd))));
+    if (int rc = take(static_cast<size_t>(H) * max_t * tp * 4u, &q)) return rc;
+    p.s = static_cast<float*>(q);
+    if (int rc = take(static_cast<size_t>(H) * max_t * tp * 2u, &q)) return rc;
+    p.phi = q;
+    if (int rc = take(static_cast<size_t>(H) * max_t * tp * 2u, &q)) return rc;
+    p.plo = q;
+    if (int rc = take(static_cast<size_t>(hd) * tp * 4u, &q)) return rc;
+    p.vt = static_cast<float*>(q);
     p.max_t = max_t;
+    return VRT_OK;
+}
+
+// Causal local/global attention of one block over qkv rows [T][q | k | v] (q, k normed and
+// rotated; q also as f16 hi/lo in qhi/qlo) into att hi/lo [T][H * hd], all on MFMA:
+// S_h = Q_h K^T (key tiles no query sees skipped), masked softmax -> P_h, O_h = P_h V.
+static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, const float* qkv, const _Float16* qhi,
+                        const _Float16* qlo, _Float16* att_hi, _Float16* att_lo, hipStream_t s) {
+    const PfState& p = g->pf;
+    const uint32_t H = g->cfg.head_count, hd = g->cfg.head_dim, qw = H * hd, nqkv = qw + 2u * hd;
+    const uint32_t Tp = pf_pad(T);
+    const uint32_t window = Ly.slots >= g->cfg.context_length ? 0u : Ly.slots;
+    {   // S_h = Q_h K^T: [H][T][Tp]
+        PfGemm G{};
+        G.ahi = qhi;
+        G.alo = qlo;
+        G.lda = qw;
+        G.a_bs = hd;
+        G.b = qkv + qw;
+        G.ldb = nqkv;
+        G.c = p.s;
+        G.ldc = Tp;
+        G.c_bs = static_cast<uint64_t>(T) * Tp;
+        G.M = T;
+        G.N = T;
+        G.K = hd;
+        G.window = window;
+        if (int rc = pf_launch<kGemmB32 | kGemmCausalS>(G, H, s)) return rc;
+    }
+    {
+        const float* S = p.s;
+        float scale = g->P.attn_scale;
+        uint32_t t = T, tp = Tp, w = window;
+        _Float16* phi = static_cast<_Float16*>(p.phi);
+        _Float16* plo = static_cast<_Float16*>(p.plo);
+        void* args[] = {&S, &t, &tp, &scale, &w, &phi, &plo};
+        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_softmax), dim3(T, H), dim3(kPfThreads), args, 0, s));
+    }
+    {
+        uint32_t t = T, tp = Tp, n = nqkv, voff = qw + hd;
+        float* vt = p.vt;
+        void* args[] = {const_cast<float**>(&qkv), &t, &tp, &n, &voff, &vt};
+        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_vt), dim3(Tp / 32u, hd / 32u), dim3(kPfThreads),
+                                      args, 0, s));
+    }
+    {   // O_h = P_h V -> att[:, h * hd ..]
+        PfGemm G{};
+        G.ahi = static_cast<const _Float16*>(p.phi);
+        G.alo = static_cast<const _Float16*>(p.plo);
+        G.lda = Tp;
+        G.a_bs = static_cast<uint64_t>(T) * Tp;
+        G.b = p.vt;
+        G.ldb = Tp;
+        G.chi = att_hi;
+        G.clo = att_lo;
+        G.ldc = qw;
+        G.c_bs = hd;
+        G.M = T;
+        G.N = hd;
+        G.K = Tp;
+        G.window = window;
+        if (int rc = pf_launch<kGemmB32 | kGemmCausalO | kGemmOut16>(G, H, s)) return rc;
+    }
     return VRT_OK;
 }
 
@@ -484,8 +584,8 @@ int pf_run(vrt_g3* g, uint32_t T) {
     float* big = p.big;
     float eps = P.eps;
     G3State* st = P.st;
-    auto launch = [&](const void* fn, dim3 grid, void** args, size_t smem) -> int {
-        VRT_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(kPfThreads), args, smem, s));
+    auto launch = [&](const void* fn, dim3 grid, void** args) -> int {
+        VRT_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(kPfThreads), args, 0, s));
         return VRT_OK;
     };
     {
@@ -493,7 +593,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
         const uint32_t* tok = P.tokens;
         float es = P.emb_scale;
         void* args[] = {&te, &tok, &d, &es, &h};
-        if (int rc = launch(reinterpret_cast<const void*>(&k_pf_embed), dim3(T), args, 0)) return rc;
+        if (int rc = launch(reinterpret_cast<const void*>(&k_pf_embed), dim3(T), args)) return rc;
     }
     for (uint32_t l = 0; l < L; ++l) {
         const LayerParams& Ly = g->layers[l];
@@ -503,7 +603,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
             const float* wnext = Ly.attn_norm;
             uint32_t blk = l ? l - 1u : 0u;
             void* args[] = {&h, &f, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args, 0)) return rc;
+            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }
         if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, big, s)) return rc;
         {
@@ -514,17 +614,11 @@ int pf_run(vrt_g3* g, uint32_t T) {
             float* kc = Ly.kc;
             float* vc = Ly.vc;
             uint32_t slots = Ly.slots;
-            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_qk), dim3(T), args, 0)) return rc;
+            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo};
+            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_qk), dim3(T), args)) return rc;
         }
-        {
-            uint32_t window = Ly.slots >= g->cfg.context_length ? 0u : Ly.slots;
-            float scale = P.attn_scale;
-            const float* qkv = big;
-            void* args[] = {&qkv, &T, &H, &window, &scale, &ahi, &alo};
-            const dim3 grid((T + kPfQT - 1u) / kPfQT, H);
-            if (int rc = launch(pf_attn_fn(hd), grid, args, pf_attn_smem(hd))) return rc;
-        }
+        // q (hi/lo in ahi/alo) is consumed by S = Q K^T before O = P V overwrites ahi/alo
+        if (int rc = pf_attention(g, Ly, T, big, ahi, alo, ahi, alo, s)) return rc;
         if (int rc = pf_gemm(g, ahi, alo, T, qw, {{Ly.wo, d}}, x, s)) return rc;
         {   // attention output into the residual, then the FFN norm
             const float* f = x;
@@ -532,13 +626,13 @@ int pf_run(vrt_g3* g, uint32_t T) {
             const float* wnext = Ly.ffn_norm;
             uint32_t blk = l;
             void* args[] = {&h, &f, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args, 0)) return rc;
+            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }
         if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wg, F}, {Ly.wu, F}}, big, s)) return rc;
         {
             const float* gu = big;
             void* args[] = {&gu, &F, &ahi, &alo};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_gelu), dim3(T), args, 0)) return rc;
+            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_gelu), dim3(T), args)) return rc;
         }
         if (int rc = pf_gemm(g, ahi, alo, T, F, {{Ly.wd, d}}, x, s)) return rc;
     }
