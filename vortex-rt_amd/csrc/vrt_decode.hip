@@ -71,16 +71,17 @@ constexpr uint32_t kVec = 4;                 // vector elements per thread (vect
 constexpr uint32_t kSpinLimit = 1u << 21;    // polls before a hand-off is declared lost
 constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
 constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x query heads) per block
-constexpr uint32_t kLmUnits = 3;             // 16-byte LM-head loads per thread per tile
+constexpr uint32_t kLmUnits = 4;             // 16-byte LM-head loads per thread per tile
+constexpr uint32_t kLmDepth = 3;             // LM-head tiles in flight per workgroup
 constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
 constexpr uint32_t kGrpPerWave = kGrp / kMkWaves;
 constexpr uint32_t kPartRound = 12 * kMkThreads;   // attention partials gathered per wait
 constexpr int kRsrcFlags = 0x00020000;       // raw buffer resource, 32-bit data format
-// Cache policy of exchange and KV-cache accesses: system scope (sc0 sc1). Measured on MI355X,
-// a tagged exchange among 256 workgroups on all eight XCDs completes in 2.6 us per round with
-// system-scope stores and loads against 4.3 us with device-scope (sc1) ones.
+// Cache policy of exchange and KV-cache accesses: system scope (sc0 sc1), coherent across the
+// XCDs' L2s. (A tagged exchange among 256 workgroups takes ~2.6 us per round on MI355X with
+// either system- or device-scope stores and loads.)
 constexpr int kCoherent = 17;                // buffer-load aux bits: sc0 | sc1
-constexpr uint32_t kMarks = 32;              // sub-phase trace marks
+constexpr uint32_t kMarks = 40;              // sub-phase trace marks (the last two: shader clock)
 
 struct MkLayer {
     const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
@@ -472,12 +473,14 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
         MK_MARK(2);
         const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(f, d), fail), d, g_mk.eps);
         MK_MARK(4);   // every wave has its inputs
+        MK_MARK(29);
         if (fail) return false;
 #pragma unroll
         for (uint32_t k = 0; k < kVec; ++k) hv[k] = f[k] * (sc * wpost[k]) + hv[k];   // src/gemma3.cpp:1849-1855
     }
     int bad = vec_nonfinite(hv, d);
     const float sc2 = mk_rms_scale(blk_sum(R, vec_sumsq(hv, d), bad), d, g_mk.eps);
+    MK_MARK(30);   // after the attention-norm reduction
     if (bad && w == 0 && tid == 0 && l > 0) mk_flag_min(l - 1u);   // :1857-1863
 #pragma unroll
     for (uint32_t k = 0; k < kVec; ++k) {
@@ -863,7 +866,9 @@ __device__ __attribute__((noinline)) bool mk_phase_e(uint32_t l, uint32_t tagb, 
 
 // End of the step: fold the last block's f into h, output norm (src/gemma3.cpp:1866-1868);
 // the normed hidden state goes to xs (LM head input) and, from workgroup 0, to g_mk.hidden.
-__device__ __attribute__((noinline)) bool mk_phase_fold(uint32_t tagb) {
+// Final residual (the last block's FFN output, post-FFW norm) and output norm into m.xs
+// (src/gemma3.cpp:1849-1868); workgroup 0 also writes the hidden state.
+__device__ __forceinline__ bool mk_fold(uint32_t tagb) {
 #pragma clang fp contract(off)
     MK_LOCALS;
     MK_UNIFORM(tagb);
@@ -897,11 +902,17 @@ __device__ __attribute__((noinline)) bool mk_phase_fold(uint32_t tagb) {
     return true;
 }
 
+__device__ __attribute__((noinline)) bool mk_phase_fold(uint32_t tagb) {
+    MK_UNIFORM(tagb);
+    return mk_fold(tagb);
+}
+
 // Tied Q8_0 LM head over this workgroup's rows, local greedy argmax published with tag tLM.
 template <int SD>
-__device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tLM, uint32_t want_logits, bool tr) {
+__device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tLM, uint32_t want_logits, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
+    MK_UNIFORM(tagb);
     MK_UNIFORM(tLM);
     MK_UNIFORM(want_logits);
     __shared__ float s_v[kMkWaves];
@@ -909,11 +920,15 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tLM, uint32_t wan
     const uint32_t r_begin = min(g_mk.V, w * g_mk.lm_rows), r_end = min(g_mk.V, r_begin + g_mk.lm_rows);
     const uint32_t TR = g_mk.lm_tile_rows;
     const uint32_t ntiles = (r_end - r_begin + TR - 1u) / TR;
-    // first two tiles in flight before the limbs are built
-    LmTile tl0, tl1;
-    uint32_t pre0 = 0u, pre1 = 0u, n160 = 0u, n161 = 0u;
-    if (ntiles > 0) lm_tile_load(r_begin, min(r_end, r_begin + TR), rb_d, tl0, pre0, n160);
-    if (ntiles > 1) lm_tile_load(r_begin + TR, min(r_end, r_begin + 2u * TR), rb_d, tl1, pre1, n161);
+    // the first kLmDepth tiles are in flight before the final residual is gathered
+    LmTile tl[kLmDepth];
+    uint32_t pre[kLmDepth], n16[kLmDepth];
+#pragma unroll
+    for (uint32_t i = 0; i < kLmDepth; ++i) {
+        pre[i] = n16[i] = 0u;
+        if (i < ntiles) lm_tile_load(r_begin + i * TR, min(r_end, r_begin + (i + 1u) * TR), rb_d, tl[i], pre[i], n16[i]);
+    }
+    if (!mk_fold(tagb)) return false;
     MK_MARK(23);
     build_limbs(m.xs, d, m.L);
     XLimb xl[1];
@@ -929,8 +944,8 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tLM, uint32_t wan
         lm_tile_store(tl, n16, tile);
         const uint32_t pre_cur = pre;
         __syncthreads();
-        if (ti + 2u < ntiles) {
-            const uint32_t n0 = r_begin + (ti + 2u) * TR;
+        if (ti + kLmDepth < ntiles) {
+            const uint32_t n0 = r_begin + (ti + kLmDepth) * TR;
             lm_tile_load(n0, min(r_end, n0 + TR), rb_d, tl, pre, n16);
         }
         const uint32_t nrows = t1 - t0;
@@ -959,10 +974,12 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tLM, uint32_t wan
         }
         __syncthreads();
     };
-    for (uint32_t ti = 0; ti < ntiles; ti += 2u) {
-        consume(ti, tl0, pre0, n160);
-        if (ti == 0u) MK_MARK(25);
-        if (ti + 1u < ntiles) consume(ti + 1u, tl1, pre1, n161);
+    for (uint32_t ti = 0; ti < ntiles; ti += kLmDepth) {
+#pragma unroll
+        for (uint32_t i = 0; i < kLmDepth; ++i) {
+            if (ti + i < ntiles) consume(ti + i, tl[i], pre[i], n16[i]);
+            if (ti + i == 0u) MK_MARK(25);
+        }
     }
     MK_MARK(26);
     wave_argmax(bv, bi);
@@ -1096,12 +1113,15 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             ok = ok && (w >= g_mk.ne || mk_phase_e<SF>(l, tagb, tr));
             MK_TRACE(5u * l + 5u);
         }
-        ok = ok && mk_phase_fold(tagb);
-        if (!ok) break;
-        MK_TRACE(5u * L + 1u);
-        if (s >= lm_from) {   // LM head + local argmax (src/gemma3.cpp:1138-1185)
-            ok = mk_phase_lm<SD>(tagb + nph, want_logits, g_mk.trace_slots != 0u && si == 0u);
+        if (s >= lm_from) {   // final norm, LM head + local argmax (src/gemma3.cpp:1138-1185)
+            MK_TRACE(5u * L + 1u);
+            ok = ok && mk_phase_lm<SD>(tagb, tagb + nph, want_logits, g_mk.trace_slots != 0u && si == 0u);
+            if (!ok) break;
             prev_lm_tag = tagb + nph;
+        } else {
+            ok = ok && mk_phase_fold(tagb);
+            if (!ok) break;
+            MK_TRACE(5u * L + 1u);
         }
         MK_TRACE(5u * L + 2u);
         if (g_mk.trace_slots != 0u && si == 0u && tid == 0u)
