@@ -74,7 +74,6 @@ constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x q
 constexpr uint32_t kLmUnits = 4;             // 16-byte LM-head loads per thread per tile
 constexpr uint32_t kLmDepth = 3;             // LM-head tiles in flight per workgroup
 constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
-constexpr uint32_t kGrpPerWave = kGrp / kMkWaves;
 constexpr uint32_t kPartRound = 12 * kMkThreads;   // attention partials gathered per wait
 constexpr int kRsrcFlags = 0x00020000;       // raw buffer resource, 32-bit data format
 // Cache policy of exchange and KV-cache accesses: system scope (sc0 sc1), coherent across the
@@ -95,7 +94,7 @@ struct MkLayer {
 // Byte offsets of the dynamic LDS carve-up. `u` is phase-local scratch shared by the
 // attention partial sums (B), the gathered chunk partials (C) and the LM-head tile.
 struct MkLds {
-    uint32_t h, xs, la, lb, lc, ls, sq, sc, mw, gu, red, u, total;
+    uint32_t h, xs, xa, xd, ya, yd, nwa0, nwa1, nwd0, nwd1, any, la, lb, lc, ls, sq, sc, mw, gu, red, u, total;
 };
 
 constexpr uint32_t kMkLdsBytes = 120u * 1024u;   // static LDS of the persistent kernel
@@ -133,6 +132,25 @@ __constant__ MkParams g_mk;
 __constant__ MkLayer g_mk_layers[kMkMaxLayers];
 
 __shared__ __align__(16) unsigned char g_mk_lds[kMkLdsBytes];
+
+// Workgroup OR of `pred` behind one plain barrier: each wave's ballot goes to its word of flag
+// set `id` in LDS, every thread reads the set after the barrier. (HIP's __syncthreads_or is a
+// generic reduction that reads the dispatch packet and takes three barriers.) A set is rewritten
+// only by the next use of the same call site, after other barriers, so no reader sees it change.
+constexpr uint32_t kAnySets = 8;
+__device__ __forceinline__ bool blk_any(int pred, uint32_t id) {
+    uint32_t* f = reinterpret_cast<uint32_t*>(g_mk_lds + g_mk.lds.any) + id * kMkWaves;
+    const bool wa = __builtin_amdgcn_ballot_w64(pred != 0) != 0u;
+    if ((threadIdx.x & 63u) == 0u) f[threadIdx.x >> 6] = wa ? 1u : 0u;
+    __syncthreads();
+    uint32_t r = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kMkWaves; ++k) r |= f[k];
+    return r != 0u;
+}
+// call sites of blk_any (flag sets)
+constexpr uint32_t kAnyGather0 = 0, kAnyGather1 = 1, kAnyGatherE = 2, kAnyArgmax = 3, kAnyB = 4, kAnyA = 5, kAnyD = 6,
+                   kAnyFold = 7;
 
 // ---- tagged exchange -----------------------------------------------------------------------
 
@@ -224,9 +242,10 @@ __device__ __forceinline__ int ll_wait_at(const u64* src, uint32_t n, const uint
     return ll_poll<MAXK>(r, off, live, tag, out);
 }
 
-// ll_wait into LDS dst[0..n), then a barrier; false (in every thread) if abandoned.
+// ll_wait into LDS dst[0..n), then a barrier (flag set any_id); false (in every thread) if
+// abandoned.
 template <int MAXK>
-__device__ __forceinline__ bool ll_gather(const u64* src, uint32_t n, uint32_t tag, float* dst) {
+__device__ __forceinline__ bool ll_gather(const u64* src, uint32_t n, uint32_t tag, float* dst, uint32_t any_id) {
     float v[MAXK];
     const int fail = ll_wait<MAXK>(src, n, tag, v);
 #pragma unroll
@@ -234,7 +253,7 @@ __device__ __forceinline__ bool ll_gather(const u64* src, uint32_t n, uint32_t t
         const uint32_t i = threadIdx.x + static_cast<uint32_t>(k) * kMkThreads;
         if (i < n) dst[i] = v[k];
     }
-    return __syncthreads_or(fail) == 0;
+    return !blk_any(fail, any_id);
 }
 
 // ---- workgroup reductions (one barrier each) ----------------------------------------------------
@@ -282,8 +301,16 @@ __device__ __forceinline__ float mk_gelu(float x) {
 // ---- LDS views -----------------------------------------------------------------------------
 
 struct MkSmem {
-    float* h;       // residual stream: element i belongs to thread i % kMkThreads
-    float* xs;      // matvec input
+    float* h;       // residual stream (wave 0 only)
+    float* xs;      // matvec input of phases C and E
+    float* xa;      // normed input of phase A and of the LM head
+    float* xd;      // normed input of phase D
+    float* ya;      // gathered residual input of phase A and of the final fold
+    float* yd;      // gathered residual input of phase D
+    float* nwa0;    // norm weights staged for phase A and the fold (post, next)
+    float* nwa1;
+    float* nwd0;    // norm weights staged for phase D
+    float* nwd1;
     LimbLds L;      // LM-head activation limbs
     float* sq;      // phase B: q | k | v
     float* sc;      // phase B scores; argmax partials
@@ -298,6 +325,14 @@ __device__ __forceinline__ MkSmem mk_smem() {
     MkSmem m;
     m.h = reinterpret_cast<float*>(smem + g_mk.lds.h);
     m.xs = reinterpret_cast<float*>(smem + g_mk.lds.xs);
+    m.xa = reinterpret_cast<float*>(smem + g_mk.lds.xa);
+    m.xd = reinterpret_cast<float*>(smem + g_mk.lds.xd);
+    m.ya = reinterpret_cast<float*>(smem + g_mk.lds.ya);
+    m.yd = reinterpret_cast<float*>(smem + g_mk.lds.yd);
+    m.nwa0 = reinterpret_cast<float*>(smem + g_mk.lds.nwa0);
+    m.nwa1 = reinterpret_cast<float*>(smem + g_mk.lds.nwa1);
+    m.nwd0 = reinterpret_cast<float*>(smem + g_mk.lds.nwd0);
+    m.nwd1 = reinterpret_cast<float*>(smem + g_mk.lds.nwd1);
     m.L = LimbLds{reinterpret_cast<int8_t*>(smem + g_mk.lds.la), reinterpret_cast<int8_t*>(smem + g_mk.lds.lb),
                   reinterpret_cast<int8_t*>(smem + g_mk.lds.lc), reinterpret_cast<float*>(smem + g_mk.lds.ls)};
     m.sq = reinterpret_cast<float*>(smem + g_mk.lds.sq);
@@ -435,8 +470,192 @@ __device__ __forceinline__ void lm_tile_store(const LmTile& t, uint32_t n16, uin
 // and down-projection workgroups (the first ones).
 __device__ __forceinline__ uint32_t bunit_of(uint32_t w, uint32_t nwg) { return nwg - 1u - w; }
 
+// Full-wave sums of N independent values (uniform results), the N DPP chains interleaved step
+// by step so that each chain's hazard wait is filled by the others.
+template <int N>
+__device__ __forceinline__ void wave_red_sum_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_mov<0xB1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_mov<0x4E>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_mov<0x141>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_mov<0x140>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_or_zero<0x142, 0xa>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_or_zero<0x143, 0xc>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 63));
+}
+
+// Polls 16-byte units (two tagged words each) at byte offsets off[k] of r until both tags of
+// every unit equal `tag` (or !live); out[2k], out[2k+1] get the two values of unit k. Returns
+// 0, or 1 if the wait was abandoned (abort raised).
+template <int MAXK>
+__device__ __forceinline__ int ll_poll2(__amdgpu_buffer_rsrc_t r, const int (&off)[MAXK], const bool (&live)[MAXK],
+                                        uint32_t tag, float (&out)[2 * MAXK]) {
+    v4u v[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, off[k], 0, kCoherent);
+    int fail = 0;
+    uint32_t spins = 0;
+    for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) ready &= (v[k].y == tag && v[k].w == tag) || !live[k];
+        if (ready) break;
+        if ((++spins & 63u) == 0u && (spins > kSpinLimit || mk_aborted())) {
+            fail = 1;
+            mk_abort();
+            break;
+        }
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, off[k], 0, kCoherent);
+    }
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        out[2 * k] = __uint_as_float(v[k].x);
+        out[2 * k + 1] = __uint_as_float(v[k].z);
+    }
+    return fail;
+}
+
+// 1.0f / std::sqrt(float(sum_sq / n) + eps) for n a power of two: sum_sq * (1/n) is the exact
+// quotient, one multiply instead of the double-precision division sequence.
+__device__ __forceinline__ float mk_rms_scale_pow2(double ss, uint32_t n, float eps) {
+#pragma clang fp contract(off)
+    return 1.0f / sqrtf(static_cast<float>(ss * (1.0 / static_cast<double>(n))) + eps);
+}
+
+// Copies n floats (n % 4 == 0) of src into LDS dst with direct global->LDS loads issued by the
+// calling wave: lane i moves 16 bytes of each 1 KB row. No registers hold the data; the loads
+// complete in issue order with the wave's other vector-memory loads. dst holds whole 1 KB rows
+// (units past n repeat the last unit of src).
+__device__ __forceinline__ void wave_stage_lds(const float* src, float* dst, uint32_t n) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n16 = n >> 2;
+    for (uint32_t r = 0; r * 64u < n16; ++r) {
+        const uint32_t u = min(r * 64u + lane, n16 - 1u);
+        __builtin_amdgcn_global_load_lds((const VRT_AS_GLOBAL void*)(src + 4u * u),
+                                         (__attribute__((address_space(3))) void*)(dst + 256u * r), 16, 0, 0);
+    }
+}
+
+// Residual update and RMSNorm of the d-vector residual stream h, which every workgroup keeps in
+// LDS. All threads gather y (two tagged words per 16-byte unit) into LDS, wave 0 meanwhile
+// stages the two norm weight vectors into LDS; after one barrier every wave computes the whole
+// update on its own (lane i: element pairs (2j, 2j + 1), j = i + 64k), so no second barrier is
+// needed, and the waves write identical values to h and x:
+//   h = y * (rms(y) * w_post) + h   if ysrc != nullptr        (src/gemma3.cpp:1703-1711, :1849-1855)
+//   x = (h * rms(h)) * w_next        (INTO: rms_norm_into, :991-996, :1713-1718)
+//   x = h * (rms(h) * w_next)        (!INTO: rms_norm_inplace, the output norm :1866-1868)
+// with rms(v) = 1.0f / sqrtf(float(sum double(v)^2 / d) + eps) (:967-983). x goes to x_lds and,
+// from wave 0, to x_glob if given. `bad` is set when h has a non-finite element (:1857-1863).
+// y_lds and the staging areas belong to one call site: a later call site may run while slower
+// waves still read this one's. Returns 1 if the gather was abandoned.
+template <int EP, bool INTO>
+__device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const float* w_post, const float* w_next,
+                                        float* hl, float* x_lds, float* x_glob, uint32_t d, float eps, int& bad,
+                                        float* nw_post, float* nw_next, float* y_lds, uint32_t any_id, bool tr = false) {
+#pragma clang fp contract(off)
+    auto mark = [&](uint32_t k) {
+        if (tr && threadIdx.x == 0u)
+            gp(g_mk.trace)[blockIdx.x * g_mk.trace_slots + g_mk.trace_slots - kMarks + k] = __builtin_amdgcn_s_memrealtime();
+    };
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t npair = d >> 1u;
+    if (wave == 0u) {   // the norm weights travel to LDS while the gather waits
+        wave_stage_lds(w_next, nw_next, d);
+        if (ysrc) wave_stage_lds(w_post, nw_post, d);
+    }
+    int fail = 0;
+    if (ysrc) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(ysrc), 0, static_cast<int>(d * 8u), kRsrcFlags);
+        int off[2];
+        bool live[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t j = threadIdx.x + kMkThreads * k;
+            live[k] = j < npair;
+            off[k] = live[k] ? static_cast<int>(j * 16u) : 0x7ffffff0;   // past the buffer: no access
+        }
+        float y[4];
+        fail = ll_poll2<2>(r, off, live, tag, y);
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            if (live[k]) reinterpret_cast<float2*>(y_lds)[threadIdx.x + kMkThreads * k] = make_float2(y[2 * k], y[2 * k + 1]);
+    }
+    if (wave == 0u) __builtin_amdgcn_s_waitcnt(0);   // the staged weights are in LDS (vmcnt covers LDS loads)
+    mark(31);
+    if (blk_any(fail, any_id)) return 1;
+    mark(32);
+    float2 h[EP];
+    bool live[EP];
+#pragma unroll
+    for (int k = 0; k < EP; ++k) {
+        const uint32_t j = lane + 64u * static_cast<uint32_t>(k);
+        live[k] = j < npair;
+        h[k] = live[k] ? reinterpret_cast<const float2*>(hl)[j] : make_float2(0.0f, 0.0f);
+    }
+    if (ysrc) {
+        float2 y[EP];
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < EP; ++k) {
+            y[k] = live[k] ? reinterpret_cast<const float2*>(y_lds)[lane + 64u * k] : make_float2(0.0f, 0.0f);
+            ss += static_cast<double>(y[k].x) * static_cast<double>(y[k].x);
+            ss += static_cast<double>(y[k].y) * static_cast<double>(y[k].y);
+        }
+        const float sc = mk_rms_scale(wave_red_sum_d(ss), d, eps);
+#pragma unroll
+        for (int k = 0; k < EP; ++k) {
+            const float2 wp = reinterpret_cast<const float2*>(nw_post)[live[k] ? lane + 64u * k : 0u];
+            h[k].x = y[k].x * (sc * wp.x) + h[k].x;
+            h[k].y = y[k].y * (sc * wp.y) + h[k].y;
+        }
+    }
+    int nf = 0;
+    double ss2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < EP; ++k)
+        if (live[k]) {
+            nf |= !__builtin_isfinite(h[k].x) || !__builtin_isfinite(h[k].y);
+            ss2 += static_cast<double>(h[k].x) * static_cast<double>(h[k].x);
+            ss2 += static_cast<double>(h[k].y) * static_cast<double>(h[k].y);
+        }
+    bad = __builtin_amdgcn_ballot_w64(nf != 0) != 0u;
+    const float sc2 = mk_rms_scale(wave_red_sum_d(ss2), d, eps);
+    mark(33);
+#pragma unroll
+    for (int k = 0; k < EP; ++k)
+        if (live[k]) {
+            const uint32_t j = lane + 64u * k;
+            const float2 wn = reinterpret_cast<const float2*>(nw_next)[j];
+            float2 x;
+            if constexpr (INTO) {
+                x.x = h[k].x * sc2 * wn.x;
+                x.y = h[k].y * sc2 * wn.y;
+            } else {
+                x.x = h[k].x * (sc2 * wn.x);
+                x.y = h[k].y * (sc2 * wn.y);
+            }
+            reinterpret_cast<float2*>(hl)[j] = h[k];
+            reinterpret_cast<float2*>(x_lds)[j] = x;
+            if (x_glob && wave == 0u) {
+                gp(x_glob)[2u * j] = x.x;
+                gp(x_glob)[2u * j + 1u] = x.y;
+            }
+        }
+    return 0;
+}
+
 // Phase A: fold f of block l-1 into h, RMSNorm(attn_norm), rows of [Wq | Wk | Wv].
-template <int SD>
+template <int SD, int EP>
 __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
@@ -446,9 +665,6 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     MK_TAGS(l);
     const MkLayer& Ly = g_mk_layers[l];
     MK_MARK(0);
-    float wpost[kVec], wattn[kVec], hv[kVec];
-    vec_load(Ly.attn_norm, d, wattn);
-    if (l > 0) vec_load(g_mk_layers[l - 1u].post_ffw, d, wpost);
     // producers: every workgroup that is not an attention chunk of this block at this position
     uint32_t v0 = 0, v1 = 0;
     const uint32_t nprod = g_mk.nwg - n_bunits(Ly.slots, pos);
@@ -462,48 +678,36 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     RowBatch<SD, 1, 1> rb;
     batch_load<SD, 1, 1>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
     MK_MARK(1);
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = tid + k * kMkThreads;
-        hv[k] = i < d ? m.h[i] : 0.0f;
-    }
-    if (l > 0) {
-        float f[kVec];
-        int fail = ll_wait<kVec>(g_mk.x_f, d, tagb + 5u * (l - 1u) + 5u, f);
-        MK_MARK(2);
-        const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(f, d), fail), d, g_mk.eps);
-        MK_MARK(4);   // every wave has its inputs
-        MK_MARK(29);
-        if (fail) return false;
-#pragma unroll
-        for (uint32_t k = 0; k < kVec; ++k) hv[k] = f[k] * (sc * wpost[k]) + hv[k];   // src/gemma3.cpp:1849-1855
-    }
-    int bad = vec_nonfinite(hv, d);
-    const float sc2 = mk_rms_scale(blk_sum(R, vec_sumsq(hv, d), bad), d, g_mk.eps);
-    MK_MARK(30);   // after the attention-norm reduction
+    int bad = 0;
+    if (mk_resid<EP, true>(l > 0 ? g_mk.x_f : nullptr, tagb + 5u * (l - 1u) + 5u,
+                           l > 0 ? g_mk_layers[l - 1u].post_ffw : nullptr, Ly.attn_norm, m.h, m.xa, nullptr, d,
+                           g_mk.eps, bad, m.nwa0, m.nwa1, m.ya, kAnyA, tr))
+        return false;
     if (bad && w == 0 && tid == 0 && l > 0) mk_flag_min(l - 1u);   // :1857-1863
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = tid + k * kMkThreads;
-        if (i < d) {
-            m.h[i] = hv[k];
-            m.xs[i] = hv[k] * sc2 * wattn[k];                                      // :991-996
-        }
-    }
-    __syncthreads();
     MK_MARK(3);
     u64* out = g_mk.x_qkv;
-    batch_consume_x<SD, 1, 1>(rb, nblk_d, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tA); });
+    batch_consume_x<SD, 1, 1>(rb, nblk_d, m.xa, [&](uint32_t v, float val) { ll_stf(out + v, val, tA); });
     MK_MARK(5);
     return true;
 }
 
-// Phase B: one workgroup per (chunk c, query head h). QK-norm and RoPE of q_h and k
-// (src/gemma3.cpp:1045-1104, :1371-1424), the KV append by head 0 of the chunk holding the
-// current position (:1590-1600), then online softmax attention of q_h over the chunk's
-// positions (:1602-1696). Publishes the unnormalised partial {acc[hd], m, l} of (c, h).
-// Waves take positions t = g0 + wave + 8i of each 32-position group; lane owns 4 head dims.
-__device__ __attribute__((noinline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
+constexpr uint32_t kBWaves = 4;                    // waves of an attention unit that take positions
+constexpr uint32_t kBGrp = 32;                     // positions per group (all working waves)
+constexpr uint32_t kBPos = kBGrp / kBWaves;        // positions per wave per group
+
+// Phase B: one workgroup per (chunk c, query head h); waves 0..3 work, the others wait at the
+// closing barrier. Lane i of a wave owns head dims 4i..4i+3. Every working wave gathers its
+// lanes' q_h, k and v itself, applies QK-norm (src/gemma3.cpp:1045-1104) and RoPE
+// (:1371-1424; the partner dims e +- head_dim/2 come from another lane of the same wave), and
+// runs an online softmax over its positions t = c0 + wave + 4i of the chunk (:1602-1696), in
+// groups of 32 positions whose K/V rows are loaded one group ahead (a window chunk is one
+// group, loaded before the wait for q, k, v), so
+// the wave needs no barrier until the four partials {m, l, acc} are merged through LDS. Wave 0
+// of head 0 of the chunk holding the current position appends k and v to the cache
+// (:1590-1600). Publishes the unnormalised partial {acc[hd] of head h, m, l} of (c, h).
+// Inlined into the kernel: as a call it would save and restore callee-saved registers through
+// scratch.
+__device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
     MK_UNIFORM(l);
@@ -520,198 +724,195 @@ __device__ __attribute__((noinline)) bool mk_phase_b(uint32_t l, uint32_t pos, u
     MK_MARK(6);
     const uint32_t c0 = t_first + c * clen;
     const uint32_t c1 = min(pos + 1u, c0 + clen);
+    const uint32_t uw = __builtin_amdgcn_readfirstlane(wave);   // scalar: positions and branches on SALU
+    const bool worker = uw < kBWaves;
     const uint32_t dl = lane * 4u;                 // this lane's 4 head dims
-    const bool dlive = dl < hd;
-    // this thread's gathered elements j = tid, tid + 512 of [q_h | k | v] (3 hd values)
-    const uint32_t nj = 3u * hd;
-    float wn[2], cs[2], sn[2];
-    uint32_t src[2];
-    {
-        const VRT_AS_GLOBAL float* ct = gp(Ly.global ? g_mk.cos_g : g_mk.cos_l) + static_cast<uint64_t>(pos) * half;
-        const VRT_AS_GLOBAL float* st = gp(Ly.global ? g_mk.sin_g : g_mk.sin_l) + static_cast<uint64_t>(pos) * half;
+    const bool dlive = worker && dl < hd;
+    const bool lo = dl < half;                     // first half of the RoPE pairs
+    const uint32_t e0 = lo ? dl : dl - half;       // RoPE index of dim dl
+    const int partner = static_cast<int>(lo ? lane + (half >> 2) : lane - (half >> 2));
+    float* ra = m.u;                               // [kBWaves][hd] partial sums
+    float* rml = m.mw;                             // [kBWaves] m, then [kBWaves] l
+    int fail = 0;
+    if (worker) {
+        // this wave's K/V rows of the first group, from the cache (device-coherent)
+        const uint32_t kv_bytes = Ly.slots * hd * 4u;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
+        auto kv_off = [&](uint32_t t) { return ((t % Ly.slots) * hd + dl) * 4u; };
+        auto cached = [&](uint32_t t, uint32_t g1) { return t < g1 && t != pos && dlive; };
+        v4u kr[kBPos], vr[kBPos];
+        {
+            const uint32_t g1 = min(c1, c0 + kBGrp);
 #pragma unroll
-        for (uint32_t k = 0; k < 2u; ++k) {
-            const uint32_t j = tid + k * kMkThreads;
-            const uint32_t e = j % hd;
-            src[k] = j < hd ? h * hd + j : qw - hd + j;
-            wn[k] = j < hd ? gp(Ly.q_norm)[e] : (j < 2u * hd ? gp(Ly.k_norm)[e] : 1.0f);
-            cs[k] = (j < 2u * hd && e < half) ? ct[e] : 0.0f;
-            sn[k] = (j < 2u * hd && e < half) ? st[e] : 0.0f;
-        }
-    }
-    // this wave's K/V rows of the first group, from the cache (device-coherent)
-    const uint32_t kv_bytes = Ly.slots * hd * 4u;
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
-    v4u kr[kGrpPerWave], vr[kGrpPerWave];
-#pragma unroll
-    for (uint32_t i = 0; i < kGrpPerWave; ++i) kr[i] = vr[i] = v4u{0u, 0u, 0u, 0u};
-    auto kv_off = [&](uint32_t t) { return ((t % Ly.slots) * hd + dl) * 4u; };
-    auto cached = [&](uint32_t t, uint32_t g1) { return t < g1 && t != pos && dlive; };
-    {
-        const uint32_t g1 = min(c1, c0 + kGrp);
-#pragma unroll
-        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
-            const uint32_t t = c0 + wave + kMkWaves * i;
-            if (cached(t, g1)) {
-                kr[i] = co_ld4(rk, kv_off(t));
-                vr[i] = co_ld4(rv, kv_off(t));
+            for (uint32_t i = 0; i < kBPos; ++i) {
+                kr[i] = vr[i] = v4u{0u, 0u, 0u, 0u};
+                const uint32_t t = c0 + uw + kBWaves * i;
+                if (cached(t, g1)) {
+                    kr[i] = co_ld4(rk, kv_off(t));
+                    vr[i] = co_ld4(rv, kv_off(t));
+                }
             }
         }
-    }
-    float qv[2];
-    int fail = ll_wait_at<2>(g_mk.x_qkv, nqkv, src, nj, tA, qv);
-    MK_MARK(7);
-    // QK-norm: sums of squares of q_h (j < hd) and k (hd <= j < 2hd), one barrier
-    {
+        // norm weights and RoPE factors of this lane's dims
+        float wq[4], wk[4], cs[4], sn[4];
+        {
+            const VRT_AS_GLOBAL float* ct = gp(Ly.global ? g_mk.cos_g : g_mk.cos_l) + static_cast<uint64_t>(pos) * half;
+            const VRT_AS_GLOBAL float* st = gp(Ly.global ? g_mk.sin_g : g_mk.sin_l) + static_cast<uint64_t>(pos) * half;
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) {
+                wq[e] = dlive ? gp(Ly.q_norm)[dl + e] : 0.0f;
+                wk[e] = dlive ? gp(Ly.k_norm)[dl + e] : 0.0f;
+                cs[e] = dlive ? ct[e0 + e] : 0.0f;
+                sn[e] = dlive ? st[e0 + e] : 0.0f;
+            }
+        }
+        // q_h, k, v of this lane's dims
+        float qkv[12];
+        {
+            const __amdgpu_buffer_rsrc_t rq =
+                __builtin_amdgcn_make_buffer_rsrc(g_mk.x_qkv, 0, static_cast<int>(nqkv * 8u), kRsrcFlags);
+            const int oq = static_cast<int>((h * hd + dl) * 8u), ok = static_cast<int>((qw + dl) * 8u),
+                      ov = static_cast<int>((qw + hd + dl) * 8u);
+            const int off[6] = {oq, oq + 16, ok, ok + 16, ov, ov + 16};
+            const bool live6[6] = {dlive, dlive, dlive, dlive, dlive, dlive};
+            fail = ll_poll2<6>(rq, off, live6, tA, qkv);
+        }
+        MK_MARK(7);
+        float q[4], k[4], v[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            q[e] = dlive ? qkv[e] : 0.0f;
+            k[e] = dlive ? qkv[4 + e] : 0.0f;
+            v[e] = dlive ? qkv[8 + e] : 0.0f;
+        }
+        // QK-norm: sums of squares of q_h and k over the wave
         double sq_q = 0.0, sq_k = 0.0;
 #pragma unroll
-        for (uint32_t k = 0; k < 2u; ++k) {
-            const uint32_t j = tid + k * kMkThreads;
-            const double x2 = static_cast<double>(qv[k]) * static_cast<double>(qv[k]);
-            if (j < hd) sq_q += x2;
-            else if (j < 2u * hd) sq_k += x2;
+        for (uint32_t e = 0; e < 4u; ++e) {
+            sq_q += static_cast<double>(q[e]) * static_cast<double>(q[e]);
+            sq_k += static_cast<double>(k[e]) * static_cast<double>(k[e]);
         }
         sq_q = wave_red_sum_d(sq_q);
         sq_k = wave_red_sum_d(sq_k);
-        double* red = m.red + 4u * kMkWaves;   // [2][waves] past the blk_sum slots
-        if (lane == 0) {
-            red[wave] = sq_q;
-            red[kMkWaves + wave] = sq_k;
-        }
-        if (__syncthreads_or(fail)) return false;
-        MK_MARK(27);   // every wave has its inputs
-        double ssq = 0.0, ssk = 0.0;
+        const float scq = mk_rms_scale_pow2(sq_q, hd, g_mk.eps), sck = mk_rms_scale_pow2(sq_k, hd, g_mk.eps);
 #pragma unroll
-        for (uint32_t q = 0; q < kMkWaves; ++q) {
-            ssq += red[q];
-            ssk += red[kMkWaves + q];
+        for (uint32_t e = 0; e < 4u; ++e) {
+            q[e] = q[e] * scq * wq[e];
+            k[e] = k[e] * sck * wk[e];
         }
-        const float scq = mk_rms_scale(ssq, hd, g_mk.eps), sck = mk_rms_scale(ssk, hd, g_mk.eps);
+        // RoPE (NeoX halves): (a, b) = (x[e], x[e + half]) -> (a c - b s, b c + a s)
+        float qo[4], ko[4];
 #pragma unroll
-        for (uint32_t k = 0; k < 2u; ++k) {
-            const uint32_t j = tid + k * kMkThreads;
-            if (j < nj) m.sq[j] = j < hd ? qv[k] * scq * wn[k] : (j < 2u * hd ? qv[k] * sck * wn[k] : qv[k]);
-        }
-    }
-    __syncthreads();
-    // RoPE: the thread holding element e < half of q_h or k rotates the pair (e, e + half)
-#pragma unroll
-    for (uint32_t k = 0; k < 2u; ++k) {
-        const uint32_t j = tid + k * kMkThreads;
-        if (j < 2u * hd && (j % hd) < half) {
-            const float a = m.sq[j], b = m.sq[j + half];
-            m.sq[j] = a * cs[k] - b * sn[k];
-            m.sq[j + half] = b * cs[k] + a * sn[k];
-        }
-    }
-    __syncthreads();
-    MK_MARK(8);
-    const float* sk = m.sq + hd;
-    const float* sv = sk + hd;
-    // KV append by head 0 of the chunk that holds the current position; the other heads use
-    // their own copy of the new row
-    if (h == 0u && c1 == pos + 1u) {
-        const uint64_t slot = static_cast<uint64_t>(pos % Ly.slots) * hd;
-        for (uint32_t i = tid; i < hd; i += kMkThreads) {
-            co_stf(Ly.kc + slot + i, sk[i]);
-            co_stf(Ly.vc + slot + i, sv[i]);
-        }
-        __builtin_amdgcn_s_waitcnt(0);   // complete before this workgroup publishes its partial
-    }
-    float qr[4];
-#pragma unroll
-    for (uint32_t e = 0; e < 4u; ++e) qr[e] = dlive ? m.sq[dl + e] : 0.0f;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = -INFINITY, l_run = 0.0f;
-    float* sc = m.sc;   // [kGrp]: scores, then exp weights
-    for (uint32_t g0 = c0; g0 < c1; g0 += kGrp) {
-        const uint32_t g1 = min(c1, g0 + kGrp);
-        const uint32_t n = g1 - g0;
-#pragma unroll
-        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
-            const uint32_t t = g0 + wave + kMkWaves * i;
-            if (t == pos && dlive) {
-                kr[i] = v4u{__float_as_uint(sk[dl]), __float_as_uint(sk[dl + 1]), __float_as_uint(sk[dl + 2]),
-                            __float_as_uint(sk[dl + 3])};
-                vr[i] = v4u{__float_as_uint(sv[dl]), __float_as_uint(sv[dl + 1]), __float_as_uint(sv[dl + 2]),
-                            __float_as_uint(sv[dl + 3])};
-            }
+        for (uint32_t e = 0; e < 4u; ++e) {
+            qo[e] = __shfl(q[e], partner);
+            ko[e] = __shfl(k[e], partner);
         }
 #pragma unroll
-        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
-            const uint32_t t = g0 + wave + kMkWaves * i;
-            if (t < g1) {   // wave-uniform
+        for (uint32_t e = 0; e < 4u; ++e) {
+            q[e] = lo ? q[e] * cs[e] - qo[e] * sn[e] : q[e] * cs[e] + qo[e] * sn[e];
+            k[e] = lo ? k[e] * cs[e] - ko[e] * sn[e] : k[e] * cs[e] + ko[e] * sn[e];
+        }
+        MK_MARK(8);
+        // KV append by wave 0 of head 0 of the chunk that holds the current position; every
+        // wave uses its own copy of the new row
+        const bool appender = h == 0u && c1 == pos + 1u && uw == 0u;
+        if (appender && dlive && !fail) {
+            const uint32_t so = ((pos % Ly.slots) * hd + dl) * 4u;
+            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(k[0]), __float_as_uint(k[1]),
+                                                       __float_as_uint(k[2]), __float_as_uint(k[3])},
+                                                   rk, static_cast<int>(so), 0, kCoherent);
+            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                       __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                                   rv, static_cast<int>(so), 0, kCoherent);
+        }
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float m_run = -INFINITY, l_run = 0.0f;
+        const float attn_scale = g_mk.attn_scale;
+        for (uint32_t g0 = c0; g0 < c1; g0 += kBGrp) {
+            const uint32_t g1 = min(c1, g0 + kBGrp);
+            float s[kBPos];
+#pragma unroll
+            for (uint32_t i = 0; i < kBPos; ++i) {
+                const uint32_t t = g0 + uw + kBWaves * i;
+                if (t == pos && dlive) {
+                    kr[i] = v4u{__float_as_uint(k[0]), __float_as_uint(k[1]), __float_as_uint(k[2]), __float_as_uint(k[3])};
+                    vr[i] = v4u{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+                }
                 float p = 0.0f;
-                if (dlive)   // lanes past head_dim hold no key
 #pragma unroll
-                    for (uint32_t e = 0; e < 4u; ++e) p += qr[e] * __uint_as_float(kr[i][e]);
-                p = wave_red_sum(p);
-                if (lane == 0) sc[t - g0] = p * g_mk.attn_scale;
+                for (uint32_t e = 0; e < 4u; ++e) p += q[e] * __uint_as_float(kr[i][e]);
+                s[i] = p;
             }
-        }
-        // the next group's keys load while this group's softmax and values run
-        const uint32_t n0 = g0 + kGrp, n1 = min(c1, n0 + kGrp);
+            wave_red_sum_n<kBPos>(s);   // wave-uniform scores
 #pragma unroll
-        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
-            const uint32_t t = n0 + wave + kMkWaves * i;
-            if (cached(t, n1)) kr[i] = co_ld4(rk, kv_off(t));
-        }
-        __syncthreads();
-        if (wave == 0) {
-            const float mx = wave_red_max(lane < n ? sc[lane] : -INFINITY);
+            for (uint32_t i = 0; i < kBPos; ++i) s[i] = g0 + uw + kBWaves * i < g1 ? s[i] * attn_scale : -INFINITY;
+            // the next group's keys load while this group's softmax and values run
+            const uint32_t n0 = g0 + kBGrp, n1 = min(c1, n0 + kBGrp);
+#pragma unroll
+            for (uint32_t i = 0; i < kBPos; ++i) {
+                const uint32_t t = n0 + uw + kBWaves * i;
+                if (cached(t, n1)) kr[i] = co_ld4(rk, kv_off(t));
+            }
+            float mx = s[0];
+#pragma unroll
+            for (uint32_t i = 1; i < kBPos; ++i) mx = fmaxf(mx, s[i]);
             const float m_new = fmaxf(m_run, mx);
-            float e = 0.0f;
-            if (lane < n) {
-                e = expf(sc[lane] - m_new);
-                sc[lane] = e;
+            if (m_new != -INFINITY) {   // this wave has a position in the group (or before it)
+                const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+                float ls = 0.0f;
+                float pw[kBPos];
+#pragma unroll
+                for (uint32_t i = 0; i < kBPos; ++i) {
+                    pw[i] = s[i] == -INFINITY ? 0.0f : expf(s[i] - m_new);
+                    ls += pw[i];
+                }
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) {
+                    float a = acc[e] * r;
+#pragma unroll
+                    for (uint32_t i = 0; i < kBPos; ++i) a += pw[i] * __uint_as_float(vr[i][e]);
+                    acc[e] = a;
+                }
+                l_run = l_run * r + ls;
+                m_run = m_new;
             }
-            const float ls = wave_red_sum(e);
-            if (lane == 0) { m.mw[0] = m_new; m.mw[1] = ls; }
-        }
-        __syncthreads();
-        {
-            const float m_new = m.mw[0];
-            const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
 #pragma unroll
-            for (uint32_t e = 0; e < 4u; ++e) acc[e] *= r;
-            l_run = l_run * r + m.mw[1];
-            m_run = m_new;
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
-            const uint32_t t = g0 + wave + kMkWaves * i;
-            if (t < g1 && dlive) {
-                const float pw = sc[t - g0];
-#pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) acc[e] += pw * __uint_as_float(vr[i][e]);
+            for (uint32_t i = 0; i < kBPos; ++i) {
+                const uint32_t t = n0 + uw + kBWaves * i;
+                if (cached(t, n1)) vr[i] = co_ld4(rv, kv_off(t));
             }
         }
-#pragma unroll
-        for (uint32_t i = 0; i < kGrpPerWave; ++i) {
-            const uint32_t t = n0 + wave + kMkWaves * i;
-            if (cached(t, n1)) vr[i] = co_ld4(rv, kv_off(t));
+        if (dlive) *reinterpret_cast<float4*>(ra + uw * hd + dl) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        if (lane == 0) {
+            rml[uw] = m_run;
+            rml[kBWaves + uw] = l_run;
         }
-        __syncthreads();
+        // the appended row is complete before this wave publishes its share of the partial
+        if (appender) __builtin_amdgcn_s_waitcnt(0);
     }
     MK_MARK(9);
-    // sum the waves' partials and publish {acc[hd] of head h, m, l}
-    float* ra = m.u;   // [waves][hd]
-    if (dlive) {
-#pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) ra[wave * hd + dl + e] = acc[e];
-    }
-    __syncthreads();
+    if (blk_any(fail, kAnyB)) return false;
+    // merge the waves: acc = sum_w e^(m_w - M) acc_w, l = sum_w e^(m_w - M) l_w (fixed order)
     u64* part = g_mk.x_part + static_cast<uint64_t>(c) * part_stride;
-    for (uint32_t j = tid; j < hd; j += kMkThreads) {
+    if (tid < hd) {
+        float M = rml[0];
+#pragma unroll
+        for (uint32_t k = 1; k < kBWaves; ++k) M = fmaxf(M, rml[k]);
+        float f[kBWaves];
+#pragma unroll
+        for (uint32_t k = 0; k < kBWaves; ++k) f[k] = rml[k] == -INFINITY ? 0.0f : expf(rml[k] - M);
         float sacc = 0.0f;
 #pragma unroll
-        for (uint32_t k = 0; k < kMkWaves; ++k) sacc += ra[k * hd + j];
-        ll_stf(part + h * hd + j, sacc, tB);
-    }
-    if (tid == 0) {
-        ll_stf(part + qw + h, m_run, tB);
-        ll_stf(part + qw + H + h, l_run, tB);
+        for (uint32_t k = 0; k < kBWaves; ++k) sacc += f[k] * ra[k * hd + tid];
+        ll_stf(part + h * hd + tid, sacc, tB);
+        if (tid == 0) {
+            float L = 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < kBWaves; ++k) L += f[k] * rml[kBWaves + k];
+            ll_stf(part + qw + h, M, tB);
+            ll_stf(part + qw + H + h, L, tB);
+        }
     }
     MK_MARK(10);
     return true;
@@ -748,7 +949,9 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
     float* parts = m.u;
     const uint32_t ntot = nch * part_stride;
     for (uint32_t o = 0; o < ntot; o += kPartRound)
-        if (!ll_gather<kPartRound / kMkThreads>(g_mk.x_part + o, min(kPartRound, ntot - o), tB, parts + o)) return false;
+        if (!ll_gather<kPartRound / kMkThreads>(g_mk.x_part + o, min(kPartRound, ntot - o), tB, parts + o,
+                                                 (o / kPartRound) & 1u ? kAnyGather1 : kAnyGather0))
+            return false;
     MK_MARK(12);
     float* wts = m.mw;   // [8][kMaxChunks] weights, then den [8]
     if (tid < H) {
@@ -781,7 +984,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
 
 // Phase D: h = RMSNorm(o, post_attn) + h, x = RMSNorm(h, ffn_norm), gate/up row pairs,
 // g = gelu_tanh(gate) * up (src/gemma3.cpp:1703-1801, shaders/gelu_mul.comp:23-31).
-template <int SD>
+template <int SD, int EP>
 __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
@@ -791,9 +994,6 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     MK_TAGS(l);
     const MkLayer& Ly = g_mk_layers[l];
     MK_MARK(15);
-    float wpa[kVec], wffn[kVec], hv[kVec], o[kVec];
-    vec_load(Ly.post_attn, d, wpa);
-    vec_load(Ly.ffn_norm, d, wffn);
     uint32_t p0 = 0, p1 = 0;
     const uint32_t nprod = g_mk.nwg - n_bunits(Ly.slots, pos);
     if (w < nprod) split_range(F, nprod, w, p0, p1);
@@ -802,32 +1002,13 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     auto rowp = [=](uint32_t v) { return ((v & 1u) ? wu : wg) + static_cast<uint64_t>(v >> 1) * rb_d; };
     RowBatch<SD, 1, 2> rb;
     batch_load<SD, 1, 2>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = tid + k * kMkThreads;
-        hv[k] = i < d ? m.h[i] : 0.0f;
-    }
-    int fail = ll_wait<kVec>(g_mk.x_o, d, tC, o);
-    MK_MARK(16);
-    const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(o, d), fail), d, g_mk.eps);
-    MK_MARK(28);   // every wave has its inputs
-    if (fail) return false;
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) hv[k] = o[k] * (sc * wpa[k]) + hv[k];      // :1703-1711
     int none = 0;
-    const float sc2 = mk_rms_scale(blk_sum(R, vec_sumsq(hv, d), none), d, g_mk.eps);
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = tid + k * kMkThreads;
-        if (i < d) {
-            m.h[i] = hv[k];
-            m.xs[i] = hv[k] * sc2 * wffn[k];                                         // :1713-1718
-        }
-    }
-    __syncthreads();
+    if (mk_resid<EP, true>(g_mk.x_o, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps, none, m.nwd0,
+                           m.nwd1, m.yd, kAnyD))
+        return false;
     MK_MARK(17);
     float* gu = m.gu;
-    batch_consume_x<SD, 1, 2>(rb, nblk_d, m.xs, [&](uint32_t v, float val) { gu[v - v0] = val; });
+    batch_consume_x<SD, 1, 2>(rb, nblk_d, m.xd, [&](uint32_t v, float val) { gu[v - v0] = val; });
     __syncthreads();
     MK_MARK(18);
     u64* out = g_mk.x_g;
@@ -856,7 +1037,7 @@ __device__ __attribute__((noinline)) bool mk_phase_e(uint32_t l, uint32_t tagb, 
     auto rowp = [=](uint32_t v) { return wd + static_cast<uint64_t>(v) * rb_f; };
     RowBatch<SF, 1, 1> rb;
     batch_load<SF, 1, 1>(rowp, nblk_f, g_mk.arena_end, v0, v1, wave, rb);
-    if (!ll_gather<kVec>(g_mk.x_g, F, tD, m.xs)) return false;
+    if (!ll_gather<kVec>(g_mk.x_g, F, tD, m.xs, kAnyGatherE)) return false;
     MK_MARK(21);
     u64* out = g_mk.x_f;
     batch_consume_x<SF, 1, 1>(rb, nblk_f, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tE); });
@@ -868,47 +1049,26 @@ __device__ __attribute__((noinline)) bool mk_phase_e(uint32_t l, uint32_t tagb, 
 // the normed hidden state goes to xs (LM head input) and, from workgroup 0, to g_mk.hidden.
 // Final residual (the last block's FFN output, post-FFW norm) and output norm into m.xs
 // (src/gemma3.cpp:1849-1868); workgroup 0 also writes the hidden state.
+template <int EP>
 __device__ __forceinline__ bool mk_fold(uint32_t tagb) {
-#pragma clang fp contract(off)
     MK_LOCALS;
     MK_UNIFORM(tagb);
-    float wpost[kVec], wout[kVec], hv[kVec], f[kVec];
-    vec_load(g_mk_layers[L - 1u].post_ffw, d, wpost);
-    vec_load(g_mk.out_norm, d, wout);
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = tid + k * kMkThreads;
-        hv[k] = i < d ? m.h[i] : 0.0f;
-    }
-    int fail = ll_wait<kVec>(g_mk.x_f, d, tagb + 5u * (L - 1u) + 5u, f);
-    const float sc = mk_rms_scale(blk_sum(R, vec_sumsq(f, d), fail), d, g_mk.eps);
-    if (fail) return false;
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) hv[k] = f[k] * (sc * wpost[k]) + hv[k];
-    int bad = vec_nonfinite(hv, d);
-    const float sc3 = mk_rms_scale(blk_sum(R, vec_sumsq(hv, d), bad), d, g_mk.eps);
+    int bad = 0;
+    if (mk_resid<EP, false>(g_mk.x_f, tagb + 5u * (L - 1u) + 5u, g_mk_layers[L - 1u].post_ffw, g_mk.out_norm, m.h, m.xa,
+                            w == 0 ? g_mk.hidden : nullptr, d, g_mk.eps, bad, m.nwa0, m.nwa1, m.ya, kAnyFold))
+        return false;
     if (bad && w == 0 && tid == 0) mk_flag_min(L - 1u);
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = tid + k * kMkThreads;
-        if (i < d) {
-            const float hn = hv[k] * (sc3 * wout[k]);
-            m.h[i] = hv[k];
-            m.xs[i] = hn;
-            if (w == 0) gp(g_mk.hidden)[i] = hn;
-        }
-    }
-    __syncthreads();
     return true;
 }
 
+template <int EP>
 __device__ __attribute__((noinline)) bool mk_phase_fold(uint32_t tagb) {
     MK_UNIFORM(tagb);
-    return mk_fold(tagb);
+    return mk_fold<EP>(tagb);
 }
 
 // Tied Q8_0 LM head over this workgroup's rows, local greedy argmax published with tag tLM.
-template <int SD>
+template <int SD, int EP>
 __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tLM, uint32_t want_logits, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
@@ -928,9 +1088,9 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
         pre[i] = n16[i] = 0u;
         if (i < ntiles) lm_tile_load(r_begin + i * TR, min(r_end, r_begin + (i + 1u) * TR), rb_d, tl[i], pre[i], n16[i]);
     }
-    if (!mk_fold(tagb)) return false;
+    if (!mk_fold<EP>(tagb)) return false;
     MK_MARK(23);
-    build_limbs(m.xs, d, m.L);
+    build_limbs(m.xa, d, m.L);
     XLimb xl[1];
     lane_limbs<SD, 1>(m.L, nblk_d, xl);
     MK_MARK(24);
@@ -1009,7 +1169,7 @@ __device__ __attribute__((noinline)) MkArg mk_reduce_argmax(uint32_t tag) {
     __shared__ float s_v[kMkWaves];
     __shared__ uint32_t s_i[kMkWaves];
     float* buf = m.sc;   // 2 * nwg floats
-    const bool good = ll_gather<2>(g_mk.x_am, 2u * g_mk.nwg, tag, buf);
+    const bool good = ll_gather<2>(g_mk.x_am, 2u * g_mk.nwg, tag, buf, kAnyArgmax);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (uint32_t k = tid; k < g_mk.nwg; k += kMkThreads) {
@@ -1028,21 +1188,26 @@ __device__ __attribute__((noinline)) MkArg mk_reduce_argmax(uint32_t tag) {
     return MkArg{bi, bv, good};
 }
 
-// The step embedding: dequantised row * sqrt(d) (src/gemma3.cpp:1106-1136), this thread's
-// elements of h.
+// The step embedding: dequantised row * sqrt(d) (src/gemma3.cpp:1106-1136), written to h by
+// wave 0 in its pair layout.
 __device__ __attribute__((noinline)) void mk_embed(uint32_t token) {
 #pragma clang fp contract(off)
     MK_LOCALS;
     MK_UNIFORM(token);
+    if (__builtin_amdgcn_readfirstlane(wave) != 0u) return;   // h belongs to wave 0
     const VRT_AS_GLOBAL uint8_t* row = gp(g_mk.tok_embd) + static_cast<uint64_t>(token) * rb_d;
-    for (uint32_t i = tid; i < d; i += kMkThreads) {
+    for (uint32_t j = lane; 2u * j < d; j += 64u) {
+        const uint32_t i = 2u * j;
         const VRT_AS_GLOBAL uint8_t* b = row + (i >> 5) * 34u;
         const float sc = half_bits_to_float(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
-        m.h[i] = (sc * static_cast<float>(static_cast<int8_t>(b[2 + (i & 31u)]))) * g_mk.emb_scale;
+        float2 v;
+        v.x = (sc * static_cast<float>(static_cast<int8_t>(b[2 + (i & 31u)]))) * g_mk.emb_scale;
+        v.y = (sc * static_cast<float>(static_cast<int8_t>(b[3 + (i & 31u)]))) * g_mk.emb_scale;
+        reinterpret_cast<float2*>(m.h)[j] = v;
     }
 }
 
-template <int SD, int SA, int SF>
+template <int SD, int SA, int SF, int EP>
 __global__ void __launch_bounds__(kMkThreads, 1)
 k_decode(uint32_t nsteps, uint32_t tag0) {
     const uint32_t w = blockIdx.x;
@@ -1100,7 +1265,7 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
 
         for (uint32_t l = 0; l < L && ok; ++l) {
             const bool tr = g_mk.trace_slots != 0u && si == 0u && l == 1u;   // sub-phase marks of block 1
-            ok = mk_phase_a<SD>(l, s, tagb, tr);
+            ok = mk_phase_a<SD, EP>(l, s, tagb, tr);
             MK_TRACE(5u * l + 1u);
             // B, C and E run on a subset of the workgroups; the others skip the call (and its
             // register save/restore through scratch) entirely
@@ -1108,18 +1273,18 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             MK_TRACE(5u * l + 2u);
             ok = ok && (w >= g_mk.nc || mk_phase_c<SA>(l, s, tagb, tr));
             MK_TRACE(5u * l + 3u);
-            ok = ok && mk_phase_d<SD>(l, s, tagb, tr);
+            ok = ok && mk_phase_d<SD, EP>(l, s, tagb, tr);
             MK_TRACE(5u * l + 4u);
             ok = ok && (w >= g_mk.ne || mk_phase_e<SF>(l, tagb, tr));
             MK_TRACE(5u * l + 5u);
         }
         if (s >= lm_from) {   // final norm, LM head + local argmax (src/gemma3.cpp:1138-1185)
             MK_TRACE(5u * L + 1u);
-            ok = ok && mk_phase_lm<SD>(tagb, tagb + nph, want_logits, g_mk.trace_slots != 0u && si == 0u);
+            ok = ok && mk_phase_lm<SD, EP>(tagb, tagb + nph, want_logits, g_mk.trace_slots != 0u && si == 0u);
             if (!ok) break;
             prev_lm_tag = tagb + nph;
         } else {
-            ok = ok && mk_phase_fold(tagb);
+            ok = ok && mk_phase_fold<EP>(tagb);
             if (!ok) break;
             MK_TRACE(5u * L + 1u);
         }
@@ -1182,16 +1347,20 @@ static MkDeviceSlot* device_slots() {
     return s;
 }
 
-template <int SD, int SA, int SF>
-static const void* mk_fn() { return reinterpret_cast<const void*>(&k_decode<SD, SA, SF>); }
+template <int SD, int SA, int SF, int EP>
+static const void* mk_fn() { return reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP>); }
 
-static const void* mk_pick(int sd, int sa, int sf) {
-#define VRT_MK(a, b, c) if (sd == a && sa == b && sf == c) return mk_fn<a, b, c>();
-    VRT_MK(32, 32, 64)   // Gemma-3-270M: d 640, 4 x 256 heads, FFN 2048
-    VRT_MK(4, 4, 8)      // d 128, 2 x 64 heads, FFN 256 (test shape)
-    VRT_MK(32, 64, 64)
-    VRT_MK(16, 16, 32)
-    VRT_MK(8, 8, 16)
+// Row-slot widths of the three matvec input lengths (d, H * head_dim, FFN) and the residual
+// pairs per lane, ep = ceil(d / 128); the smallest instantiated EP >= ep is taken.
+static const void* mk_pick(int sd, int sa, int sf, int ep) {
+#define VRT_MK(a, b, c, e) if (sd == a && sa == b && sf == c && ep <= e) return mk_fn<a, b, c, e>();
+    VRT_MK(32, 32, 64, 5)   // Gemma-3-270M: d 640, 4 x 256 heads, FFN 2048
+    VRT_MK(32, 32, 64, 8)
+    VRT_MK(4, 4, 8, 1)      // d 128, 2 x 64 heads, FFN 256 (test shape)
+    VRT_MK(32, 64, 64, 5)
+    VRT_MK(32, 64, 64, 8)
+    VRT_MK(16, 16, 32, 4)
+    VRT_MK(8, 8, 16, 2)
 #undef VRT_MK
     return nullptr;
 }
@@ -1232,7 +1401,7 @@ int mk_setup(vrt_g3* g) {
         return VRT_OK;
     MvShape sd, sa, sf;
     if (!mv_shape(d, &sd) || !mv_shape(qw, &sa) || !mv_shape(F, &sf) || sd.NB != 1 || sa.NB != 1 || sf.NB != 1) return VRT_OK;
-    const void* fn = mk_pick(sd.S, sa.S, sf.S);
+    const void* fn = mk_pick(sd.S, sa.S, sf.S, static_cast<int>((d + 127u) / 128u));
     if (!fn) return VRT_OK;
     int coop = 0;
     VRT_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, g->ctx->device));
@@ -1278,6 +1447,15 @@ int mk_setup(vrt_g3* g) {
     auto take = [&](uint32_t bytes) { const uint32_t o = off; off += (bytes + 15u) & ~15u; return o; };
     P.lds.h = take(d * 4u);
     P.lds.xs = take(kmax * 4u);
+    P.lds.xa = take(d * 4u);
+    P.lds.xd = take(d * 4u);
+    P.lds.ya = take(d * 4u);
+    P.lds.yd = take(d * 4u);
+    P.lds.nwa0 = take((d + 255u) / 256u * 1024u);   // whole 1 KB rows of the staging loads
+    P.lds.nwa1 = take((d + 255u) / 256u * 1024u);
+    P.lds.nwd0 = take((d + 255u) / 256u * 1024u);
+    P.lds.nwd1 = take((d + 255u) / 256u * 1024u);
+    P.lds.any = take(kAnySets * kMkWaves * 4u);
     P.lds.la = take(d);
     P.lds.lb = take(d);
     P.lds.lc = take(d);
