@@ -25,6 +25,7 @@ namespace vrt {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kPfThreads = 256;
 constexpr uint32_t kPfTile = 64;     // attention score rows are padded to a multiple of this
@@ -65,13 +66,15 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_embed(const uint8_t* tok_embd
     }
 }
 
-// One row t per workgroup (n <= 8 * kPfThreads). With f (the previous sublayer's output):
-// h = (f * scale(f)) * w_post + h (src/gemma3.cpp:1703-1711, :1849-1855). Then, with w_next:
+// One row t per workgroup (n <= 8 * kPfThreads). With f (the previous sublayer's output, the
+// sum of nsplit partial rows f + s * sstride added in order s = 0, 1, ...):
+// h = f * (scale(f) * w_post) + h (rms_norm_inplace then add_inplace, src/gemma3.cpp:1036-1042,
+// :1703-1711, :1849-1855). Then, with w_next:
 // the GEMM input (h * scale(h)) * w_next as f16 hi/lo (:991-996). nonfinite: lowest block
 // whose residual went non-finite (:1857-1863), reported through st->nonfinite.
-__global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f, const float* w_post,
-                                                        const float* w_next, uint32_t n, float eps, _Float16* xhi,
-                                                        _Float16* xlo, G3State* st, uint32_t block) {
+__global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f, uint32_t nsplit, uint64_t sstride,
+                                                        const float* w_post, const float* w_next, uint32_t n, float eps,
+                                                        _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block) {
 #pragma clang fp contract(off)
     __shared__ double red[4];
     const uint32_t t = blockIdx.x;
@@ -89,7 +92,9 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t i = threadIdx.x + k * kPfThreads;
-            fv[k] = i < n ? fr[i] : 0.0f;
+            fv[k] = 0.0f;
+            if (i < n)
+                for (uint32_t q = 0; q < nsplit; ++q) fv[k] += fr[q * sstride + i];
             ss += static_cast<double>(fv[k]) * static_cast<double>(fv[k]);
         }
         const float sc = pf_rms_scale(pf_sum(ss, red), n, eps);
@@ -98,7 +103,7 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
         for (int k = 0; k < 8; ++k) {
             const uint32_t i = threadIdx.x + k * kPfThreads;
             if (i < n) {
-                hv[k] = (fv[k] * sc) * w_post[i] + hv[k];
+                hv[k] = fv[k] * (sc * w_post[i]) + hv[k];
                 hr[i] = hv[k];
                 bad |= !__builtin_isfinite(hv[k]);
             }
@@ -345,6 +350,196 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_gemm(PfGemm G) {
     }
 }
 
+// ---- Q8_0 weight GEMM, LDS-tiled ------------------------------------------------------------
+//
+// C[M][N] = A[M][K] (f16 hi/lo) x W^T with W the Q8_0 rows (segments concatenated along N).
+// Workgroup tile: 64 rows of A x 64 * WN rows of W; wave w computes rows 32 (w / 2) and the
+// WN 32-column MFMA tiles from 32 WN (w % 2). K advances 64 (two Q8_0 blocks) per step through
+// two LDS stages: A as f16 hi and lo [64][64], W as its exact int8 quants in f16 [64 WN][64]
+// plus the fp32 block scales; one barrier per step hands a stage over. Per Q8_0 block and tile the
+// two f16 MFMA chains (A hi, A lo) accumulate the exact products in fp32 and the block's partial
+// is scaled by the column's scale into the fp32 accumulator, as in k_pf_gemm. blockIdx.z splits
+// K: split z covers K blocks [z nkb / S, (z + 1) nkb / S) and writes C + z * c_bs; the consumer
+// adds the S partial tiles in split order.
+constexpr uint32_t kQgBM = 64;
+constexpr uint32_t kQgBK = 64;
+constexpr uint32_t kQgPitch = kQgBK * 2u + 16u;   // LDS row pitch in bytes (f16 rows, padded)
+
+constexpr uint32_t kQgDepth = 5;   // K steps loaded together into registers
+
+template <int WN, int NWN>
+__global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
+    constexpr uint32_t NT = 128u * NWN;          // threads: 2 x NWN waves
+    constexpr uint32_t BN = 32u * WN * NWN;      // W rows per tile
+    constexpr uint32_t AU = 2u * kQgBM * 8u / NT / 2u;   // A 16-byte units per thread and array
+    __shared__ __align__(16) unsigned char s_a[2][2][kQgBM * kQgPitch];   // [stage][hi, lo]
+    __shared__ __align__(16) unsigned char s_w[2][BN * kQgPitch];          // [stage] quants
+    __shared__ float s_sc[2][BN][2];                                       // [stage][row][block]
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t kh = lane >> 5, l32 = lane & 31u;
+    const uint32_t m0 = blockIdx.y * kQgBM, n0 = blockIdx.x * BN;
+    const uint32_t nkb = G.K >> 5;                                         // Q8_0 blocks along K
+    const uint32_t S = gridDim.z, z = blockIdx.z;
+    const uint32_t kb_lo = nkb * z / S, kb_hi = nkb * (z + 1u) / S;
+    const uint32_t nsteps = (kb_hi - kb_lo + 1u) / 2u;
+    const uint64_t row_bytes = static_cast<uint64_t>(nkb) * 34u;
+
+    // One K step in registers: A units u = 2t, 2t + 1 of hi and of lo (row u / 8, k 8 (u % 8)
+    // .. + 7 of the step), and the 34-byte W block of thread t < 2 BN (row t / 2, block t % 2).
+    struct Stage {
+        v4u a[2][AU];  // [hi, lo][unit]
+        uint32_t d[8]; // dwords at the block start rounded down to 4 bytes
+        uint32_t u0;   // 16 bits at that start + 32, 16 bits at the block start + 32
+        uint32_t u1;
+        uint32_t sh;   // block start & 3 (0 or 2)
+        bool wl;       // W block live
+    };
+    typedef const __attribute__((address_space(1))) v4u* gv4;
+    const uint32_t wr = tid >> 1, wb = tid & 1u;
+    static_assert(2u * BN <= NT, "one W block per thread");
+    const bool wlive_t = tid < 2u * BN && n0 + wr < G.N;
+    const uint8_t* wrow = G.w[0];
+    {
+        uint32_t r = wlive_t ? n0 + wr : 0u;
+        if (G.nseg > 1u && r >= G.rows[0]) {
+            r -= G.rows[0];
+            wrow = G.w[1];
+            if (G.nseg > 2u && r >= G.rows[1]) {
+                r -= G.rows[1];
+                wrow = G.w[2];
+            }
+        }
+        wrow += static_cast<uint64_t>(r) * row_bytes;
+    }
+    // Every load is issued unconditionally at a clamped, in-bounds address (dead data is zeroed
+    // when it is stored): with no branch around a load the compiler counts the loads in flight
+    // exactly, so the wait for step j's data does not also wait for the later steps of the ring.
+    typedef const __attribute__((address_space(1))) uint32_t* gu32;
+    typedef const __attribute__((address_space(1))) uint16_t* gu16;
+    auto load = [&](uint32_t step, Stage& R) {
+        const uint32_t kb = kb_lo + 2u * step;
+#pragma unroll
+        for (uint32_t j = 0; j < AU; ++j) {
+            const uint32_t u = AU * tid + j, r = u >> 3, c = u & 7u;
+            const uint32_t k = 32u * kb + 8u * c;
+            const uint32_t rr = min(m0 + r, G.M - 1u), kk = min(k, 32u * kb_hi - 8u);
+            const uint64_t o = (static_cast<uint64_t>(rr) * G.lda + kk) * 2u;
+            R.a[0][j] = *reinterpret_cast<gv4>(reinterpret_cast<uintptr_t>(G.ahi) + o);
+            R.a[1][j] = *reinterpret_cast<gv4>(reinterpret_cast<uintptr_t>(G.alo) + o);
+        }
+        const uint32_t b = kb + wb;
+        R.wl = wlive_t && b < kb_hi;
+        // the block's 34 bytes: 8 dwords from its start rounded down (2 bytes before it when the
+        // start is 2 mod 4), then the 16 bits at that start + 32 and at the block start + 32; no
+        // byte past the block is read
+        const uintptr_t base = reinterpret_cast<uintptr_t>(wrow) + 34u * min(b, kb_hi - 1u);
+        const uintptr_t lb = base & ~uintptr_t(3);
+        R.sh = static_cast<uint32_t>(base & 3u);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) R.d[j] = reinterpret_cast<gu32>(lb)[j];
+        R.u0 = *reinterpret_cast<gu16>(lb + 32u);
+        R.u1 = *reinterpret_cast<gu16>(base + 32u);
+    };
+    auto store = [&](const Stage& R, uint32_t st, uint32_t step) {
+        const uint32_t kb = kb_lo + 2u * step;
+#pragma unroll
+        for (uint32_t j = 0; j < AU; ++j) {
+            const uint32_t u = AU * tid + j, r = u >> 3, c = u & 7u;
+            const bool live = m0 + r < G.M && 32u * kb + 8u * c < 32u * kb_hi;
+#pragma unroll
+            for (uint32_t p = 0; p < 2; ++p)
+                *reinterpret_cast<v4u*>(&s_a[st][p][r * kQgPitch + c * 16u]) = live ? R.a[p][j] : v4u{0u, 0u, 0u, 0u};
+        }
+        if (tid >= 2u * BN) return;
+        // quants at window offset sh + 2: shift 2 (sh == 0) or whole dwords from d[1] (sh == 2)
+        const uint32_t d8 = R.sh ? (R.u0 | (R.u1 << 16)) : R.u0;
+        uint32_t q[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t hi = j < 7 ? R.d[j + 1] : d8;
+            q[j] = R.wl ? (R.sh ? hi : __builtin_amdgcn_alignbyte(hi, R.d[j], 2u)) : 0u;
+        }
+        unsigned char* dst = &s_w[st][wr * kQgPitch + wb * 64u];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {   // 8 quants (two dwords) -> 8 f16 per 16-byte store
+            half8 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(q[2 * j] >> (8 * i))));
+                v[4 + i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(q[2 * j + 1] >> (8 * i))));
+            }
+            *reinterpret_cast<half8*>(dst + 16u * j) = v;
+        }
+        s_sc[st][wr][wb] = R.wl ? half_bits_to_float(R.sh ? (R.d[0] >> 16) : (R.d[0] & 0xffffu)) : 0.0f;
+    };
+
+    const uint32_t wm = wave / NWN, wn = wave % NWN;
+    float16v acc[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[j] = float16v{};
+    auto compute = [&](uint32_t st) {
+        const unsigned char* pa_hi = &s_a[st][0][(32u * wm + l32) * kQgPitch + 16u * kh];
+        const unsigned char* pa_lo = &s_a[st][1][(32u * wm + l32) * kQgPitch + 16u * kh];
+#pragma unroll
+        for (uint32_t b = 0; b < 2; ++b) {   // the step's two Q8_0 blocks
+            half8 ah[2], al[2];
+#pragma unroll
+            for (uint32_t ks = 0; ks < 2; ++ks) {
+                ah[ks] = *reinterpret_cast<const half8*>(pa_hi + 64u * b + 32u * ks);
+                al[ks] = *reinterpret_cast<const half8*>(pa_lo + 64u * b + 32u * ks);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const uint32_t nl = 32u * (WN * wn + j) + l32;   // the lane's column in the tile
+                const unsigned char* pw = &s_w[st][nl * kQgPitch + 64u * b + 16u * kh];
+                const half8 w0 = *reinterpret_cast<const half8*>(pw), w1 = *reinterpret_cast<const half8*>(pw + 32u);
+                float16v p = {};
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], w0, p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0], w0, p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], w1, p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1], w1, p, 0, 0, 0);
+                const float sc = s_sc[st][nl][b];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[j][r] += sc * p[r];
+            }
+        }
+    };
+
+    // kQgDepth steps are loaded into registers together, then stored to the two LDS stages in
+    // turn (one barrier per step): the later steps' loads overlap the earlier steps' MFMAs. The
+    // loads are consumed in the loop iteration that issues them, so the compiler waits for
+    // exactly the step it stores (a value carried across the back edge would make it wait for
+    // every load in flight).
+    Stage R[kQgDepth];
+    for (uint32_t i = 0; i < nsteps; i += kQgDepth) {
+#pragma unroll
+        for (uint32_t u = 0; u < kQgDepth; ++u)
+            if (i + u < nsteps) load(i + u, R[u]);
+#pragma unroll
+        for (uint32_t u = 0; u < kQgDepth; ++u) {
+            const uint32_t j = i + u;
+            if (j < nsteps) {
+                // stage j & 1 was last read by step j - 2, which every wave finished before the
+                // barrier of step j - 1
+                store(R[u], j & 1u, j);
+                __syncthreads();
+                compute(j & 1u);
+            }
+        }
+    }
+    float* c = G.c + static_cast<uint64_t>(z) * G.c_bs;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        const uint32_t col = n0 + 32u * (WN * wn + j) + l32;
+        if (col >= G.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = m0 + 32u * wm + 8u * (r / 4) + 4u * kh + (r % 4);
+            if (row < G.M) c[static_cast<uint64_t>(row) * G.ldc + col] = acc[j][r];
+        }
+    }
+}
+
 // Masked softmax of score row (head z, query t): keys j of [max(0, t + 1 - window), t]
 // (window 0: all j <= t), p_j = exp(scale * s_j - max) / sum, the sum in double
 // (src/gemma3.cpp:1602-1696); p as f16 hi/lo over the row's first ceil((t + 1) / 64) * 64
@@ -446,9 +641,22 @@ static int pf_launch(const PfGemm& G, uint32_t batch, hipStream_t s) {
     return VRT_OK;
 }
 
-// C[M][N] = A[M][K] (f16 hi/lo) x W^T, W = Q8_0 matrices concatenated along N.
+template <int WN, int NWN>
+static int pf_launch_q8(const PfGemm& G, uint32_t splits, hipStream_t s) {
+    constexpr uint32_t BN = 32u * WN * NWN;
+    const dim3 grid((G.N + BN - 1u) / BN, (G.M + kQgBM - 1u) / kQgBM, splits);
+    PfGemm arg = G;
+    void* args[] = {&arg};
+    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_gemm_q8<WN, NWN>), grid, dim3(128u * NWN), args,
+                                  0, s));
+    return VRT_OK;
+}
+
+// C[M][N] = A[M][K] (f16 hi/lo) x W^T, W = Q8_0 matrices concatenated along N. With splits > 1
+// the K blocks are split and C holds the partial products C + z * M * N, z < splits.
 static int pf_gemm(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t M, uint32_t K,
-                   std::initializer_list<std::pair<const uint8_t*, uint32_t>> segs, float* c, hipStream_t s) {
+                   std::initializer_list<std::pair<const uint8_t*, uint32_t>> segs, float* c, uint32_t splits,
+                   hipStream_t s) {
     PfGemm G{};
     G.ahi = ahi;
     G.alo = alo;
@@ -464,10 +672,21 @@ static int pf_gemm(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t
     G.M = M;
     G.K = K;
     if (K % 32u != 0u || G.N % 32u != 0u) return set_error(VRT_ERR_INVALID, "prefill GEMM shape not supported");
-    return pf_launch<0>(G, 1, s);
+    G.c_bs = static_cast<uint64_t>(M) * G.N;
+    splits = std::max(1u, std::min(splits, (K / 32u) / 2u));
+    const uint32_t mt = (M + kQgBM - 1u) / kQgBM;
+    if (G.N % 128u == 0u && (G.N / 128u) * mt >= 128u) return pf_launch_q8<1, 4>(G, splits, s);
+    return pf_launch_q8<1, 2>(G, splits, s);
+}
+
+// K splits of the 640-row projections (O and down): enough workgroups to cover the CUs.
+static uint32_t pf_splits(uint32_t M, uint32_t N) {
+    const uint32_t tiles = ((M + kQgBM - 1u) / kQgBM) * ((N + 63u) / 64u);
+    return std::min(4u, std::max(1u, 256u / std::max(1u, tiles)));
 }
 
 static uint32_t pf_pad(uint32_t T) { return (T + kPfTile - 1u) / kPfTile * kPfTile; }
+constexpr uint32_t kPfMaxSplits = 4;   // K splits of the O and down projections (pf_splits)
 
 int pf_setup(vrt_g3* g, uint32_t max_t) {
     const uint32_t d = g->cfg.embedding_length, H = g->cfg.head_count, hd = g->cfg.head_dim;
@@ -485,7 +704,7 @@ int pf_setup(vrt_g3* g, uint32_t max_t) {
     void* q;
     if (int rc = take(static_cast<size_t>(max_t) * d * 4u, &q)) return rc;
     p.h = static_cast<float*>(q);
-    if (int rc = take(static_cast<size_t>(max_t) * d * 4u, &q)) return rc;
+    if (int rc = take(static_cast<size_t>(max_t) * d * 4u * kPfMaxSplits, &q)) return rc;
     p.x = static_cast<float*>(q);
     if (int rc = take(static_cast<size_t>(max_t) * kmax * 2u, &q)) return rc;
     p.ahi = q;
@@ -595,6 +814,9 @@ int pf_run(vrt_g3* g, uint32_t T) {
         void* args[] = {&te, &tok, &d, &es, &h};
         if (int rc = launch(reinterpret_cast<const void*>(&k_pf_embed), dim3(T), args)) return rc;
     }
+    const uint32_t s_o = pf_splits(T, d);        // split partials of the O and down projections
+    uint64_t xs = static_cast<uint64_t>(T) * d;  // one partial [T][d]
+    uint32_t s_down = 1;                         // splits of the previous block's down projection
     for (uint32_t l = 0; l < L; ++l) {
         const LayerParams& Ly = g->layers[l];
         {   // previous block's FFN output into the residual, then the attention norm
@@ -602,10 +824,10 @@ int pf_run(vrt_g3* g, uint32_t T) {
             const float* wpost = l ? g->layers[l - 1].post_ffw : nullptr;
             const float* wnext = Ly.attn_norm;
             uint32_t blk = l ? l - 1u : 0u;
-            void* args[] = {&h, &f, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
+            void* args[] = {&h, &f, &s_down, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
             if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }
-        if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, big, s)) return rc;
+        if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, big, 1, s)) return rc;
         {
             const float* qn = Ly.q_norm;
             const float* kn = Ly.k_norm;
@@ -619,22 +841,26 @@ int pf_run(vrt_g3* g, uint32_t T) {
         }
         // q (hi/lo in ahi/alo) is consumed by S = Q K^T before O = P V overwrites ahi/alo
         if (int rc = pf_attention(g, Ly, T, big, ahi, alo, ahi, alo, s)) return rc;
-        if (int rc = pf_gemm(g, ahi, alo, T, qw, {{Ly.wo, d}}, x, s)) return rc;
+        uint32_t so = s_o;
+        if (int rc = pf_gemm(g, ahi, alo, T, qw, {{Ly.wo, d}}, x, so, s)) return rc;
+        so = std::max(1u, std::min(so, (qw / 32u) / 2u));
         {   // attention output into the residual, then the FFN norm
             const float* f = x;
             const float* wpost = Ly.post_attn;
             const float* wnext = Ly.ffn_norm;
             uint32_t blk = l;
-            void* args[] = {&h, &f, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
+            void* args[] = {&h, &f, &so, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
             if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }
-        if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wg, F}, {Ly.wu, F}}, big, s)) return rc;
+        if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wg, F}, {Ly.wu, F}}, big, 1, s)) return rc;
         {
             const float* gu = big;
             void* args[] = {&gu, &F, &ahi, &alo};
             if (int rc = launch(reinterpret_cast<const void*>(&k_pf_gelu), dim3(T), args)) return rc;
         }
-        if (int rc = pf_gemm(g, ahi, alo, T, F, {{Ly.wd, d}}, x, s)) return rc;
+        // the last block's output row feeds the LM head directly: no split partials there
+        s_down = l + 1u < L ? std::max(1u, std::min(s_o, (F / 32u) / 2u)) : 1u;
+        if (int rc = pf_gemm(g, ahi, alo, T, F, {{Ly.wd, d}}, x, s_down, s)) return rc;
     }
     // last position: its FFN output and residual feed the decode step's final norm + LM head
     VRT_HIP_CHECK(hipMemcpyAsync(P.f, x + static_cast<uint64_t>(T - 1u) * d, d * 4u, hipMemcpyDeviceToDevice, s));
