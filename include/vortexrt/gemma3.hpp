@@ -5,6 +5,7 @@
 #include "vortexrt/argmax.hpp"
 #include "vortexrt/gguf.hpp"
 #include "vortexrt/q8_matvec.hpp"
+#include "vortexrt/tokenizer.hpp"
 
 #include <cstddef>
 #include <cstdint>
@@ -82,7 +83,8 @@ public:
     [[nodiscard]] Gemma3SingleTokenResult decode_token(std::uint32_t token_id, std::uint32_t position,
                                                        std::size_t top_k = 1);
 
-    // Text tokenisation is not part of this build: throws std::runtime_error.
+    // Whitespace-normalised highest-scoring segmentation into vocabulary pieces, BOS first
+    // when add_bos (src/gemma3.cpp:1920-2062); see Gemma3Tokenizer.
     [[nodiscard]] std::vector<std::uint32_t> tokenize(const std::string& text, bool add_bos = true) const;
     [[nodiscard]] Gemma3GenerationResult generate_greedy(const std::string& prompt, std::size_t max_new_tokens);
 
@@ -105,7 +107,7 @@ private:
     bool fuse_projections_ = true;
     std::unique_ptr<Buffer> weights_arena_;
     vrt_g3* g3_ = nullptr;
-    const GgufValue* tokenizer_tokens_ = nullptr;
+    std::unique_ptr<Gemma3Tokenizer> tokenizer_;
     std::uint32_t tokenizer_bos_id_ = 2;
     std::uint32_t tokenizer_eos_id_ = 1;
 };

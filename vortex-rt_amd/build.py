@@ -2,6 +2,7 @@
 
   _build/libvrt_hip.so   HIP kernels + the C ABI declared in include/vrt_hip.h
   _build/libvortexrt.so  the vortexrt:: C++ surface (include/vortexrt/*.hpp) over the C ABI
+  _build/vortexrt-gemma  the Gemma 3 command line (csrc/cli/gemma_main.cpp) over libvortexrt.so
 
 Every HIP source is compiled for gfx950 with packed-fp32 instruction selection disabled.
 Only the vrt_* symbols are exported from libvrt_hip.so.
@@ -71,6 +72,21 @@ def build_cpp() -> str:
     return LIB_CPP
 
 
+CLI = {"gemma_main.cpp": "vortexrt-gemma"}   # command-line programs: source -> executable
+
+
+def build_cli() -> list:
+    """The command-line programs of csrc/cli, linked against libvortexrt.so (rpath $ORIGIN)."""
+    out = []
+    for src, exe in CLI.items():
+        path = os.path.join(OUT, exe)
+        _run(["g++"] + CXX_FLAGS + ["-o", path + ".tmp", os.path.join(CSRC, "cli", src), "-L" + OUT, "-lvortexrt",
+                                    "-lvrt_hip", "-Wl,-rpath,$ORIGIN"])
+        os.replace(path + ".tmp", path)
+        out.append(path)
+    return out
+
+
 CPP_TESTS = os.path.join(REPO, "tests", "cpp")
 
 
@@ -95,6 +111,7 @@ def build_cpp_tests(jobs: int = 8) -> list:
 def build_all(jobs: int = 8):
     build_hip(jobs)
     build_cpp()
+    build_cli()
     build_cpp_tests(jobs)
 
 

@@ -68,13 +68,10 @@ Gemma3Model::Gemma3Model(const std::string& gguf_path, DeviceContext& context, c
         throw std::runtime_error("Unsupported token_embd.weight layout");
     config_.vocab_size = static_cast<std::uint32_t>(emb.dimensions[1]);
 
-    if (const auto* toks = gguf_.find_metadata("tokenizer.ggml.tokens"); toks && toks->is_array())
-        tokenizer_tokens_ = toks;
-    const auto bos = gguf_.metadata_u64("tokenizer.ggml.bos_token_id").value_or(2);
-    if (bos >= config_.vocab_size) throw std::runtime_error("Gemma 3 BOS token id is out of range");
-    tokenizer_bos_id_ = static_cast<std::uint32_t>(bos);
-    const auto eos = gguf_.metadata_u64("tokenizer.ggml.eos_token_id").value_or(1);
-    tokenizer_eos_id_ = static_cast<std::uint32_t>(std::min<std::uint64_t>(eos, std::numeric_limits<std::uint32_t>::max()));
+    // the tokenizer index (src/gemma3.cpp:289-454): incomplete metadata fails the load
+    tokenizer_ = std::make_unique<Gemma3Tokenizer>(gguf_, config_.vocab_size);
+    tokenizer_bos_id_ = tokenizer_->bos_id();
+    tokenizer_eos_id_ = tokenizer_->eos_id();
 
     // arena: the whole tensor-data section, uploaded in chunks
     const std::uint64_t arena_bytes = gguf_.file_size() - gguf_.data_offset();
@@ -179,8 +176,8 @@ Gemma3SingleTokenResult Gemma3Model::run_single_token(std::uint32_t token_id, st
     return r;
 }
 
-std::vector<std::uint32_t> Gemma3Model::tokenize(const std::string&, bool) const {
-    throw std::runtime_error("Gemma 3 text tokenisation is not part of the MI355X build; pass token ids");
+std::vector<std::uint32_t> Gemma3Model::tokenize(const std::string& text, bool add_bos) const {
+    return tokenizer_->tokenize(text, add_bos);
 }
 
 Gemma3GenerationResult Gemma3Model::generate_greedy(const std::string& prompt, std::size_t max_new_tokens) {
@@ -223,38 +220,10 @@ Gemma3GenerationResult Gemma3Model::generate_greedy_from_bos(std::size_t max_new
     return generate_greedy_tokens(std::vector<std::uint32_t>{tokenizer_bos_id_}, max_new_tokens);
 }
 
-std::string Gemma3Model::token_piece(std::uint32_t token_id) const {
-    if (tokenizer_tokens_ == nullptr || token_id >= tokenizer_tokens_->array.size()) return {};
-    return tokenizer_tokens_->array[token_id].as_string().value_or(std::string{});
-}
+std::string Gemma3Model::token_piece(std::uint32_t token_id) const { return tokenizer_->token_piece(token_id); }
 
 // Control ids 0..3 print nothing, <0xNN> byte pieces print their byte, and the SentencePiece
 // space marker U+2581 prints as a space (src/gemma3.cpp:1251-1299).
-std::string Gemma3Model::decode_piece(std::uint32_t token_id) const {
-    if (token_id <= 3) return {};
-    std::string piece = token_piece(token_id);
-    auto hex = [](char c) -> int {
-        if (c >= '0' && c <= '9') return c - '0';
-        if (c >= 'a' && c <= 'f') return c - 'a' + 10;
-        if (c >= 'A' && c <= 'F') return c - 'A' + 10;
-        return -1;
-    };
-    if (piece.size() == 6 && piece.compare(0, 3, "<0x") == 0 && piece[5] == '>') {
-        const int hi = hex(piece[3]), lo = hex(piece[4]);
-        if (hi >= 0 && lo >= 0) return std::string(1, static_cast<char>((hi << 4) | lo));
-    }
-    static const std::string kSpace = "\xE2\x96\x81";
-    std::string out;
-    out.reserve(piece.size());
-    for (std::size_t i = 0; i < piece.size();) {
-        if (piece.compare(i, kSpace.size(), kSpace) == 0) {
-            out += ' ';
-            i += kSpace.size();
-        } else {
-            out += piece[i++];
-        }
-    }
-    return out;
-}
+std::string Gemma3Model::decode_piece(std::uint32_t token_id) const { return tokenizer_->decode_piece(token_id); }
 
 }  // namespace vortexrt

@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from gguf import (GGML_F32, GGML_Q8_0, GgufWriter, T_ARR, T_F32, T_I32, T_STR, T_U32)
+from gguf import (GGML_F32, GGML_Q8_0, GgufWriter, T_ARR, T_BOOL, T_F32, T_I32, T_STR, T_U32)
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -224,6 +224,23 @@ def write_gemma3_gguf(path, seed: int = 0, n_layers: int = 18, d_model: int = 64
         q8(p + "ffn_down.weight", d_model, ffn)
     w.write(path)
     return path
+
+
+def write_tokenizer_gguf(path, pieces, scores, types, bos=2, eos=1, unk=3, add_space_prefix=None):
+    """A metadata-only GGUF carrying a tokenizer vocabulary (tokenizer.ggml.* keys of
+    src/gemma3.cpp:289-454), for the tokenizer tests; add_space_prefix None leaves the key out."""
+    w = GgufWriter(alignment=32)
+    w.add("general.architecture", T_STR, "gemma3")
+    w.add("tokenizer.ggml.model", T_STR, "llama")
+    w.add("tokenizer.ggml.tokens", T_ARR, (T_STR, list(pieces)))
+    w.add("tokenizer.ggml.scores", T_ARR, (T_F32, np.asarray(scores, dtype=np.float32)))
+    w.add("tokenizer.ggml.token_type", T_ARR, (T_I32, np.asarray(types, dtype=np.int32)))
+    w.add("tokenizer.ggml.bos_token_id", T_U32, bos)
+    w.add("tokenizer.ggml.eos_token_id", T_U32, eos)
+    w.add("tokenizer.ggml.unknown_token_id", T_U32, unk)
+    if add_space_prefix is not None:
+        w.add("tokenizer.ggml.add_space_prefix", T_BOOL, bool(add_space_prefix))
+    w.write(path)
 
 
 TINY = dict(n_layers=6, d_model=128, n_heads=2, head_dim=64, ffn=256, vocab=1000, context=256, window=8)
