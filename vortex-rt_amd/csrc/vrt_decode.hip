@@ -72,7 +72,8 @@ constexpr uint32_t kSpinLimit = 1u << 21;    // polls before a hand-off is decla
 constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
 constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x query heads) per block
 constexpr uint32_t kLmUnits = 4;             // 16-byte LM-head loads per thread per tile
-constexpr uint32_t kLmDepth = 3;             // LM-head tiles in flight per workgroup
+constexpr uint32_t kLmRing = 3;              // LM-head tiles in flight per workgroup (LDS ring)
+constexpr uint32_t kLmTileBytes = kLmUnits * 512u * 16u;
 constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
 constexpr uint32_t kPartRound = 12 * kMkThreads;   // attention partials gathered per wait
 constexpr int kRsrcFlags = 0x00020000;       // raw buffer resource, 32-bit data format
@@ -97,7 +98,7 @@ struct MkLds {
     uint32_t h, xs, xa, xd, ya, yd, nwa0, nwa1, nwd0, nwd1, any, la, lb, lc, ls, sq, sc, mw, gu, red, u, total;
 };
 
-constexpr uint32_t kMkLdsBytes = 120u * 1024u;   // static LDS of the persistent kernel
+constexpr uint32_t kMkLdsBytes = 144u * 1024u;   // static LDS of the persistent kernel
 
 struct MkParams {
     uint32_t d, H, hd, F, V, L, ctx_len, eos;
@@ -404,34 +405,38 @@ __device__ __forceinline__ void q8_load_lds(const uint8_t* tile, uint32_t off, Q
     for (int j = 0; j < 9; ++j) r.d[j] = lb[j];
 }
 
-struct LmTile {
-    v4u u[kLmUnits];
-};
-
-// Loads rows [r0, r1) of the LM head (16-byte units of the 16-byte aligned span) into
-// registers. Branch-free: units past the span re-load its last unit. The host only enables
-// this kernel when the table is followed by at least 16 readable bytes of the arena.
-__device__ __forceinline__ void lm_tile_load(uint32_t r0, uint32_t r1, uint64_t row_bytes, LmTile& t,
-                                             uint32_t& pre, uint32_t& n16) {
+// Copies rows [r0, r1) of the LM head, as the 16-byte units of their 16-byte aligned span, into
+// an LDS tile with direct global->LDS loads (unit j of the span at tile byte 16 j; pre = the
+// offset of row r0 in the span). Thread t moves units t + kMkThreads k, k < kLmUnits: each
+// wave's instruction writes 64 consecutive units. Branch-free: units past the span re-load its
+// last unit (the host only enables this kernel when the table is followed by at least 16
+// readable bytes of the arena). Non-temporal: the table is streamed once per step.
+__device__ __forceinline__ uint32_t lm_tile_issue(uint32_t r0, uint32_t r1, uint64_t row_bytes, uint8_t* tile) {
     const uintptr_t s = reinterpret_cast<uintptr_t>(g_mk.tok_embd) + static_cast<uint64_t>(r0) * row_bytes;
     const uintptr_t a0 = s & ~uintptr_t(15);
-    pre = static_cast<uint32_t>(s - a0);
+    const uint32_t pre = static_cast<uint32_t>(s - a0);
     const uint64_t nbytes = pre + static_cast<uint64_t>(r1 - r0) * row_bytes;
-    n16 = static_cast<uint32_t>((nbytes + 15u) / 16u);
+    const uint32_t n16 = static_cast<uint32_t>((nbytes + 15u) / 16u);
+    const uint32_t wave = threadIdx.x >> 6;
 #pragma unroll
     for (uint32_t k = 0; k < kLmUnits; ++k) {
         const uint32_t j = threadIdx.x + k * kMkThreads;
         const uintptr_t p = a0 + static_cast<uintptr_t>(j < n16 ? j : n16 - 1u) * 16u;
-        t.u[k] = __builtin_nontemporal_load(reinterpret_cast<const VRT_AS_GLOBAL v4u*>(p));
+        __builtin_amdgcn_global_load_lds((const VRT_AS_GLOBAL void*)p,
+                                         (__attribute__((address_space(3))) void*)(tile + 16u * (k * kMkThreads + 64u * wave)),
+                                         16, 0, 2 /* nt */);
     }
+    return pre;
 }
 
-__device__ __forceinline__ void lm_tile_store(const LmTile& t, uint32_t n16, uint8_t* lds) {
-#pragma unroll
-    for (uint32_t k = 0; k < kLmUnits; ++k) {
-        const uint32_t j = threadIdx.x + k * kMkThreads;
-        if (j < n16) *reinterpret_cast<v4u*>(lds + 16u * j) = t.u[k];
-    }
+// Waits until this wave's LM-head tile loads issued before the last `later` tiles are complete
+// (vector-memory operations complete in issue order; a later store only makes the wait longer).
+__device__ __forceinline__ void lm_wait_tiles(uint32_t later) {
+    static_assert(kLmUnits * (kLmRing - 1u) <= 15u, "vmcnt immediate");
+    // s_waitcnt: vmcnt in bits 3:0, expcnt (7) and lgkmcnt (15) left unconstrained
+    if (later >= 2u) __builtin_amdgcn_s_waitcnt(0x0F70 | (2u * kLmUnits));
+    else if (later == 1u) __builtin_amdgcn_s_waitcnt(0x0F70 | kLmUnits);
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 // =============================================================================================
@@ -556,6 +561,16 @@ __device__ __forceinline__ void wave_stage_lds(const float* src, float* dst, uin
 // from wave 0, to x_glob if given. `bad` is set when h has a non-finite element (:1857-1863).
 // y_lds and the staging areas belong to one call site: a later call site may run while slower
 // waves still read this one's. Returns 1 if the gather was abandoned.
+// Pairwise sum of N doubles (a short dependency chain; the squares it sums are exact).
+template <int N>
+__device__ __forceinline__ double tree_sum(double (&v)[N]) {
+#pragma unroll
+    for (int s = 1; s < N; s *= 2)
+#pragma unroll
+        for (int i = 0; i + s < N; i += 2 * s) v[i] += v[i + s];
+    return v[0];
+}
+
 template <int EP, bool INTO>
 __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const float* w_post, const float* w_next,
                                         float* hl, float* x_lds, float* x_glob, uint32_t d, float eps, int& bad,
@@ -604,14 +619,14 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
     }
     if (ysrc) {
         float2 y[EP];
-        double ss = 0.0;
+        double sq[2 * EP];
 #pragma unroll
         for (int k = 0; k < EP; ++k) {
             y[k] = live[k] ? reinterpret_cast<const float2*>(y_lds)[lane + 64u * k] : make_float2(0.0f, 0.0f);
-            ss += static_cast<double>(y[k].x) * static_cast<double>(y[k].x);
-            ss += static_cast<double>(y[k].y) * static_cast<double>(y[k].y);
+            sq[2 * k] = static_cast<double>(y[k].x) * static_cast<double>(y[k].x);
+            sq[2 * k + 1] = static_cast<double>(y[k].y) * static_cast<double>(y[k].y);
         }
-        const float sc = mk_rms_scale(wave_red_sum_d(ss), d, eps);
+        const float sc = mk_rms_scale(wave_red_sum_d(tree_sum(sq)), d, eps);
 #pragma unroll
         for (int k = 0; k < EP; ++k) {
             const float2 wp = reinterpret_cast<const float2*>(nw_post)[live[k] ? lane + 64u * k : 0u];
@@ -620,16 +635,16 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
         }
     }
     int nf = 0;
-    double ss2 = 0.0;
+    double sq2[2 * EP];
 #pragma unroll
-    for (int k = 0; k < EP; ++k)
-        if (live[k]) {
-            nf |= !__builtin_isfinite(h[k].x) || !__builtin_isfinite(h[k].y);
-            ss2 += static_cast<double>(h[k].x) * static_cast<double>(h[k].x);
-            ss2 += static_cast<double>(h[k].y) * static_cast<double>(h[k].y);
-        }
+    for (int k = 0; k < EP; ++k) {
+        const float2 v = live[k] ? h[k] : make_float2(0.0f, 0.0f);
+        nf |= !__builtin_isfinite(v.x) || !__builtin_isfinite(v.y);
+        sq2[2 * k] = static_cast<double>(v.x) * static_cast<double>(v.x);
+        sq2[2 * k + 1] = static_cast<double>(v.y) * static_cast<double>(v.y);
+    }
     bad = __builtin_amdgcn_ballot_w64(nf != 0) != 0u;
-    const float sc2 = mk_rms_scale(wave_red_sum_d(ss2), d, eps);
+    const float sc2 = mk_rms_scale(wave_red_sum_d(tree_sum(sq2)), d, eps);
     mark(33);
 #pragma unroll
     for (int k = 0; k < EP; ++k)
@@ -953,25 +968,50 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
                                                  (o / kPartRound) & 1u ? kAnyGather1 : kAnyGather0))
             return false;
     MK_MARK(12);
+    // Chunk weights: wave h < H takes head h, lane c chunk c (M, e_c = exp(m_c - M) and
+    // den = sum_c double(e_c) * double(l_c) by DPP over the 16 lanes of row 0).
     float* wts = m.mw;   // [8][kMaxChunks] weights, then den [8]
-    if (tid < H) {
-        const uint32_t h = tid;
-        float M = -INFINITY;
-        for (uint32_t q = 0; q < nch; ++q) M = fmaxf(M, parts[q * part_stride + qw + h]);
-        double den = 0.0;
-        for (uint32_t q = 0; q < nch; ++q) {
-            const float e = expf(parts[q * part_stride + qw + h] - M);
-            wts[h * kMaxChunks + q] = e;
-            den += static_cast<double>(e) * static_cast<double>(parts[q * part_stride + qw + H + h]);
+    static_assert(kMaxChunks <= 16u, "one DPP row of chunks");
+    if (wave < H) {
+        const uint32_t h = wave;
+        const bool on = lane < nch;
+        const uint32_t base = (on ? lane : 0u) * part_stride;
+        const float mq = on ? parts[base + qw + h] : -INFINITY;
+        const float lq = parts[base + qw + H + h];
+        float M = fmaxf(mq, dpp_mov<0xB1>(mq));
+        M = fmaxf(M, dpp_mov<0x4E>(M));
+        M = fmaxf(M, dpp_mov<0x141>(M));
+        M = fmaxf(M, dpp_mov<0x140>(M));
+        const float e = on ? expf(mq - M) : 0.0f;
+        double den = on ? static_cast<double>(e) * static_cast<double>(lq) : 0.0;
+        den += dpp_d<0xB1, 0xf>(den, false);
+        den += dpp_d<0x4E, 0xf>(den, false);
+        den += dpp_d<0x141, 0xf>(den, false);
+        den += dpp_d<0x140, 0xf>(den, false);
+        if (on) wts[h * kMaxChunks + lane] = e;
+        if (lane == 0u) {
+            wts[8u * kMaxChunks + h] = static_cast<float>(den);
+            if (!(den > 0.0) || !__builtin_isfinite(den)) mk_flag_min(0x40000000u | l);   // :1666-1670
         }
-        wts[8u * kMaxChunks + h] = static_cast<float>(den);
-        if (!(den > 0.0) || !__builtin_isfinite(den)) mk_flag_min(0x40000000u | l);   // :1666-1670
     }
     __syncthreads();
+    // att[idx] = sum_c e_c acc_c[idx] / den, the chunks in order, four loads in flight
     for (uint32_t idx = tid; idx < qw; idx += kMkThreads) {
         const uint32_t h = idx / hd;
+        const float* wh = wts + h * kMaxChunks;
         float num = 0.0f;
-        for (uint32_t q = 0; q < nch; ++q) num += wts[h * kMaxChunks + q] * parts[q * part_stride + idx];
+        uint32_t q = 0;
+        for (; q + 4u <= nch; q += 4u) {
+            float wv[4], av[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                wv[k] = wh[q + k];
+                av[k] = parts[(q + k) * part_stride + idx];
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) num += wv[k] * av[k];
+        }
+        for (; q < nch; ++q) num += wh[q] * parts[q * part_stride + idx];
         m.xs[idx] = num / wts[8u * kMaxChunks + h];
     }
     __syncthreads();
@@ -1077,17 +1117,21 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
     MK_UNIFORM(want_logits);
     __shared__ float s_v[kMkWaves];
     __shared__ uint32_t s_i[kMkWaves];
-    const uint32_t r_begin = min(g_mk.V, w * g_mk.lm_rows), r_end = min(g_mk.V, r_begin + g_mk.lm_rows);
-    const uint32_t TR = g_mk.lm_tile_rows;
-    const uint32_t ntiles = (r_end - r_begin + TR - 1u) / TR;
-    // the first kLmDepth tiles are in flight before the final residual is gathered
-    LmTile tl[kLmDepth];
-    uint32_t pre[kLmDepth], n16[kLmDepth];
+    // Tiles of TR rows are dealt round-robin: tile ti of this workgroup is tile w + ti * nwg of the
+    // table, so the workgroups stream one contiguous window of the table at a time.
+    const uint32_t TR = g_mk.lm_tile_rows, nwg = g_mk.nwg;
+    const uint32_t tiles = (g_mk.V + TR - 1u) / TR;
+    const uint32_t ntiles = w < tiles ? (tiles - w + nwg - 1u) / nwg : 0u;
+    auto tile_row = [&](uint32_t ti) { return (w + ti * nwg) * TR; };
+    // the first kLmRing tiles are in flight before the final residual is gathered
+    uint8_t* ring = reinterpret_cast<uint8_t*>(m.u);
+    auto issue = [&](uint32_t ti) {
+        const uint32_t r0 = tile_row(ti);
+        return lm_tile_issue(r0, min(g_mk.V, r0 + TR), rb_d, ring + (ti % kLmRing) * kLmTileBytes);
+    };
 #pragma unroll
-    for (uint32_t i = 0; i < kLmDepth; ++i) {
-        pre[i] = n16[i] = 0u;
-        if (i < ntiles) lm_tile_load(r_begin + i * TR, min(r_end, r_begin + (i + 1u) * TR), rb_d, tl[i], pre[i], n16[i]);
-    }
+    for (uint32_t i = 0; i < kLmRing; ++i)
+        if (i < ntiles) (void)issue(i);
     if (!mk_fold<EP>(tagb)) return false;
     MK_MARK(23);
     build_limbs(m.xa, d, m.L);
@@ -1098,22 +1142,20 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
     uint32_t bi = 0xffffffffu;
     constexpr uint32_t RPW = 64u / SD;
     const uint32_t slot = lane / SD, sl = lane % SD;
-    uint8_t* tile = reinterpret_cast<uint8_t*>(m.u);
-    auto consume = [&](uint32_t ti, LmTile& tl, uint32_t& pre, uint32_t& n16) {
-        const uint32_t t0 = r_begin + ti * TR, t1 = min(r_end, t0 + TR);
-        lm_tile_store(tl, n16, tile);
-        const uint32_t pre_cur = pre;
-        __syncthreads();
-        if (ti + kLmDepth < ntiles) {
-            const uint32_t n0 = r_begin + (ti + kLmDepth) * TR;
-            lm_tile_load(n0, min(r_end, n0 + TR), rb_d, tl, pre, n16);
-        }
+    const bool lane_on = sl < nblk_d;
+    for (uint32_t ti = 0; ti < ntiles; ++ti) {
+        const uint32_t t0 = tile_row(ti), t1 = min(g_mk.V, t0 + TR);
+        const uint8_t* tile = ring + (ti % kLmRing) * kLmTileBytes;
+        const uint32_t pre_cur = static_cast<uint32_t>(
+            (reinterpret_cast<uintptr_t>(g_mk.tok_embd) + static_cast<uint64_t>(t0) * rb_d) & 15u);
+        lm_wait_tiles(min(kLmRing - 1u, ntiles - 1u - ti));
+        __syncthreads();   // every wave's share of tile ti is in LDS
         const uint32_t nrows = t1 - t0;
         for (uint32_t rg = wave * RPW; rg < nrows; rg += kMkWaves * RPW) {   // wave-uniform trip count
             const uint32_t r = rg + slot;
             const bool live = r < nrows;
             float acc = 0.0f;
-            if (live && sl < nblk_d) {
+            if (live && lane_on) {
                 Q8Raw raw;
                 q8_load_lds(tile, pre_cur + r * static_cast<uint32_t>(rb_d) + 34u * sl, raw);
                 acc = q8_dot(raw, xl[0]);
@@ -1132,13 +1174,10 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
                 if (am_better(tot, v, bv, bi)) { bv = tot; bi = v; }
             }
         }
-        __syncthreads();
-    };
-    for (uint32_t ti = 0; ti < ntiles; ti += kLmDepth) {
-#pragma unroll
-        for (uint32_t i = 0; i < kLmDepth; ++i) {
-            if (ti + i < ntiles) consume(ti + i, tl[i], pre[i], n16[i]);
-            if (ti + i == 0u) MK_MARK(25);
+        if (ti == 0u) MK_MARK(25);
+        if (ti + kLmRing < ntiles) {
+            __syncthreads();   // tile ti's slot is read by every wave before it is refilled
+            (void)issue(ti + kLmRing);
         }
     }
     MK_MARK(26);
@@ -1435,7 +1474,7 @@ int mk_setup(vrt_g3* g) {
     P.max_chunks = max_chunks;
     P.lm_rows = (c.vocab_size + nwg - 1u) / nwg;
     const uint64_t rb = static_cast<uint64_t>(d / 32u) * 34u;
-    P.lm_tile_rows = static_cast<uint32_t>(std::min<uint64_t>(P.lm_rows, (kLmUnits * kMkThreads * 16u - 16u) / rb));
+    P.lm_tile_rows = static_cast<uint32_t>(std::min<uint64_t>(P.lm_rows, (kLmTileBytes - 16u) / rb));
     if (P.lm_tile_rows == 0u) { mk_destroy(g); return VRT_OK; }
     uint32_t slots_max = 1;
     for (const auto& Ly : g->layers) slots_max = std::max(slots_max, Ly.slots);
@@ -1465,7 +1504,7 @@ int mk_setup(vrt_g3* g) {
     P.lds.mw = take((8u * kMaxChunks + 16u) * 4u);
     P.lds.gu = take(2u * ((F + nprod - 1u) / nprod + 1u) * 4u);
     P.lds.red = take((4u + 9u) * kMkWaves * 8u);
-    P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + 2u * H)) * 4u, kLmUnits * kMkThreads * 16u + 16u));
+    P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + 2u * H)) * 4u, kLmRing * kLmTileBytes));
     P.lds.total = off;
     mk->lds_bytes = off;
     if (off > kMkLdsBytes) { mk_destroy(g); return VRT_OK; }
