@@ -69,6 +69,7 @@ constexpr uint32_t kMkThreads = 512;         // 8 waves: two per SIMD
 constexpr uint32_t kMkWaves = kMkThreads / 64;
 constexpr uint32_t kVec = 4;                 // vector elements per thread (vectors <= 2048)
 constexpr uint32_t kSpinLimit = 1u << 21;    // polls before a hand-off is declared lost
+constexpr int kPollSleep = 4;                // s_sleep between unsuccessful polls (64 clocks each)
 constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
 constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x query heads) per block
 constexpr uint32_t kLmUnits = 4;             // 16-byte LM-head loads per thread per tile
@@ -201,6 +202,7 @@ __device__ __forceinline__ int ll_poll(__amdgpu_buffer_rsrc_t r, const int (&off
             mk_abort();
             break;
         }
+        __builtin_amdgcn_s_sleep(kPollSleep);   // back off: fewer polls in flight while the data is far off
         __asm__ volatile("" ::: "memory");
 #pragma unroll
         for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b64(r, off[k], 0, kCoherent);
@@ -350,6 +352,16 @@ __device__ __forceinline__ void split_range(uint32_t total, uint32_t parts, uint
     b = static_cast<uint32_t>(static_cast<uint64_t>(total) * (idx + 1u) / parts);
 }
 
+// As split_range, in granules of kLine words: a producer's range of tagged exchange words
+// starts on a 64-byte line and no two producers write the same line. (Producers on different
+// XCDs writing one line cost ~0.5 us per exchange on MI355X.)
+constexpr uint32_t kLine = 8;   // tagged words per 64-byte line
+__device__ __forceinline__ void split_lines(uint32_t total, uint32_t parts, uint32_t idx, uint32_t& a, uint32_t& b) {
+    split_range((total + kLine - 1u) / kLine, parts, idx, a, b);
+    a = min(total, a * kLine);
+    b = min(total, b * kLine);
+}
+
 // Attention split of a history of `hist` positions: number of chunks and chunk length.
 // Chunk c runs on workgroup nwg - 1 - c; every other workgroup produces rows in phases A and
 // D. So every workgroup either produces in A/D or publishes an attention chunk, which is what
@@ -447,7 +459,7 @@ __device__ __forceinline__ void lm_wait_tiles(uint32_t later) {
     const MkSmem m = mk_smem();                                                                             \
     const uint32_t w = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;                    \
     const uint32_t d = g_mk.d, H = g_mk.H, hd = g_mk.hd, F = g_mk.F, L = g_mk.L;                                           \
-    const uint32_t qw = H * hd, nqkv = qw + 2u * hd, half = hd >> 1, part_stride = qw + 2u * H;             \
+    const uint32_t qw = H * hd, nqkv = qw + 2u * hd, half = hd >> 1, part_stride = qw + kLine * H;             \
     const uint32_t nblk_d = d >> 5, nblk_a = qw >> 5, nblk_f = F >> 5;                                      \
     const uint64_t rb_d = static_cast<uint64_t>(nblk_d) * 34u, rb_a = static_cast<uint64_t>(nblk_a) * 34u,  \
                    rb_f = static_cast<uint64_t>(nblk_f) * 34u;                                              \
@@ -495,6 +507,25 @@ __device__ __forceinline__ void wave_red_sum_n(float (&v)[N]) {
     for (int i = 0; i < N; ++i) v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 63));
 }
 
+// Sums v[0..7] over the wave and transposes: lane l ends with the total of v[l & 7]. Three
+// exchanges inside each group of 8 lanes (lanes l and 7 - l, then l ^ 2, then l ^ 1) each
+// halve the values a lane carries; lanes l ^ 8, l ^ 16 and l ^ 32 then hold the same
+// position. Partners add the same two operands, so every lane of a position gets the same bits.
+__device__ __forceinline__ float wave_sum8_t(const float (&v)[8]) {
+    const uint32_t lane = __lane_id();
+    const bool b2 = (lane & 4u) != 0u, b1 = (lane & 2u) != 0u, b0 = (lane & 1u) != 0u;
+    float a[4], b[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = (b2 ? v[i + 4] : v[i]) + dpp_mov<0x141>(b2 ? v[i] : v[i + 4]);   // row_half_mirror
+#pragma unroll
+    for (int i = 0; i < 2; ++i) b[i] = (b1 ? a[i + 2] : a[i]) + dpp_mov<0x4E>(b1 ? a[i] : a[i + 2]);    // quad_perm [2,3,0,1]
+    float c = (b0 ? b[1] : b[0]) + dpp_mov<0xB1>(b0 ? b[0] : b[1]);                                    // quad_perm [1,0,3,2]
+    c += dpp_mov<0x128>(c);   // row_ror:8
+    c += swz_xor16(c);
+    c += __shfl_xor(c, 32);
+    return c;
+}
+
 // Polls 16-byte units (two tagged words each) at byte offsets off[k] of r until both tags of
 // every unit equal `tag` (or !live); out[2k], out[2k+1] get the two values of unit k. Returns
 // 0, or 1 if the wait was abandoned (abort raised).
@@ -516,6 +547,7 @@ __device__ __forceinline__ int ll_poll2(__amdgpu_buffer_rsrc_t r, const int (&of
             mk_abort();
             break;
         }
+        __builtin_amdgcn_s_sleep(kPollSleep);   // back off: fewer polls in flight while the data is far off
         __asm__ volatile("" ::: "memory");
 #pragma unroll
         for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, off[k], 0, kCoherent);
@@ -574,7 +606,8 @@ __device__ __forceinline__ double tree_sum(double (&v)[N]) {
 template <int EP, bool INTO>
 __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const float* w_post, const float* w_next,
                                         float* hl, float* x_lds, float* x_glob, uint32_t d, float eps, int& bad,
-                                        float* nw_post, float* nw_next, float* y_lds, uint32_t any_id, bool tr = false) {
+                                        float* nw_post, float* nw_next, float* y_lds, uint32_t any_id, bool tr = false,
+                                        uint32_t mk0 = 31u) {
 #pragma clang fp contract(off)
     auto mark = [&](uint32_t k) {
         if (tr && threadIdx.x == 0u)
@@ -606,9 +639,9 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
             if (live[k]) reinterpret_cast<float2*>(y_lds)[threadIdx.x + kMkThreads * k] = make_float2(y[2 * k], y[2 * k + 1]);
     }
     if (wave == 0u) __builtin_amdgcn_s_waitcnt(0);   // the staged weights are in LDS (vmcnt covers LDS loads)
-    mark(31);
+    mark(mk0);
     if (blk_any(fail, any_id)) return 1;
-    mark(32);
+    mark(mk0 + 1u);
     float2 h[EP];
     bool live[EP];
 #pragma unroll
@@ -645,7 +678,7 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
     }
     bad = __builtin_amdgcn_ballot_w64(nf != 0) != 0u;
     const float sc2 = mk_rms_scale(wave_red_sum_d(tree_sum(sq2)), d, eps);
-    mark(33);
+    mark(mk0 + 2u);
 #pragma unroll
     for (int k = 0; k < EP; ++k)
         if (live[k]) {
@@ -683,7 +716,7 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     // producers: every workgroup that is not an attention chunk of this block at this position
     uint32_t v0 = 0, v1 = 0;
     const uint32_t nprod = g_mk.nwg - n_bunits(Ly.slots, pos);
-    if (w < nprod) split_range(nqkv, nprod, w, v0, v1);
+    if (w < nprod) split_lines(nqkv, nprod, w, v0, v1);
     const uint8_t *wq = Ly.wq, *wk = Ly.wk, *wv = Ly.wv;
     auto rowp = [=](uint32_t v) -> const uint8_t* {
         return v < qw ? wq + static_cast<uint64_t>(v) * rb_d
@@ -712,14 +745,18 @@ constexpr uint32_t kBPos = kBGrp / kBWaves;        // positions per wave per gro
 
 // Phase B: one workgroup per (chunk c, query head h); waves 0..3 work, the others wait at the
 // closing barrier. Lane i of a wave owns head dims 4i..4i+3. Every working wave gathers its
-// lanes' q_h, k and v itself, applies QK-norm (src/gemma3.cpp:1045-1104) and RoPE
-// (:1371-1424; the partner dims e +- head_dim/2 come from another lane of the same wave), and
-// runs an online softmax over its positions t = c0 + wave + 4i of the chunk (:1602-1696), in
-// groups of 32 positions whose K/V rows are loaded one group ahead (a window chunk is one
-// group, loaded before the wait for q, k, v), so
-// the wave needs no barrier until the four partials {m, l, acc} are merged through LDS. Wave 0
-// of head 0 of the chunk holding the current position appends k and v to the cache
-// (:1590-1600). Publishes the unnormalised partial {acc[hd] of head h, m, l} of (c, h).
+// lanes' q_h, k and v itself, applies
+// QK-norm (src/gemma3.cpp:1045-1104) and RoPE (:1371-1424; the partner dims e +- head_dim/2
+// come from another lane of the same wave), and runs an online softmax over its cached
+// positions t = c0 + wave + 4i of the chunk (:1602-1696), in groups of 32 positions whose K/V
+// rows are loaded one group ahead (a window chunk is one group, loaded before the wait for
+// q, k, v). A group's 8 scores per wave are reduced and transposed together, so that lane l
+// holds the score of its position l & 7: the max, the exponentials and the masks are one
+// lane-parallel operation per group. The current position is taken from registers by the
+// wave whose turn it is. No barrier until the four partials {m, l, acc} are merged through
+// LDS. Wave 0 of head 0 of
+// the chunk holding the current position appends k and v to the cache (:1590-1600).
+// Publishes the unnormalised partial {acc[hd] of head h, m, l} of (c, h).
 // Inlined into the kernel: as a call it would save and restore callee-saved registers through
 // scratch.
 __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
@@ -754,16 +791,20 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         const uint32_t kv_bytes = Ly.slots * hd * 4u;
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
-        auto kv_off = [&](uint32_t t) { return ((t % Ly.slots) * hd + dl) * 4u; };
-        auto cached = [&](uint32_t t, uint32_t g1) { return t < g1 && t != pos && dlive; };
+        // cached positions [c0, cend); the current position itself comes from registers
+        const uint32_t cend = c1 == pos + 1u ? pos : c1;
+        // byte offset of this lane's dims of position t (past the buffer for dead lanes: no access)
+        auto kv_off = [&](uint32_t t) { return dlive ? static_cast<int>(((t % Ly.slots) * hd + dl) * 4u) : 0x7ffffff0; };
+        // how many of this wave's positions g0 + uw + kBWaves i fall below g1 (wave-uniform)
+        auto nvalid = [&](uint32_t g0, uint32_t g1) { return g1 > g0 + uw ? (g1 - g0 - uw + kBWaves - 1u) / kBWaves : 0u; };
         v4u kr[kBPos], vr[kBPos];
         {
-            const uint32_t g1 = min(c1, c0 + kBGrp);
+            const uint32_t nv = nvalid(c0, min(cend, c0 + kBGrp));
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i) {
                 kr[i] = vr[i] = v4u{0u, 0u, 0u, 0u};
-                const uint32_t t = c0 + uw + kBWaves * i;
-                if (cached(t, g1)) {
+                if (i < nv) {
+                    const uint32_t t = c0 + uw + kBWaves * i;
                     kr[i] = co_ld4(rk, kv_off(t));
                     vr[i] = co_ld4(rv, kv_off(t));
                 }
@@ -844,58 +885,74 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         float m_run = -INFINITY, l_run = 0.0f;
         const float attn_scale = g_mk.attn_scale;
-        for (uint32_t g0 = c0; g0 < c1; g0 += kBGrp) {
-            const uint32_t g1 = min(c1, g0 + kBGrp);
-            float s[kBPos];
+        static_assert(kBPos == 8u, "one position per lane of each group of 8 lanes");
+        const uint32_t pl = lane & 7u;   // the position of this wave's group that this lane scores
+        for (uint32_t g0 = c0; g0 < cend; g0 += kBGrp) {
+            const uint32_t nv = nvalid(g0, min(cend, g0 + kBGrp));
+            float part[kBPos];
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i) {
-                const uint32_t t = g0 + uw + kBWaves * i;
-                if (t == pos && dlive) {
-                    kr[i] = v4u{__float_as_uint(k[0]), __float_as_uint(k[1]), __float_as_uint(k[2]), __float_as_uint(k[3])};
-                    vr[i] = v4u{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
-                }
                 float p = 0.0f;
 #pragma unroll
                 for (uint32_t e = 0; e < 4u; ++e) p += q[e] * __uint_as_float(kr[i][e]);
-                s[i] = p;
+                part[i] = p;
             }
-            wave_red_sum_n<kBPos>(s);   // wave-uniform scores
-#pragma unroll
-            for (uint32_t i = 0; i < kBPos; ++i) s[i] = g0 + uw + kBWaves * i < g1 ? s[i] * attn_scale : -INFINITY;
+            // lane l: the score of position g0 + uw + kBWaves (l & 7). The reduction runs in every
+            // lane (its exchanges read all of them); the mask comes after.
+            const float st = wave_sum8_t(part);
+            const float sl = pl < nv ? st * attn_scale : -INFINITY;
             // the next group's keys load while this group's softmax and values run
-            const uint32_t n0 = g0 + kBGrp, n1 = min(c1, n0 + kBGrp);
+            const uint32_t n0 = g0 + kBGrp;
+            const uint32_t nn = n0 < cend ? nvalid(n0, min(cend, n0 + kBGrp)) : 0u;
 #pragma unroll
-            for (uint32_t i = 0; i < kBPos; ++i) {
-                const uint32_t t = n0 + uw + kBWaves * i;
-                if (cached(t, n1)) kr[i] = co_ld4(rk, kv_off(t));
+            for (uint32_t i = 0; i < kBPos; ++i)
+                if (i < nn) kr[i] = co_ld4(rk, kv_off(n0 + uw + kBWaves * i));
+            if (nv != 0u) {   // this wave has a position in the group
+                float mx = fmaxf(sl, dpp_mov<0xB1>(sl));
+                mx = fmaxf(mx, dpp_mov<0x4E>(mx));
+                mx = fmaxf(mx, dpp_mov<0x141>(mx));
+                mx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
+                const float m_new = fmaxf(m_run, mx);
+                if (m_new != -INFINITY) {
+                    const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+                    const float pe = sl == -INFINITY ? 0.0f : expf(sl - m_new);
+                    float pw[kBPos];
+                    float ls = 0.0f;
+#pragma unroll
+                    for (uint32_t i = 0; i < kBPos; ++i) {
+                        pw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), i));
+                        ls += pw[i];
+                    }
+#pragma unroll
+                    for (uint32_t e = 0; e < 4u; ++e) {
+                        float a = acc[e] * r;
+#pragma unroll
+                        for (uint32_t i = 0; i < kBPos; ++i) a += pw[i] * __uint_as_float(vr[i][e]);
+                        acc[e] = a;
+                    }
+                    l_run = l_run * r + ls;
+                    m_run = m_new;
+                }
             }
-            float mx = s[0];
 #pragma unroll
-            for (uint32_t i = 1; i < kBPos; ++i) mx = fmaxf(mx, s[i]);
-            const float m_new = fmaxf(m_run, mx);
-            if (m_new != -INFINITY) {   // this wave has a position in the group (or before it)
+            for (uint32_t i = 0; i < kBPos; ++i)
+                if (i < nn) vr[i] = co_ld4(rv, kv_off(n0 + uw + kBWaves * i));
+        }
+        // the current position, from registers, by the wave whose turn it is
+        if (c1 == pos + 1u && uw == (pos - c0) % kBWaves) {
+            float sp[1] = {0.0f};
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) sp[0] += q[e] * k[e];
+            wave_red_sum_n<1>(sp);
+            const float sc = sp[0] * attn_scale;
+            const float m_new = fmaxf(m_run, sc);
+            if (m_new != -INFINITY) {
                 const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-                float ls = 0.0f;
-                float pw[kBPos];
+                const float pw = sc == -INFINITY ? 0.0f : expf(sc - m_new);
 #pragma unroll
-                for (uint32_t i = 0; i < kBPos; ++i) {
-                    pw[i] = s[i] == -INFINITY ? 0.0f : expf(s[i] - m_new);
-                    ls += pw[i];
-                }
-#pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) {
-                    float a = acc[e] * r;
-#pragma unroll
-                    for (uint32_t i = 0; i < kBPos; ++i) a += pw[i] * __uint_as_float(vr[i][e]);
-                    acc[e] = a;
-                }
-                l_run = l_run * r + ls;
+                for (uint32_t e = 0; e < 4u; ++e) acc[e] = acc[e] * r + pw * v[e];
+                l_run = l_run * r + pw;
                 m_run = m_new;
-            }
-#pragma unroll
-            for (uint32_t i = 0; i < kBPos; ++i) {
-                const uint32_t t = n0 + uw + kBWaves * i;
-                if (cached(t, n1)) vr[i] = co_ld4(rv, kv_off(t));
             }
         }
         if (dlive) *reinterpret_cast<float4*>(ra + uw * hd + dl) = make_float4(acc[0], acc[1], acc[2], acc[3]);
@@ -911,22 +968,28 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     // merge the waves: acc = sum_w e^(m_w - M) acc_w, l = sum_w e^(m_w - M) l_w (fixed order)
     u64* part = g_mk.x_part + static_cast<uint64_t>(c) * part_stride;
     if (tid < hd) {
-        float M = rml[0];
-#pragma unroll
-        for (uint32_t k = 1; k < kBWaves; ++k) M = fmaxf(M, rml[k]);
+        // wave weights f_k = e^(m_k - M): lane k computes f_k, then every lane takes them by readlane
+        const float mk = lane < kBWaves ? rml[lane] : -INFINITY;
+        float M = fmaxf(mk, dpp_mov<0xB1>(mk));
+        M = fmaxf(M, dpp_mov<0x4E>(M));
+        M = fmaxf(M, dpp_mov<0x141>(M));   // lanes 0..7: the max over the waves
+        static_assert(kBWaves <= 8u, "DPP max over one half row (lanes past kBWaves hold -inf)");
+        const float fk = lane < kBWaves && mk != -INFINITY ? expf(mk - M) : 0.0f;
+        const float lk = lane < kBWaves ? rml[kBWaves + lane] : 0.0f;
         float f[kBWaves];
 #pragma unroll
-        for (uint32_t k = 0; k < kBWaves; ++k) f[k] = rml[k] == -INFINITY ? 0.0f : expf(rml[k] - M);
+        for (uint32_t k = 0; k < kBWaves; ++k) f[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fk), k));
         float sacc = 0.0f;
 #pragma unroll
         for (uint32_t k = 0; k < kBWaves; ++k) sacc += f[k] * ra[k * hd + tid];
         ll_stf(part + h * hd + tid, sacc, tB);
-        if (tid == 0) {
+        if (tid < kLine) {   // this unit's line: m, l, then padding (every word is tagged)
             float L = 0.0f;
 #pragma unroll
-            for (uint32_t k = 0; k < kBWaves; ++k) L += f[k] * rml[kBWaves + k];
-            ll_stf(part + qw + h, M, tB);
-            ll_stf(part + qw + H + h, L, tB);
+            for (uint32_t k = 0; k < kBWaves; ++k)
+                L += f[k] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lk), k));
+            const float Mu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(M), 0));
+            ll_stf(part + qw + kLine * h + tid, tid == 0u ? Mu : (tid == 1u ? L : 0.0f), tB);
         }
     }
     MK_MARK(10);
@@ -976,8 +1039,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
         const uint32_t h = wave;
         const bool on = lane < nch;
         const uint32_t base = (on ? lane : 0u) * part_stride;
-        const float mq = on ? parts[base + qw + h] : -INFINITY;
-        const float lq = parts[base + qw + H + h];
+        const float mq = on ? parts[base + qw + kLine * h] : -INFINITY;
+        const float lq = parts[base + qw + kLine * h + 1u];
         float M = fmaxf(mq, dpp_mov<0xB1>(mq));
         M = fmaxf(M, dpp_mov<0x4E>(M));
         M = fmaxf(M, dpp_mov<0x141>(M));
@@ -1036,7 +1099,7 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     MK_MARK(15);
     uint32_t p0 = 0, p1 = 0;
     const uint32_t nprod = g_mk.nwg - n_bunits(Ly.slots, pos);
-    if (w < nprod) split_range(F, nprod, w, p0, p1);
+    if (w < nprod) split_lines(F, nprod, w, p0, p1);
     const uint32_t v0 = 2u * p0, v1 = 2u * p1;
     const uint8_t *wg = Ly.wg, *wu = Ly.wu;
     auto rowp = [=](uint32_t v) { return ((v & 1u) ? wu : wg) + static_cast<uint64_t>(v >> 1) * rb_d; };
@@ -1044,7 +1107,7 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     batch_load<SD, 1, 2>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
     int none = 0;
     if (mk_resid<EP, true>(g_mk.x_o, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps, none, m.nwd0,
-                           m.nwd1, m.yd, kAnyD))
+                           m.nwd1, m.yd, kAnyD, tr, 27u))
         return false;
     MK_MARK(17);
     float* gu = m.gu;
@@ -1187,8 +1250,8 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
     if (tid == 0) {
         for (uint32_t k = 1; k < kMkWaves; ++k)
             if (am_better(s_v[k], s_i[k], s_v[0], s_i[0])) { s_v[0] = s_v[k]; s_i[0] = s_i[k]; }
-        ll_stf(g_mk.x_am + 2u * w, s_v[0], tLM);
-        ll_st(g_mk.x_am + 2u * w + 1u, s_i[0], tLM);
+        ll_stf(g_mk.x_am + kLine * w, s_v[0], tLM);   // one 64-byte line per workgroup
+        ll_st(g_mk.x_am + kLine * w + 1u, s_i[0], tLM);
     }
     __syncthreads();
     return true;
@@ -1208,7 +1271,24 @@ __device__ __attribute__((noinline)) MkArg mk_reduce_argmax(uint32_t tag) {
     __shared__ float s_v[kMkWaves];
     __shared__ uint32_t s_i[kMkWaves];
     float* buf = m.sc;   // 2 * nwg floats
-    const bool good = ll_gather<2>(g_mk.x_am, 2u * g_mk.nwg, tag, buf, kAnyArgmax);
+    bool good;
+    {   // value and index of workgroup k: words kLine k and kLine k + 1
+        uint32_t idx[2];
+        float v[2];
+        const uint32_t nj = 2u * g_mk.nwg;
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; ++k) {
+            const uint32_t j = tid + k * kMkThreads;
+            idx[k] = j < nj ? (j >> 1) * kLine + (j & 1u) : 0u;
+        }
+        const int fail = ll_wait_at<2>(g_mk.x_am, kLine * g_mk.nwg, idx, nj, tag, v);
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; ++k) {
+            const uint32_t j = tid + k * kMkThreads;
+            if (j < nj) buf[j] = v[k];
+        }
+        good = !blk_any(fail, kAnyArgmax);
+    }
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (uint32_t k = tid; k < g_mk.nwg; k += kMkThreads) {
@@ -1458,8 +1538,10 @@ int mk_setup(vrt_g3* g) {
     // every workgroup must cover its share of the all-workgroup phases in one batch
     const uint32_t max_chunks = std::min(kMaxChunks, kMaxBUnits / H);
     const uint32_t nprod = nwg - H * max_chunks;
-    if (nwg < 2u * H * max_chunks || nwg > 512u || 3u * hd > 2u * kMkThreads || (nqkv + nprod - 1u) / nprod > cap_d ||
-        2u * ((F + nprod - 1u) / nprod) > 2u * cap_d || nqkv > kVec * kMkThreads) {
+    // most rows of one producer under the line-granular split
+    auto max_rows = [&](uint32_t total) { return ((total + kLine - 1u) / kLine + nprod - 1u) / nprod * kLine; };
+    if (nwg < 2u * H * max_chunks || nwg > 512u || 3u * hd > 2u * kMkThreads || max_rows(nqkv) > cap_d ||
+        max_rows(F) > cap_d || nqkv > kVec * kMkThreads) {
         mk_destroy(g);
         return VRT_OK;
     }
@@ -1504,7 +1586,7 @@ int mk_setup(vrt_g3* g) {
     P.lds.mw = take((8u * kMaxChunks + 16u) * 4u);
     P.lds.gu = take(2u * ((F + nprod - 1u) / nprod + 1u) * 4u);
     P.lds.red = take((4u + 9u) * kMkWaves * 8u);
-    P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + 2u * H)) * 4u, kLmRing * kLmTileBytes));
+    P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + kLine * H)) * 4u, kLmRing * kLmTileBytes));
     P.lds.total = off;
     mk->lds_bytes = off;
     if (off > kMkLdsBytes) { mk_destroy(g); return VRT_OK; }
@@ -1513,7 +1595,7 @@ int mk_setup(vrt_g3* g) {
     void* p;
     if (int rc = mk_alloc(mk, nqkv * 8u, &p)) return rc;
     P.x_qkv = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, static_cast<size_t>(kMaxChunks) * (qw + 2u * H) * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, static_cast<size_t>(kMaxChunks) * (qw + kLine * H) * 8u, &p)) return rc;
     P.x_part = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
     P.x_o = static_cast<u64*>(p);
@@ -1521,7 +1603,7 @@ int mk_setup(vrt_g3* g) {
     P.x_g = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
     P.x_f = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, 2u * nwg * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, kLine * nwg * 8u, &p)) return rc;
     P.x_am = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, 64, &p)) return rc;
     P.abort_flag = static_cast<uint32_t*>(p);
@@ -1581,11 +1663,11 @@ int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uin
     uint64_t cnt = 0;
     switch (which) {
     case 0: src = P.x_qkv; cnt = qw + 2u * P.hd; break;
-    case 1: src = P.x_part; cnt = static_cast<uint64_t>(kMaxChunks) * (qw + 2u * P.H); break;
+    case 1: src = P.x_part; cnt = static_cast<uint64_t>(kMaxChunks) * (qw + kLine * P.H); break;
     case 2: src = P.x_o; cnt = P.d; break;
     case 3: src = P.x_g; cnt = P.F; break;
     case 4: src = P.x_f; cnt = P.d; break;
-    case 5: src = P.x_am; cnt = 2u * P.nwg; break;
+    case 5: src = P.x_am; cnt = kLine * P.nwg; break;
     default: return set_error(VRT_ERR_INVALID, "unknown exchange buffer %u", which);
     }
     *n = cnt;
@@ -1612,12 +1694,12 @@ int mk_run(vrt_g3* g, uint32_t nsteps) {
         const uint32_t d = g->cfg.embedding_length, F = g->cfg.feed_forward_length;
         const uint32_t qw = g->cfg.head_count * g->cfg.head_dim;
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_qkv, 0, (qw + 2u * g->cfg.head_dim) * 8u, g->ctx->stream));
-        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_part, 0, static_cast<size_t>(kMaxChunks) * (qw + 2u * g->cfg.head_count) * 8u,
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_part, 0, static_cast<size_t>(kMaxChunks) * (qw + kLine * g->cfg.head_count) * 8u,
                                      g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_o, 0, d * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_g, 0, F * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_f, 0, d * 8u, g->ctx->stream));
-        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_am, 0, 2u * mk->grid * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_am, 0, kLine * mk->grid * 8u, g->ctx->stream));
         g->mk_tag = 1u;
     }
     uint32_t tag0 = g->mk_tag;
