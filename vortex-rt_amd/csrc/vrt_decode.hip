@@ -70,6 +70,7 @@ constexpr uint32_t kMkWaves = kMkThreads / 64;
 constexpr uint32_t kVec = 4;                 // vector elements per thread (vectors <= 2048)
 constexpr uint32_t kSpinLimit = 1u << 21;    // polls before a hand-off is declared lost
 constexpr int kPollSleep = 4;                // s_sleep between unsuccessful polls (64 clocks each)
+constexpr uint32_t kResidWaves = 4;          // waves that compute a residual fold + norm (one per SIMD)
 constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
 constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x query heads) per block
 constexpr uint32_t kLmUnits = 4;             // 16-byte LM-head loads per thread per tile
@@ -304,7 +305,7 @@ __device__ __forceinline__ float mk_gelu(float x) {
 // ---- LDS views -----------------------------------------------------------------------------
 
 struct MkSmem {
-    float* h;       // residual stream (wave 0 only)
+    float* h;       // residual stream
     float* xs;      // matvec input of phases C and E
     float* xa;      // normed input of phase A and of the LM head
     float* xd;      // normed input of phase D
@@ -639,66 +640,75 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
             if (live[k]) reinterpret_cast<float2*>(y_lds)[threadIdx.x + kMkThreads * k] = make_float2(y[2 * k], y[2 * k + 1]);
     }
     if (wave == 0u) __builtin_amdgcn_s_waitcnt(0);   // the staged weights are in LDS (vmcnt covers LDS loads)
-    mark(mk0);
-    if (blk_any(fail, any_id)) return 1;
-    mark(mk0 + 1u);
+    // Waves 0..kResidWaves-1 (one per SIMD) compute the fold and both norms, each for the whole
+    // vector (the sums need every element); the others wait at the closing barrier. h is read
+    // before the barrier below and rewritten after it, so no wave reads a rewritten h.
+    const bool comp = wave < kResidWaves;
     float2 h[EP];
     bool live[EP];
 #pragma unroll
     for (int k = 0; k < EP; ++k) {
         const uint32_t j = lane + 64u * static_cast<uint32_t>(k);
         live[k] = j < npair;
-        h[k] = live[k] ? reinterpret_cast<const float2*>(hl)[j] : make_float2(0.0f, 0.0f);
+        h[k] = comp && live[k] ? reinterpret_cast<const float2*>(hl)[j] : make_float2(0.0f, 0.0f);
     }
-    if (ysrc) {
-        float2 y[EP];
-        double sq[2 * EP];
+    mark(mk0);
+    if (blk_any(fail, any_id)) return 1;
+    mark(mk0 + 1u);
+    if (comp) {
+        if (ysrc) {
+            float2 y[EP];
+            double sq[2 * EP];
 #pragma unroll
-        for (int k = 0; k < EP; ++k) {
-            y[k] = live[k] ? reinterpret_cast<const float2*>(y_lds)[lane + 64u * k] : make_float2(0.0f, 0.0f);
-            sq[2 * k] = static_cast<double>(y[k].x) * static_cast<double>(y[k].x);
-            sq[2 * k + 1] = static_cast<double>(y[k].y) * static_cast<double>(y[k].y);
-        }
-        const float sc = mk_rms_scale(wave_red_sum_d(tree_sum(sq)), d, eps);
-#pragma unroll
-        for (int k = 0; k < EP; ++k) {
-            const float2 wp = reinterpret_cast<const float2*>(nw_post)[live[k] ? lane + 64u * k : 0u];
-            h[k].x = y[k].x * (sc * wp.x) + h[k].x;
-            h[k].y = y[k].y * (sc * wp.y) + h[k].y;
-        }
-    }
-    int nf = 0;
-    double sq2[2 * EP];
-#pragma unroll
-    for (int k = 0; k < EP; ++k) {
-        const float2 v = live[k] ? h[k] : make_float2(0.0f, 0.0f);
-        nf |= !__builtin_isfinite(v.x) || !__builtin_isfinite(v.y);
-        sq2[2 * k] = static_cast<double>(v.x) * static_cast<double>(v.x);
-        sq2[2 * k + 1] = static_cast<double>(v.y) * static_cast<double>(v.y);
-    }
-    bad = __builtin_amdgcn_ballot_w64(nf != 0) != 0u;
-    const float sc2 = mk_rms_scale(wave_red_sum_d(tree_sum(sq2)), d, eps);
-    mark(mk0 + 2u);
-#pragma unroll
-    for (int k = 0; k < EP; ++k)
-        if (live[k]) {
-            const uint32_t j = lane + 64u * k;
-            const float2 wn = reinterpret_cast<const float2*>(nw_next)[j];
-            float2 x;
-            if constexpr (INTO) {
-                x.x = h[k].x * sc2 * wn.x;
-                x.y = h[k].y * sc2 * wn.y;
-            } else {
-                x.x = h[k].x * (sc2 * wn.x);
-                x.y = h[k].y * (sc2 * wn.y);
+            for (int k = 0; k < EP; ++k) {
+                y[k] = live[k] ? reinterpret_cast<const float2*>(y_lds)[lane + 64u * k] : make_float2(0.0f, 0.0f);
+                sq[2 * k] = static_cast<double>(y[k].x) * static_cast<double>(y[k].x);
+                sq[2 * k + 1] = static_cast<double>(y[k].y) * static_cast<double>(y[k].y);
             }
-            reinterpret_cast<float2*>(hl)[j] = h[k];
-            reinterpret_cast<float2*>(x_lds)[j] = x;
-            if (x_glob && wave == 0u) {
-                gp(x_glob)[2u * j] = x.x;
-                gp(x_glob)[2u * j + 1u] = x.y;
+            const float sc = mk_rms_scale(wave_red_sum_d(tree_sum(sq)), d, eps);
+#pragma unroll
+            for (int k = 0; k < EP; ++k) {
+                const float2 wp = reinterpret_cast<const float2*>(nw_post)[live[k] ? lane + 64u * k : 0u];
+                h[k].x = y[k].x * (sc * wp.x) + h[k].x;
+                h[k].y = y[k].y * (sc * wp.y) + h[k].y;
             }
         }
+        int nf = 0;
+        double sq2[2 * EP];
+#pragma unroll
+        for (int k = 0; k < EP; ++k) {
+            const float2 v = live[k] ? h[k] : make_float2(0.0f, 0.0f);
+            nf |= !__builtin_isfinite(v.x) || !__builtin_isfinite(v.y);
+            sq2[2 * k] = static_cast<double>(v.x) * static_cast<double>(v.x);
+            sq2[2 * k + 1] = static_cast<double>(v.y) * static_cast<double>(v.y);
+        }
+        bad = __builtin_amdgcn_ballot_w64(nf != 0) != 0u;   // used by wave 0
+        const float sc2 = mk_rms_scale(wave_red_sum_d(tree_sum(sq2)), d, eps);
+        mark(mk0 + 2u);
+#pragma unroll
+        for (int k = 0; k < EP; ++k)
+            if (live[k]) {
+                const uint32_t j = lane + 64u * k;
+                const float2 wn = reinterpret_cast<const float2*>(nw_next)[j];
+                float2 x;
+                if constexpr (INTO) {
+                    x.x = h[k].x * sc2 * wn.x;
+                    x.y = h[k].y * sc2 * wn.y;
+                } else {
+                    x.x = h[k].x * (sc2 * wn.x);
+                    x.y = h[k].y * (sc2 * wn.y);
+                }
+                if (static_cast<uint32_t>(k) % kResidWaves == wave) {   // the computing waves share the writes
+                    reinterpret_cast<float2*>(hl)[j] = h[k];
+                    reinterpret_cast<float2*>(x_lds)[j] = x;
+                }
+                if (x_glob && wave == 0u) {
+                    gp(x_glob)[2u * j] = x.x;
+                    gp(x_glob)[2u * j + 1u] = x.y;
+                }
+            }
+    }
+    __syncthreads();   // h and x are complete for every wave
     return 0;
 }
 
@@ -1313,17 +1323,19 @@ __device__ __attribute__((noinline)) void mk_embed(uint32_t token) {
 #pragma clang fp contract(off)
     MK_LOCALS;
     MK_UNIFORM(token);
-    if (__builtin_amdgcn_readfirstlane(wave) != 0u) return;   // h belongs to wave 0
-    const VRT_AS_GLOBAL uint8_t* row = gp(g_mk.tok_embd) + static_cast<uint64_t>(token) * rb_d;
-    for (uint32_t j = lane; 2u * j < d; j += 64u) {
-        const uint32_t i = 2u * j;
-        const VRT_AS_GLOBAL uint8_t* b = row + (i >> 5) * 34u;
-        const float sc = half_bits_to_float(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
-        float2 v;
-        v.x = (sc * static_cast<float>(static_cast<int8_t>(b[2 + (i & 31u)]))) * g_mk.emb_scale;
-        v.y = (sc * static_cast<float>(static_cast<int8_t>(b[3 + (i & 31u)]))) * g_mk.emb_scale;
-        reinterpret_cast<float2*>(m.h)[j] = v;
+    if (__builtin_amdgcn_readfirstlane(wave) == 0u) {   // wave 0 writes h
+        const VRT_AS_GLOBAL uint8_t* row = gp(g_mk.tok_embd) + static_cast<uint64_t>(token) * rb_d;
+        for (uint32_t j = lane; 2u * j < d; j += 64u) {
+            const uint32_t i = 2u * j;
+            const VRT_AS_GLOBAL uint8_t* b = row + (i >> 5) * 34u;
+            const float sc = half_bits_to_float(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
+            float2 v;
+            v.x = (sc * static_cast<float>(static_cast<int8_t>(b[2 + (i & 31u)]))) * g_mk.emb_scale;
+            v.y = (sc * static_cast<float>(static_cast<int8_t>(b[3 + (i & 31u)]))) * g_mk.emb_scale;
+            reinterpret_cast<float2*>(m.h)[j] = v;
+        }
     }
+    __syncthreads();   // the next residual fold reads h before its first barrier
 }
 
 template <int SD, int SA, int SF, int EP>
