@@ -122,19 +122,14 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
     }
 }
 
-// g = gelu_tanh(gate) * up for row t (gu = [gate(F) | up(F)] per row), as f16 hi/lo
-// (shaders/gelu_mul.comp:23-31).
-__global__ void __launch_bounds__(kPfThreads) k_pf_gelu(const float* gu, uint32_t F, _Float16* xhi, _Float16* xlo) {
+// gelu_tanh(gate) * up (shaders/gelu_mul.comp:23-31), every operation rounded to fp32.
+__device__ __forceinline__ float pf_gelu_mul(float x, float up) {
 #pragma clang fp contract(off)
-    const uint32_t t = blockIdx.x;
-    const float* r = gu + static_cast<uint64_t>(t) * 2u * F;
-    for (uint32_t i = threadIdx.x; i < F; i += kPfThreads) {
-        const float x = r[i];
-        const float cubic = x * x * x;
-        const float g = 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * cubic)));
-        pf_split(g * r[F + i], xhi + static_cast<uint64_t>(t) * F + i, xlo + static_cast<uint64_t>(t) * F + i);
-    }
+    const float cubic = x * x * x;
+    const float g = 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * cubic)));
+    return g * up;
 }
+
 
 // ---- GEMM on MFMA: Q8_0 weights or fp32 rows as B ---------------------------------------------
 
@@ -157,6 +152,7 @@ struct PfGemm {
     uint64_t c_bs;
     uint32_t M, N, K;
     uint32_t window;         // causal modes: keys older than window positions are skipped (0: none)
+    uint32_t glu;            // Q8_0 GEMM: w[0] = gate, w[1] = up (N = 2F), output gelu_tanh(gate) * up
 };
 
 // One 32 x 32 tile of C per workgroup (v_mfma_f32_32x32x16_f16); the four waves split the
@@ -365,7 +361,8 @@ constexpr uint32_t kQgBM = 64;
 constexpr uint32_t kQgBK = 64;
 constexpr uint32_t kQgPitch = kQgBK * 2u + 16u;   // LDS row pitch in bytes (f16 rows, padded)
 
-constexpr uint32_t kQgDepth = 5;   // K steps loaded together into registers
+constexpr uint32_t kQgAhead = 4;   // K steps whose loads are in flight ahead of the one computed
+constexpr uint32_t kQgChunk = 12;  // K steps per straight-line chunk of the main loop
 
 template <int WN, int NWN>
 __global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
@@ -399,7 +396,10 @@ __global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
     static_assert(2u * BN <= NT, "one W block per thread");
     const bool wlive_t = tid < 2u * BN && n0 + wr < G.N;
     const uint8_t* wrow = G.w[0];
-    {
+    if (G.glu) {   // 64-column groups: 32 gate rows, then the same 32 up rows
+        const uint32_t n = wlive_t ? n0 + wr : 0u;
+        wrow = ((n & 63u) < 32u ? G.w[0] : G.w[1]) + static_cast<uint64_t>(32u * (n >> 6) + (n & 31u)) * row_bytes;
+    } else {
         uint32_t r = wlive_t ? n0 + wr : 0u;
         if (G.nseg > 1u && r >= G.rows[0]) {
             r -= G.rows[0];
@@ -505,27 +505,56 @@ __global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
         }
     };
 
-    // kQgDepth steps are loaded into registers together, then stored to the two LDS stages in
-    // turn (one barrier per step): the later steps' loads overlap the earlier steps' MFMAs. The
-    // loads are consumed in the loop iteration that issues them, so the compiler waits for
-    // exactly the step it stores (a value carried across the back edge would make it wait for
-    // every load in flight).
-    Stage R[kQgDepth];
-    for (uint32_t i = 0; i < nsteps; i += kQgDepth) {
+    // The K loop runs in straight-line chunks of kQgChunk steps with a ring of kQgAhead register
+    // stages: step j's loads are issued kQgAhead steps before it is stored to LDS, so they
+    // overlap the MFMAs of the steps in between. Every load is issued unconditionally (clamped,
+    // in-bounds addresses; steps past the end re-load the last one and are never stored), and
+    // no loaded value crosses a chunk boundary: with no branch around a load and no value live
+    // across a back edge, the compiler waits for exactly the step it stores.
+    static_assert(kQgAhead <= kQgChunk, "ring inside a chunk");
+    for (uint32_t i = 0; i < nsteps; i += kQgChunk) {
+        Stage R[kQgAhead];
+        auto clamp = [&](uint32_t j) { return min(i + j, nsteps - 1u); };
 #pragma unroll
-        for (uint32_t u = 0; u < kQgDepth; ++u)
-            if (i + u < nsteps) load(i + u, R[u]);
+        for (uint32_t u = 0; u < kQgAhead; ++u) load(clamp(u), R[u]);
 #pragma unroll
-        for (uint32_t u = 0; u < kQgDepth; ++u) {
+        for (uint32_t u = 0; u < kQgChunk; ++u) {
             const uint32_t j = i + u;
             if (j < nsteps) {
                 // stage j & 1 was last read by step j - 2, which every wave finished before the
                 // barrier of step j - 1
-                store(R[u], j & 1u, j);
+                store(R[u % kQgAhead], j & 1u, j);
                 __syncthreads();
-                compute(j & 1u);
+            }
+            if (u + kQgAhead < kQgChunk) load(clamp(u + kQgAhead), R[u % kQgAhead]);
+            if (j < nsteps) compute(j & 1u);
+        }
+    }
+    if (G.glu) {
+        // the wave holding a group's up columns hands them to the wave holding its gate columns
+        // (gelu_tanh(gate) * up, shaders/gelu_mul.comp:23-31)
+        static_assert(WN == 1, "one 32-column MFMA tile per wave");
+        __syncthreads();   // every wave is done reading the LDS stages
+        float* xch = reinterpret_cast<float*>(&s_a[0][0][0]);
+        const uint32_t pair = wm * (NWN / 2u) + (wn >> 1);
+        if (wn & 1u) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xch[(pair * 16u + r) * 64u + lane] = acc[0][r];
+        }
+        __syncthreads();
+        if (wn & 1u) return;
+        const uint32_t F = G.N / 2u;
+        const uint32_t col = n0 / 2u + 32u * (wn >> 1) + l32;
+        if (col >= F) return;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = m0 + 32u * wm + 8u * (r / 4) + 4u * kh + (r % 4);
+            if (row < G.M) {
+                const uint64_t o = static_cast<uint64_t>(row) * G.ldc + col;
+                pf_split(pf_gelu_mul(acc[0][r], xch[(pair * 16u + r) * 64u + lane]), G.chi + o, G.clo + o);
             }
         }
+        return;
     }
     float* c = G.c + static_cast<uint64_t>(z) * G.c_bs;
 #pragma unroll
@@ -677,6 +706,32 @@ static int pf_gemm(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t
     const uint32_t mt = (M + kQgBM - 1u) / kQgBM;
     if (G.N % 128u == 0u && (G.N / 128u) * mt >= 128u) return pf_launch_q8<1, 4>(G, splits, s);
     return pf_launch_q8<1, 2>(G, splits, s);
+}
+
+// gelu_tanh(A Wg^T) * (A Wu^T) as f16 hi/lo [M][F] (row stride F): the gate/up GEMM with the
+// product in its epilogue (src/gemma3.cpp:1720-1801 up to the down projection), one K split.
+static int pf_gemm_glu(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t M, uint32_t K, const uint8_t* wg,
+                       const uint8_t* wu, uint32_t F, _Float16* ohi, _Float16* olo, hipStream_t s) {
+    PfGemm G{};
+    G.ahi = ahi;
+    G.alo = alo;
+    G.lda = K;
+    G.w[0] = wg;
+    G.w[1] = wu;
+    G.rows[0] = G.rows[1] = F;
+    G.nseg = 2u;
+    G.N = 2u * F;
+    G.w_end = g->P.arena_end;
+    G.chi = ohi;
+    G.clo = olo;
+    G.ldc = F;
+    G.M = M;
+    G.K = K;
+    G.glu = 1u;
+    if (K % 32u != 0u || F % 32u != 0u) return set_error(VRT_ERR_INVALID, "prefill GEMM shape not supported");
+    const uint32_t mt = (M + kQgBM - 1u) / kQgBM;
+    if (G.N % 128u == 0u && (G.N / 128u) * mt >= 128u) return pf_launch_q8<1, 4>(G, 1u, s);
+    return pf_launch_q8<1, 2>(G, 1u, s);
 }
 
 // K splits of the 640-row projections (O and down): enough workgroups to cover the CUs.
@@ -852,15 +907,13 @@ int pf_run(vrt_g3* g, uint32_t T) {
             void* args[] = {&h, &f, &so, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
             if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }
-        if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wg, F}, {Ly.wu, F}}, big, 1, s)) return rc;
-        {
-            const float* gu = big;
-            void* args[] = {&gu, &F, &ahi, &alo};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_gelu), dim3(T), args)) return rc;
-        }
+        // gelu(gate) * up as f16 hi/lo in `big` (the gate/up GEMM still reads ahi/alo)
+        _Float16* ghi = reinterpret_cast<_Float16*>(big);
+        _Float16* glo = ghi + static_cast<uint64_t>(T) * F;
+        if (int rc = pf_gemm_glu(g, ahi, alo, T, d, Ly.wg, Ly.wu, F, ghi, glo, s)) return rc;
         // the last block's output row feeds the LM head directly: no split partials there
         s_down = l + 1u < L ? std::max(1u, std::min(s_o, (F / 32u) / 2u)) : 1u;
-        if (int rc = pf_gemm(g, ahi, alo, T, F, {{Ly.wd, d}}, x, s_down, s)) return rc;
+        if (int rc = pf_gemm(g, ghi, glo, T, F, {{Ly.wd, d}}, x, s_down, s)) return rc;
     }
     // last position: its FFN output and residual feed the decode step's final norm + LM head
     VRT_HIP_CHECK(hipMemcpyAsync(P.f, x + static_cast<uint64_t>(T - 1u) * d, d * 4u, hipMemcpyDeviceToDevice, s));
