@@ -1551,9 +1551,9 @@ int mk_setup(vrt_g3* g) {
     const uint32_t max_chunks = std::min(kMaxChunks, kMaxBUnits / H);
     const uint32_t nprod = nwg - H * max_chunks;
     // most rows of one producer under the line-granular split
-    auto max_rows = [&](uint32_t total) { return ((total + kLine - 1u) / kLine + nprod - 1u) / nprod * kLine; };
-    if (nwg < 2u * H * max_chunks || nwg > 512u || 3u * hd > 2u * kMkThreads || max_rows(nqkv) > cap_d ||
-        max_rows(F) > cap_d || nqkv > kVec * kMkThreads) {
+    auto max_rows = [&](uint32_t total, uint32_t gr) { return ((total + gr - 1u) / gr + nprod - 1u) / nprod * gr; };
+    if (nwg < 2u * H * max_chunks || nwg > 512u || 3u * hd > 2u * kMkThreads || max_rows(nqkv, kLine) > cap_d ||
+        max_rows(F, kLine) > cap_d || nqkv > kVec * kMkThreads) {
         mk_destroy(g);
         return VRT_OK;
     }
@@ -1561,8 +1561,10 @@ int mk_setup(vrt_g3* g) {
     P.eos = g->P.eos;
     P.eps = g->P.eps; P.emb_scale = g->P.emb_scale; P.attn_scale = g->P.attn_scale;
     P.nwg = nwg;
-    P.nc = std::min(nwg, (d + cap_a - 1u) / cap_a);
-    P.ne = std::min(nwg, (d + cap_f - 1u) / cap_f);
+    // C and E: four output rows (half a 64-byte line) per workgroup: more workgroups, shorter
+    // matvecs (C's workgroups stay clear of the attention units at the end)
+    P.nc = std::min(nwg - H * max_chunks, (d + std::min(cap_a, kLine / 2u) - 1u) / std::min(cap_a, kLine / 2u));
+    P.ne = std::min(nwg, (d + std::min(cap_f, kLine / 2u) - 1u) / std::min(cap_f, kLine / 2u));
     if ((d + P.nc - 1u) / P.nc > cap_a || (d + P.ne - 1u) / P.ne > cap_f) { mk_destroy(g); return VRT_OK; }
     P.chunk_min = 32u;
     P.max_chunks = max_chunks;
