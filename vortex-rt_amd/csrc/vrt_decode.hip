@@ -179,87 +179,6 @@ __device__ __forceinline__ void mk_flag_min(uint32_t v) {
     __hip_atomic_fetch_min(gp(&g_mk.st->nonfinite), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls word off[k] / 8 of the buffer r for each k < MAXK with live[k], until every live tag
-// equals `tag`; the values land in out[k]. Returns 0, or 1 if the wait was abandoned (abort
-// raised); the caller turns the per-thread result into a workgroup decision at its next
-// barrier. The polls are system-coherent buffer loads (a load past the buffer's range
-// returns 0 and is never used). Each round re-issues every load, then waits once, so a
-// round's loads are in flight together; the compiler barrier keeps the loads inside the loop.
-template <int MAXK>
-__device__ __forceinline__ int ll_poll(__amdgpu_buffer_rsrc_t r, const int (&off)[MAXK], const bool (&live)[MAXK],
-                                       uint32_t tag, float (&out)[MAXK]) {
-    v2u v[MAXK];
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b64(r, off[k], 0, kCoherent);
-    int fail = 0;
-    uint32_t spins = 0;
-    for (;;) {
-        bool ready = true;
-#pragma unroll
-        for (int k = 0; k < MAXK; ++k) ready &= v[k].y == tag || !live[k];
-        if (ready) break;
-        if ((++spins & 63u) == 0u && (spins > kSpinLimit || mk_aborted())) {
-            fail = 1;
-            mk_abort();
-            break;
-        }
-        __builtin_amdgcn_s_sleep(kPollSleep);   // back off: fewer polls in flight while the data is far off
-        __asm__ volatile("" ::: "memory");
-#pragma unroll
-        for (int k = 0; k < MAXK; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b64(r, off[k], 0, kCoherent);
-    }
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k) out[k] = __uint_as_float(v[k].x);
-    return fail;
-}
-
-// Polls src[i] for i = tid + kMkThreads * k (k < MAXK, i < n); see ll_poll.
-template <int MAXK>
-__device__ __forceinline__ int ll_wait(const u64* src, uint32_t n, uint32_t tag, float (&out)[MAXK]) {
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(src), 0, static_cast<int>(n * 8u), kRsrcFlags);
-    int off[MAXK];
-    bool live[MAXK];
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k) {
-        const uint32_t i = threadIdx.x + static_cast<uint32_t>(k) * kMkThreads;
-        off[k] = static_cast<int>(i * 8u);
-        live[k] = i < n;
-    }
-    return ll_poll<MAXK>(r, off, live, tag, out);
-}
-
-// As ll_wait, for this thread's elements j = tid + kMkThreads * k (j < nj) at arbitrary
-// word indices idx[k] of src[0..n).
-template <int MAXK>
-__device__ __forceinline__ int ll_wait_at(const u64* src, uint32_t n, const uint32_t (&idx)[MAXK], uint32_t nj,
-                                          uint32_t tag, float (&out)[MAXK]) {
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(src), 0, static_cast<int>(n * 8u), kRsrcFlags);
-    int off[MAXK];
-    bool live[MAXK];
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k) {
-        off[k] = static_cast<int>(idx[k] * 8u);
-        live[k] = threadIdx.x + static_cast<uint32_t>(k) * kMkThreads < nj;
-    }
-    return ll_poll<MAXK>(r, off, live, tag, out);
-}
-
-// ll_wait into LDS dst[0..n), then a barrier (flag set any_id); false (in every thread) if
-// abandoned.
-template <int MAXK>
-__device__ __forceinline__ bool ll_gather(const u64* src, uint32_t n, uint32_t tag, float* dst, uint32_t any_id) {
-    float v[MAXK];
-    const int fail = ll_wait<MAXK>(src, n, tag, v);
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k) {
-        const uint32_t i = threadIdx.x + static_cast<uint32_t>(k) * kMkThreads;
-        if (i < n) dst[i] = v[k];
-    }
-    return !blk_any(fail, any_id);
-}
-
 // ---- workgroup reductions (one barrier each) ----------------------------------------------------
 
 struct BlkRed {
@@ -529,7 +448,9 @@ __device__ __forceinline__ float wave_sum8_t(const float (&v)[8]) {
 
 // Polls 16-byte units (two tagged words each) at byte offsets off[k] of r until both tags of
 // every unit equal `tag` (or !live); out[2k], out[2k+1] get the two values of unit k. Returns
-// 0, or 1 if the wait was abandoned (abort raised).
+// 0, or 1 if the wait was abandoned (abort raised); the caller turns the per-thread result
+// into a workgroup decision at its next barrier. The polls are system-coherent buffer loads
+// (a load past the buffer's range returns 0 and is never used), backing off between rounds.
 template <int MAXK>
 __device__ __forceinline__ int ll_poll2(__amdgpu_buffer_rsrc_t r, const int (&off)[MAXK], const bool (&live)[MAXK],
                                         uint32_t tag, float (&out)[2 * MAXK]) {
@@ -559,6 +480,29 @@ __device__ __forceinline__ int ll_poll2(__amdgpu_buffer_rsrc_t r, const int (&of
         out[2 * k + 1] = __uint_as_float(v[k].z);
     }
     return fail;
+}
+
+// Gathers the tagged words src[0..n) (n even) into LDS dst[0..n), then a barrier (flag set
+// any_id); false (in every thread) if abandoned. Thread t polls the 16-byte pairs
+// t + kMkThreads p, p < MAXP: half the requests of word-sized polls.
+template <int MAXP>
+__device__ __forceinline__ bool ll_gather2(const u64* src, uint32_t n, uint32_t tag, float* dst, uint32_t any_id) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(src), 0, static_cast<int>(n * 8u), kRsrcFlags);
+    int off[MAXP];
+    bool live[MAXP];
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+        const uint32_t j = threadIdx.x + static_cast<uint32_t>(p) * kMkThreads;
+        live[p] = 2u * j < n;
+        off[p] = live[p] ? static_cast<int>(j * 16u) : 0x7ffffff0;   // past the buffer: no access
+    }
+    float v[2 * MAXP];
+    const int fail = ll_poll2<MAXP>(r, off, live, tag, v);
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p)
+        if (live[p]) reinterpret_cast<float2*>(dst)[threadIdx.x + p * kMkThreads] = make_float2(v[2 * p], v[2 * p + 1]);
+    return !blk_any(fail, any_id);
 }
 
 // 1.0f / std::sqrt(float(sum_sq / n) + eps) for n a power of two: sum_sq * (1/n) is the exact
@@ -1037,7 +981,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
     float* parts = m.u;
     const uint32_t ntot = nch * part_stride;
     for (uint32_t o = 0; o < ntot; o += kPartRound)
-        if (!ll_gather<kPartRound / kMkThreads>(g_mk.x_part + o, min(kPartRound, ntot - o), tB, parts + o,
+        if (!ll_gather2<kPartRound / kMkThreads / 2>(g_mk.x_part + o, min(kPartRound, ntot - o), tB, parts + o,
                                                  (o / kPartRound) & 1u ? kAnyGather1 : kAnyGather0))
             return false;
     MK_MARK(12);
@@ -1150,7 +1094,7 @@ __device__ __attribute__((noinline)) bool mk_phase_e(uint32_t l, uint32_t tagb, 
     auto rowp = [=](uint32_t v) { return wd + static_cast<uint64_t>(v) * rb_f; };
     RowBatch<SF, 1, 1> rb;
     batch_load<SF, 1, 1>(rowp, nblk_f, g_mk.arena_end, v0, v1, wave, rb);
-    if (!ll_gather<kVec>(g_mk.x_g, F, tD, m.xs, kAnyGatherE)) return false;
+    if (!ll_gather2<kVec / 2>(g_mk.x_g, F, tD, m.xs, kAnyGatherE)) return false;
     MK_MARK(21);
     u64* out = g_mk.x_f;
     batch_consume_x<SF, 1, 1>(rb, nblk_f, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tE); });
@@ -1282,20 +1226,19 @@ __device__ __attribute__((noinline)) MkArg mk_reduce_argmax(uint32_t tag) {
     __shared__ uint32_t s_i[kMkWaves];
     float* buf = m.sc;   // 2 * nwg floats
     bool good;
-    {   // value and index of workgroup k: words kLine k and kLine k + 1
-        uint32_t idx[2];
+    {   // value and index of workgroup k: the 16-byte pair at words kLine k, kLine k + 1
+        static_assert(kMkThreads >= 512u, "one pair per thread for up to 512 workgroups");
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            g_mk.x_am, 0, static_cast<int>(kLine * g_mk.nwg * 8u), kRsrcFlags);
+        int off[1];
+        bool live[1];
+        live[0] = tid < g_mk.nwg;
+        off[0] = live[0] ? static_cast<int>(tid * kLine * 8u) : 0x7ffffff0;   // past the buffer: no access
         float v[2];
-        const uint32_t nj = 2u * g_mk.nwg;
-#pragma unroll
-        for (uint32_t k = 0; k < 2u; ++k) {
-            const uint32_t j = tid + k * kMkThreads;
-            idx[k] = j < nj ? (j >> 1) * kLine + (j & 1u) : 0u;
-        }
-        const int fail = ll_wait_at<2>(g_mk.x_am, kLine * g_mk.nwg, idx, nj, tag, v);
-#pragma unroll
-        for (uint32_t k = 0; k < 2u; ++k) {
-            const uint32_t j = tid + k * kMkThreads;
-            if (j < nj) buf[j] = v[k];
+        const int fail = ll_poll2<1>(r, off, live, tag, v);
+        if (live[0]) {
+            buf[2u * tid] = v[0];
+            buf[2u * tid + 1u] = v[1];
         }
         good = !blk_any(fail, kAnyArgmax);
     }
