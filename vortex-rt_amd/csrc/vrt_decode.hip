@@ -73,8 +73,9 @@ constexpr int kPollSleep = 4;                // s_sleep between unsuccessful pol
 constexpr uint32_t kResidWaves = 4;          // waves that compute a residual fold + norm (one per SIMD)
 constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
 constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x query heads) per block
-constexpr uint32_t kLmUnits = 4;             // 16-byte LM-head loads per thread per tile
-constexpr uint32_t kLmRing = 3;              // LM-head tiles in flight per workgroup (LDS ring)
+constexpr uint32_t kLmUnits = 3;             // 16-byte LM-head loads per thread per tile
+constexpr uint32_t kLmRing = 4;              // LM-head tile slots in LDS
+constexpr uint32_t kLmAhead = kLmRing - 1u;  // tiles in flight while one is computed
 constexpr uint32_t kLmTileBytes = kLmUnits * 512u * 16u;
 constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
 constexpr uint32_t kPartRound = 12 * kMkThreads;   // attention partials gathered per wait
@@ -364,7 +365,7 @@ __device__ __forceinline__ uint32_t lm_tile_issue(uint32_t r0, uint32_t r1, uint
 // Waits until this wave's LM-head tile loads issued before the last `later` tiles are complete
 // (vector-memory operations complete in issue order; a later store only makes the wait longer).
 __device__ __forceinline__ void lm_wait_tiles(uint32_t later) {
-    static_assert(kLmUnits * (kLmRing - 1u) <= 15u, "vmcnt immediate");
+    static_assert(kLmUnits * (kLmAhead - 1u) <= 15u, "vmcnt immediate");
     // s_waitcnt: vmcnt in bits 3:0, expcnt (7) and lgkmcnt (15) left unconstrained
     if (later >= 2u) __builtin_amdgcn_s_waitcnt(0x0F70 | (2u * kLmUnits));
     else if (later == 1u) __builtin_amdgcn_s_waitcnt(0x0F70 | kLmUnits);
@@ -1140,50 +1141,60 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
     const uint32_t tiles = (g_mk.V + TR - 1u) / TR;
     const uint32_t ntiles = w < tiles ? (tiles - w + nwg - 1u) / nwg : 0u;
     auto tile_row = [&](uint32_t ti) { return (w + ti * nwg) * TR; };
-    // the first kLmRing tiles are in flight before the final residual is gathered
+    // the first kLmAhead tiles are in flight before the final residual is gathered
     uint8_t* ring = reinterpret_cast<uint8_t*>(m.u);
     auto issue = [&](uint32_t ti) {
         const uint32_t r0 = tile_row(ti);
         return lm_tile_issue(r0, min(g_mk.V, r0 + TR), rb_d, ring + (ti % kLmRing) * kLmTileBytes);
     };
 #pragma unroll
-    for (uint32_t i = 0; i < kLmRing; ++i)
+    for (uint32_t i = 0; i < kLmAhead; ++i)
         if (i < ntiles) (void)issue(i);
     if (!mk_fold<EP>(tagb)) return false;
     MK_MARK(23);
     build_limbs(m.xa, d, m.L);
-    XLimb xl[1];
-    lane_limbs<SD, 1>(m.L, nblk_d, xl);
+    // row slots of LS lanes, LNB blocks per lane: 20-block rows fill 16-lane slots with four
+    // lanes holding two blocks, four rows per wave
+    constexpr int LS = SD >= 32 ? SD / 2 : SD;
+    constexpr int LNB = SD / LS;
+    XLimb xl[LNB];
+    lane_limbs<LS, LNB>(m.L, nblk_d, xl);
     MK_MARK(24);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
-    constexpr uint32_t RPW = 64u / SD;
-    const uint32_t slot = lane / SD, sl = lane % SD;
-    const bool lane_on = sl < nblk_d;
+    constexpr uint32_t RPW = 64u / LS;
+    const uint32_t slot = lane / LS, sl = lane % LS;
     for (uint32_t ti = 0; ti < ntiles; ++ti) {
         const uint32_t t0 = tile_row(ti), t1 = min(g_mk.V, t0 + TR);
         const uint8_t* tile = ring + (ti % kLmRing) * kLmTileBytes;
         const uint32_t pre_cur = static_cast<uint32_t>(
             (reinterpret_cast<uintptr_t>(g_mk.tok_embd) + static_cast<uint64_t>(t0) * rb_d) & 15u);
-        lm_wait_tiles(min(kLmRing - 1u, ntiles - 1u - ti));
-        __syncthreads();   // every wave's share of tile ti is in LDS
+        lm_wait_tiles(min(kLmAhead - 1u, ntiles - 1u - ti));
+        // every wave's share of tile ti is in LDS, and every wave is done with tile ti - 1,
+        // whose slot now takes tile ti + kLmAhead
+        __syncthreads();
+        if (ti + kLmAhead < ntiles) (void)issue(ti + kLmAhead);
         const uint32_t nrows = t1 - t0;
         for (uint32_t rg = wave * RPW; rg < nrows; rg += kMkWaves * RPW) {   // wave-uniform trip count
             const uint32_t r = rg + slot;
             const bool live = r < nrows;
             float acc = 0.0f;
-            if (live && lane_on) {
-                Q8Raw raw;
-                q8_load_lds(tile, pre_cur + r * static_cast<uint32_t>(rb_d) + 34u * sl, raw);
-                acc = q8_dot(raw, xl[0]);
+#pragma unroll
+            for (int b = 0; b < LNB; ++b) {
+                const uint32_t blk = sl + static_cast<uint32_t>(b) * LS;
+                if (live && blk < nblk_d) {
+                    Q8Raw raw;
+                    q8_load_lds(tile, pre_cur + r * static_cast<uint32_t>(rb_d) + 34u * blk, raw);
+                    acc += q8_dot(raw, xl[b]);
+                }
             }
             float tot;
-            if constexpr (SD == 64) {
+            if constexpr (LS == 64) {
                 const float hsum = slot_sum<32>(acc);
                 tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 0)) +
                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 32));
             } else {
-                tot = slot_sum<SD>(acc);
+                tot = slot_sum<LS>(acc);
             }
             if (live && sl == 0u) {
                 const uint32_t v = t0 + r;
@@ -1192,10 +1203,6 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
             }
         }
         if (ti == 0u) MK_MARK(25);
-        if (ti + kLmRing < ntiles) {
-            __syncthreads();   // tile ti's slot is read by every wave before it is refilled
-            (void)issue(ti + kLmRing);
-        }
     }
     MK_MARK(26);
     wave_argmax(bv, bi);
@@ -1513,7 +1520,14 @@ int mk_setup(vrt_g3* g) {
     P.max_chunks = max_chunks;
     P.lm_rows = (c.vocab_size + nwg - 1u) / nwg;
     const uint64_t rb = static_cast<uint64_t>(d / 32u) * 34u;
-    P.lm_tile_rows = static_cast<uint32_t>(std::min<uint64_t>(P.lm_rows, (kLmTileBytes - 16u) / rb));
+    {   // whole passes of the LM-head loop per tile (row slots of sd/2 lanes for 32- and 64-lane shapes)
+        const uint32_t ls = sd.S >= 32 ? sd.S / 2u : sd.S, rpp = kMkWaves * (64u / ls);
+        // margin: the span's alignment offset (< 16 bytes) and the 4 bytes a block read may
+        // take past the last row
+        uint64_t tr = (kLmTileBytes - 24u) / rb;
+        if (tr >= rpp) tr = tr / rpp * rpp;
+        P.lm_tile_rows = static_cast<uint32_t>(std::min<uint64_t>(P.lm_rows, tr));
+    }
     if (P.lm_tile_rows == 0u) { mk_destroy(g); return VRT_OK; }
     uint32_t slots_max = 1;
     for (const auto& Ly : g->layers) slots_max = std::max(slots_max, Ly.slots);
