@@ -73,6 +73,32 @@ def test_tiny_generate_matches_oracle(ctx, tiny_model, tiny_g3):
     assert np.array_equal(got, ref)
 
 
+def test_generate_stops_at_eos(ctx, tiny_model, tmp_path):
+    """EOS is appended and then ends the generation (src/gemma3.cpp:2134-2141), on the
+    persistent kernel and on the multi-kernel path: the same weights with EOS set to a token
+    the greedy loop produces stop right after it."""
+    prompt = synth.uniform_ids(5, 5, 2, 1000)
+    m = oracle.Model(tiny_model)
+    free = m.generate(prompt, 30)
+    m.close()
+    k = next(i for i in range(3, free.size) if free[i] not in free[:i])
+    path = str(tmp_path / "tiny_eos.gguf")
+    synth.write_gemma3_gguf(path, seed=11, eos=int(free[k]), **synth.TINY)
+    m = oracle.Model(path)
+    ref = m.generate(prompt, 30)
+    m.close()
+    assert np.array_equal(ref, free[:k + 1])
+    g = vrt.Gemma3(ctx, path)
+    try:
+        for persistent in (True, False):
+            if persistent and not g.persistent_available():
+                continue
+            g.set_persistent(persistent)
+            assert np.array_equal(g.generate(prompt, 30), ref), f"persistent={persistent}"
+    finally:
+        g.close()
+
+
 def test_graph_replay_equals_eager(ctx, tiny_g3):
     toks = synth.uniform_ids(8, 20, 2, 1000)
     tiny_g3.set_graph(True)

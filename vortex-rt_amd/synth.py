@@ -159,13 +159,14 @@ def write_gemma3_gguf(path, seed: int = 0, n_layers: int = 18, d_model: int = 64
                       head_dim: int = 256, ffn: int = 2048, vocab: int = 262144, context: int = 32768,
                       window: int = 512, eps: float = 1e-6, rope_global: float = 1.0e6,
                       weight_std: float = 0.02, norm_std: float = 0.1, with_window: bool = True,
-                      embd_std: float | None = None):
+                      embd_std: float | None = None, eos: int = 1):
     """A random-init Gemma-3-architecture GGUF carrying every key the reference executor
     requires (src/gemma3.cpp:174-257, :289-313) and the tensor set of :456-505.
     Norm weights are stored as 1 + N(0, norm_std^2): Gemma GGUFs fold the (1 + w)
     convention into the stored value (src/gemma3.cpp:991-996). embd_std (default
     weight_std) sets the tied embedding / LM head alone, so a model whose block
-    projections are all zero (weight_std=0) still has a non-trivial embedding."""
+    projections are all zero (weight_std=0) still has a non-trivial embedding. eos sets
+    tokenizer.ggml.eos_token_id (the weights do not depend on it)."""
     w = GgufWriter(alignment=32)
     w.add("general.architecture", T_STR, "gemma3")
     w.add("general.alignment", T_U32, 32)
@@ -193,7 +194,7 @@ def write_gemma3_gguf(path, seed: int = 0, n_layers: int = 18, d_model: int = 64
     w.add("tokenizer.ggml.scores", T_ARR, (T_F32, np.linspace(0, -1, vocab, dtype=np.float32)))
     w.add("tokenizer.ggml.token_type", T_ARR, (T_I32, np.asarray(types, dtype=np.int32)))
     w.add("tokenizer.ggml.bos_token_id", T_U32, 2)
-    w.add("tokenizer.ggml.eos_token_id", T_U32, 1)
+    w.add("tokenizer.ggml.eos_token_id", T_U32, eos)
     w.add("tokenizer.ggml.unknown_token_id", T_U32, 3)
 
     def q8(name, rows, cols, std=weight_std):
