@@ -78,7 +78,8 @@ constexpr uint32_t kLmRing = 4;              // LM-head tile slots in LDS
 constexpr uint32_t kLmAhead = kLmRing - 1u;  // tiles in flight while one is computed
 constexpr uint32_t kLmTileBytes = kLmUnits * 512u * 16u;
 constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
-constexpr uint32_t kPartRound = 12 * kMkThreads;   // attention partials gathered per wait
+constexpr uint32_t kPartRound = 24 * kMkThreads;   // attention partials gathered per wait (many chunks)
+constexpr uint32_t kPartRoundS = 12 * kMkThreads;  // the same when they all fit in one smaller round
 constexpr int kRsrcFlags = 0x00020000;       // raw buffer resource, 32-bit data format
 // Cache policy of exchange and KV-cache accesses: system scope (sc0 sc1), coherent across the
 // XCDs' L2s. (A tagged exchange among 256 workgroups takes ~2.6 us per round on MI355X with
@@ -694,9 +695,9 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     return true;
 }
 
-constexpr uint32_t kBWaves = 4;                    // waves of an attention unit that take positions
-constexpr uint32_t kBGrp = 32;                     // positions per group (all working waves)
-constexpr uint32_t kBPos = kBGrp / kBWaves;        // positions per wave per group
+constexpr uint32_t kBMaxWaves = 8;                 // waves of an attention unit that take positions (at most)
+constexpr uint32_t kBPos = 8;                      // positions per wave per group
+constexpr uint32_t kBLongChunk = 128;              // chunks at least this long use all kBMaxWaves waves
 
 // Phase B: one workgroup per (chunk c, query head h); waves 0..3 work, the others wait at the
 // closing barrier. Lane i of a wave owns head dims 4i..4i+3. Every working wave gathers its
@@ -732,14 +733,16 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     const uint32_t c0 = t_first + c * clen;
     const uint32_t c1 = min(pos + 1u, c0 + clen);
     const uint32_t uw = __builtin_amdgcn_readfirstlane(wave);   // scalar: positions and branches on SALU
-    const bool worker = uw < kBWaves;
+    // waves taking positions: four (one per SIMD) for short chunks, all eight for long ones
+    const uint32_t nbw = clen >= kBLongChunk ? kBMaxWaves : 4u, grp = nbw * kBPos;
+    const bool worker = uw < nbw;
     const uint32_t dl = lane * 4u;                 // this lane's 4 head dims
     const bool dlive = worker && dl < hd;
     const bool lo = dl < half;                     // first half of the RoPE pairs
     const uint32_t e0 = lo ? dl : dl - half;       // RoPE index of dim dl
     const int partner = static_cast<int>(lo ? lane + (half >> 2) : lane - (half >> 2));
-    float* ra = m.u;                               // [kBWaves][hd] partial sums
-    float* rml = m.mw;                             // [kBWaves] m, then [kBWaves] l
+    float* ra = m.u;                               // [kBMaxWaves][hd] partial sums
+    float* rml = m.mw;                             // [kBMaxWaves] m, then [kBMaxWaves] l
     int fail = 0;
     if (worker) {
         // this wave's K/V rows of the first group, from the cache (device-coherent)
@@ -750,16 +753,16 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         const uint32_t cend = c1 == pos + 1u ? pos : c1;
         // byte offset of this lane's dims of position t (past the buffer for dead lanes: no access)
         auto kv_off = [&](uint32_t t) { return dlive ? static_cast<int>(((t % Ly.slots) * hd + dl) * 4u) : 0x7ffffff0; };
-        // how many of this wave's positions g0 + uw + kBWaves i fall below g1 (wave-uniform)
-        auto nvalid = [&](uint32_t g0, uint32_t g1) { return g1 > g0 + uw ? (g1 - g0 - uw + kBWaves - 1u) / kBWaves : 0u; };
+        // how many of this wave's positions g0 + uw + nbw i fall below g1 (wave-uniform)
+        auto nvalid = [&](uint32_t g0, uint32_t g1) { return g1 > g0 + uw ? (g1 - g0 - uw + nbw - 1u) / nbw : 0u; };
         v4u kr[kBPos], vr[kBPos];
         {
-            const uint32_t nv = nvalid(c0, min(cend, c0 + kBGrp));
+            const uint32_t nv = nvalid(c0, min(cend, c0 + grp));
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i) {
                 kr[i] = vr[i] = v4u{0u, 0u, 0u, 0u};
                 if (i < nv) {
-                    const uint32_t t = c0 + uw + kBWaves * i;
+                    const uint32_t t = c0 + uw + nbw * i;
                     kr[i] = co_ld4(rk, kv_off(t));
                     vr[i] = co_ld4(rv, kv_off(t));
                 }
@@ -842,8 +845,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         const float attn_scale = g_mk.attn_scale;
         static_assert(kBPos == 8u, "one position per lane of each group of 8 lanes");
         const uint32_t pl = lane & 7u;   // the position of this wave's group that this lane scores
-        for (uint32_t g0 = c0; g0 < cend; g0 += kBGrp) {
-            const uint32_t nv = nvalid(g0, min(cend, g0 + kBGrp));
+        for (uint32_t g0 = c0; g0 < cend; g0 += grp) {
+            const uint32_t nv = nvalid(g0, min(cend, g0 + grp));
             float part[kBPos];
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i) {
@@ -852,16 +855,16 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                 for (uint32_t e = 0; e < 4u; ++e) p += q[e] * __uint_as_float(kr[i][e]);
                 part[i] = p;
             }
-            // lane l: the score of position g0 + uw + kBWaves (l & 7). The reduction runs in every
+            // lane l: the score of position g0 + uw + nbw (l & 7). The reduction runs in every
             // lane (its exchanges read all of them); the mask comes after.
             const float st = wave_sum8_t(part);
             const float sl = pl < nv ? st * attn_scale : -INFINITY;
             // the next group's keys load while this group's softmax and values run
-            const uint32_t n0 = g0 + kBGrp;
-            const uint32_t nn = n0 < cend ? nvalid(n0, min(cend, n0 + kBGrp)) : 0u;
+            const uint32_t n0 = g0 + grp;
+            const uint32_t nn = n0 < cend ? nvalid(n0, min(cend, n0 + grp)) : 0u;
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i)
-                if (i < nn) kr[i] = co_ld4(rk, kv_off(n0 + uw + kBWaves * i));
+                if (i < nn) kr[i] = co_ld4(rk, kv_off(n0 + uw + nbw * i));
             if (nv != 0u) {   // this wave has a position in the group
                 float mx = fmaxf(sl, dpp_mov<0xB1>(sl));
                 mx = fmaxf(mx, dpp_mov<0x4E>(mx));
@@ -891,10 +894,10 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             }
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i)
-                if (i < nn) vr[i] = co_ld4(rv, kv_off(n0 + uw + kBWaves * i));
+                if (i < nn) vr[i] = co_ld4(rv, kv_off(n0 + uw + nbw * i));
         }
         // the current position, from registers, by the wave whose turn it is
-        if (c1 == pos + 1u && uw == (pos - c0) % kBWaves) {
+        if (c1 == pos + 1u && uw == (pos - c0) % nbw) {
             float sp[1] = {0.0f};
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e) sp[0] += q[e] * k[e];
@@ -913,7 +916,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         if (dlive) *reinterpret_cast<float4*>(ra + uw * hd + dl) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         if (lane == 0) {
             rml[uw] = m_run;
-            rml[kBWaves + uw] = l_run;
+            rml[kBMaxWaves + uw] = l_run;
         }
         // the appended row is complete before this wave publishes its share of the partial
         if (appender) __builtin_amdgcn_s_waitcnt(0);
@@ -924,25 +927,26 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     u64* part = g_mk.x_part + static_cast<uint64_t>(c) * part_stride;
     if (tid < hd) {
         // wave weights f_k = e^(m_k - M): lane k computes f_k, then every lane takes them by readlane
-        const float mk = lane < kBWaves ? rml[lane] : -INFINITY;
+        const float mk = lane < nbw ? rml[lane] : -INFINITY;
         float M = fmaxf(mk, dpp_mov<0xB1>(mk));
         M = fmaxf(M, dpp_mov<0x4E>(M));
         M = fmaxf(M, dpp_mov<0x141>(M));   // lanes 0..7: the max over the waves
-        static_assert(kBWaves <= 8u, "DPP max over one half row (lanes past kBWaves hold -inf)");
-        const float fk = lane < kBWaves && mk != -INFINITY ? expf(mk - M) : 0.0f;
-        const float lk = lane < kBWaves ? rml[kBWaves + lane] : 0.0f;
-        float f[kBWaves];
+        static_assert(kBMaxWaves <= 8u, "DPP max over one half row (lanes past nbw hold -inf)");
+        const float fk = lane < nbw && mk != -INFINITY ? expf(mk - M) : 0.0f;
+        const float lk = lane < nbw ? rml[kBMaxWaves + lane] : 0.0f;
+        float f[kBMaxWaves];
 #pragma unroll
-        for (uint32_t k = 0; k < kBWaves; ++k) f[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fk), k));
+        for (uint32_t k = 0; k < kBMaxWaves; ++k) f[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fk), k));
         float sacc = 0.0f;
 #pragma unroll
-        for (uint32_t k = 0; k < kBWaves; ++k) sacc += f[k] * ra[k * hd + tid];
+        for (uint32_t k = 0; k < kBMaxWaves; ++k)
+            if (k < nbw) sacc += f[k] * ra[k * hd + tid];   // the other waves' slots are stale
         ll_stf(part + h * hd + tid, sacc, tB);
         if (tid < kLine) {   // this unit's line: m, l, then padding (every word is tagged)
             float L = 0.0f;
 #pragma unroll
-            for (uint32_t k = 0; k < kBWaves; ++k)
-                L += f[k] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lk), k));
+            for (uint32_t k = 0; k < kBMaxWaves; ++k)
+                if (k < nbw) L += f[k] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lk), k));
             const float Mu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(M), 0));
             ll_stf(part + qw + kLine * h + tid, tid == 0u ? Mu : (tid == 1u ? L : 0.0f), tB);
         }
@@ -968,23 +972,28 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
     MK_UNIFORM(pos);
     MK_TAGS(l);
     const MkLayer& Ly = g_mk_layers[l];
-    if (w >= g_mk.nc) return true;
-    MK_MARK(11);
     const uint32_t hist = min(pos + 1u, Ly.slots);
     uint32_t nch, clen;
     attn_split(hist, g_mk.max_chunks, g_mk.chunk_min, nch, clen);
+    const uint32_t nc = g_mk.nc;
+    if (w >= nc) return true;
+    MK_MARK(11);
     uint32_t v0, v1;
-    split_range(d, g_mk.nc, w, v0, v1);
+    split_range(d, nc, w, v0, v1);
     const uint8_t* wo = Ly.wo;
     auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
     RowBatch<SA, 1, 1> rb;
     batch_load<SA, 1, 1>(rowp, nblk_a, g_mk.arena_end, v0, v1, wave, rb);
     float* parts = m.u;
     const uint32_t ntot = nch * part_stride;
-    for (uint32_t o = 0; o < ntot; o += kPartRound)
-        if (!ll_gather2<kPartRound / kMkThreads / 2>(g_mk.x_part + o, min(kPartRound, ntot - o), tB, parts + o,
-                                                 (o / kPartRound) & 1u ? kAnyGather1 : kAnyGather0))
-            return false;
+    if (ntot <= kPartRoundS) {   // few chunks: one round with fewer polls per thread
+        if (!ll_gather2<kPartRoundS / kMkThreads / 2>(g_mk.x_part, ntot, tB, parts, kAnyGather0)) return false;
+    } else {
+        for (uint32_t o = 0; o < ntot; o += kPartRound)
+            if (!ll_gather2<kPartRound / kMkThreads / 2>(g_mk.x_part + o, min(kPartRound, ntot - o), tB, parts + o,
+                                                         (o / kPartRound) & 1u ? kAnyGather1 : kAnyGather0))
+                return false;
+    }
     MK_MARK(12);
     // Chunk weights: wave h < H takes head h, lane c chunk c (M, e_c = exp(m_c - M) and
     // den = sum_c double(e_c) * double(l_c) by DPP over the 16 lanes of row 0).
