@@ -699,17 +699,17 @@ constexpr uint32_t kBMaxWaves = 8;                 // waves of an attention unit
 constexpr uint32_t kBPos = 8;                      // positions per wave per group
 constexpr uint32_t kBLongChunk = 128;              // chunks at least this long use all kBMaxWaves waves
 
-// Phase B: one workgroup per (chunk c, query head h); waves 0..3 work, the others wait at the
-// closing barrier. Lane i of a wave owns head dims 4i..4i+3. Every working wave gathers its
-// lanes' q_h, k and v itself, applies
+// Phase B: one workgroup per (chunk c, query head h); waves 0..3 work (all eight for chunks of
+// kBLongChunk positions or more), the others wait at the closing barrier. Lane i of a wave owns
+// head dims 4i..4i+3. Every working wave gathers its lanes' q_h, k and v itself, applies
 // QK-norm (src/gemma3.cpp:1045-1104) and RoPE (:1371-1424; the partner dims e +- head_dim/2
 // come from another lane of the same wave), and runs an online softmax over its cached
-// positions t = c0 + wave + 4i of the chunk (:1602-1696), in groups of 32 positions whose K/V
-// rows are loaded one group ahead (a window chunk is one group, loaded before the wait for
-// q, k, v). A group's 8 scores per wave are reduced and transposed together, so that lane l
+// positions t = c0 + wave + n i of the chunk (n working waves; :1602-1696), in groups of 8 n
+// positions whose K/V rows are loaded one group ahead (a short chunk is one group, loaded
+// before the wait for q, k, v). A group's 8 scores per wave are reduced and transposed together, so that lane l
 // holds the score of its position l & 7: the max, the exponentials and the masks are one
 // lane-parallel operation per group. The current position is taken from registers by the
-// wave whose turn it is. No barrier until the four partials {m, l, acc} are merged through
+// wave whose turn it is. No barrier until the n partials {m, l, acc} are merged through
 // LDS. Wave 0 of head 0 of
 // the chunk holding the current position appends k and v to the cache (:1590-1600).
 // Publishes the unnormalised partial {acc[hd] of head h, m, l} of (c, h).
