@@ -99,7 +99,7 @@ struct MkLayer {
 // Byte offsets of the dynamic LDS carve-up. `u` is phase-local scratch shared by the
 // attention partial sums (B), the gathered chunk partials (C) and the LM-head tile.
 struct MkLds {
-    uint32_t h, xs, xa, xd, ya, yd, nwa0, nwa1, nwd0, nwd1, any, la, lb, lc, ls, sq, sc, mw, gu, red, u, total;
+    uint32_t h, xs, xa, xd, ya, yd, nwa0, nwa1, nwd0, nwd1, any, la, lb, lc, ls, sc, mw, gu, u, total;
 };
 
 constexpr uint32_t kMkLdsBytes = 144u * 1024u;   // static LDS of the persistent kernel
@@ -164,9 +164,6 @@ __device__ __forceinline__ void ll_st(u64* p, uint32_t bits, uint32_t tag) {
                        __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ void ll_stf(u64* p, float v, uint32_t tag) { ll_st(p, __float_as_uint(v), tag); }
-__device__ __forceinline__ void co_stf(float* p, float v) {
-    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
 // 16 bytes at byte `off` of a buffer, device-coherent (bypasses a possibly stale local L2).
 __device__ __forceinline__ v4u co_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, kCoherent);
@@ -179,34 +176,6 @@ __device__ __forceinline__ void mk_abort() {
 }
 __device__ __forceinline__ void mk_flag_min(uint32_t v) {
     __hip_atomic_fetch_min(gp(&g_mk.st->nonfinite), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---- workgroup reductions (one barrier each) ----------------------------------------------------
-
-struct BlkRed {
-    double* red;   // LDS: [2][kMkWaves] sums, then [2][kMkWaves] flags as doubles
-    uint32_t n;    // calls so far: slots alternate, so a slot is rewritten only two barriers later
-};
-
-// Workgroup sum of v (fixed order: DPP within each wave, then waves 0..7), and the OR of flag.
-__device__ __forceinline__ double blk_sum(BlkRed& R, double v, int& flag) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t slot = (R.n++ & 1u) * kMkWaves;
-    v = wave_red_sum_d(v);
-    const float f = wave_red_max(flag ? 1.0f : 0.0f);
-    if (lane == 0) {
-        R.red[slot + wave] = v;
-        R.red[2u * kMkWaves + slot + wave] = f;
-    }
-    __syncthreads();
-    double s = 0.0, fl = 0.0;
-#pragma unroll
-    for (uint32_t k = 0; k < kMkWaves; ++k) {
-        s += R.red[slot + k];
-        fl += R.red[2u * kMkWaves + slot + k];
-    }
-    flag = fl != 0.0;
-    return s;
 }
 
 // 1.0f / std::sqrt(float(sum_sq / n) + eps) (src/gemma3.cpp:967-983).
@@ -237,11 +206,9 @@ struct MkSmem {
     float* nwd0;    // norm weights staged for phase D
     float* nwd1;
     LimbLds L;      // LM-head activation limbs
-    float* sq;      // phase B: q | k | v
     float* sc;      // phase B scores; argmax partials
     float* mw;      // phase B/C per-head scalars
     float* gu;      // phase D gate/up values of this workgroup
-    double* red;    // block reductions
     float* u;       // phase-local scratch
 };
 
@@ -260,11 +227,9 @@ __device__ __forceinline__ MkSmem mk_smem() {
     m.nwd1 = reinterpret_cast<float*>(smem + g_mk.lds.nwd1);
     m.L = LimbLds{reinterpret_cast<int8_t*>(smem + g_mk.lds.la), reinterpret_cast<int8_t*>(smem + g_mk.lds.lb),
                   reinterpret_cast<int8_t*>(smem + g_mk.lds.lc), reinterpret_cast<float*>(smem + g_mk.lds.ls)};
-    m.sq = reinterpret_cast<float*>(smem + g_mk.lds.sq);
     m.sc = reinterpret_cast<float*>(smem + g_mk.lds.sc);
     m.mw = reinterpret_cast<float*>(smem + g_mk.lds.mw);
     m.gu = reinterpret_cast<float*>(smem + g_mk.lds.gu);
-    m.red = reinterpret_cast<double*>(smem + g_mk.lds.red);
     m.u = reinterpret_cast<float*>(smem + g_mk.lds.u);
     return m;
 }
@@ -299,31 +264,6 @@ __device__ __forceinline__ uint32_t n_bunits(uint32_t slots, uint32_t pos) {
     uint32_t nch, clen;
     attn_split(min(pos + 1u, slots), g_mk.max_chunks, g_mk.chunk_min, nch, clen);
     return nch * g_mk.H;
-}
-
-// Loads this thread's elements i = tid + kMkThreads * k of a static vector (norm weights).
-__device__ __forceinline__ void vec_load(const float* src, uint32_t n, float (&r)[kVec]) {
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k) {
-        const uint32_t i = threadIdx.x + k * kMkThreads;
-        r[k] = gp(src)[i < n ? i : n - 1u];   // branch-free: clamped, then ignored past n
-    }
-}
-
-__device__ __forceinline__ double vec_sumsq(const float (&r)[kVec], uint32_t n) {
-    double acc = 0.0;
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k)
-        if (threadIdx.x + k * kMkThreads < n) acc += static_cast<double>(r[k]) * static_cast<double>(r[k]);
-    return acc;
-}
-
-__device__ __forceinline__ int vec_nonfinite(const float (&r)[kVec], uint32_t n) {
-    int bad = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < kVec; ++k)
-        if (threadIdx.x + k * kMkThreads < n) bad |= !__builtin_isfinite(r[k]);
-    return bad;
 }
 
 // ---- LM head tiles ---------------------------------------------------------------------------
@@ -385,10 +325,9 @@ __device__ __forceinline__ void lm_wait_tiles(uint32_t later) {
     const uint32_t nblk_d = d >> 5, nblk_a = qw >> 5, nblk_f = F >> 5;                                      \
     const uint64_t rb_d = static_cast<uint64_t>(nblk_d) * 34u, rb_a = static_cast<uint64_t>(nblk_a) * 34u,  \
                    rb_f = static_cast<uint64_t>(nblk_f) * 34u;                                              \
-    BlkRed R{m.red, 0u};                                                                                     \
     (void)w; (void)tid; (void)lane; (void)wave; (void)d; (void)H; (void)hd; (void)F; (void)L; (void)qw;     \
     (void)nqkv; (void)half; (void)part_stride; (void)nblk_d; (void)nblk_a; (void)nblk_f; (void)rb_d;         \
-    (void)rb_a; (void)rb_f; (void)R
+    (void)rb_a; (void)rb_f
 
 // Sub-phase mark k (< kMarks) of the traced block, in the last kMarks trace slots.
 #define MK_MARK(k)                                                                                        \
@@ -1561,11 +1500,9 @@ int mk_setup(vrt_g3* g) {
     P.lds.lb = take(d);
     P.lds.lc = take(d);
     P.lds.ls = take(d / 32u * 4u);
-    P.lds.sq = take((H + 2u) * hd * 4u);
     P.lds.sc = take(std::max(8u * kGrp, 2u * nwg) * 4u);
     P.lds.mw = take((8u * kMaxChunks + 16u) * 4u);
     P.lds.gu = take(2u * ((F + nprod - 1u) / nprod + 1u) * 4u);
-    P.lds.red = take((4u + 9u) * kMkWaves * 8u);
     P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + kLine * H)) * 4u, kLmRing * kLmTileBytes));
     P.lds.total = off;
     mk->lds_bytes = off;

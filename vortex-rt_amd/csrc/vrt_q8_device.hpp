@@ -63,18 +63,6 @@ __device__ __forceinline__ float dpp_or_zero(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
 }
 
-__device__ __forceinline__ float wave_red_sum(float v) {
-    v = slot_sum<16>(v);                        // every lane: its row's total
-    v += dpp_or_zero<0x142, 0xa>(v);            // row_bcast:15 into rows 1 and 3
-    v += dpp_or_zero<0x143, 0xc>(v);            // row_bcast:31 into rows 2 and 3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_max_mov(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
 __device__ __forceinline__ float wave_red_max(float v) {
     v = fmaxf(v, dpp_mov<0xB1>(v));
     v = fmaxf(v, dpp_mov<0x4E>(v));
