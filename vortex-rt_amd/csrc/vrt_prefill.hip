@@ -597,37 +597,26 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_softmax(const float* S, uint3
     }
 }
 
-// V^T of one block: vt[d][t] = v_t[d] for the rows t < T of qkv, zero for T <= t < Tp.
-__global__ void __launch_bounds__(kPfThreads) k_pf_vt(const float* qkv, uint32_t T, uint32_t Tp, uint32_t nqkv,
-                                                      uint32_t voff, float* vt) {
-    __shared__ float tile[32][33];
-    const uint32_t t0 = blockIdx.x * 32u, d0 = blockIdx.y * 32u;
-    const uint32_t tx = threadIdx.x & 31u, ty = threadIdx.x >> 5;   // 32 x 8
-    for (uint32_t r = ty; r < 32u; r += 8u) {
-        const uint32_t t = t0 + r;
-        tile[r][tx] = t < T ? qkv[static_cast<uint64_t>(t) * nqkv + voff + d0 + tx] : 0.0f;
-    }
-    __syncthreads();
-    for (uint32_t r = ty; r < 32u; r += 8u) {
-        const uint32_t t = t0 + tx;
-        if (t < Tp) vt[static_cast<uint64_t>(d0 + r) * Tp + t] = tile[tx][r];
-    }
-}
-
 // ---- QK-norm, RoPE, KV cache ------------------------------------------------------------
 
 // Row t of qkv = [q (H heads x hd) | k (hd) | v (hd)]: QK-norm per head (src/gemma3.cpp:
 // 1045-1104), NeoX RoPE at position t (:1371-1424), in place (q also as f16 hi/lo rows of
 // qhi/qlo); then k and v go to the KV cache slot t % slots when position t is still in the
-// window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600).
+// window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600), and
+// v to column t of vt = V^T [hd][Tp], the B operand of O = P V. One workgroup per column
+// t < Tp: those with t >= T write the zero padding columns (their weights in P are zero).
 __global__ void __launch_bounds__(kPfThreads) k_pf_qk(float* qkv, uint32_t T, uint32_t H, uint32_t hd, const float* q_norm,
                                                       const float* k_norm, const float* cos_t, const float* sin_t,
                                                       float eps, float* kc, float* vc, uint32_t slots, _Float16* qhi,
-                                                      _Float16* qlo) {
+                                                      _Float16* qlo, uint32_t Tp, float* vt) {
 #pragma clang fp contract(off)
     __shared__ double red[4];
     __shared__ float xs[256];
     const uint32_t t = blockIdx.x;
+    if (t >= T) {   // whole workgroup
+        if (threadIdx.x < hd) vt[static_cast<uint64_t>(threadIdx.x) * Tp + t] = 0.0f;
+        return;
+    }
     const uint32_t nqkv = (H + 2u) * hd, half = hd >> 1;
     float* row = qkv + static_cast<uint64_t>(t) * nqkv;
     const uint32_t i = threadIdx.x;
@@ -657,6 +646,7 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_qk(float* qkv, uint32_t T, ui
         kc[slot + i] = row[H * hd + i];
         vc[slot + i] = row[(H + 1u) * hd + i];
     }
+    if (i < hd) vt[static_cast<uint64_t>(i) * Tp + t] = row[(H + 1u) * hd + i];
 }
 
 // ---- host side --------------------------------------------------------------------------
@@ -814,13 +804,6 @@ static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, const floa
         void* args[] = {&S, &t, &tp, &scale, &w, &phi, &plo};
         VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_softmax), dim3(T, H), dim3(kPfThreads), args, 0, s));
     }
-    {
-        uint32_t t = T, tp = Tp, n = nqkv, voff = qw + hd;
-        float* vt = p.vt;
-        void* args[] = {const_cast<float**>(&qkv), &t, &tp, &n, &voff, &vt};
-        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_vt), dim3(Tp / 32u, hd / 32u), dim3(kPfThreads),
-                                      args, 0, s));
-    }
     {   // O_h = P_h V -> att[:, h * hd ..]
         PfGemm G{};
         G.ahi = static_cast<const _Float16*>(p.phi);
@@ -891,8 +874,10 @@ int pf_run(vrt_g3* g, uint32_t T) {
             float* kc = Ly.kc;
             float* vc = Ly.vc;
             uint32_t slots = Ly.slots;
-            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_qk), dim3(T), args)) return rc;
+            uint32_t tp = pf_pad(T);
+            float* vt = g->pf.vt;
+            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &tp, &vt};
+            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_qk), dim3(tp), args)) return rc;
         }
         // q (hi/lo in ahi/alo) is consumed by S = Q K^T before O = P V overwrites ahi/alo
         if (int rc = pf_attention(g, Ly, T, big, ahi, alo, ahi, alo, s)) return rc;
