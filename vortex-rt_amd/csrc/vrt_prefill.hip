@@ -605,48 +605,70 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_softmax(const float* S, uint3
 // window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600), and
 // v to column t of vt = V^T [hd][Tp], the B operand of O = P V. One workgroup per column
 // t < Tp: those with t >= T write the zero padding columns (their weights in P are zero).
-__global__ void __launch_bounds__(kPfThreads) k_pf_qk(float* qkv, uint32_t T, uint32_t H, uint32_t hd, const float* q_norm,
-                                                      const float* k_norm, const float* cos_t, const float* sin_t,
-                                                      float eps, float* kc, float* vc, uint32_t slots, _Float16* qhi,
-                                                      _Float16* qlo, uint32_t Tp, float* vt) {
+// One wave per head (lane l: dims l + 64 e): the sum of squares is a wave reduction and the
+// RoPE partners come through the wave's own LDS row, so the kernel has no barrier.
+constexpr uint32_t kPfQkMaxWaves = 8;
+__global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32_t T, uint32_t H, uint32_t hd,
+                                                            const float* q_norm, const float* k_norm,
+                                                            const float* cos_t, const float* sin_t, float eps,
+                                                            float* kc, float* vc, uint32_t slots, _Float16* qhi,
+                                                            _Float16* qlo, uint32_t Tp, float* vt) {
 #pragma clang fp contract(off)
-    __shared__ double red[4];
-    __shared__ float xs[256];
+    __shared__ float xs[kPfQkMaxWaves][256];
     const uint32_t t = blockIdx.x;
     if (t >= T) {   // whole workgroup
-        if (threadIdx.x < hd) vt[static_cast<uint64_t>(threadIdx.x) * Tp + t] = 0.0f;
+        for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) vt[static_cast<uint64_t>(i) * Tp + t] = 0.0f;
         return;
     }
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t nqkv = (H + 2u) * hd, half = hd >> 1;
     float* row = qkv + static_cast<uint64_t>(t) * nqkv;
-    const uint32_t i = threadIdx.x;
-    for (uint32_t hh = 0; hh <= H; ++hh) {   // H query heads, then the key head
+    float* xw = xs[wave];
+    const bool keep = t + slots >= T;
+    const uint64_t slot = static_cast<uint64_t>(t % slots) * hd;
+    for (uint32_t hh = wave; hh <= H; hh += nw) {   // H query heads, then the key head
         float* x = row + hh * hd;
-        const float v = i < hd ? x[i] : 0.0f;
-        const float sc = pf_rms_scale(pf_sum(static_cast<double>(v) * static_cast<double>(v), red), hd, eps);
         const float* w = hh < H ? q_norm : k_norm;
-        const float y = i < hd ? (v * sc) * w[i] : 0.0f;
-        if (i < hd) xs[i] = y;
-        __syncthreads();
-        if (i < hd) {
-            const uint32_t e = i < half ? i : i - half;
-            const float c = cos_t[static_cast<uint64_t>(t) * half + e], s = sin_t[static_cast<uint64_t>(t) * half + e];
-            const float a = xs[e], b = xs[e + half];
-            const float y2 = i < half ? a * c - b * s : b * c + a * s;
-            x[i] = y2;
-            if (hh < H) {   // the query as the attention GEMM's A operand, [T][H * hd]
-                const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
-                pf_split(y2, qhi + o, qlo + o);
+        float v[4];
+        double sq = 0.0;
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const uint32_t i = lane + 64u * e;
+            v[e] = i < hd ? x[i] : 0.0f;
+            sq += static_cast<double>(v[e]) * static_cast<double>(v[e]);
+        }
+        const float sc = pf_rms_scale(wave_red_sum_d(sq), hd, eps);
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const uint32_t i = lane + 64u * e;
+            if (i < hd) xw[i] = (v[e] * sc) * w[i];
+        }
+        // the partners are other lanes' values: a wave's LDS accesses complete in order
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const uint32_t i = lane + 64u * e;
+            if (i < hd) {
+                const uint32_t ei = i < half ? i : i - half;
+                const float c = cos_t[static_cast<uint64_t>(t) * half + ei], s = sin_t[static_cast<uint64_t>(t) * half + ei];
+                const float a = xw[ei], b = xw[ei + half];
+                const float y2 = i < half ? a * c - b * s : b * c + a * s;
+                x[i] = y2;
+                if (hh < H) {   // the query as the attention GEMM's A operand, [T][H * hd]
+                    const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
+                    pf_split(y2, qhi + o, qlo + o);
+                } else if (keep) {
+                    kc[slot + i] = y2;
+                }
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();   // this head's reads of xw come before the next head's writes
     }
-    if (t + slots >= T && i < hd) {
-        const uint64_t slot = static_cast<uint64_t>(t % slots) * hd;
-        kc[slot + i] = row[H * hd + i];
-        vc[slot + i] = row[(H + 1u) * hd + i];
+    for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {   // v is not normed
+        const float vv = row[(H + 1u) * hd + i];
+        if (keep) vc[slot + i] = vv;
+        vt[static_cast<uint64_t>(i) * Tp + t] = vv;
     }
-    if (i < hd) vt[static_cast<uint64_t>(i) * Tp + t] = row[(H + 1u) * hd + i];
 }
 
 // ---- host side --------------------------------------------------------------------------
@@ -877,7 +899,8 @@ int pf_run(vrt_g3* g, uint32_t T) {
             uint32_t tp = pf_pad(T);
             float* vt = g->pf.vt;
             void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &tp, &vt};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_qk), dim3(tp), args)) return rc;
+            const uint32_t waves = std::min(H + 1u, kPfQkMaxWaves);
+            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_qk), dim3(tp), dim3(64u * waves), args, 0, s));
         }
         // q (hi/lo in ahi/alo) is consumed by S = Q K^T before O = P V overwrites ahi/alo
         if (int rc = pf_attention(g, Ly, T, big, ahi, alo, ahi, alo, s)) return rc;
