@@ -77,7 +77,6 @@ constexpr uint32_t kLmUnits = 3;             // 16-byte LM-head loads per thread
 constexpr uint32_t kLmRing = 4;              // LM-head tile slots in LDS
 constexpr uint32_t kLmAhead = kLmRing - 1u;  // tiles in flight while one is computed
 constexpr uint32_t kLmTileBytes = kLmUnits * 512u * 16u;
-constexpr uint32_t kGrp = 32;                // attention positions per online-softmax group
 constexpr uint32_t kPartRound = 24 * kMkThreads;   // attention partials gathered per wait (many chunks)
 constexpr uint32_t kPartRoundS = 12 * kMkThreads;  // the same when they all fit in one smaller round
 constexpr int kRsrcFlags = 0x00020000;       // raw buffer resource, 32-bit data format
@@ -206,7 +205,7 @@ struct MkSmem {
     float* nwd0;    // norm weights staged for phase D
     float* nwd1;
     LimbLds L;      // LM-head activation limbs
-    float* sc;      // phase B scores; argmax partials
+    float* sc;      // argmax partials (2 nwg words)
     float* mw;      // phase B/C per-head scalars
     float* gu;      // phase D gate/up values of this workgroup
     float* u;       // phase-local scratch
@@ -1500,7 +1499,7 @@ int mk_setup(vrt_g3* g) {
     P.lds.lb = take(d);
     P.lds.lc = take(d);
     P.lds.ls = take(d / 32u * 4u);
-    P.lds.sc = take(std::max(8u * kGrp, 2u * nwg) * 4u);
+    P.lds.sc = take(2u * nwg * 4u);
     P.lds.mw = take((8u * kMaxChunks + 16u) * 4u);
     P.lds.gu = take(2u * ((F + nprod - 1u) / nprod + 1u) * 4u);
     P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + kLine * H)) * 4u, kLmRing * kLmTileBytes));
