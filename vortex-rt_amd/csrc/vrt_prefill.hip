@@ -38,10 +38,11 @@ __device__ __forceinline__ void pf_split(float x, _Float16* hi, _Float16* lo) {
     *lo = static_cast<_Float16>(x - static_cast<float>(h));
 }
 
-// Workgroup double sum (fixed order: 4 waves, DPP inside each).
+// Workgroup double sum (fixed order: 4 waves, DPP inside each) behind one barrier. red[0..4)
+// belongs to this call: a second sum in the same kernel takes other slots, so no thread can
+// still be reading them when they are written.
 __device__ __forceinline__ double pf_sum(double v, double* red) {
     v = wave_red_sum_d(v);
-    __syncthreads();
     if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = v;
     __syncthreads();
     return red[0] + red[1] + red[2] + red[3];
@@ -76,7 +77,7 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
                                                         const float* w_post, const float* w_next, uint32_t n, float eps,
                                                         _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block) {
 #pragma clang fp contract(off)
-    __shared__ double red[4];
+    __shared__ double red[2][4];   // one set per sum
     const uint32_t t = blockIdx.x;
     float* hr = h + static_cast<uint64_t>(t) * n;
     float hv[8];
@@ -97,7 +98,7 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
                 for (uint32_t q = 0; q < nsplit; ++q) fv[k] += fr[q * sstride + i];
             ss += static_cast<double>(fv[k]) * static_cast<double>(fv[k]);
         }
-        const float sc = pf_rms_scale(pf_sum(ss, red), n, eps);
+        const float sc = pf_rms_scale(pf_sum(ss, red[0]), n, eps);
         int bad = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -114,7 +115,7 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
     double ss = 0.0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) ss += static_cast<double>(hv[k]) * static_cast<double>(hv[k]);
-    const float sc = pf_rms_scale(pf_sum(ss, red), n, eps);
+    const float sc = pf_rms_scale(pf_sum(ss, red[1]), n, eps);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const uint32_t i = threadIdx.x + k * kPfThreads;
