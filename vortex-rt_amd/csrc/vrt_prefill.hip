@@ -28,6 +28,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kPfThreads = 256;
+constexpr uint32_t kPfMaxSplits = 4;   // K splits of the O and down projections (pf_splits)
 constexpr uint32_t kPfTile = 64;     // attention score rows are padded to a multiple of this
 
 // ---- row kernels ---------------------------------------------------------------------------
@@ -88,14 +89,23 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
     }
     if (f) {
         const float* fr = f + static_cast<uint64_t>(t) * n;
+        // every partial is loaded before the first add (nsplit <= kPfMaxSplits), then the
+        // partials are added in split order
+        float fp[8][kPfMaxSplits];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t i = threadIdx.x + k * kPfThreads;
+#pragma unroll
+            for (uint32_t q = 0; q < kPfMaxSplits; ++q) fp[k][q] = i < n && q < nsplit ? fr[q * sstride + i] : 0.0f;
+        }
         float fv[8];
         double ss = 0.0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t i = threadIdx.x + k * kPfThreads;
             fv[k] = 0.0f;
-            if (i < n)
-                for (uint32_t q = 0; q < nsplit; ++q) fv[k] += fr[q * sstride + i];
+#pragma unroll
+            for (uint32_t q = 0; q < kPfMaxSplits; ++q)
+                if (q < nsplit) fv[k] += fp[k][q];
             ss += static_cast<double>(fv[k]) * static_cast<double>(fv[k]);
         }
         const float sc = pf_rms_scale(pf_sum(ss, red[0]), n, eps);
@@ -750,11 +760,10 @@ static int pf_gemm_glu(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint
 // K splits of the 640-row projections (O and down): enough workgroups to cover the CUs.
 static uint32_t pf_splits(uint32_t M, uint32_t N) {
     const uint32_t tiles = ((M + kQgBM - 1u) / kQgBM) * ((N + 63u) / 64u);
-    return std::min(4u, std::max(1u, 256u / std::max(1u, tiles)));
+    return std::min(kPfMaxSplits, std::max(1u, 256u / std::max(1u, tiles)));
 }
 
 static uint32_t pf_pad(uint32_t T) { return (T + kPfTile - 1u) / kPfTile * kPfTile; }
-constexpr uint32_t kPfMaxSplits = 4;   // K splits of the O and down projections (pf_splits)
 
 int pf_setup(vrt_g3* g, uint32_t max_t) {
     const uint32_t d = g->cfg.embedding_length, H = g->cfg.head_count, hd = g->cfg.head_dim;
