@@ -47,16 +47,25 @@ def step_bytes(cfg, pos: int) -> int:
     return total
 
 
+TRAFFIC_SUMMARY = os.path.join("profiles", "decode_gemma3_270m_pmc.json")
+
+
 def load_traffic(steps: int):
-    """HBM bytes per k_decode launch of `steps` steps, from the committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE per decode step, calibrated against a copy of known size)."""
-    p = os.path.join(REPO, "profiles", "decode_gemma3_270m_pmc.json")
+    """HBM bytes per k_decode launch of `steps` steps and where the figure comes from: the
+    committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE per decode step, calibrated against
+    a copy of known size), scaled to `steps`. This run does not measure it."""
+    p = os.path.join(REPO, TRAFFIC_SUMMARY)
     try:
         with open(p) as fp:
-            per_step = json.load(fp)["hbm_bytes_per_step"]
+            summary = json.load(fp)
+        per_step = summary["hbm_bytes_per_step"]
     except (OSError, ValueError, KeyError):
-        return None
-    return int(per_step * steps)
+        return None, None
+    src = (f"{TRAFFIC_SUMMARY}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of k_decode, calibrated, "
+           f"{per_step / 1e6:.1f} MB per step, scaled to {steps} steps (not measured by this run)")
+    if "command" in summary:
+        src += f"; command: {summary['command']}"
+    return int(per_step * steps), src
 
 
 def phase_split(g, prompt, cfg, steps: int = 24):
@@ -92,7 +101,9 @@ def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256):
     ctx.record(ev1)
     ms = ctx.elapsed_ms(ev0, ev1)
     ctx.sync()
-    g.collect()
+    toks = g.collect()
+    if toks.size < steps + 1:
+        raise SystemExit(f"[bench] long context: EOS after {toks.size} generated tokens; the timed steps did not all run")
     total = sum(step_bytes(cfg, n_prompt + i) for i in range(steps))
     gbps = total / (ms / 1e3) / 1e9
     return {"workload": f"{n_prompt}-token prompt (untimed prefill), {steps} timed greedy decode steps at positions "
@@ -141,6 +152,59 @@ def prefill_bench(ctx, g, cfg, T: int = 512, reps: int = 5):
             "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "note": "projection GEMMs issue two f16 MFMAs per product (activation hi + lo parts); utilisation "
                     "counts the algorithmic FLOPs only"}
+
+
+def q8_bytes(rows: int, k: int) -> int:
+    return rows * (k // 32) * 34
+
+
+def kernel_legs(ctx, iters: int = 200):
+    """The standalone entry points on their workloads: one Q8_0 matvec at 2048 x 640 and at
+    640 x 2048 (W ~ N(0, 0.02), seed 0, x ~ N(0, 1)), and the decoder-layer projection block
+    (fused Q/K/V triplet 1024 + 256 + 256 rows x 640; fused FFN 2048 x 640 gate/up with the GELU
+    product, 640 x 2048 down). Each is launched `iters` times back to back between two events on
+    the library's stream; bytes are the weights plus fp32 inputs and outputs, once per call."""
+    import synth
+    import vrt
+    out = {}
+
+    def timed(fn, nbytes):
+        fn()
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for _ in range(iters):
+            fn()
+        ctx.record(e1)
+        ms = ctx.elapsed_ms(e0, e1)
+        us = ms * 1e3 / iters
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"us_per_call": round(us, 3), "bytes": nbytes, "gbps": round(gbps, 1),
+                "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+    for rows, k in ((2048, 640), (640, 2048)):
+        w = synth.q8_matrix(0, f"bench.w{rows}x{k}", rows, k)
+        wd = ctx.upload(w)
+        xd = ctx.upload(synth.normal_f32(1, k))
+        yd = ctx.alloc(rows * 4)
+        out[f"matvec_{rows}x{k}"] = timed(lambda: vrt.q8_matvec(ctx, wd, 0, xd, yd, k, rows),
+                                          q8_bytes(rows, k) + 4 * (k + rows))
+    d, qw, hd, F = 640, 1024, 256, 2048
+    mats = [synth.q8_matrix(0, f"bench.{n}", r, c) for n, r, c in
+            (("q", qw, d), ("k", hd, d), ("v", hd, d), ("gate", F, d), ("up", F, d), ("down", d, F))]
+    offs = np.cumsum([0] + [m.size for m in mats])
+    wd = ctx.upload(np.concatenate(mats))
+    xd = ctx.upload(synth.normal_f32(2, d))
+    yq = ctx.alloc((qw + 2 * hd) * 4)
+    ws = ctx.alloc(2 * F * 4)
+    yf = ctx.alloc(d * 4)
+    out["qkv_triplet_640"] = timed(lambda: vrt.q8_matvec_multi(ctx, wd, offs[:3], (qw, hd, hd), d, xd, yq),
+                                   q8_bytes(qw + 2 * hd, d) + 4 * (d + qw + 2 * hd))
+    out["ffn_640_2048"] = timed(lambda: vrt.q8_ffn(ctx, wd, int(offs[3]), int(offs[4]), int(offs[5]), d, F, d, xd, ws, yf),
+                                2 * q8_bytes(F, d) + q8_bytes(d, F) + 4 * (2 * d))
+    out["note"] = (f"{iters} back-to-back calls between two events (launch gaps included); the FFN is two "
+                   "launches (gate/up with the GELU product, then down)")
+    return out
 
 
 def synth_ids(seed: int, n: int, vocab: int):
@@ -197,6 +261,8 @@ def main():
     ap.add_argument("--no-phases", action="store_true", help="skip the traced per-phase split")
     ap.add_argument("--no-long", action="store_true", help="skip the 8192-token long-context measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token batched prefill measurement")
+    ap.add_argument("--no-kernels", action="store_true",
+                    help="skip the standalone matvec / QKV / FFN measurements (single-matvec and layer-block workloads)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
@@ -244,7 +310,9 @@ def main():
     ctx.sync()
     toks = g.collect()
     if toks.size < args.steps + 1:
-        print(f"[bench] EOS after {toks.size} tokens; timed steps after it were skipped", file=sys.stderr)
+        # the kernel stopped at EOS: fewer than --steps steps ran inside the timed region
+        raise SystemExit(f"[bench] EOS after {toks.size} generated tokens: only {max(toks.size - 1, 0)} of the "
+                         f"{args.steps} timed decode steps ran; no throughput is reported")
     k = min(warm.size, toks.size)
     if not np.array_equal(warm[:k], toks[:k]):
         raise SystemExit("[bench] nondeterministic greedy tokens between warm-up and timed run")
@@ -254,9 +322,11 @@ def main():
     total_bytes = sum(step_bytes(cfg, n_prompt + i) for i in range(args.steps))
     gbps = total_bytes / (ms / 1e3) / 1e9
 
+    traffic, traffic_src = load_traffic(args.steps)
     phases = None if args.no_phases else phase_split(g, prompt, cfg)
     longctx = None if args.no_long else long_context(ctx, g, cfg)
     prefill = None if args.no_prefill else prefill_bench(ctx, g, cfg)
+    kernels = None if args.no_kernels else kernel_legs(ctx)
 
     out = {
         "metric": METRIC,
@@ -289,13 +359,15 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": load_traffic(args.steps),
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "mean_launch_us": round(ms * 1e3, 1),
             "algorithmic_bytes_per_launch": total_bytes,
         },
         "phase_us_per_step": phases,
         "long_context": longctx,
         "prefill": prefill,
+        "kernels": kernels,
         "cpu_baseline": None,
     }
     g.close()

@@ -107,8 +107,9 @@ int vrt_q8_matvec_multi(vrt_ctx* ctx, const void* weights, uint64_t weights_byte
 
 /* Q8MatVecPipeline::run_staged_ffn, include/vortexrt/q8_matvec.hpp:57-72 and
  * src/q8_matvec.cpp:1360-2004: gate = Wg x, up = Wu x, h = gelu_tanh(gate) * up,
- * y = Wd h. workspace holds [gate | up] (2 * ffn_dim floats); gate ends up holding h
- * as in the reference's workspace. */
+ * y = Wd h. Two launches: gate/up with the GELU product as its epilogue, then down.
+ * workspace (2 * ffn_dim floats) ends up holding [h | up], the gate half holding h as in
+ * the reference's workspace. */
 int vrt_q8_ffn(vrt_ctx* ctx, const void* weights, uint64_t weights_bytes,
                uint32_t gate_offset, uint32_t up_offset, uint32_t down_offset,
                uint32_t input_dim, uint32_t ffn_dim, uint32_t output_dim,

@@ -29,15 +29,18 @@ class G3Info(C.Structure):
          ("eos_id", C.c_uint32), ("bos_id", C.c_uint32)]
 
 
-_lib = None
+_libs = {}
 
 
-def lib():
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
+def lib(path: str | None = None):
+    """The oracle library at `path` (default: the built liboracle.so). Other paths load
+    variants compiled from patched copies of vrt_oracle.c (the wiring tests' mutants)."""
+    path = path or LIB_PATH
+    L = _libs.get(path)
+    if L is None:
+        if path == LIB_PATH and not os.path.exists(path):
             build()
-        L = C.CDLL(LIB_PATH)
+        L = C.CDLL(path)
         P, F, U32, U64, I = C.c_void_p, C.c_float, C.c_uint32, C.c_uint64, C.c_int
         sig = {
             "or_f32_to_f16": (C.c_uint16, [F]),
@@ -70,8 +73,8 @@ def lib():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        _lib = L
-    return _lib
+        _libs[path] = L
+    return L
 
 
 def _p(a):
@@ -189,35 +192,36 @@ def attention(q, keys, values, heads, head_dim, scale):
 class Model:
     """The whole-model oracle (src/gemma3.cpp executor restated) over a GGUF file."""
 
-    def __init__(self, path: str, lanes: int = 8):
+    def __init__(self, path: str, lanes: int = 8, lib_path: str | None = None):
+        self.L = lib(lib_path)
         err = C.create_string_buffer(512)
-        self.h = lib().or_g3_open(str(path).encode(), lanes, err, 512)
+        self.h = self.L.or_g3_open(str(path).encode(), lanes, err, 512)
         if not self.h:
             raise RuntimeError(err.value.decode())
         info = G3Info()
-        lib().or_g3_get_info(self.h, C.byref(info))
+        self.L.or_g3_get_info(self.h, C.byref(info))
         self.info = info
 
     def close(self):
         if self.h:
-            lib().or_g3_close(self.h)
+            self.L.or_g3_close(self.h)
             self.h = None
 
     def __del__(self):
         self.close()
 
     def reset(self):
-        lib().or_g3_reset(self.h)
+        self.L.or_g3_reset(self.h)
 
     def decode(self, token: int, pos: int, want_logits: bool = True, logits: bool = False):
         d = self.info.embedding_length
         hidden = np.empty(d, dtype=np.float32)
         lg = np.empty(self.info.vocab_size, dtype=np.float32) if logits else None
         ai, av = C.c_uint32(), C.c_float()
-        rc = lib().or_g3_decode(self.h, token, pos, 1 if want_logits else 0, _p(hidden),
-                                _p(lg) if lg is not None else None, C.byref(ai), C.byref(av))
+        rc = self.L.or_g3_decode(self.h, token, pos, 1 if want_logits else 0, _p(hidden),
+                                 _p(lg) if lg is not None else None, C.byref(ai), C.byref(av))
         if rc:
-            raise RuntimeError(lib().or_g3_error(self.h).decode())
+            raise RuntimeError(self.L.or_g3_error(self.h).decode())
         return dict(hidden=hidden, logits=lg, index=int(ai.value) if want_logits else None,
                     value=float(av.value) if want_logits else None)
 
@@ -225,9 +229,9 @@ class Model:
         pr = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.empty(max(max_new, 1), dtype=np.uint32)
         n = C.c_uint32()
-        rc = lib().or_g3_generate(self.h, _p(pr), pr.size, max_new, _p(out), C.byref(n))
+        rc = self.L.or_g3_generate(self.h, _p(pr), pr.size, max_new, _p(out), C.byref(n))
         if rc:
-            raise RuntimeError(lib().or_g3_error(self.h).decode())
+            raise RuntimeError(self.L.or_g3_error(self.h).decode())
         return out[: n.value].copy()
 
 

@@ -265,33 +265,42 @@ void or_apply_rope(float* v, uint32_t heads, uint32_t head_dim, const float* c, 
 int or_attention(const float* q, const float* keys, const float* values, uint32_t history,
                  uint32_t heads, uint32_t head_dim, float scale, float* out) {
     float* scores = (float*)malloc(sizeof(float) * (history ? history : 1));
-    if (!scores) return -2;
+    float* probs = (float*)malloc(sizeof(float) * (history ? history : 1));
+    if (!scores || !probs) { free(scores); free(probs); return -2; }
     memset(out, 0, sizeof(float) * heads * head_dim);
+    /* Long histories split the independent work over threads without changing any result: each
+     * score is its own dot product, and each output dimension keeps the time-ordered sum. */
+    const int par = history >= 256;
     for (uint32_t h = 0; h < heads; ++h) {
         const float* qh = q + (size_t)h * head_dim;
-        float max_score = -INFINITY;
+#pragma omp parallel for schedule(static) if (par)
         for (uint32_t t = 0; t < history; ++t) {
             const float* kt = keys + (size_t)t * head_dim;
             double dot = 0.0;
             for (uint32_t d = 0; d < head_dim; ++d) dot += (double)qh[d] * (double)kt[d];
             scores[t] = (float)dot * scale;
-            max_score = max_score < scores[t] ? scores[t] : max_score; /* std::max(a, b) */
         }
+        float max_score = -INFINITY;
+        for (uint32_t t = 0; t < history; ++t)
+            max_score = max_score < scores[t] ? scores[t] : max_score; /* std::max(a, b) */
         double den = 0.0;
         for (uint32_t t = 0; t < history; ++t) {
             const float e = expf(scores[t] - max_score);
             scores[t] = e;
             den += e;
         }
-        if (!(den > 0.0) || !isfinite(den)) { free(scores); return -1; }
+        if (!(den > 0.0) || !isfinite(den)) { free(scores); free(probs); return -1; }
+        for (uint32_t t = 0; t < history; ++t) probs[t] = (float)((double)scores[t] / den);
         float* oh = out + (size_t)h * head_dim;
-        for (uint32_t t = 0; t < history; ++t) {
-            const float p = (float)((double)scores[t] / den);
-            const float* vt = values + (size_t)t * head_dim;
-            for (uint32_t d = 0; d < head_dim; ++d) oh[d] += p * vt[d];
+#pragma omp parallel for schedule(static) if (par)
+        for (uint32_t d = 0; d < head_dim; ++d) {
+            float acc = 0.0f;
+            for (uint32_t t = 0; t < history; ++t) acc += probs[t] * values[(size_t)t * head_dim + d];
+            oh[d] = acc;
         }
     }
     free(scores);
+    free(probs);
     return 0;
 }
 

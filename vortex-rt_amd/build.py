@@ -99,8 +99,8 @@ def build_cpp_tests(jobs: int = 8) -> list:
 
     def one(src):
         exe = os.path.join(out_dir, os.path.basename(src)[:-4])
-        _run(["g++"] + CXX_FLAGS + ["-I" + CPP_TESTS, "-o", exe + ".tmp", src, "-L" + OUT, "-lvortexrt", "-lvrt_hip",
-                                    rpath])
+        _run(["g++"] + CXX_FLAGS + ["-I" + CPP_TESTS, "-I" + CSRC, "-o", exe + ".tmp", src, "-L" + OUT, "-lvortexrt",
+                                    "-lvrt_hip", rpath])
         os.replace(exe + ".tmp", exe)
         return exe
 

@@ -42,6 +42,7 @@
 #include <new>
 #include <vector>
 
+#include "vrt_g3_errors.hpp"
 #include "vrt_g3_internal.hpp"
 #include "vrt_internal.hpp"
 #include "vrt_q8_device.hpp"
@@ -625,7 +626,7 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
                            l > 0 ? g_mk_layers[l - 1u].post_ffw : nullptr, Ly.attn_norm, m.h, m.xa, nullptr, d,
                            g_mk.eps, bad, m.nwa0, m.nwa1, m.ya, kAnyA, tr))
         return false;
-    if (bad && w == 0 && tid == 0 && l > 0) mk_flag_min(l - 1u);   // :1857-1863
+    if (bad && w == 0 && tid == 0 && l > 0) mk_flag_min(g3_code_nonfinite(l - 1u));   // :1857-1863
     MK_MARK(3);
     u64* out = g_mk.x_qkv;
     batch_consume_x<SD, 1, 1>(rb, nblk_d, m.xa, [&](uint32_t v, float val) { ll_stf(out + v, val, tA); });
@@ -956,7 +957,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
         if (on) wts[h * kMaxChunks + lane] = e;
         if (lane == 0u) {
             wts[8u * kMaxChunks + h] = static_cast<float>(den);
-            if (!(den > 0.0) || !__builtin_isfinite(den)) mk_flag_min(0x40000000u | l);   // :1666-1670
+            if (!(den > 0.0) || !__builtin_isfinite(den)) mk_flag_min(g3_code_softmax(l));   // :1666-1670
         }
     }
     __syncthreads();
@@ -1062,7 +1063,7 @@ __device__ __forceinline__ bool mk_fold(uint32_t tagb) {
     if (mk_resid<EP, false>(g_mk.x_f, tagb + 5u * (L - 1u) + 5u, g_mk_layers[L - 1u].post_ffw, g_mk.out_norm, m.h, m.xa,
                             w == 0 ? g_mk.hidden : nullptr, d, g_mk.eps, bad, m.nwa0, m.nwa1, m.ya, kAnyFold))
         return false;
-    if (bad && w == 0 && tid == 0) mk_flag_min(L - 1u);
+    if (bad && w == 0 && tid == 0) mk_flag_min(g3_code_nonfinite(L - 1u));
     return true;
 }
 
@@ -1340,7 +1341,7 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
         if (tid == 0) {
             gp(g_mk.st)->step = s;
             gp(g_mk.st)->stop = stop;
-            if (!ok) mk_flag_min(0x20000000u);
+            if (!ok) mk_flag_min(kG3HandoffLost);
         }
     }
 }
@@ -1357,19 +1358,25 @@ struct MkState {
     size_t lds_bytes = 0;
     uint32_t grid = 0;
     uint32_t trace_slots = 0;      // slots per workgroup when tracing is enabled
+    bool registered = false;       // counted in its device slot's users
     std::vector<void*> allocs;
 };
 
-// Who last wrote g_mk / g_mk_layers on a device, and the event after its last launch.
+// Who last wrote g_mk / g_mk_layers on a device, and the event after its last launch. The
+// event lives while at least one executor with a persistent kernel exists on the device: the
+// last one to go destroys it, so no HIP object outlives the executors (nothing is released by
+// a static destructor at process exit).
 constexpr int kMaxDevices = 64;
 struct MkDeviceSlot {
     std::mutex mu;
     const MkState* owner = nullptr;
     uint64_t version = 0;
+    uint32_t users = 0;            // live executors with a persistent kernel on the device
     hipEvent_t last = nullptr;
     hipStream_t last_stream = nullptr;
 };
-// Never destroyed: executors released during process exit may still lock it.
+// Heap-allocated and never freed: the slots themselves hold no HIP resource once their last
+// executor is gone, and executors released late in process exit may still lock them.
 static MkDeviceSlot* device_slots() {
     static MkDeviceSlot* s = new MkDeviceSlot[kMaxDevices];
     return s;
@@ -1408,6 +1415,13 @@ void mk_destroy(vrt_g3* g) {
         MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
         std::lock_guard<std::mutex> lock(ds.mu);
         if (ds.owner == g->mk) ds.owner = nullptr;
+        if (g->mk->registered && --ds.users == 0u) {
+            // the last executor on the device: its stream is drained by the caller
+            if (ds.last) (void)hipEventDestroy(ds.last);
+            ds.last = nullptr;
+            ds.last_stream = nullptr;
+            ds.version = 0;
+        }
     }
     for (void* p : g->mk->allocs) (void)hipFree(p);
     delete g->mk;
@@ -1550,6 +1564,12 @@ int mk_setup(vrt_g3* g) {
     mk->fn = fn;
     mk->grid = nwg;
     g->mk_tag = 1u;
+    {
+        MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
+        std::lock_guard<std::mutex> lock(ds.mu);
+        ++ds.users;
+        mk->registered = true;
+    }
     return VRT_OK;
 }
 
@@ -1590,6 +1610,11 @@ int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uin
     VRT_REQUIRE(cap >= cnt, "exchange buffer needs %llu words", static_cast<unsigned long long>(cnt));
     VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
     VRT_HIP_CHECK(hipMemcpy(out, src, cnt * 8u, hipMemcpyDeviceToHost));
+    return VRT_OK;
+}
+
+int mk_read_abort(vrt_g3* g, uint32_t* dst) {
+    VRT_HIP_CHECK(hipMemcpyAsync(dst, g->mk->P.abort_flag, 4, hipMemcpyDeviceToHost, g->ctx->stream));
     return VRT_OK;
 }
 

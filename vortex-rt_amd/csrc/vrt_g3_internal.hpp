@@ -18,7 +18,7 @@ struct G3State {
     uint32_t lm_from;      // steps >= lm_from run the LM head
     uint32_t feed_until;   // tokens[s+1] comes from the host when s+1 < feed_until
     uint32_t want_logits;  // LM head also writes the logits
-    uint32_t nonfinite;    // first block whose output hidden state was non-finite (~0u: none)
+    uint32_t nonfinite;    // first failure (vrt_g3_errors.hpp codes; ~0u: none)
     uint32_t pad[2];
     uint32_t tickets[8];   // last-workgroup counters (self-resetting)
 };
@@ -63,6 +63,7 @@ struct LayerParams {
     uint32_t global;
     uint32_t attn_grid;   // workgroups of k_attn
     uint32_t chunk_max;   // max positions per attention workgroup
+    uint32_t index;       // block number
 };
 
 struct LaunchDesc {
@@ -121,6 +122,8 @@ int mk_setup(vrt_g3* g);
 int mk_run(vrt_g3* g, uint32_t nsteps);
 void mk_destroy(vrt_g3* g);
 int mk_clear_abort(vrt_g3* g);
+// Enqueues a copy of the abort word into host memory at *dst (stream-ordered, no sync).
+int mk_read_abort(vrt_g3* g, uint32_t* dst);
 int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int mk_set_trace(vrt_g3* g, bool on);
 // Batched prefill (vrt_prefill.hip): workspace for up to max_t positions, and one prefill of T

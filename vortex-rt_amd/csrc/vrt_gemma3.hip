@@ -26,6 +26,7 @@
 #include <new>
 #include <vector>
 
+#include "vrt_g3_errors.hpp"
 #include "vrt_g3_internal.hpp"
 #include "vrt_internal.hpp"
 #include "vrt_q8_device.hpp"
@@ -104,7 +105,7 @@ __device__ __forceinline__ void flag_nonfinite(const float (&h)[kMaxE], uint32_t
     for (int k = 0; k < kMaxE; ++k)
         if (threadIdx.x + static_cast<uint32_t>(k) * kThreads < n && !__builtin_isfinite(h[k])) bad = 1.0;
     bad = wg_sum_f64(bad, red);
-    if (bad != 0.0 && threadIdx.x == 0) atomicMin(&st->nonfinite, block);
+    if (bad != 0.0 && threadIdx.x == 0) atomicMin(&st->nonfinite, g3_code_nonfinite(block));
 }
 
 // =========================================================================================
@@ -318,7 +319,7 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
             num += wgt * static_cast<double>(pc[2u * H + h * hd + i]);
         }
         P.att[idx] = static_cast<float>(num / den);
-        if (!(den > 0.0) || !__builtin_isfinite(den)) atomicMin(&P.st->nonfinite, 0x40000000u | Lc.global);
+        if (!(den > 0.0) || !__builtin_isfinite(den)) atomicMin(&P.st->nonfinite, g3_code_softmax(Lc.index));
     }
     if (threadIdx.x == 0) P.st->tickets[0] = 0u;
 }
@@ -719,26 +720,22 @@ static int g3_fail_reset(vrt_g3* g, int code, const char* msg) {
     return code;
 }
 
-// Reads the step state back and maps device-side failures to the reference's messages.
+// Reads the step state back (and the persistent kernel's abort word) and maps device-side
+// failures to the reference's messages; a raised abort word is cleared for the next launch.
 static int g3_check_state(vrt_g3* g, G3State* out) {
     VRT_HIP_CHECK(hipMemcpyAsync(g->host_ctl, g->P.st, sizeof(G3State), hipMemcpyDeviceToHost, g->ctx->stream));
+    uint32_t* abort_word = &g->host_ctl->pad[0];
+    if (g->mk) {
+        if (int rc = mk_read_abort(g, abort_word)) return rc;
+    }
     VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
     *out = *g->host_ctl;
-    if (out->nonfinite != 0xffffffffu) {
-        char msg[128];
-        int code = VRT_ERR_NUMERIC;
-        if (out->nonfinite & 0x40000000u) {
-            std::snprintf(msg, sizeof msg, "Gemma 3 attention softmax failed");
-        } else if (out->nonfinite == 0x20000000u) {
-            // a persistent-kernel hand-off timed out; clear its abort flag for the next launch
-            std::snprintf(msg, sizeof msg, "Gemma 3 decode: device hand-off timed out");
-            if (int rc = mk_clear_abort(g)) return rc;
-            code = VRT_ERR_HIP;
-        } else {
-            std::snprintf(msg, sizeof msg, "Non-finite value after Gemma 3 block %u", out->nonfinite);
-        }
-        return g3_fail_reset(g, code, msg);
+    const uint32_t abort_flag = g->mk ? *abort_word : 0u;
+    const G3Failure f = g3_map_failure(out->nonfinite, abort_flag);
+    if (abort_flag != 0u) {
+        if (int rc = mk_clear_abort(g)) return rc;
     }
+    if (f.code != VRT_OK) return g3_fail_reset(g, f.code, f.msg);
     return VRT_OK;
 }
 
@@ -854,6 +851,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
         if (int rc = g3_upload(g, Ly.ffn_norm, d * 4u, &Lp.ffn_norm)) return fail(rc);
         if (int rc = g3_upload(g, Ly.post_ffw_norm, d * 4u, &Lp.post_ffw)) return fail(rc);
         Lp.global = ((l + 1u) % 6u) == 0u ? 1u : 0u;                                // :1301-1307
+        Lp.index = l;
         Lp.slots = (!Lp.global && c.sliding_window) ? std::min(c.sliding_window, c.context_length) : c.context_length;
         const size_t kv = static_cast<size_t>(Lp.slots) * hd * 4u;
         if (int rc = g3_alloc(g, kv, &p)) return fail(rc);

@@ -17,6 +17,7 @@
 #include <initializer_list>
 #include <utility>
 
+#include "vrt_g3_errors.hpp"
 #include "vrt_g3_internal.hpp"
 #include "vrt_q8_device.hpp"
 
@@ -119,7 +120,7 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
                 bad |= !__builtin_isfinite(hv[k]);
             }
         }
-        if (bad) atomicMin(&st->nonfinite, block);
+        if (bad) atomicMin(&st->nonfinite, g3_code_nonfinite(block));
     }
     if (!w_next) return;
     double ss = 0.0;
@@ -585,7 +586,8 @@ __global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
 // (src/gemma3.cpp:1602-1696); p as f16 hi/lo over the row's first ceil((t + 1) / 64) * 64
 // columns, zero outside the range (the O = P V GEMM reads up to there).
 __global__ void __launch_bounds__(kPfThreads) k_pf_softmax(const float* S, uint32_t T, uint32_t Tp, float scale,
-                                                           uint32_t window, _Float16* phi, _Float16* plo) {
+                                                           uint32_t window, _Float16* phi, _Float16* plo,
+                                                           G3State* st, uint32_t block) {
 #pragma clang fp contract(off)
     __shared__ double redd[4];
     __shared__ float redf[4];
@@ -601,7 +603,10 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_softmax(const float* S, uint3
     mx = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
     double den = 0.0;
     for (uint32_t j = j0 + threadIdx.x; j <= t; j += kPfThreads) den += static_cast<double>(expf(S[row + j] * scale - mx));
-    const float inv_den = static_cast<float>(1.0 / pf_sum(den, redd));
+    const double den_all = pf_sum(den, redd);
+    if (threadIdx.x == 0u && (!(den_all > 0.0) || !__builtin_isfinite(den_all)))   // :1666-1670
+        atomicMin(&st->nonfinite, g3_code_softmax(block));
+    const float inv_den = static_cast<float>(1.0 / den_all);
     for (uint32_t j = threadIdx.x; j < jend; j += kPfThreads) {
         const float p = (j >= j0 && j <= t) ? expf(S[row + j] * scale - mx) * inv_den : 0.0f;
         pf_split(p, phi + row + j, plo + row + j);
@@ -833,7 +838,9 @@ static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, const floa
         uint32_t t = T, tp = Tp, w = window;
         _Float16* phi = static_cast<_Float16*>(p.phi);
         _Float16* plo = static_cast<_Float16*>(p.plo);
-        void* args[] = {&S, &t, &tp, &scale, &w, &phi, &plo};
+        G3State* st = g->P.st;
+        uint32_t blk = Ly.index;
+        void* args[] = {&S, &t, &tp, &scale, &w, &phi, &plo, &st, &blk};
         VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_softmax), dim3(T, H), dim3(kPfThreads), args, 0, s));
     }
     {   // O_h = P_h V -> att[:, h * hd ..]
@@ -921,7 +928,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
             const float* f = x;
             const float* wpost = Ly.post_attn;
             const float* wnext = Ly.ffn_norm;
-            uint32_t blk = l;
+            uint32_t blk = Ly.index;
             void* args[] = {&h, &f, &so, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
             if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }

@@ -150,6 +150,74 @@ __global__ void __launch_bounds__(256) k_gelu_mul(float* __restrict__ gate, cons
     if (i < n) gate[i] = gelu_tanh_dev(gate[i]) * up[i];
 }
 
+// Gate/up half of the fused FFN (src/q8_matvec.cpp:1360-2004 with shaders/gelu_mul.comp as its
+// epilogue): pair i is gate row i and up row i, computed by two neighbouring row slots of one
+// wave (S <= 32, so a wave holds whole pairs); the even slot then writes h[i] = gelu_tanh(gate)
+// * up (and up[i] for the workspace image). Pairs [pairs_per_wg * blockIdx.x, ...) per workgroup.
+template <int S, int NB, int U>
+__global__ void __launch_bounds__(256) k_ffn_gateup(const uint8_t* gate_w, const uint8_t* up_w, uint64_t row_bytes,
+                                                    uint32_t K, const uint8_t* w_end, const float* __restrict__ x,
+                                                    float* __restrict__ h, float* __restrict__ up_out, uint32_t F,
+                                                    uint32_t pairs_per_wg) {
+#pragma clang fp contract(off)
+    static_assert(S <= 32, "a wave must hold whole gate/up pairs");
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* xs = reinterpret_cast<float*>(smem);
+    LimbLds L{reinterpret_cast<int8_t*>(xs + K), reinterpret_cast<int8_t*>(xs + K) + K,
+              reinterpret_cast<int8_t*>(xs + K) + 2 * K, reinterpret_cast<float*>(reinterpret_cast<int8_t*>(xs + K) + 3 * K)};
+    for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) xs[i] = x[i];
+    __syncthreads();
+    build_limbs(xs, K, L);
+    const uint32_t nblk = K >> 5;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t slot = lane / S, sl = lane % S;
+    XLimb xl[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+        if (b < nblk) load_limb(L, b, xl[n]);
+    }
+    constexpr uint32_t RPW = 64u / S;   // virtual rows per wave pass: RPW / 2 pairs
+    const uint32_t v_begin = 2u * blockIdx.x * pairs_per_wg;
+    const uint32_t v_end = min(2u * F, v_begin + 2u * pairs_per_wg);
+    if (v_begin >= v_end) return;
+    const uint32_t ngroups = (v_end - v_begin + RPW - 1u) / RPW;
+    for (uint32_t g0 = wave; g0 < ngroups; g0 += U * nwaves) {
+        Q8Raw raw[U][NB];
+        uint32_t vrow[U];
+        bool live[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t g = g0 + static_cast<uint32_t>(u) * nwaves;
+            vrow[u] = v_begin + g * RPW + slot;
+            live[u] = g < ngroups && vrow[u] < v_end;
+            const uint8_t* rp = ((vrow[u] & 1u) ? up_w : gate_w) + static_cast<uint64_t>(vrow[u] >> 1) * row_bytes;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+                if (live[u] && b < nblk) q8_load(rp + 34u * b, w_end, raw[u][n]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const uint32_t b = sl + static_cast<uint32_t>(n) * S;
+                if (live[u] && b < nblk) acc += q8_dot(raw[u][n], xl[n]);
+            }
+            const float tot = slot_sum<S>(acc);
+            // the up total of this pair, from the odd slot next to it (every lane takes part)
+            const float upv = __shfl(tot, static_cast<int>(min(lane + static_cast<uint32_t>(S), 63u)));
+            if (live[u] && sl == 0u && (slot & 1u) == 0u) {
+                const uint32_t i = vrow[u] >> 1;
+                h[i] = gelu_tanh_dev(tot) * upv;
+                up_out[i] = upv;
+            }
+        }
+    }
+}
+
 struct AmPartial {
     float value;
     uint32_t index;
@@ -244,6 +312,45 @@ __global__ void __launch_bounds__(256) k_dequantize(const uint8_t* __restrict__ 
     const uint8_t* b = blocks + (i >> 5) * 34u;
     const float s = half_bits_to_float(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
     out[i] = s * static_cast<float>(static_cast<int8_t>(b[2 + (i & 31u)]));
+}
+
+// The gate/up launch of the fused FFN into the workspace image ws = [h | up]: gelu_tanh(gate) *
+// up into ws[0..F), up into ws[F..2F). K of more than 32 blocks (64-lane row slots) runs the
+// gate/up matvec and the GELU as two kernels.
+static int launch_ffn_gateup(hipStream_t stream, const uint8_t* gate_w, const uint8_t* up_w, uint32_t K, uint32_t F,
+                             const uint8_t* w_end, const float* x, float* ws) {
+    float* h = ws;
+    float* up_out = ws + F;
+    MvShape sh;
+    VRT_REQUIRE(mv_shape(K, &sh), "Q8 fused FFN input_dim %u is outside the supported range (32..16384)", K);
+    const uint64_t row_bytes = static_cast<uint64_t>(K / 32u) * 34u;
+    auto go = [&](auto kern, uint32_t S) -> int {
+        const uint32_t pairs_per_pass = 4u * (64u / S) / 2u;   // 4 waves per workgroup
+        uint32_t groups = (F + pairs_per_pass - 1u) / pairs_per_pass;
+        uint32_t grid = std::min<uint32_t>(groups, 2048u);
+        const uint32_t per = (groups + grid - 1u) / grid * pairs_per_pass;
+        grid = (F + per - 1u) / per;
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(256), matvec_smem(K), stream, gate_w, up_w, row_bytes, K, w_end, x, h,
+                           up_out, F, per);
+        VRT_HIP_CHECK(hipGetLastError());
+        return VRT_OK;
+    };
+    switch (sh.S) {
+    case 1: return go(k_ffn_gateup<1, 1, 2>, 1);
+    case 2: return go(k_ffn_gateup<2, 1, 2>, 2);
+    case 4: return go(k_ffn_gateup<4, 1, 2>, 4);
+    case 8: return go(k_ffn_gateup<8, 1, 2>, 8);
+    case 16: return go(k_ffn_gateup<16, 1, 4>, 16);
+    case 32: return go(k_ffn_gateup<32, 1, 4>, 32);
+    default: {
+        const uint8_t* gu[2] = {gate_w, up_w};
+        const uint32_t gu_rows[2] = {F, F};
+        if (int rc = launch_matvec(stream, gu, gu_rows, 2, 0, K, w_end, x, ws)) return rc;
+        hipLaunchKernelGGL(k_gelu_mul, dim3((F + 255u) / 256u), dim3(256), 0, stream, h, up_out, F);
+        VRT_HIP_CHECK(hipGetLastError());
+        return VRT_OK;
+    }
+    }
 }
 
 }  // namespace vrt
@@ -475,11 +582,8 @@ extern "C" int vrt_q8_ffn(vrt_ctx* ctx, const void* weights, uint64_t weights_by
                 "Q8 fused FFN weight buffer is too small");
     VRT_REQUIRE(ws_bytes >= 2ull * ffn_dim * sizeof(float), "Q8 fused FFN activation/staging buffer is too small");
     const auto* w = static_cast<const uint8_t*>(weights);
-    const uint8_t* gu[2] = {w + gate_off, w + up_off};
-    const uint32_t gu_rows[2] = {ffn_dim, ffn_dim};
-    if (int rc = launch_matvec(ctx->stream, gu, gu_rows, 2, 0, input_dim, w + weights_bytes, x, ws)) return rc;
-    hipLaunchKernelGGL(k_gelu_mul, dim3((ffn_dim + 255u) / 256u), dim3(256), 0, ctx->stream, ws, ws + ffn_dim, ffn_dim);
-    VRT_HIP_CHECK(hipGetLastError());
+    if (int rc = launch_ffn_gateup(ctx->stream, w + gate_off, w + up_off, input_dim, ffn_dim, w + weights_bytes, x, ws))
+        return rc;
     const uint8_t* dn = w + down_off;
     return launch_matvec(ctx->stream, &dn, &output_dim, 1, 0, ffn_dim, w + weights_bytes, ws, y);
 }

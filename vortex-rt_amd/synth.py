@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from gguf import (GGML_F32, GGML_Q8_0, GgufWriter, T_ARR, T_BOOL, T_F32, T_I32, T_STR, T_U32)
+from gguf import (GGML_F32, GGML_Q8_0, GgufFile, GgufWriter, T_ARR, T_BOOL, T_F32, T_I32, T_STR, T_U32)
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -225,6 +225,54 @@ def write_gemma3_gguf(path, seed: int = 0, n_layers: int = 18, d_model: int = 64
         q8(p + "ffn_down.weight", d_model, ffn)
     w.write(path)
     return path
+
+
+def edit_gguf(src: str, dst: str, q8_scale_exp: dict | None = None, q8_zero=(), f32: dict | None = None) -> str:
+    """Writes a copy of the GGUF file `src` to `dst` with some tensor payloads changed in place
+    (header, metadata and layout untouched):
+      q8_scale_exp {name: k}  every Q8_0 block scale of the tensor times 2**k, by moving the
+                              fp16 exponent (exact; every nonzero scale must stay a normal half);
+      q8_zero [name, ...]     every block scale of the tensor set to +0 (the matrix becomes zero);
+      f32 {name: array}       the F32 tensor's values replaced."""
+    q8_scale_exp = q8_scale_exp or {}
+    f32 = f32 or {}
+    f = GgufFile.open(src)
+    try:
+        buf = bytearray(f._mm[:])
+        for name, k in q8_scale_exp.items():
+            t = f.tensors[name]
+            assert t.type == GGML_Q8_0, name
+            start = f.data_offset + t.offset
+            blk = np.frombuffer(buf, dtype=np.uint8, count=t.nbytes(), offset=start).reshape(-1, 34).copy()
+            h = blk[:, 0].astype(np.uint16) | (blk[:, 1].astype(np.uint16) << 8)
+            e = (h >> 10) & 0x1F
+            nz = (h & 0x7FFF) != 0
+            assert np.all(~nz | ((e >= 1) & (e <= 30))), f"{name}: scale not a normal half"
+            ne = e.astype(np.int32) + k
+            assert np.all(~nz | ((ne >= 1) & (ne <= 30))), f"{name}: scaled exponent out of range"
+            h2 = np.where(nz, (h & 0x83FF) | (ne.astype(np.uint16) << 10), h).astype(np.uint16)
+            blk[:, 0] = (h2 & 0xFF).astype(np.uint8)
+            blk[:, 1] = (h2 >> 8).astype(np.uint8)
+            buf[start:start + blk.size] = blk.tobytes()
+        for name in q8_zero:
+            t = f.tensors[name]
+            assert t.type == GGML_Q8_0, name
+            start = f.data_offset + t.offset
+            blk = np.frombuffer(buf, dtype=np.uint8, count=t.nbytes(), offset=start).reshape(-1, 34).copy()
+            blk[:, 0:2] = 0
+            buf[start:start + blk.size] = blk.tobytes()
+        for name, arr in f32.items():
+            t = f.tensors[name]
+            assert t.type == GGML_F32, name
+            a = np.ascontiguousarray(arr, dtype=np.float32)
+            assert a.nbytes == t.nbytes(), name
+            start = f.data_offset + t.offset
+            buf[start:start + a.nbytes] = a.tobytes()
+    finally:
+        f.close()
+    with open(dst, "wb") as fp:
+        fp.write(buf)
+    return dst
 
 
 def write_tokenizer_gguf(path, pieces, scores, types, bos=2, eos=1, unk=3, add_space_prefix=None):
