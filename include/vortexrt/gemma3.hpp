@@ -51,8 +51,8 @@ struct Gemma3GenerationResult {
 
 class Gemma3Model {
 public:
-    // The shader paths and the lane override are accepted for signature compatibility (the
-    // kernels are built in and pick their own row widths).
+    // The shader paths are accepted for signature compatibility (the kernels are built in);
+    // q8_lane_override must be 0, 8, 16, 32 or 64 (see narrow_q8_lane_count()).
     Gemma3Model(const std::string& gguf_path, DeviceContext& context, const std::string& q8_matvec_spirv = {},
                 const std::string& q8_matvec_u8_spirv = {}, const std::string& argmax_spirv = {},
                 const std::string& q8_matvec_32_spirv = {}, const std::string& q8_matvec_u8_32_spirv = {},
@@ -66,11 +66,18 @@ public:
 
     [[nodiscard]] const Gemma3Config& config() const noexcept { return config_; }
 
-    // Projections are always fused on this path (QKV in one phase, gate/up pairs in one).
-    [[nodiscard]] bool projection_fusion_enabled() const noexcept { return fuse_projections_; }
-    void set_projection_fusion_enabled(bool enabled) noexcept { fuse_projections_ = enabled; }
-    [[nodiscard]] std::uint32_t narrow_q8_lane_count() const noexcept { return 64; }
-    [[nodiscard]] bool fused_ffn_enabled() const noexcept { return fuse_projections_; }
+    // Lane and fusion policy (src/gemma3.cpp:94-172, :656-671). On this build both are
+    // structural rather than tunable: every Q/K/V projection is one fused phase (one launch on
+    // the multi-kernel path) and every gate/up pair one phase with the GELU product fused in, so
+    // fusion is always on and set_projection_fusion_enabled() leaves it on; matvec row slots
+    // are sized per matrix from its block count (input_dim / 32 rounded up to a power of two,
+    // wave64), so narrow_q8_lane_count() reports the slot width the narrow projections
+    // (input_dim <= 1024) actually run with, whatever q8_lane_override requested (the override is
+    // validated as the reference validates it).
+    [[nodiscard]] bool projection_fusion_enabled() const noexcept { return true; }
+    void set_projection_fusion_enabled(bool) noexcept {}
+    [[nodiscard]] std::uint32_t narrow_q8_lane_count() const noexcept { return narrow_lanes_; }
+    [[nodiscard]] bool fused_ffn_enabled() const noexcept { return true; }
 
     // reset_cache(); decode_token(token_id, 0, top_k); reset_cache() (src/gemma3.cpp:1884-1893).
     [[nodiscard]] Gemma3SingleTokenResult run_single_token(std::uint32_t token_id, std::size_t top_k = 8);
@@ -104,7 +111,7 @@ private:
     GgufFile gguf_;
     DeviceContext& context_;
     Gemma3Config config_{};
-    bool fuse_projections_ = true;
+    std::uint32_t narrow_lanes_ = 32;
     std::unique_ptr<Buffer> weights_arena_;
     vrt_g3* g3_ = nullptr;
     std::unique_ptr<Gemma3Tokenizer> tokenizer_;

@@ -1,224 +1,288 @@
-// vortexrt-gemma: the command line of Vortex-RT's Gemma 3 runtime (src/gemma_main.cpp) on the
-// HIP build. Same options and the same report lines, so scripts that grep the reference's
-// output ("Layers:", "Final hidden checksum:", "Top logits:", "Prompt token ids:",
-// "Generated token ids:", "TEXT_BEGIN", "TEXT_END", "Validation: OK") run unchanged.
+// vortexrt-gemma: the Gemma 3 command line over the vortexrt:: API (libvortexrt.so, HIP).
 //
-//   vortexrt-gemma model.gguf [--token-id N] [--top-k N] [--prompt TEXT] [--generate N]
-//                  [--projection-fusion auto|on|off] [--q8-lanes auto|8|16|32|64]
-//                  [--device <index|name>]
+// Interface kept from src/gemma_main.cpp, because scripts drive and grep it
+// (.github/workflows/build.yml:81-123): the option spellings (--token-id, --top-k, --prompt,
+// --generate, --projection-fusion, --q8-lanes, --device), the report labels ("Layers:",
+// "Final hidden checksum:", "Top logits:", "Prompt token ids:", "Generated token ids:",
+// "TEXT_BEGIN" / "TEXT_END", "Fused FFN:", "Validation: OK"), the definitions of the reported
+// figures (checksum sum_i x_i * (i + 1), RMS, max |x|) and the error texts of rejected options.
 //
-// Without --generate: one forward pass of --token-id at position 0 (default 2, BOS) with the
-// final hidden state's RMS, max |x| and checksum sum_i x_i * (i + 1), and the top-k logits
-// (k = 0 skips the LM head). With --generate N (at most 128): --prompt is tokenized with BOS
-// (an empty prompt is BOS alone) and N tokens are generated greedily with the KV cache.
+// Two modes. Forward (no --generate): one token at position 0 through every block, the final
+// hidden state summarised and, unless --top-k 0, the top logits. Generate (--generate N, N <= 128):
+// the prompt is tokenized with BOS and N tokens follow greedily on the KV cache.
 #include "vortexrt/build_config.hpp"
 #include "vortexrt/gemma3.hpp"
 #include "vortexrt/vulkan_context.hpp"
 
 #include <algorithm>
+#include <cerrno>
 #include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
 #include <exception>
-#include <iomanip>
 #include <iostream>
 #include <limits>
 #include <sstream>
 #include <stdexcept>
 #include <string>
+#include <string_view>
+#include <vector>
 
 namespace {
 
-struct Options {
-    std::string model_path;
-    std::string device;
+using Clock = std::chrono::steady_clock;
+
+// ---- settings and the option table ----------------------------------------------------------
+
+struct Settings {
+    std::string model;
+    std::string device;          // "" = VORTEXRT_DEVICE or device 0
     std::string prompt;
-    std::uint32_t token_id = 2;
+    std::uint32_t token = 2;     // BOS
     std::size_t top_k = 8;
-    std::size_t generate_tokens = 0;
-    std::string projection_fusion = "auto";
-    std::uint32_t q8_lanes = 0;
+    std::size_t generate = 0;    // 0: forward mode
+    int fusion = -1;             // -1 auto, 0 off, 1 on
+    std::uint32_t lanes = 0;     // 0 = auto
 };
 
-constexpr const char* kUsage =
-    "usage: vortexrt-gemma <model.gguf> [options]\n"
-    "  --token-id N          input token id (default: 2/BOS)\n"
-    "  --top-k N             display top logits; 0 skips LM head\n"
-    "  --prompt TEXT         tokenize/prefill a text prompt before generation\n"
-    "  --generate N          greedy-generate N tokens with KV cache\n"
-    "  --projection-fusion auto|on|off\n"
-    "                        override QKV/FFN projection fusion policy\n"
-    "  --q8-lanes auto|8|16|32|64\n"
-    "                        override narrow Q8 workgroup width\n"
-    "  --device <index|name> GPU selector (index or name substring)\n";
+constexpr std::size_t kMaxGenerate = 128;
 
-unsigned long long parse_unsigned(const std::string& text, const char* option, unsigned long long max,
-                                  const char* what) {
-    std::size_t used = 0;
-    unsigned long long v = 0;
-    try {
-        v = std::stoull(text, &used, 10);
-    } catch (const std::exception&) {
-        used = 0;
-    }
-    if (text.empty() || used != text.size() || text[0] == '-' || v > max)
-        throw std::runtime_error(std::string(option) + what);
+std::uint64_t to_uint(const std::string& text, std::uint64_t max, const std::string& error) {
+    const bool digits = !text.empty() && std::all_of(text.begin(), text.end(), [](char c) { return c >= '0' && c <= '9'; });
+    if (!digits) throw std::runtime_error(error);
+    errno = 0;
+    char* end = nullptr;
+    const unsigned long long v = std::strtoull(text.c_str(), &end, 10);
+    if (errno == ERANGE || *end != '\0' || v > max) throw std::runtime_error(error);
     return v;
 }
 
-Options parse_options(int argc, char** argv) {
-    if (argc < 2)
-        throw std::runtime_error(
-            "usage: vortexrt-gemma <model.gguf> [--token-id N] [--top-k N] [--generate N] "
-            "[--projection-fusion auto|on|off] [--q8-lanes auto|8|16|32|64] [--device <index|name>]");
-    Options o{};
-    o.model_path = argv[1];
-    for (int i = 2; i < argc; ++i) {
-        const std::string arg = argv[i];
-        auto value = [&](const char* name) -> std::string {
-            if (i + 1 >= argc) throw std::runtime_error(std::string(name) + " requires a value");
-            return argv[++i];
-        };
-        if (arg == "--token-id") {
-            o.token_id = static_cast<std::uint32_t>(
-                parse_unsigned(value("--token-id"), "--token-id", std::numeric_limits<std::uint32_t>::max(), " must be a uint32"));
-        } else if (arg == "--top-k") {
-            o.top_k = parse_unsigned(value("--top-k"), "--top-k", std::numeric_limits<std::size_t>::max(), " is out of range");
-        } else if (arg == "--prompt") {
-            o.prompt = value("--prompt");
-        } else if (arg == "--generate") {
-            o.generate_tokens =
-                parse_unsigned(value("--generate"), "--generate", std::numeric_limits<std::size_t>::max(), " is out of range");
-            if (o.generate_tokens > 128) throw std::runtime_error("--generate is capped at 128 during bring-up");
-        } else if (arg == "--projection-fusion") {
-            o.projection_fusion = value("--projection-fusion");
-            if (o.projection_fusion != "auto" && o.projection_fusion != "on" && o.projection_fusion != "off")
-                throw std::runtime_error("--projection-fusion must be auto, on, or off");
-        } else if (arg == "--q8-lanes") {
-            const std::string lanes = value("--q8-lanes");
-            if (lanes == "auto") {
-                o.q8_lanes = 0;
-            } else {
-                o.q8_lanes = static_cast<std::uint32_t>(
-                    parse_unsigned(lanes, "--q8-lanes", std::numeric_limits<std::uint32_t>::max(), " must be a uint32"));
-                if (o.q8_lanes != 8u && o.q8_lanes != 16u && o.q8_lanes != 32u && o.q8_lanes != 64u)
-                    throw std::runtime_error("--q8-lanes must be auto, 8, 16, 32, or 64");
-            }
-        } else if (arg == "--device") {
-            o.device = value("--device");
-        } else if (arg == "--help" || arg == "-h") {
-            std::cout << kUsage;
+struct OptionSpec {
+    const char* name;
+    const char* arg;
+    const char* help;
+    void (*apply)(Settings&, const std::string&);
+};
+
+const OptionSpec kOptions[] = {
+    {"--token-id", "N", "token fed at position 0 in forward mode (default 2, BOS)",
+     [](Settings& s, const std::string& v) {
+         s.token = static_cast<std::uint32_t>(to_uint(v, std::numeric_limits<std::uint32_t>::max(), "--token-id must be a uint32"));
+     }},
+    {"--top-k", "N", "logits listed in forward mode (default 8; 0 stops before the LM head)",
+     [](Settings& s, const std::string& v) {
+         s.top_k = static_cast<std::size_t>(to_uint(v, std::numeric_limits<std::size_t>::max(), "--top-k is out of range"));
+     }},
+    {"--prompt", "TEXT", "text tokenized (with BOS) ahead of generation", [](Settings& s, const std::string& v) { s.prompt = v; }},
+    {"--generate", "N", "greedy tokens to generate on the KV cache (at most 128)",
+     [](Settings& s, const std::string& v) {
+         s.generate = static_cast<std::size_t>(to_uint(v, std::numeric_limits<std::size_t>::max(), "--generate is out of range"));
+         if (s.generate > kMaxGenerate) throw std::runtime_error("--generate is capped at 128 during bring-up");
+     }},
+    {"--projection-fusion", "auto|on|off", "projection fusion policy",
+     [](Settings& s, const std::string& v) {
+         if (v == "auto") s.fusion = -1;
+         else if (v == "on") s.fusion = 1;
+         else if (v == "off") s.fusion = 0;
+         else throw std::runtime_error("--projection-fusion must be auto, on, or off");
+     }},
+    {"--q8-lanes", "auto|8|16|32|64", "Q8 row-slot width request",
+     [](Settings& s, const std::string& v) {
+         const std::string err = "--q8-lanes must be auto, 8, 16, 32, or 64";
+         if (v == "auto") { s.lanes = 0; return; }
+         const auto n = to_uint(v, 64, err);
+         if (n != 8 && n != 16 && n != 32 && n != 64) throw std::runtime_error(err);
+         s.lanes = static_cast<std::uint32_t>(n);
+     }},
+    {"--device", "INDEX|NAME", "GPU by index or by a substring of its name", [](Settings& s, const std::string& v) { s.device = v; }},
+};
+
+std::string usage() {
+    std::ostringstream u;
+    u << "vortexrt-gemma MODEL.gguf [option VALUE]...\n";
+    for (const auto& o : kOptions) {
+        std::string head = std::string(o.name) + " " + o.arg;
+        if (head.size() < 32) head.resize(32, ' ');
+        u << "  " << head << " " << o.help << "\n";
+    }
+    return u.str();
+}
+
+Settings parse(int argc, char** argv) {
+    const std::vector<std::string> args(argv + 1, argv + argc);
+    if (args.empty()) throw std::runtime_error("usage: " + usage());
+    if (args[0] == "--help" || args[0] == "-h") {
+        std::cout << usage();
+        std::exit(0);
+    }
+    Settings s;
+    s.model = args[0];
+    for (std::size_t i = 1; i < args.size(); ++i) {
+        const std::string& a = args[i];
+        if (a == "--help" || a == "-h") {
+            std::cout << usage();
             std::exit(0);
-        } else {
-            throw std::runtime_error("unknown argument: " + arg);
         }
+        const auto* spec = std::find_if(std::begin(kOptions), std::end(kOptions), [&](const OptionSpec& o) { return a == o.name; });
+        if (spec == std::end(kOptions)) throw std::runtime_error("unknown argument: " + a);
+        if (i + 1 >= args.size()) throw std::runtime_error(std::string(spec->name) + " requires a value");
+        spec->apply(s, args[++i]);
     }
-    return o;
+    return s;
 }
 
-// Printable form of a piece: \n, \r, \t and bytes outside [0x20, 0x7e] escaped.
-std::string escape_piece(const std::string& piece) {
-    std::ostringstream out;
-    for (const unsigned char c : piece) {
-        if (c == '\n') {
-            out << "\\n";
-        } else if (c == '\r') {
-            out << "\\r";
-        } else if (c == '\t') {
-            out << "\\t";
-        } else if (c >= 0x20 && c < 0x7f) {
-            out << static_cast<char>(c);
-        } else {
-            out << "\\x" << std::hex << std::setw(2) << std::setfill('0') << static_cast<unsigned>(c) << std::dec
-                << std::setfill(' ');
+// ---- report ----------------------------------------------------------------------------------
+
+// "  Label: value" lines under the title, the layout the reference's report uses.
+class Report {
+public:
+    explicit Report(std::ostream& os) : os_(os) { os_ << "Vortex-RT Gemma 3 runtime\n"; }
+    template <typename T>
+    Report& line(std::string_view label, const T& value) {
+        os_ << "  " << label << ": " << value << "\n";
+        return *this;
+    }
+    Report& ids(std::string_view label, const std::vector<std::uint32_t>& v) {
+        os_ << "  " << label << ":";
+        for (const auto id : v) os_ << ' ' << id;
+        os_ << "\n";
+        return *this;
+    }
+    std::ostream& raw() { return os_; }
+    void ok() { os_ << "  Validation: OK\n"; }
+
+private:
+    std::ostream& os_;
+};
+
+// Bytes as printable ASCII: \n \r \t and anything outside 0x20..0x7e escaped.
+std::string printable(std::string_view bytes) {
+    static const char kHex[] = "0123456789abcdef";
+    std::string out;
+    out.reserve(bytes.size());
+    for (const unsigned char c : bytes) {
+        switch (c) {
+        case '\n': out += "\\n"; break;
+        case '\r': out += "\\r"; break;
+        case '\t': out += "\\t"; break;
+        default:
+            if (c < 0x20 || c > 0x7e) {
+                out += "\\x";
+                out += kHex[c >> 4];
+                out += kHex[c & 15];
+            } else {
+                out += static_cast<char>(c);
+            }
         }
     }
-    return out.str();
+    return out;
 }
 
-double ms_since(std::chrono::steady_clock::time_point t0, std::chrono::steady_clock::time_point t1) {
-    return std::chrono::duration<double, std::milli>(t1 - t0).count();
+double elapsed_ms(Clock::time_point since) {
+    return std::chrono::duration<double, std::milli>(Clock::now() - since).count();
+}
+
+// The final hidden state's summary figures.
+struct HiddenSummary {
+    double rms = 0.0;
+    float max_abs = 0.0f;
+    double checksum = 0.0;   // sum_i x_i * (i + 1)
+};
+
+HiddenSummary summarize(const std::vector<float>& h) {
+    HiddenSummary s;
+    double sum_sq = 0.0;
+    std::size_t i = 0;
+    for (const float v : h) {
+        ++i;
+        if (!std::isfinite(v)) throw std::runtime_error("final hidden state is non-finite");
+        sum_sq += static_cast<double>(v) * v;
+        s.checksum += static_cast<double>(v) * static_cast<double>(i);
+        s.max_abs = std::max(s.max_abs, std::fabs(v));
+    }
+    s.rms = h.empty() ? 0.0 : std::sqrt(sum_sq / static_cast<double>(h.size()));
+    return s;
+}
+
+// ---- the two modes -----------------------------------------------------------------------------
+
+int run_generate(vortexrt::Gemma3Model& model, const Settings& s, Report& r) {
+    r.line("Greedy generation from BOS", std::to_string(s.generate) + " token(s)");
+    const std::vector<std::uint32_t> prompt = model.tokenize(s.prompt, true);
+    r.ids("Prompt token ids", prompt);
+    const auto t0 = Clock::now();
+    const auto result = model.generate_greedy_tokens(prompt, s.generate);
+    const double ms = elapsed_ms(t0);
+    r.ids("Generated token ids", result.token_ids);
+    r.line("Generation time", std::to_string(ms) + " ms");
+    const double rate = ms > 0.0 ? 1000.0 * static_cast<double>(result.token_ids.size()) / ms : 0.0;
+    r.line("Throughput", std::to_string(rate) + " tok/s");
+    r.line("Generated text", "\"" + printable(result.text) + "\"");
+    r.raw() << "TEXT_BEGIN\n" << result.text << "\nTEXT_END\n";
+    r.ok();
+    return 0;
+}
+
+int run_forward(vortexrt::Gemma3Model& model, const Settings& s, Report& r) {
+    r.line("Token", s.token);
+    const auto t0 = Clock::now();
+    const auto result = model.run_single_token(s.token, s.top_k);
+    const double ms = elapsed_ms(t0);
+    const HiddenSummary h = summarize(result.hidden);
+    r.line("Forward time", std::to_string(ms) + " ms");
+    r.line("Final hidden RMS", h.rms);
+    r.line("Final hidden max abs", h.max_abs);
+    std::ostringstream cs;
+    cs.precision(12);
+    cs << h.checksum;
+    r.line("Final hidden checksum", cs.str());
+    if (!result.top_tokens.empty()) {
+        r.raw() << "  Top logits:\n";
+        std::size_t rank = 0;
+        for (const auto& t : result.top_tokens)
+            r.raw() << "    " << ++rank << ": id=" << t.token_id << " logit=" << t.logit << " piece=\"" << printable(t.piece)
+                    << "\"\n";
+    }
+    r.ok();
+    return 0;
+}
+
+int run(const Settings& s) {
+    const auto t_start = Clock::now();
+    vortexrt::VulkanContext device(s.device);
+    const auto t_load = Clock::now();
+    namespace bc = vortexrt::build_config;
+    // the kernel paths are the reference constructor's (ignored: the HIP kernels are built in)
+    vortexrt::Gemma3Model model(s.model, device, bc::q8_matvec_spv, bc::q8_matvec_u8_spv, bc::argmax_spv, bc::q8_matvec_32_spv,
+                                bc::q8_matvec_u8_32_spv, bc::gelu_mul_spv, bc::q8_matvec_16_spv, bc::q8_matvec_u8_16_spv,
+                                bc::q8_matvec_8_spv, bc::q8_matvec_u8_8_spv, s.lanes);
+    if (s.fusion >= 0) model.set_projection_fusion_enabled(s.fusion == 1);
+    const double load_ms = elapsed_ms(t_load), setup_ms = elapsed_ms(t_start);
+
+    const auto& c = model.config();
+    Report r(std::cout);
+    r.line("GPU", device.capabilities().name)
+        .line("Layers", c.block_count)
+        .line("Hidden", c.embedding_length)
+        .line("FFN", c.feed_forward_length)
+        .line("Heads", std::to_string(c.head_count) + " / KV " + std::to_string(c.head_count_kv))
+        .line("Head dim", c.head_dim)
+        .line("Sliding window", c.sliding_window)
+        .line("Vocab", c.vocab_size)
+        .line("Narrow Q8 kernel", std::to_string(model.narrow_q8_lane_count()) + " lanes")
+        .line("Projection fusion", model.projection_fusion_enabled() ? "enabled" : "disabled")
+        .line("Fused FFN", model.fused_ffn_enabled() ? "enabled" : "disabled")
+        .line("Model load", std::to_string(load_ms) + " ms")
+        .line("Runtime setup", std::to_string(setup_ms) + " ms");
+    return s.generate ? run_generate(model, s, r) : run_forward(model, s, r);
 }
 
 }  // namespace
 
 int main(int argc, char** argv) {
     try {
-        const Options opt = parse_options(argc, argv);
-        const auto t_runtime = std::chrono::steady_clock::now();
-        vortexrt::VulkanContext context(opt.device);
-        const auto t_model = std::chrono::steady_clock::now();
-        namespace bc = vortexrt::build_config;
-        vortexrt::Gemma3Model model(opt.model_path, context, bc::q8_matvec_spv, bc::q8_matvec_u8_spv, bc::argmax_spv,
-                                    bc::q8_matvec_32_spv, bc::q8_matvec_u8_32_spv, bc::gelu_mul_spv, bc::q8_matvec_16_spv,
-                                    bc::q8_matvec_u8_16_spv, bc::q8_matvec_8_spv, bc::q8_matvec_u8_8_spv, opt.q8_lanes);
-        if (opt.projection_fusion == "on") model.set_projection_fusion_enabled(true);
-        if (opt.projection_fusion == "off") model.set_projection_fusion_enabled(false);
-        const auto t_ready = std::chrono::steady_clock::now();
-        const auto& c = model.config();
-        std::cout << "Vortex-RT Gemma 3 runtime\n"
-                  << "  GPU: " << context.capabilities().name << "\n"
-                  << "  Layers: " << c.block_count << "\n"
-                  << "  Hidden: " << c.embedding_length << "\n"
-                  << "  FFN: " << c.feed_forward_length << "\n"
-                  << "  Heads: " << c.head_count << " / KV " << c.head_count_kv << "\n"
-                  << "  Head dim: " << c.head_dim << "\n"
-                  << "  Sliding window: " << c.sliding_window << "\n"
-                  << "  Vocab: " << c.vocab_size << "\n"
-                  << "  Narrow Q8 kernel: " << model.narrow_q8_lane_count() << " lanes\n"
-                  << "  Projection fusion: " << (model.projection_fusion_enabled() ? "enabled" : "disabled") << "\n"
-                  << "  Fused FFN: " << (model.fused_ffn_enabled() ? "enabled" : "disabled") << "\n"
-                  << "  Model load: " << ms_since(t_model, t_ready) << " ms\n"
-                  << "  Runtime setup: " << ms_since(t_runtime, t_ready) << " ms\n";
-
-        if (opt.generate_tokens != 0) {
-            std::cout << "  Greedy generation from BOS: " << opt.generate_tokens << " token(s)\n";
-            const auto prompt = model.tokenize(opt.prompt, true);
-            std::cout << "  Prompt token ids:";
-            for (const auto id : prompt) std::cout << " " << id;
-            std::cout << "\n";
-            const auto t0 = std::chrono::steady_clock::now();
-            const auto gen = model.generate_greedy_tokens(prompt, opt.generate_tokens);
-            const double ms = ms_since(t0, std::chrono::steady_clock::now());
-            std::cout << "  Generated token ids:";
-            for (const auto id : gen.token_ids) std::cout << " " << id;
-            std::cout << "\n"
-                      << "  Generation time: " << ms << " ms\n"
-                      << "  Throughput: " << (ms > 0.0 ? static_cast<double>(gen.token_ids.size()) * 1000.0 / ms : 0.0)
-                      << " tok/s\n"
-                      << "  Generated text: \"" << escape_piece(gen.text) << "\"\n"
-                      << "TEXT_BEGIN\n"
-                      << gen.text << "\nTEXT_END\n"
-                      << "  Validation: OK\n";
-            return 0;
-        }
-
-        std::cout << "  Token: " << opt.token_id << "\n";
-        const auto t0 = std::chrono::steady_clock::now();
-        const auto r = model.run_single_token(opt.token_id, opt.top_k);
-        const double ms = ms_since(t0, std::chrono::steady_clock::now());
-        double checksum = 0.0, sum_sq = 0.0;
-        float max_abs = 0.0f;
-        for (std::size_t i = 0; i < r.hidden.size(); ++i) {
-            const float v = r.hidden[i];
-            if (!std::isfinite(v)) throw std::runtime_error("final hidden state is non-finite");
-            checksum += static_cast<double>(v) * static_cast<double>(i + 1);
-            sum_sq += static_cast<double>(v) * static_cast<double>(v);
-            max_abs = std::max(max_abs, std::fabs(v));
-        }
-        std::cout << "  Forward time: " << ms << " ms\n"
-                  << "  Final hidden RMS: " << std::sqrt(sum_sq / static_cast<double>(r.hidden.size())) << "\n"
-                  << "  Final hidden max abs: " << max_abs << "\n"
-                  << "  Final hidden checksum: " << std::setprecision(12) << checksum << "\n";
-        if (!r.top_tokens.empty()) {
-            std::cout << "  Top logits:\n";
-            for (std::size_t i = 0; i < r.top_tokens.size(); ++i)
-                std::cout << "    " << i + 1 << ": id=" << r.top_tokens[i].token_id << " logit=" << r.top_tokens[i].logit
-                          << " piece=\"" << escape_piece(r.top_tokens[i].piece) << "\"\n";
-        }
-        std::cout << "  Validation: OK\n";
-        return 0;
+        return run(parse(argc, argv));
     } catch (const std::exception& e) {
         std::cerr << "vortexrt-gemma: " << e.what() << "\n";
         return 1;

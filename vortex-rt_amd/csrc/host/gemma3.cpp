@@ -41,8 +41,11 @@ const GgufTensorInfo& require_tensor(const GgufFile& f, const std::string& name,
 Gemma3Model::Gemma3Model(const std::string& gguf_path, DeviceContext& context, const std::string&, const std::string&,
                          const std::string&, const std::string&, const std::string&, const std::string&,
                          const std::string&, const std::string&, const std::string&, const std::string&,
-                         std::uint32_t)
+                         std::uint32_t q8_lane_override)
     : gguf_(gguf_path), context_(context) {
+    if (q8_lane_override != 0u && q8_lane_override != 8u && q8_lane_override != 16u && q8_lane_override != 32u &&
+        q8_lane_override != 64u)
+        throw std::runtime_error("Q8 lane override must be 0, 8, 16, 32, or 64");   // src/gemma3.cpp:163-166
     gguf_.validate();
     if (gguf_.metadata_string("general.architecture").value_or("") != "gemma3")
         throw std::runtime_error("Gemma3Model requires general.architecture=gemma3");
@@ -67,6 +70,12 @@ Gemma3Model::Gemma3Model(const std::string& gguf_path, DeviceContext& context, c
         emb.dimensions[1] > std::numeric_limits<std::uint32_t>::max())
         throw std::runtime_error("Unsupported token_embd.weight layout");
     config_.vocab_size = static_cast<std::uint32_t>(emb.dimensions[1]);
+    {   // row-slot width of the narrow projections (input_dim = embedding_length): blocks rounded up to 2^k
+        const std::uint32_t blocks = std::max(1u, config_.embedding_length / 32u);
+        std::uint32_t lanes = 1;
+        while (lanes < blocks && lanes < 64u) lanes <<= 1;
+        narrow_lanes_ = lanes;
+    }
 
     // the tokenizer index (src/gemma3.cpp:289-454): incomplete metadata fails the load
     tokenizer_ = std::make_unique<Gemma3Tokenizer>(gguf_, config_.vocab_size);
