@@ -115,6 +115,16 @@ int vrt_q8_ffn(vrt_ctx* ctx, const void* weights, uint64_t weights_bytes,
                uint32_t input_dim, uint32_t ffn_dim, uint32_t output_dim,
                const float* x, float* workspace, uint64_t workspace_bytes, float* y);
 
+/* No counterpart in the reference. vrt_q8_ffn without a workspace argument, for callers that
+ * cannot allocate device memory (code under stream capture, serving loops, harnesses that forbid
+ * hipMalloc): the [h | up] workspace is a static per-device array of the library (128 KiB), so
+ * the call allocates nothing. ffn_dim <= 16384, else VRT_ERR_INVALID. Every call on a device
+ * shares that device's array: calls on one device that overlap (two contexts, two streams) race. */
+int vrt_q8_ffn_noalloc(vrt_ctx* ctx, const void* weights, uint64_t weights_bytes,
+                       uint32_t gate_offset, uint32_t up_offset, uint32_t down_offset,
+                       uint32_t input_dim, uint32_t ffn_dim, uint32_t output_dim,
+                       const float* x, float* y);
+
 /* shaders/gelu_mul.comp: gate[i] = gelu_tanh(gate[i]) * up[i]. */
 int vrt_gelu_mul(vrt_ctx* ctx, float* gate, const float* up, uint32_t n);
 

@@ -18,6 +18,8 @@ struct vrt_ctx {
     // context are stream-ordered, so calls never overlap on it.
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // This device's address of the static workspace of vrt_q8_ffn_noalloc (hipGetSymbolAddress).
+    float* ffn_scratch = nullptr;
 };
 
 namespace vrt {

@@ -19,6 +19,12 @@ namespace vrt {
 
 static thread_local std::string t_error;
 
+// Workspace of vrt_q8_ffn_noalloc: [h | up] of up to kFfnNoAllocMax FFN rows, one copy per GPU
+// (128 KiB, held until the process ends). Host code never uses this name as an address: the
+// device address comes from hipGetSymbolAddress at context creation (vrt_ctx::ffn_scratch).
+constexpr uint32_t kFfnNoAllocMax = 16384;
+static __device__ __align__(256) float scratch[2 * kFfnNoAllocMax];
+
 int set_error(int code, const char* fmt, ...) {
     char buf[1024];
     va_list ap;
@@ -419,6 +425,12 @@ extern "C" int vrt_ctx_create(const char* selector, vrt_ctx** out) {
         e = hipMalloc(&c->scratch, c->scratch_bytes);
         if (e == hipSuccess) e = hipMemset(c->scratch, 0, c->scratch_bytes);
     }
+    if (e == hipSuccess) {   // this device's copy of the no-allocation FFN workspace (dev is current)
+        void* sp = nullptr;
+        e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        c->ffn_scratch = static_cast<float*>(sp);
+        if (e == hipSuccess && !sp) e = hipErrorInvalidSymbol;
+    }
     if (e != hipSuccess) {
         if (c->scratch) (void)hipFree(c->scratch);
         if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -586,6 +598,17 @@ extern "C" int vrt_q8_ffn(vrt_ctx* ctx, const void* weights, uint64_t weights_by
         return rc;
     const uint8_t* dn = w + down_off;
     return launch_matvec(ctx->stream, &dn, &output_dim, 1, 0, ffn_dim, w + weights_bytes, ws, y);
+}
+
+extern "C" int vrt_q8_ffn_noalloc(vrt_ctx* ctx, const void* weights, uint64_t weights_bytes, uint32_t gate_off,
+                                  uint32_t up_off, uint32_t down_off, uint32_t input_dim, uint32_t ffn_dim,
+                                  uint32_t output_dim, const float* x, float* y) {
+    VRT_REQUIRE(ctx && ctx->ffn_scratch, "vrt_q8_ffn_noalloc: null context");
+    VRT_REQUIRE(ffn_dim <= kFfnNoAllocMax, "vrt_q8_ffn_noalloc: ffn_dim %u exceeds the static workspace (%u rows)",
+                ffn_dim, kFfnNoAllocMax);
+    // the same kernels as vrt_q8_ffn, on this device's static [h | up] workspace
+    return vrt_q8_ffn(ctx, weights, weights_bytes, gate_off, up_off, down_off, input_dim, ffn_dim, output_dim, x,
+                      ctx->ffn_scratch, 2ull * kFfnNoAllocMax * sizeof(float), y);
 }
 
 extern "C" int vrt_gelu_mul(vrt_ctx* ctx, float* gate, const float* up, uint32_t n) {

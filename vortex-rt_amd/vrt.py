@@ -80,6 +80,7 @@ SIGNATURES = {
     "vrt_q8_matvec": (_I, [_P, _P, _U64, _U32, _P, _P, _U32, _U32]),
     "vrt_q8_matvec_multi": (_I, [_P, _P, _U64, _U32, _P, _P, _U32, _P, _P]),
     "vrt_q8_ffn": (_I, [_P, _P, _U64, _U32, _U32, _U32, _U32, _U32, _U32, _P, _P, _U64, _P]),
+    "vrt_q8_ffn_noalloc": (_I, [_P, _P, _U64, _U32, _U32, _U32, _U32, _U32, _U32, _P, _P]),
     "vrt_gelu_mul": (_I, [_P, _P, _P, _U32]),
     "vrt_argmax": (_I, [_P, _P, _U32, _P]),
     "vrt_q8_quantize": (_I, [_P, _P, _U64, _U32, _P]),
@@ -233,6 +234,11 @@ def q8_matvec_multi(ctx, w: DeviceBuffer, offs, dims, k: int, x: DeviceBuffer, y
 def q8_ffn(ctx, w, gate_off, up_off, down_off, k, ffn, out, x, ws, y):
     check(lib().vrt_q8_ffn(ctx.h, w.ptr, w.nbytes, gate_off, up_off, down_off, k, ffn, out, x.ptr, ws.ptr, ws.nbytes,
                            y.ptr))
+
+
+def q8_ffn_noalloc(ctx, w, gate_off, up_off, down_off, k, ffn, out, x, y):
+    """vrt_q8_ffn on the library's static per-device workspace (no allocation)."""
+    check(lib().vrt_q8_ffn_noalloc(ctx.h, w.ptr, w.nbytes, gate_off, up_off, down_off, k, ffn, out, x.ptr, y.ptr))
 
 
 def gelu_mul(ctx, gate: DeviceBuffer, up: DeviceBuffer, n: int):
