@@ -71,7 +71,6 @@ constexpr uint32_t kMkWaves = kMkThreads / 64;
 constexpr uint32_t kVec = 4;                 // vector elements per thread (vectors <= 2048)
 constexpr uint32_t kSpinLimit = 1u << 21;    // polls before a hand-off is declared lost
 constexpr int kPollSleep = 4;                // s_sleep between unsuccessful polls (64 clocks each)
-constexpr uint32_t kResidWaves = 4;          // waves that compute a residual fold + norm (one per SIMD)
 constexpr uint32_t kMaxChunks = 16;          // attention chunks per block
 constexpr uint32_t kMaxBUnits = 64;          // attention workgroups (chunks x query heads) per block
 constexpr uint32_t kLmUnits = 3;             // 16-byte LM-head loads per thread per tile
@@ -99,7 +98,7 @@ struct MkLayer {
 // Byte offsets of the dynamic LDS carve-up. `u` is phase-local scratch shared by the
 // attention partial sums (B), the gathered chunk partials (C) and the LM-head tile.
 struct MkLds {
-    uint32_t h, xs, xa, xd, ya, yd, nwa0, nwa1, nwd0, nwd1, any, la, lb, lc, ls, sc, mw, gu, u, total;
+    uint32_t h, xs, xa, xd, red, any, la, lb, lc, ls, sc, mw, gu, u, tr, total;
 };
 
 constexpr uint32_t kMkLdsBytes = 144u * 1024u;   // static LDS of the persistent kernel
@@ -154,8 +153,7 @@ __device__ __forceinline__ bool blk_any(int pred, uint32_t id) {
     return r != 0u;
 }
 // call sites of blk_any (flag sets)
-constexpr uint32_t kAnyGather0 = 0, kAnyGather1 = 1, kAnyGatherE = 2, kAnyArgmax = 3, kAnyB = 4, kAnyA = 5, kAnyD = 6,
-                   kAnyFold = 7;
+constexpr uint32_t kAnyGather0 = 0, kAnyGather1 = 1, kAnyGatherE = 2, kAnyArgmax = 3, kAnyB = 4;
 
 // ---- tagged exchange -----------------------------------------------------------------------
 
@@ -199,12 +197,6 @@ struct MkSmem {
     float* xs;      // matvec input of phases C and E
     float* xa;      // normed input of phase A and of the LM head
     float* xd;      // normed input of phase D
-    float* ya;      // gathered residual input of phase A and of the final fold
-    float* yd;      // gathered residual input of phase D
-    float* nwa0;    // norm weights staged for phase A and the fold (post, next)
-    float* nwa1;
-    float* nwd0;    // norm weights staged for phase D
-    float* nwd1;
     LimbLds L;      // LM-head activation limbs
     float* sc;      // argmax partials (2 nwg words)
     float* mw;      // phase B/C per-head scalars
@@ -219,12 +211,6 @@ __device__ __forceinline__ MkSmem mk_smem() {
     m.xs = reinterpret_cast<float*>(smem + g_mk.lds.xs);
     m.xa = reinterpret_cast<float*>(smem + g_mk.lds.xa);
     m.xd = reinterpret_cast<float*>(smem + g_mk.lds.xd);
-    m.ya = reinterpret_cast<float*>(smem + g_mk.lds.ya);
-    m.yd = reinterpret_cast<float*>(smem + g_mk.lds.yd);
-    m.nwa0 = reinterpret_cast<float*>(smem + g_mk.lds.nwa0);
-    m.nwa1 = reinterpret_cast<float*>(smem + g_mk.lds.nwa1);
-    m.nwd0 = reinterpret_cast<float*>(smem + g_mk.lds.nwd0);
-    m.nwd1 = reinterpret_cast<float*>(smem + g_mk.lds.nwd1);
     m.L = LimbLds{reinterpret_cast<int8_t*>(smem + g_mk.lds.la), reinterpret_cast<int8_t*>(smem + g_mk.lds.lb),
                   reinterpret_cast<int8_t*>(smem + g_mk.lds.lc), reinterpret_cast<float*>(smem + g_mk.lds.ls)};
     m.sc = reinterpret_cast<float*>(smem + g_mk.lds.sc);
@@ -330,10 +316,14 @@ __device__ __forceinline__ void lm_wait_tiles(uint32_t later) {
     (void)rb_a; (void)rb_f
 
 // Sub-phase mark k (< kMarks) of the traced block, in the last kMarks trace slots.
+// Trace timestamps go to a per-workgroup LDS image (an LDS store does not hold up the wave's
+// later vector-memory waits, as a global store would) that is copied out at the end of the step.
+__device__ __forceinline__ void mk_stamp(uint32_t slot, uint64_t t) {
+    reinterpret_cast<uint64_t*>(g_mk_lds + g_mk.lds.tr)[slot] = t;
+}
 #define MK_MARK(k)                                                                                        \
     do {                                                                                                  \
-        if (tr && tid == 0u)                                                                              \
-            gp(g_mk.trace)[w * g_mk.trace_slots + g_mk.trace_slots - kMarks + (k)] = __builtin_amdgcn_s_memrealtime(); \
+        if (tr && tid == 0u) mk_stamp(g_mk.trace_slots - kMarks + (k), __builtin_amdgcn_s_memrealtime());  \
     } while (0)
 
 // Scalar (uniform) copies of a phase's arguments: function arguments arrive in vector
@@ -453,33 +443,7 @@ __device__ __forceinline__ float mk_rms_scale_pow2(double ss, uint32_t n, float 
     return 1.0f / sqrtf(static_cast<float>(ss * (1.0 / static_cast<double>(n))) + eps);
 }
 
-// Copies n floats (n % 4 == 0) of src into LDS dst with direct global->LDS loads issued by the
-// calling wave: lane i moves 16 bytes of each 1 KB row. No registers hold the data; the loads
-// complete in issue order with the wave's other vector-memory loads. dst holds whole 1 KB rows
-// (units past n repeat the last unit of src).
-__device__ __forceinline__ void wave_stage_lds(const float* src, float* dst, uint32_t n) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t n16 = n >> 2;
-    for (uint32_t r = 0; r * 64u < n16; ++r) {
-        const uint32_t u = min(r * 64u + lane, n16 - 1u);
-        __builtin_amdgcn_global_load_lds((const VRT_AS_GLOBAL void*)(src + 4u * u),
-                                         (__attribute__((address_space(3))) void*)(dst + 256u * r), 16, 0, 0);
-    }
-}
-
-// Residual update and RMSNorm of the d-vector residual stream h, which every workgroup keeps in
-// LDS. All threads gather y (two tagged words per 16-byte unit) into LDS, wave 0 meanwhile
-// stages the two norm weight vectors into LDS; after one barrier every wave computes the whole
-// update on its own (lane i: element pairs (2j, 2j + 1), j = i + 64k), so no second barrier is
-// needed, and the waves write identical values to h and x:
-//   h = y * (rms(y) * w_post) + h   if ysrc != nullptr        (src/gemma3.cpp:1703-1711, :1849-1855)
-//   x = (h * rms(h)) * w_next        (INTO: rms_norm_into, :991-996, :1713-1718)
-//   x = h * (rms(h) * w_next)        (!INTO: rms_norm_inplace, the output norm :1866-1868)
-// with rms(v) = 1.0f / sqrtf(float(sum double(v)^2 / d) + eps) (:967-983). x goes to x_lds and,
-// from wave 0, to x_glob if given. `bad` is set when h has a non-finite element (:1857-1863).
-// y_lds and the staging areas belong to one call site: a later call site may run while slower
-// waves still read this one's. Returns 1 if the gather was abandoned.
-// Pairwise sum of N doubles (a short dependency chain; the squares it sums are exact).
+// Pairwise sum of N doubles (a short dependency chain).
 template <int N>
 __device__ __forceinline__ double tree_sum(double (&v)[N]) {
 #pragma unroll
@@ -489,110 +453,128 @@ __device__ __forceinline__ double tree_sum(double (&v)[N]) {
     return v[0];
 }
 
+// The eight wave totals of a workgroup reduction, summed in wave order (every thread gets the
+// same bits).
+__device__ __forceinline__ double sum_waves(const double* r) {
+    return ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+}
+static_assert(kMkWaves == 8, "sum_waves adds eight wave totals");
+
+// Residual update and RMSNorm of the d-vector residual stream h, which every workgroup keeps in
+// LDS, spread over all eight waves: thread t owns the element pairs j = t + 512 k (k < P). It
+// gathers its pairs of y (two tagged words per 16-byte unit) and reads its pairs of h and of the
+// norm weights (global loads issued before the gather waits); each sum of squares is a per-thread
+// double sum, a DPP wave reduction and the eight wave totals through LDS behind one barrier:
+//   h = y * (rms(y) * w_post) + h   if ysrc != nullptr        (src/gemma3.cpp:1703-1711, :1849-1855)
+//   x = (h * rms(h)) * w_next        (INTO: rms_norm_into, :991-996, :1713-1718)
+//   x = h * (rms(h) * w_next)        (!INTO: rms_norm_inplace, the output norm :1866-1868)
+// with rms(v) = 1.0f / sqrtf(float(sum double(v)^2 / d) + eps) (:967-983). Each thread rewrites
+// only its own pairs of h; x goes to x_lds and, if given, to x_glob. `bad` is set when h has a
+// non-finite element (:1857-1863). Ends with a barrier; returns 1 if the gather was abandoned
+// (the same decision in every thread).
 template <int EP, bool INTO>
 __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const float* w_post, const float* w_next,
                                         float* hl, float* x_lds, float* x_glob, uint32_t d, float eps, int& bad,
-                                        float* nw_post, float* nw_next, float* y_lds, uint32_t any_id, bool tr = false,
-                                        uint32_t mk0 = 31u) {
+                                        bool tr = false, uint32_t mk0 = 31u) {
 #pragma clang fp contract(off)
+    constexpr int P = (EP * 64 + static_cast<int>(kMkThreads) - 1) / static_cast<int>(kMkThreads);
     auto mark = [&](uint32_t k) {
         if (tr && threadIdx.x == 0u)
-            gp(g_mk.trace)[blockIdx.x * g_mk.trace_slots + g_mk.trace_slots - kMarks + k] = __builtin_amdgcn_s_memrealtime();
+            mk_stamp(g_mk.trace_slots - kMarks + k, __builtin_amdgcn_s_memrealtime());
     };
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t npair = d >> 1u;
-    if (wave == 0u) {   // the norm weights travel to LDS while the gather waits
-        wave_stage_lds(w_next, nw_next, d);
-        if (ysrc) wave_stage_lds(w_post, nw_post, d);
+    double* red = reinterpret_cast<double*>(g_mk_lds + g_mk.lds.red);   // [2][waves] totals
+    int* flg = reinterpret_cast<int*>(red + 2u * kMkWaves);               // [2][waves] flags
+    uint32_t j[P];
+    bool live[P];
+    float2 wp[P], wn[P], h[P], y[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        j[k] = tid + kMkThreads * static_cast<uint32_t>(k);
+        live[k] = j[k] < npair;
+        const uint32_t jj = live[k] ? j[k] : 0u;
+        wn[k] = make_float2(gp(w_next)[2u * jj], gp(w_next)[2u * jj + 1u]);
+        wp[k] = make_float2(0.0f, 0.0f);
+        if (ysrc) wp[k] = make_float2(gp(w_post)[2u * jj], gp(w_post)[2u * jj + 1u]);
+        h[k] = live[k] ? reinterpret_cast<const float2*>(hl)[jj] : make_float2(0.0f, 0.0f);
+        y[k] = make_float2(0.0f, 0.0f);
     }
-    int fail = 0;
     if (ysrc) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(ysrc), 0, static_cast<int>(d * 8u), kRsrcFlags);
-        int off[2];
-        bool live[2];
+        int off[P];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t j = threadIdx.x + kMkThreads * k;
-            live[k] = j < npair;
-            off[k] = live[k] ? static_cast<int>(j * 16u) : 0x7ffffff0;   // past the buffer: no access
+        for (int k = 0; k < P; ++k) off[k] = live[k] ? static_cast<int>(j[k] * 16u) : 0x7ffffff0;   // past: no access
+        float yv[2 * P];
+        const int fail = ll_poll2<P>(r, off, live, tag, yv);
+#pragma unroll
+        for (int k = 0; k < P; ++k) y[k] = live[k] ? make_float2(yv[2 * k], yv[2 * k + 1]) : make_float2(0.0f, 0.0f);
+        mark(mk0);
+        double sq[2 * P];
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            sq[2 * k] = static_cast<double>(y[k].x) * static_cast<double>(y[k].x);
+            sq[2 * k + 1] = static_cast<double>(y[k].y) * static_cast<double>(y[k].y);
         }
-        float y[4];
-        fail = ll_poll2<2>(r, off, live, tag, y);
+        const double s = wave_red_sum_d(tree_sum(sq));
+        const bool wf = __builtin_amdgcn_ballot_w64(fail != 0) != 0u;
+        if (lane == 0u) {
+            red[wave] = s;
+            flg[wave] = wf ? 1 : 0;
+        }
+        __syncthreads();
+        int any = 0;
 #pragma unroll
-        for (int k = 0; k < 2; ++k)
-            if (live[k]) reinterpret_cast<float2*>(y_lds)[threadIdx.x + kMkThreads * k] = make_float2(y[2 * k], y[2 * k + 1]);
+        for (uint32_t k = 0; k < kMkWaves; ++k) any |= flg[k];
+        if (any) return 1;
+        mark(mk0 + 1u);
+        const float sc = mk_rms_scale(sum_waves(red), d, eps);
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            h[k].x = y[k].x * (sc * wp[k].x) + h[k].x;
+            h[k].y = y[k].y * (sc * wp[k].y) + h[k].y;
+        }
     }
-    if (wave == 0u) __builtin_amdgcn_s_waitcnt(0);   // the staged weights are in LDS (vmcnt covers LDS loads)
-    // Waves 0..kResidWaves-1 (one per SIMD) compute the fold and both norms, each for the whole
-    // vector (the sums need every element); the others wait at the closing barrier. h is read
-    // before the barrier below and rewritten after it, so no wave reads a rewritten h.
-    const bool comp = wave < kResidWaves;
-    float2 h[EP];
-    bool live[EP];
+    int nf = 0;
+    double sq2[2 * P];
 #pragma unroll
-    for (int k = 0; k < EP; ++k) {
-        const uint32_t j = lane + 64u * static_cast<uint32_t>(k);
-        live[k] = j < npair;
-        h[k] = comp && live[k] ? reinterpret_cast<const float2*>(hl)[j] : make_float2(0.0f, 0.0f);
+    for (int k = 0; k < P; ++k) {
+        nf |= !__builtin_isfinite(h[k].x) || !__builtin_isfinite(h[k].y);
+        sq2[2 * k] = static_cast<double>(h[k].x) * static_cast<double>(h[k].x);
+        sq2[2 * k + 1] = static_cast<double>(h[k].y) * static_cast<double>(h[k].y);
     }
-    mark(mk0);
-    if (blk_any(fail, any_id)) return 1;
-    mark(mk0 + 1u);
-    if (comp) {
-        if (ysrc) {
-            float2 y[EP];
-            double sq[2 * EP];
+    const double s2 = wave_red_sum_d(tree_sum(sq2));
+    const bool wnf = __builtin_amdgcn_ballot_w64(nf != 0) != 0u;
+    if (lane == 0u) {
+        red[kMkWaves + wave] = s2;
+        flg[kMkWaves + wave] = wnf ? 1 : 0;
+    }
+    __syncthreads();
+    int anynf = 0;
 #pragma unroll
-            for (int k = 0; k < EP; ++k) {
-                y[k] = live[k] ? reinterpret_cast<const float2*>(y_lds)[lane + 64u * k] : make_float2(0.0f, 0.0f);
-                sq[2 * k] = static_cast<double>(y[k].x) * static_cast<double>(y[k].x);
-                sq[2 * k + 1] = static_cast<double>(y[k].y) * static_cast<double>(y[k].y);
+    for (uint32_t k = 0; k < kMkWaves; ++k) anynf |= flg[kMkWaves + k];
+    bad = anynf;
+    const float sc2 = mk_rms_scale(sum_waves(red + kMkWaves), d, eps);
+    mark(mk0 + 2u);
+#pragma unroll
+    for (int k = 0; k < P; ++k)
+        if (live[k]) {
+            float2 x;
+            if constexpr (INTO) {
+                x.x = h[k].x * sc2 * wn[k].x;
+                x.y = h[k].y * sc2 * wn[k].y;
+            } else {
+                x.x = h[k].x * (sc2 * wn[k].x);
+                x.y = h[k].y * (sc2 * wn[k].y);
             }
-            const float sc = mk_rms_scale(wave_red_sum_d(tree_sum(sq)), d, eps);
-#pragma unroll
-            for (int k = 0; k < EP; ++k) {
-                const float2 wp = reinterpret_cast<const float2*>(nw_post)[live[k] ? lane + 64u * k : 0u];
-                h[k].x = y[k].x * (sc * wp.x) + h[k].x;
-                h[k].y = y[k].y * (sc * wp.y) + h[k].y;
+            reinterpret_cast<float2*>(hl)[j[k]] = h[k];
+            reinterpret_cast<float2*>(x_lds)[j[k]] = x;
+            if (x_glob) {
+                gp(x_glob)[2u * j[k]] = x.x;
+                gp(x_glob)[2u * j[k] + 1u] = x.y;
             }
         }
-        int nf = 0;
-        double sq2[2 * EP];
-#pragma unroll
-        for (int k = 0; k < EP; ++k) {
-            const float2 v = live[k] ? h[k] : make_float2(0.0f, 0.0f);
-            nf |= !__builtin_isfinite(v.x) || !__builtin_isfinite(v.y);
-            sq2[2 * k] = static_cast<double>(v.x) * static_cast<double>(v.x);
-            sq2[2 * k + 1] = static_cast<double>(v.y) * static_cast<double>(v.y);
-        }
-        bad = __builtin_amdgcn_ballot_w64(nf != 0) != 0u;   // used by wave 0
-        const float sc2 = mk_rms_scale(wave_red_sum_d(tree_sum(sq2)), d, eps);
-        mark(mk0 + 2u);
-#pragma unroll
-        for (int k = 0; k < EP; ++k)
-            if (live[k]) {
-                const uint32_t j = lane + 64u * k;
-                const float2 wn = reinterpret_cast<const float2*>(nw_next)[j];
-                float2 x;
-                if constexpr (INTO) {
-                    x.x = h[k].x * sc2 * wn.x;
-                    x.y = h[k].y * sc2 * wn.y;
-                } else {
-                    x.x = h[k].x * (sc2 * wn.x);
-                    x.y = h[k].y * (sc2 * wn.y);
-                }
-                if (static_cast<uint32_t>(k) % kResidWaves == wave) {   // the computing waves share the writes
-                    reinterpret_cast<float2*>(hl)[j] = h[k];
-                    reinterpret_cast<float2*>(x_lds)[j] = x;
-                }
-                if (x_glob && wave == 0u) {
-                    gp(x_glob)[2u * j] = x.x;
-                    gp(x_glob)[2u * j + 1u] = x.y;
-                }
-            }
-    }
     __syncthreads();   // h and x are complete for every wave
     return 0;
 }
@@ -624,7 +606,7 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     int bad = 0;
     if (mk_resid<EP, true>(l > 0 ? g_mk.x_f : nullptr, tagb + 5u * (l - 1u) + 5u,
                            l > 0 ? g_mk_layers[l - 1u].post_ffw : nullptr, Ly.attn_norm, m.h, m.xa, nullptr, d,
-                           g_mk.eps, bad, m.nwa0, m.nwa1, m.ya, kAnyA, tr))
+                           g_mk.eps, bad, tr))
         return false;
     if (bad && w == 0 && tid == 0 && l > 0) mk_flag_min(g3_code_nonfinite(l - 1u));   // :1857-1863
     MK_MARK(3);
@@ -767,18 +749,6 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             k[e] = lo ? k[e] * cs[e] - ko[e] * sn[e] : k[e] * cs[e] + ko[e] * sn[e];
         }
         MK_MARK(8);
-        // KV append by wave 0 of head 0 of the chunk that holds the current position; every
-        // wave uses its own copy of the new row
-        const bool appender = h == 0u && c1 == pos + 1u && uw == 0u;
-        if (appender && dlive && !fail) {
-            const uint32_t so = ((pos % Ly.slots) * hd + dl) * 4u;
-            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(k[0]), __float_as_uint(k[1]),
-                                                       __float_as_uint(k[2]), __float_as_uint(k[3])},
-                                                   rk, static_cast<int>(so), 0, kCoherent);
-            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]),
-                                                       __float_as_uint(v[2]), __float_as_uint(v[3])},
-                                                   rv, static_cast<int>(so), 0, kCoherent);
-        }
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         float m_run = -INFINITY, l_run = 0.0f;
         const float attn_scale = g_mk.attn_scale;
@@ -852,13 +822,27 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                 m_run = m_new;
             }
         }
+        // KV append (the current position's k and v, post-norm and post-RoPE) by wave 0 of head 0
+        // of the chunk that holds the current position, after the loop so that no wait of the
+        // loop covers the stores. Positions < pos are read from the cache by the next step only;
+        // this wave's next vector-memory wait in a later phase completes the stores, and every
+        // such phase precedes a publication that the next step's attention depends on (vector
+        // memory operations complete in issue order), so no wait is needed here.
+        const bool appender = h == 0u && c1 == pos + 1u && uw == 0u;
+        if (appender && dlive && !fail) {
+            const uint32_t so = ((pos % Ly.slots) * hd + dl) * 4u;
+            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(k[0]), __float_as_uint(k[1]),
+                                                       __float_as_uint(k[2]), __float_as_uint(k[3])},
+                                                   rk, static_cast<int>(so), 0, kCoherent);
+            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                       __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                                   rv, static_cast<int>(so), 0, kCoherent);
+        }
         if (dlive) *reinterpret_cast<float4*>(ra + uw * hd + dl) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         if (lane == 0) {
             rml[uw] = m_run;
             rml[kBMaxWaves + uw] = l_run;
         }
-        // the appended row is complete before this wave publishes its share of the partial
-        if (appender) __builtin_amdgcn_s_waitcnt(0);
     }
     MK_MARK(9);
     if (blk_any(fail, kAnyB)) return false;
@@ -1009,8 +993,7 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     RowBatch<SD, 1, 2> rb;
     batch_load<SD, 1, 2>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
     int none = 0;
-    if (mk_resid<EP, true>(g_mk.x_o, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps, none, m.nwd0,
-                           m.nwd1, m.yd, kAnyD, tr, 27u))
+    if (mk_resid<EP, true>(g_mk.x_o, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps, none, tr, 27u))
         return false;
     MK_MARK(17);
     float* gu = m.gu;
@@ -1061,7 +1044,7 @@ __device__ __forceinline__ bool mk_fold(uint32_t tagb) {
     MK_UNIFORM(tagb);
     int bad = 0;
     if (mk_resid<EP, false>(g_mk.x_f, tagb + 5u * (L - 1u) + 5u, g_mk_layers[L - 1u].post_ffw, g_mk.out_norm, m.h, m.xa,
-                            w == 0 ? g_mk.hidden : nullptr, d, g_mk.eps, bad, m.nwa0, m.nwa1, m.ya, kAnyFold))
+                            w == 0 ? g_mk.hidden : nullptr, d, g_mk.eps, bad))
         return false;
     if (bad && w == 0 && tid == 0) mk_flag_min(g3_code_nonfinite(L - 1u));
     return true;
@@ -1256,8 +1239,7 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
     bool ok = true;
 #define MK_TRACE(k)                                                                                    \
     do {                                                                                               \
-        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u)                                              \
-            gp(g_mk.trace)[w * g_mk.trace_slots + (k)] = __builtin_amdgcn_s_memrealtime();                       \
+        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u) mk_stamp((k), __builtin_amdgcn_s_memrealtime()); \
     } while (0)
 
     for (uint32_t si = 0; si < nsteps && ok; ++si, ++s) {
@@ -1287,9 +1269,13 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             token = gp(g_mk.tokens)[s];
         }
         prev_lm_tag = 0u;
+        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u) {   // phases a workgroup skips keep older values
+            uint64_t* img = reinterpret_cast<uint64_t*>(g_mk_lds + g_mk.lds.tr);
+            for (uint32_t k = 0; k < g_mk.trace_slots; ++k) img[k] = gp(g_mk.trace)[w * g_mk.trace_slots + k];
+        }
         MK_TRACE(0u);
         if (g_mk.trace_slots != 0u && si == 0u && tid == 0u)   // shader-clock ticks: clock = d(memtime) / d(realtime)
-            gp(g_mk.trace)[w * g_mk.trace_slots + g_mk.trace_slots - 2u] = __builtin_amdgcn_s_memtime();
+            mk_stamp(g_mk.trace_slots - 2u, __builtin_amdgcn_s_memtime());
         mk_embed(token);
 
         for (uint32_t l = 0; l < L && ok; ++l) {
@@ -1318,8 +1304,12 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             MK_TRACE(5u * L + 1u);
         }
         MK_TRACE(5u * L + 2u);
-        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u)
-            gp(g_mk.trace)[w * g_mk.trace_slots + g_mk.trace_slots - 1u] = __builtin_amdgcn_s_memtime();
+        if (g_mk.trace_slots != 0u && si == 0u && tid == 0u) {
+            mk_stamp(g_mk.trace_slots - 1u, __builtin_amdgcn_s_memtime());
+            // the traced step is over: its stamps go to the trace buffer
+            const uint64_t* img = reinterpret_cast<const uint64_t*>(g_mk_lds + g_mk.lds.tr);
+            for (uint32_t k = 0; k < g_mk.trace_slots; ++k) gp(g_mk.trace)[w * g_mk.trace_slots + k] = img[k];
+        }
     }
 #undef MK_TRACE
 
@@ -1502,12 +1492,7 @@ int mk_setup(vrt_g3* g) {
     P.lds.xs = take(kmax * 4u);
     P.lds.xa = take(d * 4u);
     P.lds.xd = take(d * 4u);
-    P.lds.ya = take(d * 4u);
-    P.lds.yd = take(d * 4u);
-    P.lds.nwa0 = take((d + 255u) / 256u * 1024u);   // whole 1 KB rows of the staging loads
-    P.lds.nwa1 = take((d + 255u) / 256u * 1024u);
-    P.lds.nwd0 = take((d + 255u) / 256u * 1024u);
-    P.lds.nwd1 = take((d + 255u) / 256u * 1024u);
+    P.lds.red = take(2u * kMkWaves * (8u + 4u));   // residual norms: wave totals and flags, two rounds
     P.lds.any = take(kAnySets * kMkWaves * 4u);
     P.lds.la = take(d);
     P.lds.lb = take(d);
@@ -1517,6 +1502,7 @@ int mk_setup(vrt_g3* g) {
     P.lds.mw = take((8u * kMaxChunks + 16u) * 4u);
     P.lds.gu = take(2u * ((F + nprod - 1u) / nprod + 1u) * 4u);
     P.lds.u = take(std::max(std::max(kMkWaves * qw, kMaxChunks * (qw + kLine * H)) * 4u, kLmRing * kLmTileBytes));
+    P.lds.tr = take((5u * c.block_count + 3u + kMarks) * 8u);   // trace stamps of the traced step
     P.lds.total = off;
     mk->lds_bytes = off;
     if (off > kMkLdsBytes) { mk_destroy(g); return VRT_OK; }
