@@ -74,6 +74,17 @@ struct LaunchDesc {
 
 struct MkState;   // persistent decode kernel: exchange buffers and launch shape (vrt_decode.hip)
 
+// A block's weight matrices expanded once for the prefill GEMMs: the quants as f16 [N][K] and
+// the block scales as fp32 [N][K / 32]. qkv: the q, k, v rows concatenated; gu: the gate and up
+// rows interleaved in groups of 64 (32 gate rows, then the same 32 up rows).
+struct PfMatrix {
+    const void* h = nullptr;
+    const float* s = nullptr;
+};
+struct PfLayerW {
+    PfMatrix qkv, o, gu, down;
+};
+
 // Batched prefill workspace (vrt_prefill.hip); max_t == 0: prefill unavailable for the shape.
 struct PfState {
     uint32_t max_t = 0;     // prompt positions per call
@@ -86,6 +97,7 @@ struct PfState {
     void* phi = nullptr;    // [H][max_t][Tp] attention probabilities, f16 high part
     void* plo = nullptr;    //   ... and low part
     float* vt = nullptr;    // [hd][Tp] V transposed
+    std::vector<PfLayerW> lw;   // expanded weights per block (empty: the GEMMs read the Q8_0 arena)
 };
 
 }  // namespace vrt

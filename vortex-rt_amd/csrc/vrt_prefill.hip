@@ -30,6 +30,7 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kPfThreads = 256;
 constexpr uint32_t kPfMaxSplits = 4;   // K splits of the O and down projections (pf_splits)
+constexpr uint64_t kPfExpandBudget = 16ull << 30;   // device bytes for the prefill's expanded weights
 constexpr uint32_t kPfTile = 64;     // attention score rows are padded to a multiple of this
 
 // ---- row kernels ---------------------------------------------------------------------------
@@ -134,6 +135,16 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
     }
 }
 
+// out[i] = sum over s < nsplit, in order, of the split partials x[s * n + i] of one row.
+__global__ void __launch_bounds__(kPfThreads) k_pf_sum(const float* x, uint32_t nsplit, uint32_t n, float* out) {
+#pragma clang fp contract(off)
+    for (uint32_t i = threadIdx.x; i < n; i += kPfThreads) {
+        float v = 0.0f;
+        for (uint32_t q = 0; q < nsplit; ++q) v += x[static_cast<uint64_t>(q) * n + i];
+        out[i] = v;
+    }
+}
+
 // gelu_tanh(gate) * up (shaders/gelu_mul.comp:23-31), every operation rounded to fp32.
 __device__ __forceinline__ float pf_gelu_mul(float x, float up) {
 #pragma clang fp contract(off)
@@ -165,6 +176,8 @@ struct PfGemm {
     uint32_t M, N, K;
     uint32_t window;         // causal modes: keys older than window positions are skipped (0: none)
     uint32_t glu;            // Q8_0 GEMM: w[0] = gate, w[1] = up (N = 2F), output gelu_tanh(gate) * up
+    const _Float16* wh;      // expanded weights: the quants of N rows as f16 [N][K] (nullptr: Q8_0 w)
+    const float* ws;         //   and their block scales [N][K / 32]
 };
 
 // One 32 x 32 tile of C per workgroup (v_mfma_f32_32x32x16_f16); the four waves split the
@@ -376,6 +389,54 @@ constexpr uint32_t kQgPitch = kQgBK * 2u + 16u;   // LDS row pitch in bytes (f16
 constexpr uint32_t kQgAhead = 4;   // K steps whose loads are in flight ahead of the one computed
 constexpr uint32_t kQgChunk = 12;  // K steps per straight-line chunk of the main loop
 
+// Epilogue of the Q8_0 GEMMs: with G.glu the wave holding a 64-column group's up columns hands
+// them to the wave holding its gate columns through `xch` (LDS of at least NWN / 2 x 16 x 64
+// floats per 32-row band, free once the K loop is done), which writes gelu_tanh(gate) * up as
+// f16 hi/lo; otherwise the fp32 tile goes to split z's slice of C. Waves with `active` false
+// hold no tile but still pass the barriers.
+template <int WN, int NWN>
+__device__ __forceinline__ void pf_gemm_epilogue(const PfGemm& G, const float16v (&acc)[WN], uint32_t z, uint32_t m0,
+                                                 uint32_t n0, uint32_t wm, uint32_t wn, uint32_t kh, uint32_t l32,
+                                                 uint32_t lane, float* xch, bool active = true) {
+    if (G.glu) {
+        // the wave holding a group's up columns hands them to the wave holding its gate columns
+        // (gelu_tanh(gate) * up, shaders/gelu_mul.comp:23-31)
+        static_assert(WN == 1, "one 32-column MFMA tile per wave");
+        __syncthreads();   // every wave is done reading the LDS stages
+        const uint32_t pair = wm * (NWN / 2u) + (wn >> 1);
+        if (active && (wn & 1u)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xch[(pair * 16u + r) * 64u + lane] = acc[0][r];
+        }
+        __syncthreads();
+        if (!active || (wn & 1u)) return;
+        const uint32_t F = G.N / 2u;
+        const uint32_t col = n0 / 2u + 32u * (wn >> 1) + l32;
+        if (col >= F) return;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = m0 + 32u * wm + 8u * (r / 4) + 4u * kh + (r % 4);
+            if (row < G.M) {
+                const uint64_t o = static_cast<uint64_t>(row) * G.ldc + col;
+                pf_split(pf_gelu_mul(acc[0][r], xch[(pair * 16u + r) * 64u + lane]), G.chi + o, G.clo + o);
+            }
+        }
+        return;
+    }
+    if (!active) return;
+    float* c = G.c + static_cast<uint64_t>(z) * G.c_bs;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        const uint32_t col = n0 + 32u * (WN * wn + j) + l32;
+        if (col >= G.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = m0 + 32u * wm + 8u * (r / 4) + 4u * kh + (r % 4);
+            if (row < G.M) c[static_cast<uint64_t>(row) * G.ldc + col] = acc[j][r];
+        }
+    }
+}
+
 template <int WN, int NWN>
 __global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
     constexpr uint32_t NT = 128u * NWN;          // threads: 2 x NWN waves
@@ -542,43 +603,7 @@ __global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
             if (j < nsteps) compute(j & 1u);
         }
     }
-    if (G.glu) {
-        // the wave holding a group's up columns hands them to the wave holding its gate columns
-        // (gelu_tanh(gate) * up, shaders/gelu_mul.comp:23-31)
-        static_assert(WN == 1, "one 32-column MFMA tile per wave");
-        __syncthreads();   // every wave is done reading the LDS stages
-        float* xch = reinterpret_cast<float*>(&s_a[0][0][0]);
-        const uint32_t pair = wm * (NWN / 2u) + (wn >> 1);
-        if (wn & 1u) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) xch[(pair * 16u + r) * 64u + lane] = acc[0][r];
-        }
-        __syncthreads();
-        if (wn & 1u) return;
-        const uint32_t F = G.N / 2u;
-        const uint32_t col = n0 / 2u + 32u * (wn >> 1) + l32;
-        if (col >= F) return;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t row = m0 + 32u * wm + 8u * (r / 4) + 4u * kh + (r % 4);
-            if (row < G.M) {
-                const uint64_t o = static_cast<uint64_t>(row) * G.ldc + col;
-                pf_split(pf_gelu_mul(acc[0][r], xch[(pair * 16u + r) * 64u + lane]), G.chi + o, G.clo + o);
-            }
-        }
-        return;
-    }
-    float* c = G.c + static_cast<uint64_t>(z) * G.c_bs;
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-        const uint32_t col = n0 + 32u * (WN * wn + j) + l32;
-        if (col >= G.N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t row = m0 + 32u * wm + 8u * (r / 4) + 4u * kh + (r % 4);
-            if (row < G.M) c[static_cast<uint64_t>(row) * G.ldc + col] = acc[j][r];
-        }
-    }
+    pf_gemm_epilogue<WN, NWN>(G, acc, z, m0, n0, wm, wn, kh, l32, lane, reinterpret_cast<float*>(&s_a[0][0][0]));
 }
 
 // Masked softmax of score row (head z, query t): keys j of [max(0, t + 1 - window), t]
@@ -687,6 +712,185 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
     }
 }
 
+// ---- expanded weights ------------------------------------------------------------------------
+
+// One-time expansion of a Q8_0 matrix for the prefill GEMMs: row n of the expanded matrix gets
+// the quants of source row src(n) as f16 (exact: |q| <= 127) and its block scales as fp32. With
+// `glu`, the rows are the gate/up matrices interleaved in groups of 64 (32 gate rows, then the
+// same 32 up rows: the column order of the gate/up GEMM's epilogue); otherwise up to three
+// matrices are concatenated. One thread per (row, block).
+__global__ void __launch_bounds__(kPfThreads) k_pf_expand(const uint8_t* w0, const uint8_t* w1, const uint8_t* w2,
+                                                          uint32_t rows0, uint32_t rows1, uint32_t N, uint32_t nkb,
+                                                          uint32_t glu, _Float16* wh, float* ws) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * kPfThreads + threadIdx.x;
+    if (i >= static_cast<uint64_t>(N) * nkb) return;
+    const uint32_t n = static_cast<uint32_t>(i / nkb), b = static_cast<uint32_t>(i % nkb);
+    const uint8_t* src;
+    if (glu) {
+        const uint32_t grp = n >> 6, wi = n & 63u;
+        src = (wi < 32u ? w0 : w1) + static_cast<uint64_t>(32u * grp + (wi & 31u)) * nkb * 34u;
+    } else if (n < rows0) {
+        src = w0 + static_cast<uint64_t>(n) * nkb * 34u;
+    } else if (n < rows0 + rows1) {
+        src = w1 + static_cast<uint64_t>(n - rows0) * nkb * 34u;
+    } else {
+        src = w2 + static_cast<uint64_t>(n - rows0 - rows1) * nkb * 34u;
+    }
+    const uint8_t* blk = src + 34u * b;
+    ws[i] = half_bits_to_float(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
+    _Float16* dst = wh + static_cast<uint64_t>(n) * nkb * 32u + 32u * b;
+#pragma unroll
+    for (uint32_t k = 0; k < 32u; ++k) dst[k] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(blk[2 + k])));
+}
+
+// The Q8_0 GEMM of k_pf_gemm_q8 on expanded weights (G.wh, G.ws): a K step stages the f16 rows
+// of the tile's W block with plain 16-byte copies (no int8 conversion on the K loop's critical
+// path) and the two block scales per row. Same tiles, splits, LDS layout, K-loop ring and
+// epilogues as k_pf_gemm_q8, with twice the waves: wave group kw (of 2 NWN waves) computes the
+// step's Q8_0 block kw for every tile, so a SIMD runs two waves whose MFMA chains and
+// scale-and-add work overlap; the kw = 1 partial tiles are added to the kw = 0 ones through
+// LDS before the epilogue (sum of the even blocks, then of the odd ones).
+template <int WN, int NWN>
+__global__ void __launch_bounds__(256 * NWN) k_pf_gemm_h(PfGemm G) {
+    constexpr uint32_t NT = 256u * NWN;
+    constexpr uint32_t BN = 32u * WN * NWN;
+    constexpr uint32_t AU = 2u * kQgBM * 8u / NT;   // A 16-byte units per thread (hi units, then lo)
+    constexpr uint32_t WU = BN * 8u / NT;           // W 16-byte units per thread (8 per row)
+    static_assert(AU >= 1u && 2u * kQgBM * 8u % NT == 0u, "whole A units per thread");
+    static_assert(WU >= 1u && BN * 8u % NT == 0u, "whole W units per thread");
+    static_assert(BN <= NT, "one scale pair per thread");
+    __shared__ __align__(16) unsigned char s_a[2][2][kQgBM * kQgPitch];
+    __shared__ __align__(16) unsigned char s_w[2][BN * kQgPitch];
+    __shared__ float s_sc[2][BN][2];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t kh = lane >> 5, l32 = lane & 31u;
+    const uint32_t m0 = blockIdx.y * kQgBM, n0 = blockIdx.x * BN;
+    const uint32_t nkb = G.K >> 5;
+    const uint32_t S = gridDim.z, z = blockIdx.z;
+    const uint32_t kb_lo = nkb * z / S, kb_hi = nkb * (z + 1u) / S;
+    const uint32_t nsteps = (kb_hi - kb_lo + 1u) / 2u;
+    typedef const __attribute__((address_space(1))) v4u* gv4;
+    struct Stage {
+        v4u a[AU];   // unit u = AU tid + j: array u / (8 kQgBM), row (u % (8 kQgBM)) / 8, column u % 8
+        v4u w[WU];
+        float2 sc;
+    };
+    // Every load is issued at a clamped, in-bounds address (dead data is zeroed when stored).
+    auto load = [&](uint32_t step, Stage& R) {
+        const uint32_t kb = kb_lo + 2u * step;
+#pragma unroll
+        for (uint32_t j = 0; j < AU; ++j) {
+            const uint32_t u = AU * tid + j, ui = u % (8u * kQgBM), r = ui >> 3, c = ui & 7u;
+            const uint32_t k = 32u * kb + 8u * c;
+            const uint32_t rr = min(m0 + r, G.M - 1u), kk = min(k, 32u * kb_hi - 8u);
+            const uint64_t o = (static_cast<uint64_t>(rr) * G.lda + kk) * 2u;
+            R.a[j] = *reinterpret_cast<gv4>(reinterpret_cast<uintptr_t>(u < 8u * kQgBM ? G.ahi : G.alo) + o);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < WU; ++j) {
+            const uint32_t u = WU * tid + j, r = u >> 3, c = u & 7u;
+            const uint32_t rr = min(n0 + r, G.N - 1u), kk = min(32u * kb + 8u * c, 32u * kb_hi - 8u);
+            R.w[j] = *reinterpret_cast<gv4>(reinterpret_cast<uintptr_t>(G.wh) + (static_cast<uint64_t>(rr) * G.K + kk) * 2u);
+        }
+        {   // the step's two block scales of row tid (clamped to the split's last block)
+            typedef const __attribute__((address_space(1))) float* gf;
+            const uint32_t rr = min(n0 + (tid < BN ? tid : 0u), G.N - 1u), bb = min(kb, kb_hi - 1u);
+            const gf row = reinterpret_cast<gf>(reinterpret_cast<uintptr_t>(G.ws + static_cast<uint64_t>(rr) * nkb));
+            R.sc = make_float2(row[bb], row[min(bb + 1u, kb_hi - 1u)]);
+        }
+    };
+    auto store = [&](const Stage& R, uint32_t st, uint32_t step) {
+        const uint32_t kb = kb_lo + 2u * step;
+#pragma unroll
+        for (uint32_t j = 0; j < AU; ++j) {
+            const uint32_t u = AU * tid + j, ui = u % (8u * kQgBM), r = ui >> 3, c = ui & 7u;
+            const bool live = m0 + r < G.M && 32u * kb + 8u * c < 32u * kb_hi;
+            *reinterpret_cast<v4u*>(&s_a[st][u / (8u * kQgBM)][r * kQgPitch + c * 16u]) =
+                live ? R.a[j] : v4u{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < WU; ++j) {
+            const uint32_t u = WU * tid + j, r = u >> 3, c = u & 7u;
+            const bool live = n0 + r < G.N && 32u * kb + 8u * c < 32u * kb_hi;
+            *reinterpret_cast<v4u*>(&s_w[st][r * kQgPitch + c * 16u]) = live ? R.w[j] : v4u{0u, 0u, 0u, 0u};
+        }
+        if (tid < BN) {
+            const bool rl = n0 + tid < G.N;
+            s_sc[st][tid][0] = rl && kb < kb_hi ? R.sc.x : 0.0f;
+            s_sc[st][tid][1] = rl && kb + 1u < kb_hi ? R.sc.y : 0.0f;
+        }
+    };
+    const uint32_t kw = wave / (2u * NWN), wv = wave % (2u * NWN);   // block of the step, tile
+    const uint32_t wm = wv / NWN, wn = wv % NWN;
+    float16v acc[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[j] = float16v{};
+    auto compute = [&](uint32_t st) {
+        const unsigned char* pa_hi = &s_a[st][0][(32u * wm + l32) * kQgPitch + 16u * kh];
+        const unsigned char* pa_lo = &s_a[st][1][(32u * wm + l32) * kQgPitch + 16u * kh];
+        {
+            const uint32_t b = kw;
+            half8 ah[2], al[2];
+#pragma unroll
+            for (uint32_t ks = 0; ks < 2; ++ks) {
+                ah[ks] = *reinterpret_cast<const half8*>(pa_hi + 64u * b + 32u * ks);
+                al[ks] = *reinterpret_cast<const half8*>(pa_lo + 64u * b + 32u * ks);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const uint32_t nl = 32u * (WN * wn + j) + l32;
+                const unsigned char* pw = &s_w[st][nl * kQgPitch + 64u * b + 16u * kh];
+                const half8 w0 = *reinterpret_cast<const half8*>(pw), w1 = *reinterpret_cast<const half8*>(pw + 32u);
+                float16v p = {};
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], w0, p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0], w0, p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1], w1, p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1], w1, p, 0, 0, 0);
+                const float sc = s_sc[st][nl][b];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[j][r] += sc * p[r];
+            }
+        }
+    };
+    static_assert(kQgAhead <= kQgChunk, "ring inside a chunk");
+    for (uint32_t i = 0; i < nsteps; i += kQgChunk) {
+        Stage R[kQgAhead];
+        auto clamp = [&](uint32_t j) { return min(i + j, nsteps - 1u); };
+#pragma unroll
+        for (uint32_t u = 0; u < kQgAhead; ++u) load(clamp(u), R[u]);
+#pragma unroll
+        for (uint32_t u = 0; u < kQgChunk; ++u) {
+            const uint32_t j = i + u;
+            if (j < nsteps) {
+                store(R[u % kQgAhead], j & 1u, j);
+                __syncthreads();
+            }
+            if (u + kQgAhead < kQgChunk) load(clamp(u + kQgAhead), R[u % kQgAhead]);
+            if (j < nsteps) compute(j & 1u);
+        }
+    }
+    {   // odd-block partials into the even-block waves (s_w: 2 NWN WN 16 x 64 floats fit)
+        static_assert(2u * NWN * WN * 16u * 64u * 4u <= sizeof(s_w), "reduction area");
+        __syncthreads();   // every wave is done reading the LDS stages
+        float* red = reinterpret_cast<float*>(&s_w[0][0]);
+        if (kw == 1u) {
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[((wv * WN + j) * 16u + r) * 64u + lane] = acc[j][r];
+        }
+        __syncthreads();
+        if (kw == 0u) {
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[j][r] += red[((wv * WN + j) * 16u + r) * 64u + lane];
+        }
+    }
+    pf_gemm_epilogue<WN, NWN>(G, acc, z, m0, n0, wm, wn, kh, l32, lane, reinterpret_cast<float*>(&s_a[0][0][0]),
+                              kw == 0u);
+}
+
 // ---- host side --------------------------------------------------------------------------
 
 template <int MODE>
@@ -709,11 +913,35 @@ static int pf_launch_q8(const PfGemm& G, uint32_t splits, hipStream_t s) {
     return VRT_OK;
 }
 
-// C[M][N] = A[M][K] (f16 hi/lo) x W^T, W = Q8_0 matrices concatenated along N. With splits > 1
-// the K blocks are split and C holds the partial products C + z * M * N, z < splits.
+template <int WN, int NWN>
+static int pf_launch_h(const PfGemm& G, uint32_t splits, hipStream_t s) {
+    constexpr uint32_t BN = 32u * WN * NWN;
+    const dim3 grid((G.N + BN - 1u) / BN, (G.M + kQgBM - 1u) / kQgBM, splits);
+    PfGemm arg = G;
+    void* args[] = {&arg};
+    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_gemm_h<WN, NWN>), grid, dim3(256u * NWN), args,
+                                  0, s));
+    return VRT_OK;
+}
+
+// The Q8_0 GEMM's launch: on the expanded weights when `ex` holds them, else on the arena.
+static int pf_launch_w(PfGemm& G, const PfMatrix* ex, uint32_t splits, hipStream_t s) {
+    const uint32_t mt = (G.M + kQgBM - 1u) / kQgBM;
+    const bool wide = G.N % 128u == 0u && (G.N / 128u) * mt >= 128u;
+    if (ex && ex->h) {
+        G.wh = static_cast<const _Float16*>(ex->h);
+        G.ws = ex->s;
+        return wide ? pf_launch_h<1, 4>(G, splits, s) : pf_launch_h<1, 2>(G, splits, s);
+    }
+    return wide ? pf_launch_q8<1, 4>(G, splits, s) : pf_launch_q8<1, 2>(G, splits, s);
+}
+
+// C[M][N] = A[M][K] (f16 hi/lo) x W^T, W = Q8_0 matrices concatenated along N (or their
+// expansion `ex`). With splits > 1 the K blocks are split and C holds the partial products
+// C + z * M * N, z < splits.
 static int pf_gemm(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t M, uint32_t K,
-                   std::initializer_list<std::pair<const uint8_t*, uint32_t>> segs, float* c, uint32_t splits,
-                   hipStream_t s) {
+                   std::initializer_list<std::pair<const uint8_t*, uint32_t>> segs, const PfMatrix* ex, float* c,
+                   uint32_t splits, hipStream_t s) {
     PfGemm G{};
     G.ahi = ahi;
     G.alo = alo;
@@ -731,15 +959,13 @@ static int pf_gemm(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t
     if (K % 32u != 0u || G.N % 32u != 0u) return set_error(VRT_ERR_INVALID, "prefill GEMM shape not supported");
     G.c_bs = static_cast<uint64_t>(M) * G.N;
     splits = std::max(1u, std::min(splits, (K / 32u) / 2u));
-    const uint32_t mt = (M + kQgBM - 1u) / kQgBM;
-    if (G.N % 128u == 0u && (G.N / 128u) * mt >= 128u) return pf_launch_q8<1, 4>(G, splits, s);
-    return pf_launch_q8<1, 2>(G, splits, s);
+    return pf_launch_w(G, ex, splits, s);
 }
 
 // gelu_tanh(A Wg^T) * (A Wu^T) as f16 hi/lo [M][F] (row stride F): the gate/up GEMM with the
 // product in its epilogue (src/gemma3.cpp:1720-1801 up to the down projection), one K split.
 static int pf_gemm_glu(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t M, uint32_t K, const uint8_t* wg,
-                       const uint8_t* wu, uint32_t F, _Float16* ohi, _Float16* olo, hipStream_t s) {
+                       const uint8_t* wu, uint32_t F, const PfMatrix* ex, _Float16* ohi, _Float16* olo, hipStream_t s) {
     PfGemm G{};
     G.ahi = ahi;
     G.alo = alo;
@@ -757,9 +983,7 @@ static int pf_gemm_glu(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint
     G.K = K;
     G.glu = 1u;
     if (K % 32u != 0u || F % 32u != 0u) return set_error(VRT_ERR_INVALID, "prefill GEMM shape not supported");
-    const uint32_t mt = (M + kQgBM - 1u) / kQgBM;
-    if (G.N % 128u == 0u && (G.N / 128u) * mt >= 128u) return pf_launch_q8<1, 4>(G, 1u, s);
-    return pf_launch_q8<1, 2>(G, 1u, s);
+    return pf_launch_w(G, ex, 1u, s);
 }
 
 // K splits of the 640-row projections (O and down): enough workgroups to cover the CUs.
@@ -802,6 +1026,42 @@ int pf_setup(vrt_g3* g, uint32_t max_t) {
     p.plo = q;
     if (int rc = take(static_cast<size_t>(hd) * tp * 4u, &q)) return rc;
     p.vt = static_cast<float*>(q);
+    // Expanded weights: 2 bytes per quant + 4 per 32 (2.125 bytes per weight, twice the Q8_0
+    // matrices' 1.0625), made once here when they fit kPfExpandBudget.
+    const uint64_t per_layer = static_cast<uint64_t>(nqkv) * d + static_cast<uint64_t>(d) * qw +
+                               2ull * F * d + static_cast<uint64_t>(d) * F;
+    const uint64_t total = per_layer * g->layers.size() * 2u + per_layer * g->layers.size() / 8u;
+    p.lw.clear();
+    if (total <= kPfExpandBudget) {
+        p.lw.resize(g->layers.size());
+        const hipStream_t s = g->ctx->stream;
+        auto expand = [&](const uint8_t* w0, const uint8_t* w1, const uint8_t* w2, uint32_t r0, uint32_t r1, uint32_t N,
+                          uint32_t K, uint32_t glu, PfMatrix* m) -> int {
+            void* hq;
+            void* sq;
+            if (int rc = take(static_cast<size_t>(N) * K * 2u, &hq)) return rc;
+            if (int rc = take(static_cast<size_t>(N) * (K / 32u) * 4u, &sq)) return rc;
+            uint32_t nkb = K / 32u;
+            _Float16* wh = static_cast<_Float16*>(hq);
+            float* ws = static_cast<float*>(sq);
+            void* args[] = {&w0, &w1, &w2, &r0, &r1, &N, &nkb, &glu, &wh, &ws};
+            const uint64_t n = static_cast<uint64_t>(N) * nkb;
+            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_expand),
+                                          dim3(static_cast<uint32_t>((n + kPfThreads - 1u) / kPfThreads)),
+                                          dim3(kPfThreads), args, 0, s));
+            m->h = hq;
+            m->s = ws;
+            return VRT_OK;
+        };
+        for (size_t l = 0; l < g->layers.size(); ++l) {
+            const LayerParams& Ly = g->layers[l];
+            PfLayerW& w = p.lw[l];
+            if (int rc = expand(Ly.wq, Ly.wk, Ly.wv, qw, hd, nqkv, d, 0u, &w.qkv)) return rc;
+            if (int rc = expand(Ly.wo, Ly.wo, Ly.wo, d, 0u, d, qw, 0u, &w.o)) return rc;
+            if (int rc = expand(Ly.wg, Ly.wu, Ly.wu, F, F, 2u * F, d, 1u, &w.gu)) return rc;
+            if (int rc = expand(Ly.wd, Ly.wd, Ly.wd, d, 0u, d, F, 0u, &w.down)) return rc;
+        }
+    }
     p.max_t = max_t;
     return VRT_OK;
 }
@@ -891,6 +1151,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
         void* args[] = {&te, &tok, &d, &es, &h};
         if (int rc = launch(reinterpret_cast<const void*>(&k_pf_embed), dim3(T), args)) return rc;
     }
+    const PfLayerW* lw = p.lw.empty() ? nullptr : p.lw.data();
     const uint32_t s_o = pf_splits(T, d);        // split partials of the O and down projections
     uint64_t xs = static_cast<uint64_t>(T) * d;  // one partial [T][d]
     uint32_t s_down = 1;                         // splits of the previous block's down projection
@@ -904,7 +1165,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
             void* args[] = {&h, &f, &s_down, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
             if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }
-        if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, big, 1, s)) return rc;
+        if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, lw ? &lw[l].qkv : nullptr, big, 1, s)) return rc;
         {
             const float* qn = Ly.q_norm;
             const float* kn = Ly.k_norm;
@@ -922,7 +1183,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
         // q (hi/lo in ahi/alo) is consumed by S = Q K^T before O = P V overwrites ahi/alo
         if (int rc = pf_attention(g, Ly, T, big, ahi, alo, ahi, alo, s)) return rc;
         uint32_t so = s_o;
-        if (int rc = pf_gemm(g, ahi, alo, T, qw, {{Ly.wo, d}}, x, so, s)) return rc;
+        if (int rc = pf_gemm(g, ahi, alo, T, qw, {{Ly.wo, d}}, lw ? &lw[l].o : nullptr, x, so, s)) return rc;
         so = std::max(1u, std::min(so, (qw / 32u) / 2u));
         {   // attention output into the residual, then the FFN norm
             const float* f = x;
@@ -932,16 +1193,25 @@ int pf_run(vrt_g3* g, uint32_t T) {
             void* args[] = {&h, &f, &so, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
             if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
         }
-        // gelu(gate) * up as f16 hi/lo in `big` (the gate/up GEMM still reads ahi/alo)
+        // gelu(gate) * up as f16 hi/lo in `big` (the gate/up GEMM still reads ahi/alo). The last
+        // block's FFN output feeds only the LM head, so there it runs for the last position alone.
+        const bool last = l + 1u == L;
+        const uint32_t fr = last ? 1u : T;
+        const uint64_t a0 = last ? static_cast<uint64_t>(T - 1u) * d : 0u;
         _Float16* ghi = reinterpret_cast<_Float16*>(big);
-        _Float16* glo = ghi + static_cast<uint64_t>(T) * F;
-        if (int rc = pf_gemm_glu(g, ahi, alo, T, d, Ly.wg, Ly.wu, F, ghi, glo, s)) return rc;
-        // the last block's output row feeds the LM head directly: no split partials there
-        s_down = l + 1u < L ? std::max(1u, std::min(s_o, (F / 32u) / 2u)) : 1u;
-        if (int rc = pf_gemm(g, ghi, glo, T, F, {{Ly.wd, d}}, x, s_down, s)) return rc;
+        _Float16* glo = ghi + static_cast<uint64_t>(fr) * F;
+        if (int rc = pf_gemm_glu(g, ahi + a0, alo + a0, fr, d, Ly.wg, Ly.wu, F, lw ? &lw[l].gu : nullptr, ghi, glo, s))
+            return rc;
+        s_down = std::max(1u, std::min(last ? pf_splits(1u, d) : s_o, (F / 32u) / 2u));
+        if (int rc = pf_gemm(g, ghi, glo, fr, F, {{Ly.wd, d}}, lw ? &lw[l].down : nullptr, x, s_down, s)) return rc;
     }
-    // last position: its FFN output and residual feed the decode step's final norm + LM head
-    VRT_HIP_CHECK(hipMemcpyAsync(P.f, x + static_cast<uint64_t>(T - 1u) * d, d * 4u, hipMemcpyDeviceToDevice, s));
+    {   // last position: its FFN output (the split partials summed in order) and its residual
+        // feed the decode step's final norm + LM head
+        float* out = P.f;
+        uint32_t nsplit = s_down;
+        void* args[] = {&x, &nsplit, &d, &out};
+        if (int rc = launch(reinterpret_cast<const void*>(&k_pf_sum), dim3(1), args)) return rc;
+    }
     VRT_HIP_CHECK(hipMemcpyAsync(P.hmid, h + static_cast<uint64_t>(T - 1u) * d, d * 4u, hipMemcpyDeviceToDevice, s));
     return g3_enqueue_lm(g, s);
 }
