@@ -93,10 +93,15 @@ struct PfState {
     void* ahi = nullptr;    // [max_t][max(d, H*hd, F)] GEMM input, f16 high part
     void* alo = nullptr;    //   ... and low part
     float* big = nullptr;   // [max_t][max(H*hd + 2*hd, 2F)] q|k|v rows, then gate|up rows
-    float* s = nullptr;     // [H][max_t][Tp] attention scores (Tp: max_t rounded up to 64)
-    void* phi = nullptr;    // [H][max_t][Tp] attention probabilities, f16 high part
-    void* plo = nullptr;    //   ... and low part
-    float* vt = nullptr;    // [hd][Tp] V transposed
+    void* khi = nullptr;    // attention keys (Tp x hd, Tp: max_t rounded up to 64), f16 high part
+    void* klo = nullptr;    //   ... and low part
+    void* vhi = nullptr;    // attention values (Tp x hd), f16 high part
+    void* vlo = nullptr;    //   ... and low part
+    uint32_t qtmax = 0;     // 32-query tiles of max_t
+    uint32_t maxc = 0;      // key chunks per query tile, at most
+    float* opart = nullptr;     // [H][qtmax][maxc][32][hd] attention unit partials
+    float* mpart = nullptr;     // [H][qtmax][maxc][32] their maxima
+    double* lpart = nullptr;    // [H][qtmax][maxc][32] their exp sums
     std::vector<PfLayerW> lw;   // expanded weights per block (empty: the GEMMs read the Q8_0 arena)
 };
 

@@ -41,6 +41,19 @@ __device__ __forceinline__ void pf_split(float x, _Float16* hi, _Float16* lo) {
     *lo = static_cast<_Float16>(x - static_cast<float>(h));
 }
 
+// pf_split of four consecutive values (8-byte aligned destinations).
+__device__ __forceinline__ void pf_split4(f4 x, _Float16* hi, _Float16* lo) {
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    half4 h, l;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        h[k] = static_cast<_Float16>(x[k]);
+        l[k] = static_cast<_Float16>(x[k] - static_cast<float>(h[k]));
+    }
+    *reinterpret_cast<half4*>(hi) = h;
+    *reinterpret_cast<half4*>(lo) = l;
+}
+
 // Workgroup double sum (fixed order: 4 waves, DPP inside each) behind one barrier. red[0..4)
 // belongs to this call: a second sum in the same kernel takes other slots, so no thread can
 // still be reading them when they are written.
@@ -154,234 +167,38 @@ __device__ __forceinline__ float pf_gelu_mul(float x, float up) {
 }
 
 
-// ---- GEMM on MFMA: Q8_0 weights or fp32 rows as B ---------------------------------------------
+// ---- GEMM on MFMA: Q8_0 weights ---------------------------------------------------------------
 
 struct PfGemm {
     const _Float16* ahi;     // A [M][K] (row stride lda), f16 high and low parts
     const _Float16* alo;
     uint32_t lda;
-    uint64_t a_bs;           // A offset (elements) per batch index blockIdx.z
-    const uint8_t* w[3];     // B as Q8_0 matrices concatenated along N (rows[i] rows each), or
+    const uint8_t* w[3];     // W as Q8_0 matrices concatenated along N (rows[i] rows each)
     uint32_t rows[3];
     uint32_t nseg;
     const uint8_t* w_end;    //   one past the arena
-    const float* b;          // B as fp32 rows: B[n][k] = b[n * ldb + k] (+ b_bs per batch)
-    uint32_t ldb;
-    uint64_t b_bs;
-    float* c;                // C [M][N] fp32 (row stride ldc), or
+    float* c;                // C [M][N] fp32 (row stride ldc; split z at c + z * c_bs), or
     _Float16* chi;           //   C as f16 high and low parts
     _Float16* clo;
     uint32_t ldc;
     uint64_t c_bs;
     uint32_t M, N, K;
-    uint32_t window;         // causal modes: keys older than window positions are skipped (0: none)
     uint32_t glu;            // Q8_0 GEMM: w[0] = gate, w[1] = up (N = 2F), output gelu_tanh(gate) * up
     const _Float16* wh;      // expanded weights: the quants of N rows as f16 [N][K] (nullptr: Q8_0 w)
     const float* ws;         //   and their block scales [N][K / 32]
 };
 
-// One 32 x 32 tile of C per workgroup (v_mfma_f32_32x32x16_f16); the four waves split the
-// K blocks (wave w takes blocks w, w + 4, ...) and their partial tiles are summed through LDS
-// in wave order (deterministic). Lane l of a wave: A operand row m = l % 32, k = 8 * (l / 32)
-// + 0..7 of each 16-wide k step; B operand column n = l % 32, same k; accumulator element r at
-// row 8 * (r / 4) + 4 * (l / 32) + r % 4, column l % 32. Q8 B: per 32-wide block, two f16 MFMA
-// chains (A hi, A lo) against the exact quants, scaled by the column's block scale (the lane's
-// own) in fp32. fp32 B: split into f16 hi + lo in registers, three products (hi hi, lo hi,
-// hi lo) per k step. Each wave's next block loads while its current block's MFMAs run.
-constexpr int kGemmB32 = 1;       // B is fp32 rows (otherwise Q8_0)
-constexpr int kGemmCausalS = 2;   // S = Q K^T: skip key tiles no query of the row tile sees
-constexpr int kGemmCausalO = 4;   // O = P V: the K (key) range ends after the row tile's last query
-constexpr int kGemmOut16 = 8;     // C as f16 hi/lo
-constexpr uint32_t kPfGT = 32;    // GEMM tile (rows and columns)
-constexpr uint32_t kPfDepth = 3;  // K blocks in flight per wave
-template <int MODE>
-__global__ void __launch_bounds__(kPfThreads) k_pf_gemm(PfGemm G) {
-    constexpr bool BF32 = (MODE & kGemmB32) != 0, OUT16 = (MODE & kGemmOut16) != 0;
-    __shared__ float red[3][16][64];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t kh = lane >> 5, l32 = lane & 31u;
-    const uint32_t m0 = blockIdx.y * kPfGT, n0 = blockIdx.x * kPfGT;
-    uint32_t k_lo = 0, k_hi = G.K;
-    if constexpr ((MODE & (kGemmCausalS | kGemmCausalO)) != 0) {
-        const uint32_t q_last = min(G.M, m0 + kPfGT) - 1u;
-        const uint32_t k_old = (G.window != 0u && m0 + 1u > G.window) ? m0 + 1u - G.window : 0u;
-        if constexpr ((MODE & kGemmCausalS) != 0) {
-            if (n0 > q_last || n0 + kPfGT <= k_old) return;   // uniform over the workgroup
-        } else {
-            k_lo = (k_old / 32u) * 32u;
-            k_hi = min(G.K, ((q_last + 32u) / 32u) * 32u);
-        }
-    }
-    const uint32_t m = m0 + l32, n = n0 + l32;
-    const bool mlive = m < G.M, nlive = n < G.N;
-    const uint64_t zb = blockIdx.z;
-    typedef const __attribute__((address_space(1))) half8* gh8;
-    typedef const __attribute__((address_space(1))) f4* gf4;
-    const uintptr_t ahi_base = reinterpret_cast<uintptr_t>(G.ahi + zb * G.a_bs);
-    const uintptr_t alo_base = reinterpret_cast<uintptr_t>(G.alo + zb * G.a_bs);
-    const uint64_t arow = static_cast<uint64_t>(mlive ? m : 0u) * G.lda + 8u * kh;
-    auto load_a = [&](uint32_t k0, half8 (&hi)[2], half8 (&lo)[2]) {
-#pragma unroll
-        for (uint32_t ks = 0; ks < 2; ++ks) {
-            const uint64_t o = (arow + k0 + 16u * ks) * 2u;
-            hi[ks] = *reinterpret_cast<gh8>(ahi_base + o);
-            lo[ks] = *reinterpret_cast<gh8>(alo_base + o);
-        }
-    };
-    float16v acc = {};
-    const uint32_t b_lo = k_lo / 32u, b_hi = k_hi / 32u;   // this wave: blocks b_lo + wave + 4i
-    if constexpr (!BF32) {
-        const uint64_t row_bytes = static_cast<uint64_t>(G.K >> 5) * 34u;
-        const uint8_t* wrow = G.w[0];   // the lane's weight row (segments unrolled: no indexed struct)
-        {
-            uint32_t r = nlive ? n : 0u;
-            if (G.nseg > 1u && r >= G.rows[0]) {
-                r -= G.rows[0];
-                wrow = G.w[1];
-                if (G.nseg > 2u && r >= G.rows[1]) {
-                    r -= G.rows[1];
-                    wrow = G.w[2];
-                }
-            }
-            wrow += static_cast<uint64_t>(r) * row_bytes;
-        }
-        // quants 16 ks + 8 kh .. + 7 of a block as f16 (constant register indices, selected by kh)
-        auto to_half8 = [&](const Q8Raw& r, uint32_t ks) {
-            half8 v;
-            const uint32_t j = 4u * ks;
-            const uint32_t a0 = __builtin_amdgcn_alignbyte(r.d[j + 1], r.d[j], r.sh);
-            const uint32_t a1 = __builtin_amdgcn_alignbyte(r.d[j + 2], r.d[j + 1], r.sh);
-            const uint32_t a2 = __builtin_amdgcn_alignbyte(r.d[j + 3], r.d[j + 2], r.sh);
-            const uint32_t a3 = __builtin_amdgcn_alignbyte(r.d[j + 4], r.d[j + 3], r.sh);
-            const uint32_t d0 = kh ? a2 : a0, d1 = kh ? a3 : a1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(d0 >> (8 * i))));
-                v[4 + i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(d1 >> (8 * i))));
-            }
-            return v;
-        };
-        // a ring of kPfDepth blocks in flight per wave (static register sets)
-        half8 ah[kPfDepth][2], al[kPfDepth][2];
-        Q8Raw rw[kPfDepth];
-        const uint32_t b0 = b_lo + wave;
-#pragma unroll
-        for (uint32_t i = 0; i < kPfDepth; ++i) {
-            const uint32_t bb = b0 + 4u * i;
-            if (bb < b_hi) {
-                load_a(32u * bb, ah[i], al[i]);
-                q8_load(wrow + 34u * bb, G.w_end, rw[i]);
-            }
-        }
-        for (uint32_t base = b0; base < b_hi; base += 4u * kPfDepth) {
-#pragma unroll
-            for (uint32_t i = 0; i < kPfDepth; ++i) {
-                const uint32_t bb = base + 4u * i;
-                if (bb < b_hi) {
-                    const half8 w0 = to_half8(rw[i], 0u), w1 = to_half8(rw[i], 1u);
-                    float16v p1 = {}, p2 = {};
-                    p1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], w0, p1, 0, 0, 0);
-                    p2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], w0, p2, 0, 0, 0);
-                    p1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], w1, p1, 0, 0, 0);
-                    p2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], w1, p2, 0, 0, 0);
-                    const float sc = half_bits_to_float(rw[i].sbits);
-                    const uint32_t nb = bb + 4u * kPfDepth;
-                    if (nb < b_hi) {
-                        load_a(32u * nb, ah[i], al[i]);
-                        q8_load(wrow + 34u * nb, G.w_end, rw[i]);
-                    }
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[r] += sc * (p1[r] + p2[r]);
-                }
-            }
-        }
-    } else {
-        const uintptr_t b_base = reinterpret_cast<uintptr_t>(G.b + zb * G.b_bs) +
-                                 (static_cast<uint64_t>(nlive ? n : 0u) * G.ldb + 8u * kh) * 4u;
-        auto load_b = [&](uint32_t k0, f4 (&v)[4]) {   // k step 0: v[0], v[1]; k step 1: v[2], v[3]
-#pragma unroll
-            for (uint32_t ks = 0; ks < 2; ++ks) {
-                v[2 * ks] = *reinterpret_cast<gf4>(b_base + (k0 + 16u * ks) * 4u);
-                v[2 * ks + 1] = *reinterpret_cast<gf4>(b_base + (k0 + 16u * ks + 4u) * 4u);
-            }
-        };
-        half8 ah[kPfDepth][2], al[kPfDepth][2];
-        f4 bv[kPfDepth][4];
-        const uint32_t b0 = b_lo + wave;
-#pragma unroll
-        for (uint32_t i = 0; i < kPfDepth; ++i) {
-            const uint32_t bb = b0 + 4u * i;
-            if (bb < b_hi) {
-                load_a(32u * bb, ah[i], al[i]);
-                load_b(32u * bb, bv[i]);
-            }
-        }
-        for (uint32_t base = b0; base < b_hi; base += 4u * kPfDepth) {
-#pragma unroll
-            for (uint32_t i = 0; i < kPfDepth; ++i) {
-                const uint32_t bb = base + 4u * i;
-                if (bb < b_hi) {
-                    half8 bh[2], bl[2], xh[2], xl[2];
-#pragma unroll
-                    for (uint32_t ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const float x0 = bv[i][2 * ks][j], x1 = bv[i][2 * ks + 1][j];
-                            const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
-                            bh[ks][j] = h0;
-                            bh[ks][4 + j] = h1;
-                            bl[ks][j] = static_cast<_Float16>(x0 - static_cast<float>(h0));
-                            bl[ks][4 + j] = static_cast<_Float16>(x1 - static_cast<float>(h1));
-                        }
-                        xh[ks] = ah[i][ks];
-                        xl[ks] = al[i][ks];
-                    }
-                    const uint32_t nb = bb + 4u * kPfDepth;
-                    if (nb < b_hi) {
-                        load_a(32u * nb, ah[i], al[i]);
-                        load_b(32u * nb, bv[i]);
-                    }
-#pragma unroll
-                    for (uint32_t ks = 0; ks < 2; ++ks) {
-                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh[ks], bh[ks], acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl[ks], bh[ks], acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh[ks], bl[ks], acc, 0, 0, 0);
-                    }
-                }
-            }
-        }
-    }
-    // sum the four waves' partial tiles in wave order
-    if (wave != 0u) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) red[wave - 1u][r][lane] = acc[r];
-    }
-    __syncthreads();
-    if (wave != 0u || !nlive) return;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const uint32_t row = m0 + 8u * (r / 4) + 4u * kh + (r % 4);
-        if (row < G.M) {
-            const uint64_t o = zb * G.c_bs + static_cast<uint64_t>(row) * G.ldc + n;
-            if constexpr (OUT16) pf_split(acc[r], G.chi + o, G.clo + o);
-            else G.c[o] = acc[r];
-        }
-    }
-}
-
-// ---- Q8_0 weight GEMM, LDS-tiled ------------------------------------------------------------
-//
 // C[M][N] = A[M][K] (f16 hi/lo) x W^T with W the Q8_0 rows (segments concatenated along N).
 // Workgroup tile: 64 rows of A x 64 * WN rows of W; wave w computes rows 32 (w / 2) and the
 // WN 32-column MFMA tiles from 32 WN (w % 2). K advances 64 (two Q8_0 blocks) per step through
 // two LDS stages: A as f16 hi and lo [64][64], W as its exact int8 quants in f16 [64 WN][64]
 // plus the fp32 block scales; one barrier per step hands a stage over. Per Q8_0 block and tile the
 // two f16 MFMA chains (A hi, A lo) accumulate the exact products in fp32 and the block's partial
-// is scaled by the column's scale into the fp32 accumulator, as in k_pf_gemm. blockIdx.z splits
-// K: split z covers K blocks [z nkb / S, (z + 1) nkb / S) and writes C + z * c_bs; the consumer
-// adds the S partial tiles in split order.
+// is scaled by the column's scale into the fp32 accumulator. MFMA operands
+// (v_mfma_f32_32x32x16_f16): lane l gives A[m = l % 32][k = 8 (l / 32) + j] and B[k][n = l % 32]
+// for j < 8 of each 16-wide k step; result r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4]
+// [l % 32]. blockIdx.z splits K: split z covers K blocks [z nkb / S, (z + 1) nkb / S) and writes
+// C + z * c_bs; the consumer adds the S partial tiles in split order.
 constexpr uint32_t kQgBM = 64;
 constexpr uint32_t kQgBK = 64;
 constexpr uint32_t kQgPitch = kQgBK * 2u + 16u;   // LDS row pitch in bytes (f16 rows, padded)
@@ -606,36 +423,24 @@ __global__ void __launch_bounds__(128 * NWN) k_pf_gemm_q8(PfGemm G) {
     pf_gemm_epilogue<WN, NWN>(G, acc, z, m0, n0, wm, wn, kh, l32, lane, reinterpret_cast<float*>(&s_a[0][0][0]));
 }
 
-// Masked softmax of score row (head z, query t): keys j of [max(0, t + 1 - window), t]
-// (window 0: all j <= t), p_j = exp(scale * s_j - max) / sum, the sum in double
-// (src/gemma3.cpp:1602-1696); p as f16 hi/lo over the row's first ceil((t + 1) / 64) * 64
-// columns, zero outside the range (the O = P V GEMM reads up to there).
-__global__ void __launch_bounds__(kPfThreads) k_pf_softmax(const float* S, uint32_t T, uint32_t Tp, float scale,
-                                                           uint32_t window, _Float16* phi, _Float16* plo,
-                                                           G3State* st, uint32_t block) {
-#pragma clang fp contract(off)
-    __shared__ double redd[4];
-    __shared__ float redf[4];
-    const uint32_t t = blockIdx.x, z = blockIdx.y;
-    const uint64_t row = (static_cast<uint64_t>(z) * T + t) * Tp;   // rows of Tp columns
-    const uint32_t j0 = (window != 0u && t + 1u > window) ? t + 1u - window : 0u;
-    const uint32_t jend = min(Tp, ((t + kPfTile) / kPfTile) * kPfTile);
-    float mx = -INFINITY;
-    for (uint32_t j = j0 + threadIdx.x; j <= t; j += kPfThreads) mx = fmaxf(mx, S[row + j] * scale);
-    mx = wave_red_max(mx);
-    if ((threadIdx.x & 63u) == 0u) redf[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-    double den = 0.0;
-    for (uint32_t j = j0 + threadIdx.x; j <= t; j += kPfThreads) den += static_cast<double>(expf(S[row + j] * scale - mx));
-    const double den_all = pf_sum(den, redd);
-    if (threadIdx.x == 0u && (!(den_all > 0.0) || !__builtin_isfinite(den_all)))   // :1666-1670
-        atomicMin(&st->nonfinite, g3_code_softmax(block));
-    const float inv_den = static_cast<float>(1.0 / den_all);
-    for (uint32_t j = threadIdx.x; j < jend; j += kPfThreads) {
-        const float p = (j >= j0 && j <= t) ? expf(S[row + j] * scale - mx) * inv_den : 0.0f;
-        pf_split(p, phi + row + j, plo + row + j);
-    }
+// Operand layouts of the attention keys and values (per 32-key tile, so that every MFMA operand
+// load of a wave is one contiguous 1 KB): the key rows of a tile are stored in the order pkey
+// (bits 2 and 3 of the index swapped, an involution), and for S^T = K Q^T the k step s, lane
+// half f and row m of the A operand hold K[32 tile + pkey(m)][16 s + 8 f + j], j < 8; for
+// O^T += V^T E^T the d tile dt, k step sk, lane half f and row m hold V[32 tile + 16 sk + 8 f + j]
+// [32 dt + m]. With the pkey order, S^T's result r of lane half f is key 16 (r / 8) + 8 f +
+// r % 8 of the tile, which is the key of O^T's k slot 8 f + j of k step sk = r / 8, j = r % 8.
+__device__ __forceinline__ uint32_t pf_pkey(uint32_t w) {
+    return (w & ~12u) | ((w & 4u) << 1) | ((w & 8u) >> 1);
+}
+__device__ __forceinline__ uint64_t pf_kswz(uint32_t t, uint32_t d, uint32_t hd) {
+    const uint32_t tile = t >> 5, m = pf_pkey(t & 31u);
+    return ((static_cast<uint64_t>(tile) * (hd / 16u) + (d >> 4)) * 2u + ((d >> 3) & 1u)) * 256u + m * 8u + (d & 7u);
+}
+__device__ __forceinline__ uint64_t pf_vswz(uint32_t t, uint32_t d, uint32_t hd) {
+    const uint32_t tile = t >> 5, w = t & 31u;
+    return ((static_cast<uint64_t>(tile) * (hd / 32u) + (d >> 5)) * 2u + (w >> 4)) * 512u + ((w >> 3) & 1u) * 256u +
+           (d & 31u) * 8u + (w & 7u);
 }
 
 // ---- QK-norm, RoPE, KV cache ------------------------------------------------------------
@@ -643,9 +448,10 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_softmax(const float* S, uint3
 // Row t of qkv = [q (H heads x hd) | k (hd) | v (hd)]: QK-norm per head (src/gemma3.cpp:
 // 1045-1104), NeoX RoPE at position t (:1371-1424), in place (q also as f16 hi/lo rows of
 // qhi/qlo); then k and v go to the KV cache slot t % slots when position t is still in the
-// window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600), and
-// v to column t of vt = V^T [hd][Tp], the B operand of O = P V. One workgroup per column
-// t < Tp: those with t >= T write the zero padding columns (their weights in P are zero).
+// window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600). The
+// attention operands as f16 hi/lo: k and v in the pf_kswz / pf_vswz tile layouts. One
+// workgroup per position t < Tp: those with t >= T write the zero padding keys and values
+// (keys past the prompt are masked, and zero values keep the masked products zero).
 // One wave per head (lane l: dims l + 64 e): the sum of squares is a wave reduction and the
 // RoPE partners come through the wave's own LDS row, so the kernel has no barrier.
 constexpr uint32_t kPfQkMaxWaves = 8;
@@ -653,12 +459,16 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
                                                             const float* q_norm, const float* k_norm,
                                                             const float* cos_t, const float* sin_t, float eps,
                                                             float* kc, float* vc, uint32_t slots, _Float16* qhi,
-                                                            _Float16* qlo, uint32_t Tp, float* vt) {
+                                                            _Float16* qlo, _Float16* khi, _Float16* klo, _Float16* vhi,
+                                                            _Float16* vlo) {
 #pragma clang fp contract(off)
     __shared__ float xs[kPfQkMaxWaves][256];
     const uint32_t t = blockIdx.x;
     if (t >= T) {   // whole workgroup
-        for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) vt[static_cast<uint64_t>(i) * Tp + t] = 0.0f;
+        for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
+            const uint64_t ko = pf_kswz(t, i, hd), vo = pf_vswz(t, i, hd);
+            khi[ko] = klo[ko] = vhi[vo] = vlo[vo] = static_cast<_Float16>(0.0f);
+        }
         return;
     }
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -694,12 +504,13 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
                 const float c = cos_t[static_cast<uint64_t>(t) * half + ei], s = sin_t[static_cast<uint64_t>(t) * half + ei];
                 const float a = xw[ei], b = xw[ei + half];
                 const float y2 = i < half ? a * c - b * s : b * c + a * s;
-                x[i] = y2;
-                if (hh < H) {   // the query as the attention GEMM's A operand, [T][H * hd]
+                if (hh < H) {   // the query, [T][H * hd]
                     const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
                     pf_split(y2, qhi + o, qlo + o);
-                } else if (keep) {
-                    kc[slot + i] = y2;
+                } else {
+                    const uint64_t o = pf_kswz(t, i, hd);
+                    pf_split(y2, khi + o, klo + o);
+                    if (keep) kc[slot + i] = y2;
                 }
             }
         }
@@ -708,8 +519,316 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
     for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {   // v is not normed
         const float vv = row[(H + 1u) * hd + i];
         if (keep) vc[slot + i] = vv;
-        vt[static_cast<uint64_t>(i) * Tp + t] = vv;
+        const uint64_t o = pf_vswz(t, i, hd);
+        pf_split(vv, vhi + o, vlo + o);
     }
+}
+
+// ---- causal attention ----------------------------------------------------------------------
+
+// One unit per (key chunk c, query tile i, head h): queries q0 = 32 i .. q0 + 31 of head h
+// against the keys of chunk c (A.kc keys, a multiple of 32) of the tile's key range [ks, ke)
+// (ke = min(T, q0 + 32); ks = 0, or with a local window the window's start for q0, rounded
+// down to 32). The four waves split the head dimension: wave w owns the k steps s = w mod 4 of
+// S^T = K Q^T and the d tiles dt = w mod 4 of O^T. Per 32-key tile, with lane l on query
+// q0 + l % 32: each wave's partial S^T (three f16 products of the hi/lo parts) goes through LDS
+// and every wave sums the four in wave order (the same scores in every wave), masks (key <= q,
+// inside the window, key < T) and scales them and runs the online softmax in base 2 (the
+// scale times log2 e, v_exp_f32): running max m, e_j = 2^(v_j - m), each tile's sum of e_j in
+// fp32 added to a running sum in double, its O^T tiles rescaled when m grows and O^T += V^T E^T
+// (V^T and E^T as hi/lo). The next tile's operands load during the current one.
+// A tile whose key range is one chunk is finished here (out = O / sum as f16 hi/lo into the
+// queries' own columns, which only this unit reads); otherwise the chunk's partial goes to
+// opart/mpart/lpart and k_pf_attn_merge combines them in the next launch. Same result as the
+// masked softmax of src/gemma3.cpp:1602-1696 over the full row up to the rounding of the
+// rescaling; a softmax sum that is not > 0 and finite flags the block.
+// MFMA operand layouts (v_mfma_f32_32x32x16_f16): lane l gives A[m = l % 32][k = 8 (l / 32) + j]
+// and B[k = 8 (l / 32) + j][n = l % 32], j < 8; result r of lane l is C[8 (r / 4) + 4 (l / 32) +
+// r % 4][l % 32].
+constexpr uint32_t kPfAttKC = 128;   // keys per attention chunk (a multiple of 32)
+struct PfAttn {
+    const _Float16* qhi;   // [T][H * hd] queries, normed and rotated (overwritten by the output)
+    const _Float16* qlo;
+    const _Float16* khi;   // keys in pf_kswz order (Tp / 32 tiles)
+    const _Float16* klo;
+    const _Float16* vhi;   // values in pf_vswz order
+    const _Float16* vlo;
+    _Float16* ohi;         // [T][H * hd] output
+    _Float16* olo;
+    float* opart;          // [H][qtmax][maxc][32][hd] chunk partials, sum_j e_j v_j
+    float* mpart;          // [H][qtmax][maxc][32] their maxima (base 2)
+    double* lpart;         // [H][qtmax][maxc][32] their sums of e_j
+    G3State* st;
+    uint32_t T, H, window, qtmax, maxc, block, kc;
+    float scale2;          // attention scale times log2(e): the scores in base 2
+};
+
+__device__ __forceinline__ void pf_att_range(uint32_t q0, uint32_t T, uint32_t window, uint32_t& ks, uint32_t& ke) {
+    ke = min(T, q0 + 32u);
+    ks = window != 0u && q0 + 1u > window ? (q0 + 1u - window) & ~31u : 0u;
+}
+
+template <uint32_t HD>
+__global__ void __launch_bounds__(256) k_pf_attn(PfAttn A) {
+#pragma clang fp contract(off)
+    constexpr uint32_t KS = HD / 16u;               // k steps of S^T
+    constexpr uint32_t DT = HD / 32u;               // d tiles of O^T
+    constexpr uint32_t KW = (KS + 3u) / 4u;         // k steps per wave (at most)
+    constexpr uint32_t DW = (DT + 3u) / 4u;         // d tiles per wave (at most)
+    __shared__ __align__(16) float s_s[2][4][16 * 64];   // partial S^T per wave, double-buffered
+    const uint32_t c = blockIdx.x, i = blockIdx.y, h = blockIdx.z;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, l32 = lane & 31u, hf = lane >> 5;
+    const uint32_t T = A.T, q0 = 32u * i, qw = A.H * HD;
+    uint32_t ks, ke;
+    pf_att_range(q0, T, A.window, ks, ke);
+    const uint32_t nch = (ke - ks + A.kc - 1u) / A.kc;
+    if (c >= nch) return;   // whole workgroup
+    const uint32_t k0 = ks + c * A.kc, k1 = min(ke, k0 + A.kc);
+    const uint32_t q = q0 + l32;
+    // this wave's k steps of the queries (B operand of S^T), rows past T clamped (never written)
+    v4u qb[KW][2];
+    {
+        const uint64_t qo = static_cast<uint64_t>(min(q, T - 1u)) * qw + h * HD + 8u * hf;
+#pragma unroll
+        for (uint32_t j = 0; j < KW; ++j) {
+            const uint32_t k = min(wave + 4u * j, KS - 1u);
+            qb[j][0] = *reinterpret_cast<const v4u*>(A.qhi + qo + 16u * k);
+            qb[j][1] = *reinterpret_cast<const v4u*>(A.qlo + qo + 16u * k);
+        }
+    }
+    // the operands of one 32-key tile for this wave
+    struct Ops {
+        v4u k[KW][2];       // [k step][hi, lo]
+        v4u v[DW][2][2];    // [d tile][k step][hi, lo]
+    };
+    auto load = [&](uint32_t kt, Ops& R) {
+        const uint64_t tile = kt >> 5;
+#pragma unroll
+        for (uint32_t j = 0; j < KW; ++j) {
+            const uint32_t k = min(wave + 4u * j, KS - 1u);
+            const uint64_t o = (tile * KS + k) * 512u + 8u * lane;
+            R.k[j][0] = *reinterpret_cast<const v4u*>(A.khi + o);
+            R.k[j][1] = *reinterpret_cast<const v4u*>(A.klo + o);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < DW; ++j) {
+            const uint32_t dt = min(wave + 4u * j, DT - 1u);
+#pragma unroll
+            for (uint32_t sk = 0; sk < 2u; ++sk) {
+                const uint64_t o = ((tile * DT + dt) * 2u + sk) * 512u + 8u * lane;
+                R.v[j][sk][0] = *reinterpret_cast<const v4u*>(A.vhi + o);
+                R.v[j][sk][1] = *reinterpret_cast<const v4u*>(A.vlo + o);
+            }
+        }
+    };
+    float m = -INFINITY;   // running maximum of the scaled scores of query q
+    double lsum = 0.0;     // this lane's share of sum_j e_j
+    float16v o[DW];        // O^T tiles of this wave: d = 32 dt + 8 (r / 4) + 4 hf + r % 4, query q
+#pragma unroll
+    for (uint32_t j = 0; j < DW; ++j) o[j] = float16v{};
+    // one 32-key tile: partial S^T, exchange, online softmax, O^T update (operands in R)
+    uint32_t buf = 0;
+    auto step = [&](uint32_t kt, const Ops& R) {
+        float16v sp = {};
+#pragma unroll
+        for (uint32_t j = 0; j < KW; ++j) {
+            if (wave + 4u * j >= KS) continue;
+            const half8 ah = __builtin_bit_cast(half8, R.k[j][0]), al = __builtin_bit_cast(half8, R.k[j][1]);
+            const half8 bh = __builtin_bit_cast(half8, qb[j][0]), bl = __builtin_bit_cast(half8, qb[j][1]);
+            sp = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, sp, 0, 0, 0);
+            sp = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, sp, 0, 0, 0);
+            sp = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, sp, 0, 0, 0);
+        }
+        // the four partials through LDS (buffer buf was last read two tiles ago, before the
+        // barrier of the previous tile)
+#pragma unroll
+        for (uint32_t rq = 0; rq < 4u; ++rq)
+            *reinterpret_cast<f4*>(&s_s[buf][wave][(rq * 64u + lane) * 4u]) =
+                f4{sp[4 * rq], sp[4 * rq + 1], sp[4 * rq + 2], sp[4 * rq + 3]};
+        __syncthreads();
+        float v[16];
+#pragma unroll
+        for (uint32_t rq = 0; rq < 4u; ++rq) {
+            f4 t = *reinterpret_cast<const f4*>(&s_s[buf][0][(rq * 64u + lane) * 4u]);
+#pragma unroll
+            for (uint32_t w = 1; w < 4u; ++w) {
+                const f4 u = *reinterpret_cast<const f4*>(&s_s[buf][w][(rq * 64u + lane) * 4u]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[e] += u[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * rq + e] = t[e];
+        }
+        buf ^= 1u;
+        // scores in base 2 (scale * log2 e folded in): e_j = 2^(v_j - m) = exp(scale s_j - m ln 2)
+        float tmax = -INFINITY;
+        if (kt + 31u < k1 && kt + 31u <= q0 && (A.window == 0u || kt + A.window > q0 + 31u)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {   // every key of the tile visible to every query
+                v[r] *= A.scale2;
+                tmax = fmaxf(tmax, v[r]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t key = kt + 16u * (r / 8) + 8u * hf + (r % 8);
+                const bool ok = key < k1 && key <= q && (A.window == 0u || key + A.window > q);
+                v[r] = ok ? v[r] * A.scale2 : -INFINITY;
+                tmax = fmaxf(tmax, v[r]);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mn = fmaxf(m, tmax);
+        const float base = mn == -INFINITY ? 0.0f : mn;   // nothing visible yet: every e_j is 0
+        const float alpha = __builtin_amdgcn_exp2f(m - base);
+        float e[16];
+        float es = 0.0f;   // the tile's share in fp32, then into the double sum
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            e[r] = __builtin_amdgcn_exp2f(v[r] - base);
+            es += e[r];
+        }
+        lsum = lsum * static_cast<double>(alpha) + static_cast<double>(es);
+        m = mn;
+        half8 eh[2], el[2];
+#pragma unroll
+        for (int sk = 0; sk < 2; ++sk)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = e[8 * sk + j];
+                eh[sk][j] = static_cast<_Float16>(x);
+                el[sk][j] = static_cast<_Float16>(x - static_cast<float>(eh[sk][j]));
+            }
+#pragma unroll
+        for (uint32_t j = 0; j < DW; ++j) {
+            if (wave + 4u * j >= DT) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+#pragma unroll
+            for (uint32_t sk = 0; sk < 2u; ++sk) {
+                const half8 avh = __builtin_bit_cast(half8, R.v[j][sk][0]);
+                const half8 avl = __builtin_bit_cast(half8, R.v[j][sk][1]);
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(avh, eh[sk], o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(avl, eh[sk], o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(avh, el[sk], o[j], 0, 0, 0);
+            }
+        }
+    };
+    // two operand sets in turn, the next tile's loads in flight during the current tile
+    Ops ra, rb;
+    load(k0, ra);
+    for (uint32_t kt = k0; kt < k1; kt += 64u) {
+        if (kt + 32u < k1) load(kt + 32u, rb);
+        step(kt, ra);
+        if (kt + 32u >= k1) break;
+        if (kt + 64u < k1) load(kt + 64u, ra);
+        step(kt + 32u, rb);
+    }
+    lsum += __shfl_xor(lsum, 32);   // both lane halves now hold query q's sum
+    const uint64_t unit = (static_cast<uint64_t>(h) * A.qtmax + i) * A.maxc + c;
+    if (nch == 1u) {   // the whole key range: normalise and write the output rows
+        if (q >= T) return;
+        const double den = lsum;
+        if (wave == 0u && hf == 0u && (!(den > 0.0) || !__builtin_isfinite(den)))   // :1666-1670
+            atomicMin(&A.st->nonfinite, g3_code_softmax(A.block));
+        const float inv = static_cast<float>(1.0 / den);
+        const uint64_t oo = static_cast<uint64_t>(q) * qw + h * HD;
+#pragma unroll
+        for (uint32_t j = 0; j < DW; ++j) {
+            if (wave + 4u * j >= DT) continue;
+#pragma unroll
+            for (uint32_t rq = 0; rq < 4u; ++rq) {
+                const uint32_t d = 32u * (wave + 4u * j) + 8u * rq + 4u * hf;
+                pf_split4(f4{o[j][4 * rq] * inv, o[j][4 * rq + 1] * inv, o[j][4 * rq + 2] * inv, o[j][4 * rq + 3] * inv},
+                          A.ohi + oo + d, A.olo + oo + d);
+            }
+        }
+        return;
+    }
+    float* op = A.opart + unit * 32u * HD + static_cast<uint64_t>(l32) * HD;
+#pragma unroll
+    for (uint32_t j = 0; j < DW; ++j) {
+        if (wave + 4u * j >= DT) continue;
+#pragma unroll
+        for (uint32_t rq = 0; rq < 4u; ++rq)
+            *reinterpret_cast<f4*>(op + 32u * (wave + 4u * j) + 8u * rq + 4u * hf) =
+                f4{o[j][4 * rq], o[j][4 * rq + 1], o[j][4 * rq + 2], o[j][4 * rq + 3]};
+    }
+    if (wave == 0u && hf == 0u) {
+        A.mpart[unit * 32u + l32] = m;
+        A.lpart[unit * 32u + l32] = lsum;
+    }
+}
+
+// Merge of the chunk partials of the query tiles k_pf_attn split (one workgroup per (tile, head);
+// tiles of one chunk were finished by k_pf_attn): thread t on row r = t / 8 and the eighth
+// t % 8 of the columns; in chunk order, with M the running maximum of the chunk maxima m_c,
+// den = sum_c exp(m_c - M) sum_c (double), out = sum_c exp(m_c - M) O_c / den as f16 hi/lo into
+// the queries' columns.
+template <uint32_t HD>
+__global__ void __launch_bounds__(256) k_pf_attn_merge(PfAttn A) {
+#pragma clang fp contract(off)
+    constexpr uint32_t NF = HD / 32u;   // float4 per thread
+    const uint32_t i = blockIdx.x, h = blockIdx.y, T = A.T, q0 = 32u * i;
+    uint32_t ks, ke;
+    pf_att_range(q0, T, A.window, ks, ke);
+    const uint32_t nch = (ke - ks + A.kc - 1u) / A.kc;
+    const uint32_t r = threadIdx.x >> 3, g = threadIdx.x & 7u;
+    if (nch == 1u || q0 + r >= T) return;
+    const uint64_t unit0 = (static_cast<uint64_t>(h) * A.qtmax + i) * A.maxc;
+    // chunks in groups of kG, every load of a group issued together (indices clamped to the last
+    // chunk; the clamped duplicates are not used): one round of loads for up to kG chunks
+    constexpr uint32_t kG = 4;
+    double den = 0.0;
+    f4 acc[NF];
+#pragma unroll
+    for (uint32_t k = 0; k < NF; ++k) acc[k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float M = -INFINITY;
+    for (uint32_t c0 = 0; c0 < nch; c0 += kG) {
+        float mv[kG];
+        double lv[kG];
+        f4 x[kG][NF];
+#pragma unroll
+        for (uint32_t j = 0; j < kG; ++j) {
+            const uint64_t u = unit0 + min(c0 + j, nch - 1u);
+            mv[j] = A.mpart[u * 32u + r];
+            lv[j] = A.lpart[u * 32u + r];
+            const float* src = A.opart + (u * 32u + r) * HD + g * (HD / 8u);
+#pragma unroll
+            for (uint32_t k = 0; k < NF; ++k) x[j][k] = *reinterpret_cast<const f4*>(src + 4u * k);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // the group's loads stay ahead of their first use
+        // running merge: the group's maximum rescales what is accumulated so far
+        float Mg = M;
+#pragma unroll
+        for (uint32_t j = 0; j < kG; ++j)
+            if (c0 + j < nch) Mg = fmaxf(Mg, mv[j]);
+        const float fo = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mg);
+        den *= static_cast<double>(fo);
+#pragma unroll
+        for (uint32_t k = 0; k < NF; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[k][e] *= fo;
+        M = Mg;
+#pragma unroll
+        for (uint32_t j = 0; j < kG; ++j) {
+            if (c0 + j >= nch) break;
+            const float f = __builtin_amdgcn_exp2f(mv[j] - M);
+            den += lv[j] * static_cast<double>(f);
+#pragma unroll
+            for (uint32_t k = 0; k < NF; ++k)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[k][e] += f * x[j][k][e];
+        }
+    }
+    if (g == 0u && (!(den > 0.0) || !__builtin_isfinite(den)))   // :1666-1670
+        atomicMin(&A.st->nonfinite, g3_code_softmax(A.block));
+    const float inv = static_cast<float>(1.0 / den);
+    const uint64_t oo = static_cast<uint64_t>(q0 + r) * (A.H * HD) + h * HD + g * (HD / 8u);
+#pragma unroll
+    for (uint32_t k = 0; k < NF; ++k)
+        pf_split4(f4{acc[k][0] * inv, acc[k][1] * inv, acc[k][2] * inv, acc[k][3] * inv}, A.ohi + oo + 4u * k,
+                  A.olo + oo + 4u * k);
 }
 
 // ---- expanded weights ------------------------------------------------------------------------
@@ -893,15 +1012,6 @@ __global__ void __launch_bounds__(256 * NWN) k_pf_gemm_h(PfGemm G) {
 
 // ---- host side --------------------------------------------------------------------------
 
-template <int MODE>
-static int pf_launch(const PfGemm& G, uint32_t batch, hipStream_t s) {
-    const dim3 grid((G.N + kPfGT - 1u) / kPfGT, (G.M + kPfGT - 1u) / kPfGT, batch);
-    PfGemm arg = G;
-    void* args[] = {&arg};
-    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_gemm<MODE>), grid, dim3(kPfThreads), args, 0, s));
-    return VRT_OK;
-}
-
 template <int WN, int NWN>
 static int pf_launch_q8(const PfGemm& G, uint32_t splits, hipStream_t s) {
     constexpr uint32_t BN = 32u * WN * NWN;
@@ -1018,14 +1128,18 @@ int pf_setup(vrt_g3* g, uint32_t max_t) {
     p.alo = q;
     if (int rc = take(static_cast<size_t>(max_t) * std::max(nqkv, 2u * F) * 4u, &q)) return rc;
     p.big = static_cast<float*>(q);
-    if (int rc = take(static_cast<size_t>(H) * max_t * tp * 4u, &q)) return rc;
-    p.s = static_cast<float*>(q);
-    if (int rc = take(static_cast<size_t>(H) * max_t * tp * 2u, &q)) return rc;
-    p.phi = q;
-    if (int rc = take(static_cast<size_t>(H) * max_t * tp * 2u, &q)) return rc;
-    p.plo = q;
-    if (int rc = take(static_cast<size_t>(hd) * tp * 4u, &q)) return rc;
-    p.vt = static_cast<float*>(q);
+    void** kv[] = {&p.khi, &p.klo, &p.vhi, &p.vlo};   // tp x hd f16 each
+    for (void** b : kv)
+        if (int rc = take(static_cast<size_t>(hd) * tp * 2u, b)) return rc;
+    p.qtmax = (max_t + 31u) / 32u;
+    p.maxc = (max_t + 31u + kPfAttKC - 1u) / kPfAttKC;
+    const size_t units = static_cast<size_t>(H) * p.qtmax * p.maxc;
+    if (int rc = take(units * 32u * hd * 4u, &q)) return rc;
+    p.opart = static_cast<float*>(q);
+    if (int rc = take(units * 32u * 4u, &q)) return rc;
+    p.mpart = static_cast<float*>(q);
+    if (int rc = take(units * 32u * 8u, &q)) return rc;
+    p.lpart = static_cast<double*>(q);
     // Expanded weights: 2 bytes per quant + 4 per 32 (2.125 bytes per weight, twice the Q8_0
     // matrices' 1.0625), made once here when they fit kPfExpandBudget.
     const uint64_t per_layer = static_cast<uint64_t>(nqkv) * d + static_cast<uint64_t>(d) * qw +
@@ -1066,62 +1180,61 @@ int pf_setup(vrt_g3* g, uint32_t max_t) {
     return VRT_OK;
 }
 
-// Causal local/global attention of one block over qkv rows [T][q | k | v] (q, k normed and
-// rotated; q also as f16 hi/lo in qhi/qlo) into att hi/lo [T][H * hd], all on MFMA:
-// S_h = Q_h K^T (key tiles no query sees skipped), masked softmax -> P_h, O_h = P_h V.
-static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, const float* qkv, const _Float16* qhi,
-                        const _Float16* qlo, _Float16* att_hi, _Float16* att_lo, hipStream_t s) {
-    const PfState& p = g->pf;
-    const uint32_t H = g->cfg.head_count, hd = g->cfg.head_dim, qw = H * hd, nqkv = qw + 2u * hd;
-    const uint32_t Tp = pf_pad(T);
-    const uint32_t window = Ly.slots >= g->cfg.context_length ? 0u : Ly.slots;
-    {   // S_h = Q_h K^T: [H][T][Tp]
-        PfGemm G{};
-        G.ahi = qhi;
-        G.alo = qlo;
-        G.lda = qw;
-        G.a_bs = hd;
-        G.b = qkv + qw;
-        G.ldb = nqkv;
-        G.c = p.s;
-        G.ldc = Tp;
-        G.c_bs = static_cast<uint64_t>(T) * Tp;
-        G.M = T;
-        G.N = T;
-        G.K = hd;
-        G.window = window;
-        if (int rc = pf_launch<kGemmB32 | kGemmCausalS>(G, H, s)) return rc;
-    }
-    {
-        const float* S = p.s;
-        float scale = g->P.attn_scale;
-        uint32_t t = T, tp = Tp, w = window;
-        _Float16* phi = static_cast<_Float16*>(p.phi);
-        _Float16* plo = static_cast<_Float16*>(p.plo);
-        G3State* st = g->P.st;
-        uint32_t blk = Ly.index;
-        void* args[] = {&S, &t, &tp, &scale, &w, &phi, &plo, &st, &blk};
-        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_softmax), dim3(T, H), dim3(kPfThreads), args, 0, s));
-    }
-    {   // O_h = P_h V -> att[:, h * hd ..]
-        PfGemm G{};
-        G.ahi = static_cast<const _Float16*>(p.phi);
-        G.alo = static_cast<const _Float16*>(p.plo);
-        G.lda = Tp;
-        G.a_bs = static_cast<uint64_t>(T) * Tp;
-        G.b = p.vt;
-        G.ldb = Tp;
-        G.chi = att_hi;
-        G.clo = att_lo;
-        G.ldc = qw;
-        G.c_bs = hd;
-        G.M = T;
-        G.N = hd;
-        G.K = Tp;
-        G.window = window;
-        if (int rc = pf_launch<kGemmB32 | kGemmCausalO | kGemmOut16>(G, H, s)) return rc;
-    }
+template <uint32_t HD>
+static int pf_attn_launch(const PfAttn& A, dim3 grid, hipStream_t s) {
+    PfAttn arg = A;
+    void* args[] = {&arg};
+    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_attn<HD>), grid, dim3(256), args, 0, s));
+    if (grid.x > 1u)   // some tile has several chunks
+        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_attn_merge<HD>), dim3(grid.y, grid.z),
+                                      dim3(256), args, 0, s));
     return VRT_OK;
+}
+
+// Causal local/global attention of one block (k_pf_attn) over the queries in qhi/qlo [T][H hd],
+// written back in place as the attention output.
+static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, _Float16* qhi, _Float16* qlo, hipStream_t s) {
+    const PfState& p = g->pf;
+    const uint32_t H = g->cfg.head_count, hd = g->cfg.head_dim;
+    PfAttn A{};
+    A.qhi = A.ohi = qhi;
+    A.qlo = A.olo = qlo;
+    A.khi = static_cast<const _Float16*>(p.khi);
+    A.klo = static_cast<const _Float16*>(p.klo);
+    A.vhi = static_cast<const _Float16*>(p.vhi);
+    A.vlo = static_cast<const _Float16*>(p.vlo);
+    A.opart = p.opart;
+    A.mpart = p.mpart;
+    A.lpart = p.lpart;
+    A.st = g->P.st;
+    A.T = T;
+    A.H = H;
+    A.window = Ly.slots >= g->cfg.context_length ? 0u : Ly.slots;
+    A.qtmax = p.qtmax;
+    A.maxc = p.maxc;
+    A.block = Ly.index;
+    A.scale2 = g->P.attn_scale * 1.4426950408889634f;
+    const uint32_t qt = (T + 31u) / 32u;
+    A.kc = kPfAttKC;
+    uint32_t nch = 1;
+    for (uint32_t i = 0; i < qt; ++i) {
+        const uint32_t q0 = 32u * i, ke = std::min(T, q0 + 32u);
+        const uint32_t ks = A.window != 0u && q0 + 1u > A.window ? (q0 + 1u - A.window) & ~31u : 0u;
+        nch = std::max(nch, (ke - ks + A.kc - 1u) / A.kc);
+    }
+    if (qt > p.qtmax || nch > p.maxc) return set_error(VRT_ERR_STATE, "prefill attention workspace too small");
+    const dim3 grid(nch, qt, H);
+    switch (hd) {
+    case 32: return pf_attn_launch<32>(A, grid, s);
+    case 64: return pf_attn_launch<64>(A, grid, s);
+    case 96: return pf_attn_launch<96>(A, grid, s);
+    case 128: return pf_attn_launch<128>(A, grid, s);
+    case 160: return pf_attn_launch<160>(A, grid, s);
+    case 192: return pf_attn_launch<192>(A, grid, s);
+    case 224: return pf_attn_launch<224>(A, grid, s);
+    case 256: return pf_attn_launch<256>(A, grid, s);
+    default: return set_error(VRT_ERR_INVALID, "prefill head_dim not supported");
+    }
 }
 
 // T prompt positions 0..T-1 on the context's stream; the last one runs the LM head + argmax
@@ -1175,13 +1288,16 @@ int pf_run(vrt_g3* g, uint32_t T) {
             float* vc = Ly.vc;
             uint32_t slots = Ly.slots;
             uint32_t tp = pf_pad(T);
-            float* vt = g->pf.vt;
-            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &tp, &vt};
+            _Float16* khi = static_cast<_Float16*>(p.khi);
+            _Float16* klo = static_cast<_Float16*>(p.klo);
+            _Float16* vhi = static_cast<_Float16*>(p.vhi);
+            _Float16* vlo = static_cast<_Float16*>(p.vlo);
+            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &khi, &klo, &vhi, &vlo};
             const uint32_t waves = std::min(H + 1u, kPfQkMaxWaves);
             VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_qk), dim3(tp), dim3(64u * waves), args, 0, s));
         }
-        // q (hi/lo in ahi/alo) is consumed by S = Q K^T before O = P V overwrites ahi/alo
-        if (int rc = pf_attention(g, Ly, T, big, ahi, alo, ahi, alo, s)) return rc;
+        // the attention output replaces q (hi/lo in ahi/alo)
+        if (int rc = pf_attention(g, Ly, T, ahi, alo, s)) return rc;
         uint32_t so = s_o;
         if (int rc = pf_gemm(g, ahi, alo, T, qw, {{Ly.wo, d}}, lw ? &lw[l].o : nullptr, x, so, s)) return rc;
         so = std::max(1u, std::min(so, (qw / 32u) / 2u));
