@@ -20,7 +20,6 @@ struct G3State {
     uint32_t want_logits;  // LM head also writes the logits
     uint32_t nonfinite;    // first failure (vrt_g3_errors.hpp codes; ~0u: none)
     uint32_t pad[2];
-    uint32_t tickets[8];   // last-workgroup counters (self-resetting)
 };
 
 struct LmPartial {

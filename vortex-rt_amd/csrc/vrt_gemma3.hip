@@ -191,14 +191,13 @@ __global__ void __launch_bounds__(kThreads) k_qkv(G3Params P, LayerParams Lc, co
 }
 
 // =========================================================================================
-// k_attn: QK-norm + RoPE + KV append + attention over one history chunk; the last
-// workgroup merges the chunks (split softmax: max, sum and weighted V per chunk).
+// k_attn: QK-norm + RoPE + KV append + attention over one history chunk per workgroup (split
+// softmax: max, sum and weighted V per chunk); k_attn_merge combines the chunks.
 // =========================================================================================
 
 __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
 #pragma clang fp contract(off)
     __shared__ double red[8];
-    __shared__ bool last;
     if (P.st->stop) return;
     const uint32_t pos = P.st->step;
     const uint32_t H = P.H, hd = P.hd, half = hd >> 1;
@@ -215,7 +214,6 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
     const uint32_t C = (n_hist + G - 1u) / G;
     const uint32_t c0 = t_first + blockIdx.x * C;
     const uint32_t c1 = min(pos + 1u, c0 + C);
-    const uint32_t n_act = (n_hist + C - 1u) / C;
 
     // q, k raw -> LDS, then per-head RMSNorm (src/gemma3.cpp:1045-1104) and RoPE (:1371-1424)
     const float* qkv = P.qkv;
@@ -296,17 +294,20 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
                 if (h < H) mypart[2u * H + h * hd + i] = acc[h];
         }
     }
-    // one device-scope release per workgroup (after the barrier orders the block's writes),
-    // one acquire in the last workgroup
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        last = atomicAdd(&P.st->tickets[0], 1u) == gridDim.x - 1u;
-        if (last) __threadfence();
-    }
-    __syncthreads();
-    if (!last) return;
-    // merge: att[h][i] = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c
+}
+
+// k_attn_merge: one workgroup combines k_attn's chunk partials of the step (a launch of its
+// own, so the partials are visible without a device-wide fence):
+// att[h][i] = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
+__global__ void __launch_bounds__(kThreads) k_attn_merge(G3Params P, LayerParams Lc) {
+#pragma clang fp contract(off)
+    if (P.st->stop) return;
+    const uint32_t pos = P.st->step;
+    const uint32_t H = P.H, hd = P.hd;
+    const uint32_t n_hist = min(pos + 1u, Lc.slots);
+    const uint32_t C = (n_hist + Lc.attn_grid - 1u) / Lc.attn_grid;
+    const uint32_t n_act = (n_hist + C - 1u) / C;
+    const uint32_t stride_part = 2u * H + H * hd;
     for (uint32_t idx = threadIdx.x; idx < H * hd; idx += blockDim.x) {
         const uint32_t h = idx / hd, i = idx % hd;
         float M = -INFINITY;
@@ -321,7 +322,6 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
         P.att[idx] = static_cast<float>(num / den);
         if (!(den > 0.0) || !__builtin_isfinite(den)) atomicMin(&P.st->nonfinite, g3_code_softmax(Lc.index));
     }
-    if (threadIdx.x == 0) P.st->tickets[0] = 0u;
 }
 
 // =========================================================================================
@@ -453,8 +453,8 @@ __global__ void __launch_bounds__(kThreads) k_down(G3Params P, LayerParams Lc) {
 }
 
 // =========================================================================================
-// k_lm: final residual + output norm, tied LM head fused with greedy argmax.
-// mode 0: a decode step (updates the step state); mode 1: timing (no state change).
+// k_lm: final residual + output norm, tied LM head fused with greedy argmax (per-workgroup
+// partials; k_lm_final reduces them). mode 0: a decode step; mode 1: timing (no state change).
 // =========================================================================================
 
 template <int S, int NB, int U>
@@ -464,7 +464,6 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
     __shared__ double red[8];
     __shared__ float bvs[4];
     __shared__ uint32_t bis[4];
-    __shared__ bool last;
     if (P.st->stop && mode == 0) return;
     const uint32_t s = P.st->step;
     const bool run_lm = mode != 0 || s >= P.st->lm_from;
@@ -534,18 +533,21 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
             P.lm_part[blockIdx.x] = {bvs[0], bis[0]};
         }
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        last = atomicAdd(&P.st->tickets[1], 1u) == gridDim.x - 1u;
-        if (last) __threadfence();
-    }
-    __syncthreads();
-    if (!last) return;
+}
+
+// k_lm_final: one workgroup reduces k_lm's per-workgroup argmax partials (a launch of its own, so
+// they are visible without a device-wide fence) and advances the step state: mode 0 records
+// the step's result, feeds the greedy token and stops at EOS; mode 1 (timing) records only.
+__global__ void __launch_bounds__(kThreads) k_lm_final(G3Params P, uint32_t nparts, uint32_t mode) {
+    __shared__ float bvs[4];
+    __shared__ uint32_t bis[4];
+    if (P.st->stop && mode == 0) return;
+    const uint32_t s = P.st->step;
+    const bool run_lm = mode != 0 || s >= P.st->lm_from;
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
     if (run_lm) {
-        bv = -INFINITY;
-        bi = 0xffffffffu;
-        for (uint32_t k = threadIdx.x; k < gridDim.x; k += blockDim.x) {
+        for (uint32_t k = threadIdx.x; k < nparts; k += blockDim.x) {
             const LmPartial pp = P.lm_part[k];
             if (am_better(pp.value, pp.index, bv, bi)) { bv = pp.value; bi = pp.index; }
         }
@@ -570,7 +572,6 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
         } else {
             P.results[P.ctx_len] = {bis[0], bvs[0]};
         }
-        P.st->tickets[1] = 0u;
     }
 }
 
@@ -651,6 +652,8 @@ static int g3_enqueue_step(vrt_g3* g, hipStream_t stream) {
                                  static_cast<size_t>(g->cfg.head_count) * Lc.chunk_max) * 4u + 64u;
             VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_attn), dim3(Lc.attn_grid), dim3(kThreads), args,
                                           smem, stream));
+            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_attn_merge), dim3(1), dim3(kThreads), args, 0,
+                                          stream));
         }
         {
             void* args[] = {&g->P, &Lc};
@@ -669,6 +672,9 @@ int vrt::g3_enqueue_lm(vrt_g3* g, hipStream_t stream) {
     uint32_t mode = 0;
     void* args[] = {&g->P, &last_post, &g->out_norm_dev, &g->lm_rows_per_wg, &mode};
     VRT_HIP_CHECK(hipLaunchKernel(g->ld_lm.fn, dim3(g->ld_lm.grid), dim3(kThreads), args, g->ld_lm.smem, stream));
+    uint32_t nparts = g->ld_lm.grid;
+    void* fargs[] = {&g->P, &nparts, &mode};
+    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_lm_final), dim3(1), dim3(kThreads), fargs, 0, stream));
     return VRT_OK;
 }
 
@@ -1102,16 +1108,21 @@ extern "C" int vrt_g3_time_lm_head(vrt_g3* g, uint32_t iters, float* mean_us) {
     VRT_REQUIRE(g && mean_us && iters > 0, "vrt_g3_time_lm_head: bad argument");
     hipStream_t s = g->ctx->stream;
     const float* last_post = g->layers[g->cfg.block_count - 1].post_ffw;
-    uint32_t mode = 1;
+    uint32_t mode = 1, nparts = g->ld_lm.grid;
     void* args[] = {&g->P, &last_post, &g->out_norm_dev, &g->lm_rows_per_wg, &mode};
+    void* fargs[] = {&g->P, &nparts, &mode};
     hipEvent_t a, b;
     VRT_HIP_CHECK(hipEventCreate(&a));
     VRT_HIP_CHECK(hipEventCreate(&b));
-    // warm-up launch
-    VRT_HIP_CHECK(hipLaunchKernel(g->ld_lm.fn, dim3(g->ld_lm.grid), dim3(kThreads), args, g->ld_lm.smem, s));
+    auto launch = [&]() -> int {
+        VRT_HIP_CHECK(hipLaunchKernel(g->ld_lm.fn, dim3(g->ld_lm.grid), dim3(kThreads), args, g->ld_lm.smem, s));
+        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_lm_final), dim3(1), dim3(kThreads), fargs, 0, s));
+        return VRT_OK;
+    };
+    if (int rc = launch()) return rc;   // warm-up
     VRT_HIP_CHECK(hipEventRecord(a, s));
     for (uint32_t i = 0; i < iters; ++i)
-        VRT_HIP_CHECK(hipLaunchKernel(g->ld_lm.fn, dim3(g->ld_lm.grid), dim3(kThreads), args, g->ld_lm.smem, s));
+        if (int rc = launch()) return rc;
     VRT_HIP_CHECK(hipEventRecord(b, s));
     VRT_HIP_CHECK(hipEventSynchronize(b));
     float ms = 0.0f;
