@@ -212,6 +212,29 @@ def synth_ids(seed: int, n: int, vocab: int):
     return synth.uniform_ids(seed, n, 2, vocab)
 
 
+def multikernel_leg(ctx, g, prompt, steps: int = 64):
+    """The multi-kernel decode path (a hipGraph per step: five kernels per block, the attention
+    merge and the LM head with its final reduction), timed over `steps` steps after the prompt."""
+    g.set_persistent(False)
+    g.set_graph(True)
+    try:
+        g.start(prompt, steps + 5)
+        g.step(prompt.size + 4)
+        ctx.sync()
+        ev0, ev1 = ctx.event(), ctx.event()
+        ctx.record(ev0)
+        g.step(steps)
+        ctx.record(ev1)
+        ms = ctx.elapsed_ms(ev0, ev1)
+        ctx.sync()
+        if g.collect().size < steps + 5:
+            raise SystemExit("[bench] EOS inside the multi-kernel timed steps; no throughput is reported")
+    finally:
+        g.set_persistent(True)
+    return {"workload": f"{prompt.size}-token prompt + 4 steps, then {steps} timed decode steps (hipGraph per step)",
+            "us_per_step": round(ms * 1e3 / steps, 1), "tokens_per_s": round(steps / (ms / 1e3), 1)}
+
+
 def copy_calibration(nbytes: int = 1 << 30):
     """A plain device copy of known size for scaling the PMC counters (FETCH_SIZE / WRITE_SIZE
     of this dispatch against nbytes read and nbytes written)."""
@@ -263,6 +286,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token batched prefill measurement")
     ap.add_argument("--no-kernels", action="store_true",
                     help="skip the standalone matvec / QKV / FFN measurements (single-matvec and layer-block workloads)")
+    ap.add_argument("--multikernel", action="store_true",
+                    help="also time the multi-kernel (hipGraph) decode path")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
@@ -327,6 +352,7 @@ def main():
     longctx = None if args.no_long else long_context(ctx, g, cfg)
     prefill = None if args.no_prefill else prefill_bench(ctx, g, cfg)
     kernels = None if args.no_kernels else kernel_legs(ctx)
+    multikernel = multikernel_leg(ctx, g, prompt) if args.multikernel else None
 
     out = {
         "metric": METRIC,
@@ -368,6 +394,7 @@ def main():
         "long_context": longctx,
         "prefill": prefill,
         "kernels": kernels,
+        "multikernel": multikernel,
         "cpu_baseline": None,
     }
     g.close()

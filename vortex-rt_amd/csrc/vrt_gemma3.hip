@@ -296,31 +296,47 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
     }
 }
 
-// k_attn_merge: one workgroup combines k_attn's chunk partials of the step (a launch of its
-// own, so the partials are visible without a device-wide fence):
-// att[h][i] = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
+// k_attn_merge: combines k_attn's chunk partials of the step (a launch of its own, so the
+// partials are visible without a device-wide fence), one workgroup per head:
+// att[h][i] = sum_c e^(m_c - M) acc_c[i] / sum_c e^(m_c - M) l_c, the sums in double in chunk
+// order. The chunk maxima, sums and weights go through LDS once; each thread then owns dims.
+constexpr uint32_t kAttnMaxChunks = 64;   // k_attn workgroups per block, at most
 __global__ void __launch_bounds__(kThreads) k_attn_merge(G3Params P, LayerParams Lc) {
 #pragma clang fp contract(off)
+    __shared__ float s_m[kAttnMaxChunks];
+    __shared__ float s_l[kAttnMaxChunks];
+    __shared__ double s_w[kAttnMaxChunks];
+    __shared__ double s_den;
     if (P.st->stop) return;
     const uint32_t pos = P.st->step;
-    const uint32_t H = P.H, hd = P.hd;
+    const uint32_t H = P.H, hd = P.hd, h = blockIdx.x;
     const uint32_t n_hist = min(pos + 1u, Lc.slots);
     const uint32_t C = (n_hist + Lc.attn_grid - 1u) / Lc.attn_grid;
     const uint32_t n_act = (n_hist + C - 1u) / C;
     const uint32_t stride_part = 2u * H + H * hd;
-    for (uint32_t idx = threadIdx.x; idx < H * hd; idx += blockDim.x) {
-        const uint32_t h = idx / hd, i = idx % hd;
-        float M = -INFINITY;
-        for (uint32_t c = 0; c < n_act; ++c) M = fmaxf(M, P.part[c * stride_part + h]);
-        double num = 0.0, den = 0.0;
-        for (uint32_t c = 0; c < n_act; ++c) {
-            const float* pc = P.part + c * stride_part;
-            const double wgt = static_cast<double>(expf(pc[h] - M));
-            den += wgt * static_cast<double>(pc[H + h]);
-            num += wgt * static_cast<double>(pc[2u * H + h * hd + i]);
-        }
-        P.att[idx] = static_cast<float>(num / den);
+    for (uint32_t c = threadIdx.x; c < n_act; c += blockDim.x) {
+        s_m[c] = P.part[c * stride_part + h];
+        s_l[c] = P.part[c * stride_part + H + h];
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < n_act; ++c) M = fmaxf(M, s_m[c]);
+    for (uint32_t c = threadIdx.x; c < n_act; c += blockDim.x) s_w[c] = static_cast<double>(expf(s_m[c] - M));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double den = 0.0;
+        for (uint32_t c = 0; c < n_act; ++c) den += s_w[c] * static_cast<double>(s_l[c]);
+        s_den = den;
         if (!(den > 0.0) || !__builtin_isfinite(den)) atomicMin(&P.st->nonfinite, g3_code_softmax(Lc.index));
+    }
+    __syncthreads();
+    const double den = s_den;
+    for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
+        const float* src = P.part + 2u * H + h * hd + i;
+        double num = 0.0;
+#pragma unroll 8
+        for (uint32_t c = 0; c < n_act; ++c) num += s_w[c] * static_cast<double>(src[c * stride_part]);
+        P.att[h * hd + i] = static_cast<float>(num / den);
     }
 }
 
@@ -652,8 +668,8 @@ static int g3_enqueue_step(vrt_g3* g, hipStream_t stream) {
                                  static_cast<size_t>(g->cfg.head_count) * Lc.chunk_max) * 4u + 64u;
             VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_attn), dim3(Lc.attn_grid), dim3(kThreads), args,
                                           smem, stream));
-            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_attn_merge), dim3(1), dim3(kThreads), args, 0,
-                                          stream));
+            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_attn_merge), dim3(g->cfg.head_count),
+                                          dim3(kThreads), args, 0, stream));
         }
         {
             void* args[] = {&g->P, &Lc};
@@ -865,7 +881,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
         if (int rc = g3_alloc(g, kv, &p)) return fail(rc);
         Lp.vc = static_cast<float*>(p);
         // attention split: ~64 positions per workgroup, at most 8 groups for a window and 64 for a full history
-        const uint32_t cap = Lp.global ? 64u : 8u;
+        const uint32_t cap = Lp.global ? kAttnMaxChunks : 8u;
         Lp.attn_grid = std::max(1u, std::min(cap, (Lp.slots + 63u) / 64u));
         Lp.chunk_max = (Lp.slots + Lp.attn_grid - 1u) / Lp.attn_grid;
         max_attn_grid = std::max(max_attn_grid, Lp.attn_grid);
