@@ -14,8 +14,8 @@ struct vrt_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     vrt_device_info info{};
-    // Scratch for the standalone reductions (argmax partials + ticket). Kernels on one
-    // context are stream-ordered, so calls never overlap on it.
+    // Scratch for the standalone reductions (argmax partials). Kernels on one context are
+    // stream-ordered, so calls never overlap on it.
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
     // This device's address of the static workspace of vrt_q8_ffn_noalloc (hipGetSymbolAddress).

@@ -229,12 +229,11 @@ struct AmPartial {
     uint32_t index;
 };
 
-// Per-block strided scan, block reduction, last block reduces the partials.
-__global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ x, uint32_t n, AmPartial* parts,
-                                                uint32_t* ticket, vrt_argmax_result* out) {
+// Per-block strided scan and block reduction into parts[blockIdx.x]; k_argmax_final, a launch
+// of its own (so the partials are visible without a device-wide fence), reduces the partials.
+__global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ x, uint32_t n, AmPartial* parts) {
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
-    __shared__ bool last;
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
@@ -249,19 +248,20 @@ __global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ x, uin
         for (uint32_t k = 1; k < (blockDim.x >> 6); ++k)
             if (am_better(sv[k], si[k], sv[0], si[0])) { sv[0] = sv[k]; si[0] = si[k]; }
         parts[blockIdx.x] = {sv[0], si[0]};
-        __threadfence();
-        last = atomicAdd(ticket, 1u) == gridDim.x - 1u;
-        if (last) __threadfence();
     }
-    __syncthreads();
-    if (!last) return;
-    bv = -INFINITY;
-    bi = 0xffffffffu;
-    for (uint32_t k = threadIdx.x; k < gridDim.x; k += blockDim.x) {
+}
+
+__global__ void __launch_bounds__(256) k_argmax_final(const AmPartial* parts, uint32_t nparts, vrt_argmax_result* out) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t k = threadIdx.x; k < nparts; k += blockDim.x) {
         const AmPartial p = parts[k];
         if (am_better(p.value, p.index, bv, bi)) { bv = p.value; bi = p.index; }
     }
     wave_argmax(bv, bi);
+    const uint32_t w = threadIdx.x >> 6;
     if ((threadIdx.x & 63u) == 0u) { sv[w] = bv; si[w] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -269,7 +269,6 @@ __global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ x, uin
             if (am_better(sv[k], si[k], sv[0], si[0])) { sv[0] = sv[k]; si[0] = si[k]; }
         out->index = si[0];
         out->value = sv[0];
-        *ticket = 0u;
     }
 }
 
@@ -624,8 +623,8 @@ extern "C" int vrt_argmax(vrt_ctx* ctx, const float* x, uint32_t n, vrt_argmax_r
     VRT_REQUIRE(n != 0, "ArgmaxPipeline requires non-zero input");  // src/argmax.cpp:507-511
     const uint32_t grid = std::min<uint32_t>((n + 2047u) / 2048u, 1024u);
     auto* parts = reinterpret_cast<AmPartial*>(static_cast<char*>(ctx->scratch) + 256);
-    auto* ticket = static_cast<uint32_t*>(ctx->scratch);
-    hipLaunchKernelGGL(k_argmax, dim3(grid), dim3(256), 0, ctx->stream, x, n, parts, ticket, out);
+    hipLaunchKernelGGL(k_argmax, dim3(grid), dim3(256), 0, ctx->stream, x, n, parts);
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, ctx->stream, parts, grid, out);
     VRT_HIP_CHECK(hipGetLastError());
     return VRT_OK;
 }
