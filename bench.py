@@ -33,7 +33,7 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "decode tokens/s + achieved HBM GB/s (% of roofline), Gemma3-270M-shape Q8_0, 1 GPU"
 
 
-def step_bytes(cfg, pos: int) -> int:
+def step_bytes(cfg, pos: int, kv_bytes: int = 4) -> int:
     d, H, hd, F, V, L = (cfg.embedding_length, cfg.head_count, cfg.head_dim, cfg.feed_forward_length,
                          cfg.vocab_size, cfg.block_count)
     q8 = lambda rows, k: rows * (k // 32) * 34
@@ -43,7 +43,7 @@ def step_bytes(cfg, pos: int) -> int:
     for l in range(L):
         glob = (l + 1) % 6 == 0
         slots = cfg.context_length if (glob or cfg.sliding_window == 0) else cfg.sliding_window
-        total += min(pos + 1, slots) * hd * 4 * 2
+        total += min(pos + 1, slots) * hd * kv_bytes * 2
     return total
 
 
@@ -88,9 +88,16 @@ def phase_split(g, prompt, cfg, steps: int = 24):
     return {k: round(v, 2) for k, v in out.items()}
 
 
-def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256):
+def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256, kv_f16: bool = False):
     """The long-context workload: an n_prompt-token prompt of uniform ids (seed 1) prefilled
-    untimed, then `steps` greedy decode steps timed with events (positions n_prompt..)."""
+    untimed, then `steps` greedy decode steps timed with events (positions n_prompt..). With
+    kv_f16 the executor's KV cache holds fp16 entries (2 bytes per element)."""
+    if kv_f16:
+        g.set_kv_f16(True)
+        try:
+            return long_context(ctx, g, cfg, n_prompt, steps)
+        finally:
+            g.set_kv_f16(False)
     prompt = synth_ids(1, n_prompt, cfg.vocab_size)
     g.start(prompt, steps + 1)
     g.step(n_prompt)
@@ -104,7 +111,8 @@ def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256):
     toks = g.collect()
     if toks.size < steps + 1:
         raise SystemExit(f"[bench] long context: EOS after {toks.size} generated tokens; the timed steps did not all run")
-    total = sum(step_bytes(cfg, n_prompt + i) for i in range(steps))
+    kvb = 2 if g.kv_f16 else 4
+    total = sum(step_bytes(cfg, n_prompt + i, kvb) for i in range(steps))
     gbps = total / (ms / 1e3) / 1e9
     return {"workload": f"{n_prompt}-token prompt (untimed prefill), {steps} timed greedy decode steps at positions "
                         f"{n_prompt}..{n_prompt + steps - 1}",
@@ -350,6 +358,7 @@ def main():
     traffic, traffic_src = load_traffic(args.steps)
     phases = None if args.no_phases else phase_split(g, prompt, cfg)
     longctx = None if args.no_long else long_context(ctx, g, cfg)
+    longctx16 = None if args.no_long else long_context(ctx, g, cfg, kv_f16=True)
     prefill = None if args.no_prefill else prefill_bench(ctx, g, cfg)
     kernels = None if args.no_kernels else kernel_legs(ctx)
     multikernel = multikernel_leg(ctx, g, prompt) if args.multikernel else None
@@ -392,6 +401,7 @@ def main():
         },
         "phase_us_per_step": phases,
         "long_context": longctx,
+        "long_context_kv_f16": longctx16,
         "prefill": prefill,
         "kernels": kernels,
         "multikernel": multikernel,

@@ -239,6 +239,12 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
 #define VRT_G3_OPT_PERSISTENT 2
 #define VRT_G3_OPT_QUERY_PERSISTENT 3
 #define VRT_G3_OPT_TRACE 4          /* 1: timestamp the phases of the first step of each launch */
+/* 1: the KV cache holds fp16 keys and values (IEEE round to nearest even of the fp32 k and v
+ * after QK-norm and RoPE; every position's attention, the current one's included, uses the
+ * rounded values), 2 bytes per element instead of 4. Switching resets the cache. The
+ * reference's README lists an fp16/bf16 KV cache as its next residency step
+ * (README.md:190-192); it has no implementation to follow. */
+#define VRT_G3_OPT_KV_F16 5
 
 /* Phase trace of the last persistent launch (tracing tool; no reference counterpart, which
  * only has CLI wall timers, src/gemma_main.cpp:194-232): out[w * slots + k] is the

@@ -45,6 +45,8 @@ def lib(path: str | None = None):
         sig = {
             "or_f32_to_f16": (C.c_uint16, [F]),
             "or_f16_to_f32": (F, [C.c_uint16]),
+            "or_f32_to_f16_rne": (C.c_uint16, [F]),
+            "or_f32_to_f16_rne_n": (None, [P, U64, P]),
             "or_q8_quantize_a": (None, [P, U64, U32, P]),
             "or_q8_quantize_b": (None, [P, U64, U32, P]),
             "or_q8_dequant": (None, [P, U64, P]),
@@ -67,6 +69,7 @@ def lib(path: str | None = None):
             "or_g3_decode": (I, [P, U32, U32, I, P, P, P, P]),
             "or_g3_generate": (I, [P, P, U32, U32, P, P]),
             "or_g3_error": (C.c_char_p, [P]),
+            "or_g3_set_kv_f16": (None, [P, I]),
             "or_num_threads": (I, []),
         }
         for name, (res, args) in sig.items():
@@ -83,6 +86,14 @@ def _p(a):
 
 def f32_to_f16(x: float) -> int:
     return int(lib().or_f32_to_f16(C.c_float(x)))
+
+
+def f32_to_f16_rne(x: np.ndarray) -> np.ndarray:
+    """IEEE binary16 bits of float32 values, round to nearest even (the fp16 KV rounding)."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().or_f32_to_f16_rne_n(_p(a), a.size, _p(out))
+    return out
 
 
 def f16_to_f32(h: int) -> float:
@@ -192,12 +203,14 @@ def attention(q, keys, values, heads, head_dim, scale):
 class Model:
     """The whole-model oracle (src/gemma3.cpp executor restated) over a GGUF file."""
 
-    def __init__(self, path: str, lanes: int = 8, lib_path: str | None = None):
+    def __init__(self, path: str, lanes: int = 8, lib_path: str | None = None, kv_f16: bool = False):
         self.L = lib(lib_path)
         err = C.create_string_buffer(512)
         self.h = self.L.or_g3_open(str(path).encode(), lanes, err, 512)
         if not self.h:
             raise RuntimeError(err.value.decode())
+        if kv_f16:
+            self.L.or_g3_set_kv_f16(self.h, 1)
         info = G3Info()
         self.L.or_g3_get_info(self.h, C.byref(info))
         self.info = info

@@ -46,6 +46,32 @@ uint16_t or_f32_to_f16(float f) {
 }
 
 /* src/gguf.cpp:203-235 (identical to src/q8_test_main.cpp:43-74): exact half -> float. */
+uint16_t or_f32_to_f16_rne(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u)); /* NaN, inf */
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   /* >= 65520 rounds past 65504 */
+    const uint32_t e = ax >> 23;
+    if (e < 113u) {   /* below 2^-14: a multiple of 2^-24 (subnormal half) or zero */
+        const uint32_t shift = 126u - e;   /* value = m 2^(e - 150) = (m >> shift) 2^-24 + rest */
+        if (shift > 24u) return (uint16_t)sign;
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u), halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((e - 112u) << 10) | ((ax >> 13) & 0x3ffu);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;   /* a carry moves into the exponent */
+    return (uint16_t)(sign | h);
+}
+
+void or_f32_to_f16_rne_n(const float* x, uint64_t n, uint16_t* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = or_f32_to_f16_rne(x[i]);
+}
+
 float or_f16_to_f32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
     uint32_t exponent = (h >> 10) & 31u;
@@ -397,6 +423,7 @@ struct or_g3 {
     float *inv_local, *inv_global;
     uint32_t next_pos;
     uint32_t lanes;
+    int kv_f16;
     char err[256];
 };
 
@@ -508,6 +535,7 @@ or_g3* or_g3_open(const char* path, uint32_t lanes, char* err, size_t errlen) {
         m->info.vocab_size = (uint32_t)emb->dims[1];
         m->token_embd = emb->offset;
         if (m->info.head_count_kv != 1 || m->info.value_dim != m->info.head_dim) { set_err(err, errlen, "Current Gemma 3 decoder requires one KV head and equal key/value head dimensions"); goto fail; }
+        if (m->info.head_dim > 512u) { set_err(err, errlen, "oracle: head_dim above 512 is not supported"); goto fail; }
         const tinfo_t* on = TFIND("output_norm.weight");
         if (!on || on->type != 0) { set_err(err, errlen, "Missing Gemma 3 tensor: output_norm.weight"); goto fail; }
         m->output_norm = (const float*)(m->data + on->offset);
@@ -574,8 +602,24 @@ void or_g3_reset(or_g3* m) {
     m->next_pos = 0;
 }
 
+void or_g3_set_kv_f16(or_g3* m, int on) {
+    m->kv_f16 = on != 0;
+    or_g3_reset(m);
+}
+
 /* push_back then pop_front while size > window (src/gemma3.cpp:1590-1600). */
-static int kv_push(or_layer_t* L, const float* k, const float* v, uint32_t hd) {
+static int kv_push(or_layer_t* L, const float* k_in, const float* v_in, uint32_t hd, int kv_f16) {
+    float kr[512], vr[512];   /* hd <= 512 (checked at open) */
+    const float* k = k_in;
+    const float* v = v_in;
+    if (kv_f16) {   /* the fp16 cache holds the rounded values */
+        for (uint32_t i = 0; i < hd; ++i) {
+            kr[i] = or_f16_to_f32(or_f32_to_f16_rne(k_in[i]));
+            vr[i] = or_f16_to_f32(or_f32_to_f16_rne(v_in[i]));
+        }
+        k = kr;
+        v = vr;
+    }
     if (L->cap) {
         if (!L->keys) {
             L->keys = (float*)malloc(sizeof(float) * (size_t)L->cap * hd);
@@ -644,7 +688,7 @@ static int decode_impl(or_g3* m, uint32_t token, uint32_t pos, int want_logits,
         or_rms_norm_heads(k, L->k_norm, 1, hd, eps);
         or_apply_rope(q, H, hd, L->global ? gc : lc, L->global ? gs : ls);
         or_apply_rope(k, 1, hd, L->global ? gc : lc, L->global ? gs : ls);
-        if (kv_push(L, k, v, hd)) { set_err(m->err, sizeof m->err, "out of memory"); rc = -3; goto done; }
+        if (kv_push(L, k, v, hd, m->kv_f16)) { set_err(m->err, sizeof m->err, "out of memory"); rc = -3; goto done; }
         const uint32_t hist = L->count;
         const float *K = L->keys, *V = L->vals;
         if (L->cap && L->start) { /* gather the ring in time order */

@@ -42,6 +42,11 @@ extern "C" {
 /* ---- fp16 codec (quantiser of record) ---- */
 uint16_t or_f32_to_f16(float f);                 /* src/q8_test_main.cpp:18-41 */
 float or_f16_to_f32(uint16_t h);                 /* src/gguf.cpp:203-235 */
+/* IEEE 754 binary16 conversion with round to nearest, ties to even (subnormals, overflow to
+ * infinity, quiet NaN): the rounding of the fp16 KV cache option, which the reference lists as
+ * a roadmap item (README.md:190-192) without an implementation. Bulk form for the pins. */
+uint16_t or_f32_to_f16_rne(float f);
+void or_f32_to_f16_rne_n(const float* x, uint64_t n, uint16_t* out);
 
 /* ---- Q8_0 quantisers: 34-byte blocks {f16 scale LE, int8 q[32]} along k ---- */
 /* Variant A, src/q8_test_main.cpp:93-124: q = nearbyint(v / (amax/127)), fp32 scale. */
@@ -108,6 +113,9 @@ int or_g3_decode(or_g3* m, uint32_t token, uint32_t pos, int want_logits,
 int or_g3_generate(or_g3* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
                    uint32_t* out_tokens, uint32_t* n_out);
 const char* or_g3_error(const or_g3* m);
+/* fp16 KV cache: keys and values are rounded with or_f32_to_f16_rne when they enter the cache
+ * (every position's attention, the current one's included, reads the cache). Resets the cache. */
+void or_g3_set_kv_f16(or_g3* m, int on);
 /* Threads used by the OpenMP loops (matvec rows). */
 int or_num_threads(void);
 

@@ -75,6 +75,29 @@ def test_f16_encode_against_ieee_model():
     assert oracle.f16_to_f32(oracle.f32_to_f16(odd)) == 4.0
 
 
+def test_f16_rne_against_numpy():
+    """or_f32_to_f16_rne (the fp16 KV rounding) against numpy's float32 -> float16 cast, an
+    independent IEEE round-to-nearest-even implementation: every half value, every midpoint
+    between neighbouring halves (ties) and its float32 neighbours, the subnormal and overflow
+    boundaries, signed zeros, infinities, and 4M random bit patterns."""
+    halves = np.arange(0, 0x7c00, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    mids = (halves[:-1].astype(np.float64) + halves[1:].astype(np.float64)) / 2.0
+    mids = mids.astype(np.float32)   # exact: two neighbouring halves differ in 11 significant bits
+    near = np.concatenate([np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))])
+    edges = np.array([0.0, 2.0 ** -25, 2.0 ** -24, 1.5 * 2.0 ** -25, 2.0 ** -14, 65504.0, 65519.996, 65520.0,
+                      65536.0, 1e30, np.inf, 2.0 ** -26, 3e-8], dtype=np.float32)
+    rng = np.random.default_rng(11)
+    rand = rng.integers(0, 2 ** 32, size=1 << 22, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([halves, mids, near, edges, rand])
+    x = np.concatenate([x, -x])
+    got = oracle.f32_to_f16_rne(x)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all((got[nan] & 0x7c00) == 0x7c00) and np.all((got[nan] & 0x3ff) != 0)
+
+
 def test_f16_encode_golden():
     """Hand-derived codes (ties, carries, subnormals, overflow) kept in tests/golden."""
     import json

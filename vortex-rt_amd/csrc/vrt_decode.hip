@@ -40,6 +40,7 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #include "vrt_g3_errors.hpp"
@@ -112,6 +113,7 @@ struct MkParams {
     uint32_t lm_rows;              // LM-head rows per workgroup
     uint32_t lm_tile_rows;         // rows per LDS tile
     uint32_t trace_slots;          // phase timestamps per workgroup (0: tracing off)
+    uint32_t kv_f16;               // KV cache entries as fp16 (2 bytes)
     MkLds lds;
     const uint8_t* tok_embd;
     const uint8_t* arena_end;
@@ -636,6 +638,7 @@ constexpr uint32_t kBLongChunk = 128;              // chunks at least this long 
 // Publishes the unnormalised partial {acc[hd] of head h, m, l} of (c, h).
 // Inlined into the kernel: as a call it would save and restore callee-saved registers through
 // scratch.
+template <bool KVH>
 __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
@@ -667,25 +670,38 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     int fail = 0;
     if (worker) {
         // this wave's K/V rows of the first group, from the cache (device-coherent)
-        const uint32_t kv_bytes = Ly.slots * hd * 4u;
+        constexpr uint32_t esz = KVH ? 2u : 4u;   // fp16 entries: 8 bytes per lane and position
+        const uint32_t kv_bytes = Ly.slots * hd * esz;
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
         // cached positions [c0, cend); the current position itself comes from registers
         const uint32_t cend = c1 == pos + 1u ? pos : c1;
         // byte offset of this lane's dims of position t (past the buffer for dead lanes: no access)
-        auto kv_off = [&](uint32_t t) { return dlive ? static_cast<int>(((t % Ly.slots) * hd + dl) * 4u) : 0x7ffffff0; };
+        auto kv_off = [&](uint32_t t) { return dlive ? static_cast<int>(((t % Ly.slots) * hd + dl) * esz) : 0x7ffffff0; };
+        // this lane's four dims of a cached position, as loaded (fp32 bits, or four fp16 halves
+        // that are converted where they are used, so the prefetch of the next group does not wait)
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        using KvReg = typename std::conditional<KVH, v2u, v4u>::type;
+        auto kv_ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t t) -> KvReg {
+            if constexpr (KVH) return __builtin_amdgcn_raw_buffer_load_b64(r, kv_off(t), 0, kCoherent);
+            else return co_ld4(r, kv_off(t));
+        };
+        auto kv_el = [](const KvReg& x, uint32_t e) -> float {
+            if constexpr (KVH) return static_cast<float>(__builtin_bit_cast(half4_t, x)[e]);
+            else return __uint_as_float(x[e]);
+        };
         // how many of this wave's positions g0 + uw + nbw i fall below g1 (wave-uniform)
         auto nvalid = [&](uint32_t g0, uint32_t g1) { return g1 > g0 + uw ? (g1 - g0 - uw + nbw - 1u) / nbw : 0u; };
-        v4u kr[kBPos], vr[kBPos];
+        KvReg kr[kBPos], vr[kBPos];
         {
             const uint32_t nv = nvalid(c0, min(cend, c0 + grp));
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i) {
-                kr[i] = vr[i] = v4u{0u, 0u, 0u, 0u};
+                kr[i] = vr[i] = KvReg{};
                 if (i < nv) {
                     const uint32_t t = c0 + uw + nbw * i;
-                    kr[i] = co_ld4(rk, kv_off(t));
-                    vr[i] = co_ld4(rv, kv_off(t));
+                    kr[i] = kv_ld(rk, t);
+                    vr[i] = kv_ld(rv, t);
                 }
             }
         }
@@ -748,6 +764,13 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             q[e] = lo ? q[e] * cs[e] - qo[e] * sn[e] : q[e] * cs[e] + qo[e] * sn[e];
             k[e] = lo ? k[e] * cs[e] - ko[e] * sn[e] : k[e] * cs[e] + ko[e] * sn[e];
         }
+        if constexpr (KVH) {   // the current position's key and value as the cache will hold them
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) {
+                k[e] = static_cast<float>(static_cast<_Float16>(k[e]));
+                v[e] = static_cast<float>(static_cast<_Float16>(v[e]));
+            }
+        }
         MK_MARK(8);
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         float m_run = -INFINITY, l_run = 0.0f;
@@ -761,7 +784,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             for (uint32_t i = 0; i < kBPos; ++i) {
                 float p = 0.0f;
 #pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) p += q[e] * __uint_as_float(kr[i][e]);
+                for (uint32_t e = 0; e < 4u; ++e) p += q[e] * kv_el(kr[i], e);
                 part[i] = p;
             }
             // lane l: the score of position g0 + uw + nbw (l & 7). The reduction runs in every
@@ -773,7 +796,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             const uint32_t nn = n0 < cend ? nvalid(n0, min(cend, n0 + grp)) : 0u;
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i)
-                if (i < nn) kr[i] = co_ld4(rk, kv_off(n0 + uw + nbw * i));
+                if (i < nn) kr[i] = kv_ld(rk, n0 + uw + nbw * i);
             if (nv != 0u) {   // this wave has a position in the group
                 float mx = fmaxf(sl, dpp_mov<0xB1>(sl));
                 mx = fmaxf(mx, dpp_mov<0x4E>(mx));
@@ -794,7 +817,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                     for (uint32_t e = 0; e < 4u; ++e) {
                         float a = acc[e] * r;
 #pragma unroll
-                        for (uint32_t i = 0; i < kBPos; ++i) a += pw[i] * __uint_as_float(vr[i][e]);
+                        for (uint32_t i = 0; i < kBPos; ++i) a += pw[i] * kv_el(vr[i], e);
                         acc[e] = a;
                     }
                     l_run = l_run * r + ls;
@@ -803,7 +826,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             }
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i)
-                if (i < nn) vr[i] = co_ld4(rv, kv_off(n0 + uw + nbw * i));
+                if (i < nn) vr[i] = kv_ld(rv, n0 + uw + nbw * i);
         }
         // the current position, from registers, by the wave whose turn it is
         if (c1 == pos + 1u && uw == (pos - c0) % nbw) {
@@ -830,13 +853,24 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         // memory operations complete in issue order), so no wait is needed here.
         const bool appender = h == 0u && c1 == pos + 1u && uw == 0u;
         if (appender && dlive && !fail) {
-            const uint32_t so = ((pos % Ly.slots) * hd + dl) * 4u;
-            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(k[0]), __float_as_uint(k[1]),
-                                                       __float_as_uint(k[2]), __float_as_uint(k[3])},
-                                                   rk, static_cast<int>(so), 0, kCoherent);
-            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]),
-                                                       __float_as_uint(v[2]), __float_as_uint(v[3])},
-                                                   rv, static_cast<int>(so), 0, kCoherent);
+            const uint32_t so = ((pos % Ly.slots) * hd + dl) * esz;
+            if constexpr (KVH) {   // k and v are already fp16 values: the conversion is exact
+                auto pack = [](float a, float b) {
+                    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+                };
+                __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(k[0], k[1]), pack(k[2], k[3])}, rk, static_cast<int>(so), 0,
+                                                      kCoherent);
+                __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(v[0], v[1]), pack(v[2], v[3])}, rv, static_cast<int>(so), 0,
+                                                      kCoherent);
+            } else {
+                __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(k[0]), __float_as_uint(k[1]),
+                                                           __float_as_uint(k[2]), __float_as_uint(k[3])},
+                                                       rk, static_cast<int>(so), 0, kCoherent);
+                __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                           __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                                       rv, static_cast<int>(so), 0, kCoherent);
+            }
         }
         if (dlive) *reinterpret_cast<float4*>(ra + uw * hd + dl) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         if (lane == 0) {
@@ -1219,7 +1253,7 @@ __device__ __attribute__((noinline)) void mk_embed(uint32_t token) {
     __syncthreads();   // the next residual fold reads h before its first barrier
 }
 
-template <int SD, int SA, int SF, int EP>
+template <int SD, int SA, int SF, int EP, bool KVH>
 __global__ void __launch_bounds__(kMkThreads, 1)
 k_decode(uint32_t nsteps, uint32_t tag0) {
     const uint32_t w = blockIdx.x;
@@ -1284,7 +1318,7 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             MK_TRACE(5u * l + 1u);
             // B, C and E run on a subset of the workgroups; the others skip the call (and its
             // register save/restore through scratch) entirely
-            ok = ok && (!mk_in_b(l, s) || mk_phase_b(l, s, tagb, tr));
+            ok = ok && (!mk_in_b(l, s) || mk_phase_b<KVH>(l, s, tagb, tr));
             MK_TRACE(5u * l + 2u);
             ok = ok && (w >= g_mk.nc || mk_phase_c<SA>(l, s, tagb, tr));
             MK_TRACE(5u * l + 3u);
@@ -1340,11 +1374,16 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
 // Host side
 // =============================================================================================
 
+struct MkFns {
+    const void* f32 = nullptr;
+    const void* f16 = nullptr;
+};
+
 struct MkState {
     MkParams P{};
     std::vector<MkLayer> layers;   // host image of g_mk_layers
     uint64_t version = 1;          // bumped whenever P changes
-    const void* fn = nullptr;
+    MkFns fns{};                   // k_decode for fp32 and fp16 KV entries
     size_t lds_bytes = 0;
     uint32_t grid = 0;
     uint32_t trace_slots = 0;      // slots per workgroup when tracing is enabled
@@ -1373,11 +1412,14 @@ static MkDeviceSlot* device_slots() {
 }
 
 template <int SD, int SA, int SF, int EP>
-static const void* mk_fn() { return reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP>); }
+static MkFns mk_fn() {
+    return MkFns{reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP, false>),
+                 reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP, true>)};
+}
 
 // Row-slot widths of the three matvec input lengths (d, H * head_dim, FFN) and the residual
 // pairs per lane, ep = ceil(d / 128); the smallest instantiated EP >= ep is taken.
-static const void* mk_pick(int sd, int sa, int sf, int ep) {
+static MkFns mk_pick(int sd, int sa, int sf, int ep) {
 #define VRT_MK(a, b, c, e) if (sd == a && sa == b && sf == c && ep <= e) return mk_fn<a, b, c, e>();
     VRT_MK(32, 32, 64, 5)   // Gemma-3-270M: d 640, 4 x 256 heads, FFN 2048
     VRT_MK(32, 32, 64, 8)
@@ -1387,7 +1429,7 @@ static const void* mk_pick(int sd, int sa, int sf, int ep) {
     VRT_MK(16, 16, 32, 4)
     VRT_MK(8, 8, 16, 2)
 #undef VRT_MK
-    return nullptr;
+    return MkFns{};
 }
 
 static int mk_alloc(MkState* mk, size_t bytes, void** out) {
@@ -1433,8 +1475,8 @@ int mk_setup(vrt_g3* g) {
         return VRT_OK;
     MvShape sd, sa, sf;
     if (!mv_shape(d, &sd) || !mv_shape(qw, &sa) || !mv_shape(F, &sf) || sd.NB != 1 || sa.NB != 1 || sf.NB != 1) return VRT_OK;
-    const void* fn = mk_pick(sd.S, sa.S, sf.S, static_cast<int>((d + 127u) / 128u));
-    if (!fn) return VRT_OK;
+    const MkFns fns = mk_pick(sd.S, sa.S, sf.S, static_cast<int>((d + 127u) / 128u));
+    if (!fns.f32) return VRT_OK;
     int coop = 0;
     VRT_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, g->ctx->device));
     if (!coop) return VRT_OK;
@@ -1544,10 +1586,12 @@ int mk_setup(vrt_g3* g) {
     P.logits = g->P.logits;
     P.hidden = g->P.hidden;
 
-    int per_cu = 0;
-    VRT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kMkThreads, 0));
-    if (per_cu < 1) { mk_destroy(g); return VRT_OK; }
-    mk->fn = fn;
+    for (const void* fn : {fns.f32, fns.f16}) {   // both KV element types must fit a CU
+        int per_cu = 0;
+        VRT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kMkThreads, 0));
+        if (per_cu < 1) { mk_destroy(g); return VRT_OK; }
+    }
+    mk->fns = fns;
     mk->grid = nwg;
     g->mk_tag = 1u;
     {
@@ -1562,6 +1606,13 @@ int mk_setup(vrt_g3* g) {
 int mk_set_trace(vrt_g3* g, bool on) {
     VRT_REQUIRE(g->mk, "persistent decode kernel unavailable");
     g->mk->P.trace_slots = on ? g->mk->trace_slots : 0u;
+    ++g->mk->version;
+    return VRT_OK;
+}
+
+int mk_set_kv_f16(vrt_g3* g, bool on) {
+    if (!g->mk) return VRT_OK;
+    g->mk->P.kv_f16 = on ? 1u : 0u;
     ++g->mk->version;
     return VRT_OK;
 }
@@ -1643,7 +1694,8 @@ int mk_run(vrt_g3* g, uint32_t nsteps) {
         ds.version = mk->version;
     }
     void* args[] = {&nsteps, &tag0};
-    VRT_HIP_CHECK(hipLaunchCooperativeKernel(mk->fn, dim3(mk->grid), dim3(kMkThreads), args, 0, stream));
+    VRT_HIP_CHECK(hipLaunchCooperativeKernel(mk->P.kv_f16 ? mk->fns.f16 : mk->fns.f32, dim3(mk->grid), dim3(kMkThreads),
+                                             args, 0, stream));
     if (!ds.last) VRT_HIP_CHECK(hipEventCreateWithFlags(&ds.last, hipEventDisableTiming));
     VRT_HIP_CHECK(hipEventRecord(ds.last, stream));
     ds.last_stream = stream;

@@ -30,7 +30,7 @@ struct LmPartial {
 struct G3Params {
     uint32_t d, H, hd, F, V, L, ctx_len, eos;
     float eps, emb_scale, attn_scale;
-    uint32_t pad0;
+    uint32_t kv_f16;      // KV cache entries as fp16 (VRT_G3_OPT_KV_F16)
     const uint8_t* arena_end;
     const uint8_t* tok_embd;
     G3State* st;
@@ -56,7 +56,7 @@ struct G3Params {
 struct LayerParams {
     const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
     const float *attn_norm, *q_norm, *k_norm, *post_attn, *ffn_norm, *post_ffw;
-    float* kc;
+    float* kc;            // [slots][hd] fp32, or fp16 in the first half of the buffer (kv_f16)
     float* vc;
     uint32_t slots;       // KV slots: window for local layers, context_length otherwise
     uint32_t global;
@@ -142,6 +142,7 @@ int mk_clear_abort(vrt_g3* g);
 int mk_read_abort(vrt_g3* g, uint32_t* dst);
 int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int mk_set_trace(vrt_g3* g, bool on);
+int mk_set_kv_f16(vrt_g3* g, bool on);
 // Batched prefill (vrt_prefill.hip): workspace for up to max_t positions, and one prefill of T
 // positions from position 0 whose last position runs g3_enqueue_lm.
 int pf_setup(vrt_g3* g, uint32_t max_t);

@@ -236,12 +236,28 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
         }
         __syncthreads();
     }
+    // fp16 KV: the current position's key and value as the cache will hold them
+    if (P.kv_f16) {
+        for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
+            sk[i] = static_cast<float>(static_cast<_Float16>(sk[i]));
+            sv[i] = static_cast<float>(static_cast<_Float16>(sv[i]));
+        }
+        __syncthreads();
+    }
     // KV append (slot of this position); the current position is read from LDS below
     const uint32_t slot_cur = pos % Lc.slots;
+    _Float16* kh = reinterpret_cast<_Float16*>(Lc.kc);
+    _Float16* vh = reinterpret_cast<_Float16*>(Lc.vc);
     if (blockIdx.x == 0)
         for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
-            Lc.kc[static_cast<uint64_t>(slot_cur) * hd + i] = sk[i];
-            Lc.vc[static_cast<uint64_t>(slot_cur) * hd + i] = sv[i];
+            const uint64_t o = static_cast<uint64_t>(slot_cur) * hd + i;
+            if (P.kv_f16) {
+                kh[o] = static_cast<_Float16>(sk[i]);
+                vh[o] = static_cast<_Float16>(sv[i]);
+            } else {
+                Lc.kc[o] = sk[i];
+                Lc.vc[o] = sv[i];
+            }
         }
 
     const uint32_t stride_part = 2u * H + H * hd;
@@ -250,10 +266,13 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
         // scores: wave w takes positions c0 + w, c0 + w + 4, ...; lane l covers dims l, l+64, ...
         const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
         for (uint32_t t = c0 + wave; t < c1; t += blockDim.x >> 6) {
-            const float* kt = (t == pos) ? sk : Lc.kc + static_cast<uint64_t>(t % Lc.slots) * hd;
+            const uint64_t row = static_cast<uint64_t>(t % Lc.slots) * hd;
             float kr[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) kr[j] = (lane + 64u * j < hd) ? kt[lane + 64u * j] : 0.0f;
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = lane + 64u * j;
+                kr[j] = i >= hd ? 0.0f : (t == pos ? sk[i] : (P.kv_f16 ? static_cast<float>(kh[row + i]) : Lc.kc[row + i]));
+            }
             for (uint32_t h = 0; h < H; ++h) {
                 float p = 0.0f;
 #pragma unroll
@@ -284,7 +303,8 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
         for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
             float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             for (uint32_t t = c0; t < c1; ++t) {
-                const float vv = (t == pos) ? sv[i] : Lc.vc[static_cast<uint64_t>(t % Lc.slots) * hd + i];
+                const uint64_t vo = static_cast<uint64_t>(t % Lc.slots) * hd + i;
+                const float vv = (t == pos) ? sv[i] : (P.kv_f16 ? static_cast<float>(vh[vo]) : Lc.vc[vo]);
 #pragma unroll
                 for (uint32_t h = 0; h < 8u; ++h)
                     if (h < H) acc[h] += sc[h * Lc.chunk_max + (t - c0)] * vv;
@@ -953,6 +973,20 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
     case VRT_G3_OPT_PERSISTENT: g->use_persistent = value != 0; return VRT_OK;
     case VRT_G3_OPT_QUERY_PERSISTENT: return g->mk ? VRT_OK : set_error(VRT_ERR_STATE, "persistent decode kernel unavailable");
     case VRT_G3_OPT_TRACE: return mk_set_trace(g, value != 0);
+    case VRT_G3_OPT_KV_F16: {
+        // the kernels read the flag from their parameter blocks: the captured graph (which holds
+        // G3Params by value) is dropped, the persistent kernel's block re-uploaded, the cache reset
+        const uint32_t on = value != 0 ? 1u : 0u;
+        if (g->P.kv_f16 == on) return VRT_OK;
+        VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+        g->P.kv_f16 = on;
+        if (g->graph) {
+            (void)hipGraphExecDestroy(g->graph);
+            g->graph = nullptr;
+        }
+        if (int rc = mk_set_kv_f16(g, on != 0)) return rc;
+        return vrt_g3_reset(g);
+    }
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
     }
 }

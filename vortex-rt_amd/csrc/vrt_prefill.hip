@@ -448,8 +448,10 @@ __device__ __forceinline__ uint64_t pf_vswz(uint32_t t, uint32_t d, uint32_t hd)
 // Row t of qkv = [q (H heads x hd) | k (hd) | v (hd)]: QK-norm per head (src/gemma3.cpp:
 // 1045-1104), NeoX RoPE at position t (:1371-1424), in place (q also as f16 hi/lo rows of
 // qhi/qlo); then k and v go to the KV cache slot t % slots when position t is still in the
-// window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600). The
-// attention operands as f16 hi/lo: k and v in the pf_kswz / pf_vswz tile layouts. One
+// window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600); with
+// kv_f16 the cache holds fp16 and k and v are rounded to fp16 first (the attention below then
+// sees the cached values, as the serial loop does). The attention operands as f16 hi/lo: k and
+// v in the pf_kswz / pf_vswz tile layouts. One
 // workgroup per position t < Tp: those with t >= T write the zero padding keys and values
 // (keys past the prompt are masked, and zero values keep the masked products zero).
 // One wave per head (lane l: dims l + 64 e): the sum of squares is a wave reduction and the
@@ -460,7 +462,7 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
                                                             const float* cos_t, const float* sin_t, float eps,
                                                             float* kc, float* vc, uint32_t slots, _Float16* qhi,
                                                             _Float16* qlo, _Float16* khi, _Float16* klo, _Float16* vhi,
-                                                            _Float16* vlo) {
+                                                            _Float16* vlo, uint32_t kv_f16) {
 #pragma clang fp contract(off)
     __shared__ float xs[kPfQkMaxWaves][256];
     const uint32_t t = blockIdx.x;
@@ -507,18 +509,26 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
                 if (hh < H) {   // the query, [T][H * hd]
                     const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
                     pf_split(y2, qhi + o, qlo + o);
-                } else {
+                } else {   // fp16 KV: the key as the cache holds it, for the cache and the attention
+                    const float kk = kv_f16 ? static_cast<float>(static_cast<_Float16>(y2)) : y2;
                     const uint64_t o = pf_kswz(t, i, hd);
-                    pf_split(y2, khi + o, klo + o);
-                    if (keep) kc[slot + i] = y2;
+                    pf_split(kk, khi + o, klo + o);
+                    if (keep) {
+                        if (kv_f16) reinterpret_cast<_Float16*>(kc)[slot + i] = static_cast<_Float16>(kk);
+                        else kc[slot + i] = kk;
+                    }
                 }
             }
         }
         __builtin_amdgcn_wave_barrier();   // this head's reads of xw come before the next head's writes
     }
     for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {   // v is not normed
-        const float vv = row[(H + 1u) * hd + i];
-        if (keep) vc[slot + i] = vv;
+        const float vr = row[(H + 1u) * hd + i];
+        const float vv = kv_f16 ? static_cast<float>(static_cast<_Float16>(vr)) : vr;
+        if (keep) {
+            if (kv_f16) reinterpret_cast<_Float16*>(vc)[slot + i] = static_cast<_Float16>(vv);
+            else vc[slot + i] = vv;
+        }
         const uint64_t o = pf_vswz(t, i, hd);
         pf_split(vv, vhi + o, vlo + o);
     }
@@ -1292,7 +1302,9 @@ int pf_run(vrt_g3* g, uint32_t T) {
             _Float16* klo = static_cast<_Float16*>(p.klo);
             _Float16* vhi = static_cast<_Float16*>(p.vhi);
             _Float16* vlo = static_cast<_Float16*>(p.vlo);
-            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &khi, &klo, &vhi, &vlo};
+            uint32_t kvf = P.kv_f16;
+            void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &khi, &klo, &vhi, &vlo,
+                            &kvf};
             const uint32_t waves = std::min(H + 1u, kPfQkMaxWaves);
             VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_qk), dim3(tp), dim3(64u * waves), args, 0, s));
         }

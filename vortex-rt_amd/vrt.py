@@ -20,6 +20,7 @@ OPT_USE_GRAPH = 1
 OPT_PERSISTENT = 2
 OPT_QUERY_PERSISTENT = 3
 OPT_TRACE = 4
+OPT_KV_F16 = 5
 
 
 class VrtError(RuntimeError):
@@ -346,6 +347,7 @@ class Gemma3:
         h = C.c_void_p()
         check(lib().vrt_g3_create(ctx.h, C.byref(desc), C.byref(h)))
         self.h = h.value
+        self.kv_f16 = False
         ctx._children.add(self)
         self._keep.clear()
 
@@ -369,6 +371,11 @@ class Gemma3:
 
     def set_trace(self, on: bool):
         check(lib().vrt_g3_set_option(self.h, OPT_TRACE, 1 if on else 0))
+
+    def set_kv_f16(self, on: bool):
+        """fp16 KV cache (keys and values rounded to fp16 as they enter it); resets the cache."""
+        check(lib().vrt_g3_set_option(self.h, OPT_KV_F16, 1 if on else 0))
+        self.kv_f16 = bool(on)
 
     def read_trace(self) -> np.ndarray:
         """[nwg, slots] s_memrealtime ticks (100 MHz) of the last persistent launch's first step."""
