@@ -54,16 +54,6 @@ __device__ __forceinline__ void pf_split4(f4 x, _Float16* hi, _Float16* lo) {
     *reinterpret_cast<half4*>(lo) = l;
 }
 
-// Workgroup double sum (fixed order: 4 waves, DPP inside each) behind one barrier. red[0..4)
-// belongs to this call: a second sum in the same kernel takes other slots, so no thread can
-// still be reading them when they are written.
-__device__ __forceinline__ double pf_sum(double v, double* red) {
-    v = wave_red_sum_d(v);
-    if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return red[0] + red[1] + red[2] + red[3];
-}
-
 // 1.0f / std::sqrt(float(sum_sq / n) + eps) (src/gemma3.cpp:967-983).
 __device__ __forceinline__ float pf_rms_scale(double ss, uint32_t n, float eps) {
 #pragma clang fp contract(off)
@@ -83,54 +73,67 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_embed(const uint8_t* tok_embd
     }
 }
 
-// One row t per workgroup (n <= 8 * kPfThreads). With f (the previous sublayer's output, the
-// sum of nsplit partial rows f + s * sstride added in order s = 0, 1, ...):
+// One wave per row t (four rows per workgroup, `rows` rows in all; n <= 64 NE elements, NE per
+// lane; the sums are wave reductions, with no barrier). With f (the previous sublayer's output,
+// the sum of nsplit partial rows f + s * sstride added in order s = 0, 1, ...):
 // h = f * (scale(f) * w_post) + h (rms_norm_inplace then add_inplace, src/gemma3.cpp:1036-1042,
 // :1703-1711, :1849-1855). Then, with w_next:
 // the GEMM input (h * scale(h)) * w_next as f16 hi/lo (:991-996). nonfinite: lowest block
 // whose residual went non-finite (:1857-1863), reported through st->nonfinite.
-__global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f, uint32_t nsplit, uint64_t sstride,
-                                                        const float* w_post, const float* w_next, uint32_t n, float eps,
-                                                        _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block) {
+template <uint32_t NE>
+__global__ void __launch_bounds__(kPfThreads) k_pf_norm_w(float* h, const float* f, uint32_t nsplit, uint64_t sstride,
+                                                          const float* w_post, const float* w_next, uint32_t n, float eps,
+                                                          _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block,
+                                                          uint32_t rows) {
 #pragma clang fp contract(off)
-    __shared__ double red[2][4];   // one set per sum
-    const uint32_t t = blockIdx.x;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = blockIdx.x * (kPfThreads / 64u) + (threadIdx.x >> 6);
+    if (t >= rows) return;   // whole wave
     float* hr = h + static_cast<uint64_t>(t) * n;
-    float hv[8];
+    // Every load is issued at a clamped, in-bounds index and masked afterwards, so the loads of
+    // a row are in flight together (no branch, hence no wait, between them).
+    uint32_t ic[NE];
+    bool live[NE];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t i = threadIdx.x + k * kPfThreads;
-        hv[k] = i < n ? hr[i] : 0.0f;
+    for (uint32_t k = 0; k < NE; ++k) {
+        live[k] = lane + 64u * k < n;
+        ic[k] = min(lane + 64u * k, n - 1u);
+    }
+    float hv[NE], wp[NE], wn[NE];
+#pragma unroll
+    for (uint32_t k = 0; k < NE; ++k) {
+        hv[k] = hr[ic[k]];
+        wp[k] = w_post ? w_post[ic[k]] : 0.0f;
+        wn[k] = w_next ? w_next[ic[k]] : 0.0f;
     }
     if (f) {
         const float* fr = f + static_cast<uint64_t>(t) * n;
-        // every partial is loaded before the first add (nsplit <= kPfMaxSplits), then the
-        // partials are added in split order
-        float fp[8][kPfMaxSplits];
+        // every partial is loaded before the first add, then the partials are added in split order
+        float fp[NE][kPfMaxSplits];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t i = threadIdx.x + k * kPfThreads;
+        for (uint32_t q = 0; q < kPfMaxSplits; ++q) {
+            const float* fq = fr + min(q, nsplit - 1u) * sstride;
 #pragma unroll
-            for (uint32_t q = 0; q < kPfMaxSplits; ++q) fp[k][q] = i < n && q < nsplit ? fr[q * sstride + i] : 0.0f;
+            for (uint32_t k = 0; k < NE; ++k) fp[k][q] = fq[ic[k]];
         }
-        float fv[8];
+        float fv[NE];
         double ss = 0.0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (uint32_t k = 0; k < NE; ++k) {
             fv[k] = 0.0f;
 #pragma unroll
             for (uint32_t q = 0; q < kPfMaxSplits; ++q)
                 if (q < nsplit) fv[k] += fp[k][q];
+            if (!live[k]) fv[k] = 0.0f;
             ss += static_cast<double>(fv[k]) * static_cast<double>(fv[k]);
         }
-        const float sc = pf_rms_scale(pf_sum(ss, red[0]), n, eps);
+        const float sc = pf_rms_scale(wave_red_sum_d(ss), n, eps);
         int bad = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t i = threadIdx.x + k * kPfThreads;
-            if (i < n) {
-                hv[k] = fv[k] * (sc * w_post[i]) + hv[k];
-                hr[i] = hv[k];
+        for (uint32_t k = 0; k < NE; ++k) {
+            hv[k] = fv[k] * (sc * wp[k]) + hv[k];
+            if (live[k]) {
+                hr[ic[k]] = hv[k];
                 bad |= !__builtin_isfinite(hv[k]);
             }
         }
@@ -139,12 +142,15 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm(float* h, const float* f
     if (!w_next) return;
     double ss = 0.0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) ss += static_cast<double>(hv[k]) * static_cast<double>(hv[k]);
-    const float sc = pf_rms_scale(pf_sum(ss, red[1]), n, eps);
+    for (uint32_t k = 0; k < NE; ++k) {
+        const float v = live[k] ? hv[k] : 0.0f;
+        ss += static_cast<double>(v) * static_cast<double>(v);
+    }
+    const float sc = pf_rms_scale(wave_red_sum_d(ss), n, eps);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t i = threadIdx.x + k * kPfThreads;
-        if (i < n) pf_split((hv[k] * sc) * w_next[i], xhi + static_cast<uint64_t>(t) * n + i, xlo + static_cast<uint64_t>(t) * n + i);
+    for (uint32_t k = 0; k < NE; ++k) {
+        const float y = (hv[k] * sc) * wn[k];
+        if (live[k]) pf_split(y, xhi + static_cast<uint64_t>(t) * n + ic[k], xlo + static_cast<uint64_t>(t) * n + ic[k]);
     }
 }
 
@@ -479,52 +485,70 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
     float* xw = xs[wave];
     const bool keep = t + slots >= T;
     const uint64_t slot = static_cast<uint64_t>(t % slots) * hd;
+    // Loads are issued at clamped, in-bounds indices and masked afterwards, so each group of
+    // them is in flight together (no branch, hence no wait, between them). v first: it is only
+    // stored, after the heads.
+    const uint32_t vi = min(threadIdx.x, hd - 1u);
+    const float vr = row[(H + 1u) * hd + vi];
+    uint32_t ic[4], ei[4];
+    bool live[4];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {
+        live[e] = lane + 64u * e < hd;
+        ic[e] = min(lane + 64u * e, hd - 1u);
+        ei[e] = ic[e] < half ? ic[e] : ic[e] - half;
+    }
+    float cs[4], sn[4];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {
+        cs[e] = cos_t[static_cast<uint64_t>(t) * half + ei[e]];
+        sn[e] = sin_t[static_cast<uint64_t>(t) * half + ei[e]];
+    }
     for (uint32_t hh = wave; hh <= H; hh += nw) {   // H query heads, then the key head
-        float* x = row + hh * hd;
+        const float* x = row + hh * hd;
         const float* w = hh < H ? q_norm : k_norm;
-        float v[4];
+        float v[4], wv[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            v[e] = x[ic[e]];
+            wv[e] = w[ic[e]];
+        }
         double sq = 0.0;
 #pragma unroll
         for (uint32_t e = 0; e < 4u; ++e) {
-            const uint32_t i = lane + 64u * e;
-            v[e] = i < hd ? x[i] : 0.0f;
+            if (!live[e]) v[e] = 0.0f;
             sq += static_cast<double>(v[e]) * static_cast<double>(v[e]);
         }
         const float sc = pf_rms_scale(wave_red_sum_d(sq), hd, eps);
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) {
-            const uint32_t i = lane + 64u * e;
-            if (i < hd) xw[i] = (v[e] * sc) * w[i];
-        }
+        for (uint32_t e = 0; e < 4u; ++e)
+            if (live[e]) xw[ic[e]] = (v[e] * sc) * wv[e];
         // the partners are other lanes' values: a wave's LDS accesses complete in order
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (uint32_t e = 0; e < 4u; ++e) {
-            const uint32_t i = lane + 64u * e;
-            if (i < hd) {
-                const uint32_t ei = i < half ? i : i - half;
-                const float c = cos_t[static_cast<uint64_t>(t) * half + ei], s = sin_t[static_cast<uint64_t>(t) * half + ei];
-                const float a = xw[ei], b = xw[ei + half];
-                const float y2 = i < half ? a * c - b * s : b * c + a * s;
-                if (hh < H) {   // the query, [T][H * hd]
-                    const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
-                    pf_split(y2, qhi + o, qlo + o);
-                } else {   // fp16 KV: the key as the cache holds it, for the cache and the attention
-                    const float kk = kv_f16 ? static_cast<float>(static_cast<_Float16>(y2)) : y2;
-                    const uint64_t o = pf_kswz(t, i, hd);
-                    pf_split(kk, khi + o, klo + o);
-                    if (keep) {
-                        if (kv_f16) reinterpret_cast<_Float16*>(kc)[slot + i] = static_cast<_Float16>(kk);
-                        else kc[slot + i] = kk;
-                    }
+            if (!live[e]) continue;
+            const uint32_t i = ic[e];
+            const float a = xw[ei[e]], b = xw[ei[e] + half];
+            const float y2 = i < half ? a * cs[e] - b * sn[e] : b * cs[e] + a * sn[e];
+            if (hh < H) {   // the query, [T][H * hd]
+                const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
+                pf_split(y2, qhi + o, qlo + o);
+            } else {   // fp16 KV: the key as the cache holds it, for the cache and the attention
+                const float kk = kv_f16 ? static_cast<float>(static_cast<_Float16>(y2)) : y2;
+                const uint64_t o = pf_kswz(t, i, hd);
+                pf_split(kk, khi + o, klo + o);
+                if (keep) {
+                    if (kv_f16) reinterpret_cast<_Float16*>(kc)[slot + i] = static_cast<_Float16>(kk);
+                    else kc[slot + i] = kk;
                 }
             }
         }
         __builtin_amdgcn_wave_barrier();   // this head's reads of xw come before the next head's writes
     }
     for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {   // v is not normed
-        const float vr = row[(H + 1u) * hd + i];
-        const float vv = kv_f16 ? static_cast<float>(static_cast<_Float16>(vr)) : vr;
+        const float vv0 = i == vi ? vr : row[(H + 1u) * hd + i];
+        const float vv = kv_f16 ? static_cast<float>(static_cast<_Float16>(vv0)) : vv0;
         if (keep) {
             if (kv_f16) reinterpret_cast<_Float16*>(vc)[slot + i] = static_cast<_Float16>(vv);
             else vc[slot + i] = vv;
@@ -570,6 +594,7 @@ struct PfAttn {
     double* lpart;         // [H][qtmax][maxc][32] their sums of e_j
     G3State* st;
     uint32_t T, H, window, qtmax, maxc, block, kc;
+    uint32_t qt0;          // first query tile of the launch (blockIdx.y, merge: blockIdx.x, counts from it)
     float scale2;          // attention scale times log2(e): the scores in base 2
 };
 
@@ -586,7 +611,7 @@ __global__ void __launch_bounds__(256) k_pf_attn(PfAttn A) {
     constexpr uint32_t KW = (KS + 3u) / 4u;         // k steps per wave (at most)
     constexpr uint32_t DW = (DT + 3u) / 4u;         // d tiles per wave (at most)
     __shared__ __align__(16) float s_s[2][4][16 * 64];   // partial S^T per wave, double-buffered
-    const uint32_t c = blockIdx.x, i = blockIdx.y, h = blockIdx.z;
+    const uint32_t c = blockIdx.x, i = A.qt0 + blockIdx.y, h = blockIdx.z;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, l32 = lane & 31u, hf = lane >> 5;
     const uint32_t T = A.T, q0 = 32u * i, qw = A.H * HD;
     uint32_t ks, ke;
@@ -770,20 +795,27 @@ __global__ void __launch_bounds__(256) k_pf_attn(PfAttn A) {
     }
 }
 
-// Merge of the chunk partials of the query tiles k_pf_attn split (one workgroup per (tile, head);
-// tiles of one chunk were finished by k_pf_attn): thread t on row r = t / 8 and the eighth
-// t % 8 of the columns; in chunk order, with M the running maximum of the chunk maxima m_c,
-// den = sum_c exp(m_c - M) sum_c (double), out = sum_c exp(m_c - M) O_c / den as f16 hi/lo into
-// the queries' columns.
+// Column groups of a merge workgroup's head: 4, 2 or 1 (whole float4 runs per thread).
+template <uint32_t HD>
+constexpr uint32_t pf_merge_groups() {
+    return (HD / 32u) % 4u == 0u ? 4u : ((HD / 32u) % 2u == 0u ? 2u : 1u);
+}
+
+// Merge of the chunk partials of the query tiles k_pf_attn split (one workgroup per (tile, head,
+// column group); tiles of one chunk were finished by k_pf_attn): thread t on row r = t / 8 and
+// the eighth t % 8 of the group's columns; in chunk order, with M the running maximum of the
+// chunk maxima m_c, den = sum_c exp(m_c - M) sum_c (double), out = sum_c exp(m_c - M) O_c / den
+// as f16 hi/lo into the queries' columns.
 template <uint32_t HD>
 __global__ void __launch_bounds__(256) k_pf_attn_merge(PfAttn A) {
 #pragma clang fp contract(off)
-    constexpr uint32_t NF = HD / 32u;   // float4 per thread
-    const uint32_t i = blockIdx.x, h = blockIdx.y, T = A.T, q0 = 32u * i;
+    constexpr uint32_t CG = pf_merge_groups<HD>();
+    constexpr uint32_t NF = HD / 32u / CG;   // float4 per thread
+    const uint32_t i = A.qt0 + blockIdx.x, h = blockIdx.y, T = A.T, q0 = 32u * i;
     uint32_t ks, ke;
     pf_att_range(q0, T, A.window, ks, ke);
     const uint32_t nch = (ke - ks + A.kc - 1u) / A.kc;
-    const uint32_t r = threadIdx.x >> 3, g = threadIdx.x & 7u;
+    const uint32_t r = threadIdx.x >> 3, g = blockIdx.z * 8u + (threadIdx.x & 7u);
     if (nch == 1u || q0 + r >= T) return;
     const uint64_t unit0 = (static_cast<uint64_t>(h) * A.qtmax + i) * A.maxc;
     // chunks in groups of kG, every load of a group issued together (indices clamped to the last
@@ -803,7 +835,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_merge(PfAttn A) {
             const uint64_t u = unit0 + min(c0 + j, nch - 1u);
             mv[j] = A.mpart[u * 32u + r];
             lv[j] = A.lpart[u * 32u + r];
-            const float* src = A.opart + (u * 32u + r) * HD + g * (HD / 8u);
+            const float* src = A.opart + (u * 32u + r) * HD + g * (4u * NF);
 #pragma unroll
             for (uint32_t k = 0; k < NF; ++k) x[j][k] = *reinterpret_cast<const f4*>(src + 4u * k);
         }
@@ -834,7 +866,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_merge(PfAttn A) {
     if (g == 0u && (!(den > 0.0) || !__builtin_isfinite(den)))   // :1666-1670
         atomicMin(&A.st->nonfinite, g3_code_softmax(A.block));
     const float inv = static_cast<float>(1.0 / den);
-    const uint64_t oo = static_cast<uint64_t>(q0 + r) * (A.H * HD) + h * HD + g * (HD / 8u);
+    const uint64_t oo = static_cast<uint64_t>(q0 + r) * (A.H * HD) + h * HD + g * (4u * NF);
 #pragma unroll
     for (uint32_t k = 0; k < NF; ++k)
         pf_split4(f4{acc[k][0] * inv, acc[k][1] * inv, acc[k][2] * inv, acc[k][3] * inv}, A.ohi + oo + 4u * k,
@@ -1112,6 +1144,26 @@ static uint32_t pf_splits(uint32_t M, uint32_t N) {
     return std::min(kPfMaxSplits, std::max(1u, 256u / std::max(1u, tiles)));
 }
 
+// k_pf_norm_w over `rows` rows of n <= 2048 elements (elements per lane: the smallest of 4, 8,
+// 12, 16, 24, 32 that covers n).
+static int pf_norm(float* h, const float* f, uint32_t nsplit, uint64_t sstride, const float* w_post, const float* w_next,
+                   uint32_t n, float eps, _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block, uint32_t rows,
+                   hipStream_t s) {
+    void* args[] = {&h, &f, &nsplit, &sstride, &w_post, &w_next, &n, &eps, &xhi, &xlo, &st, &block, &rows};
+    const uint32_t ne = (n + 63u) / 64u;
+    const void* fn = ne <= 4u    ? reinterpret_cast<const void*>(&k_pf_norm_w<4>)
+                     : ne <= 8u  ? reinterpret_cast<const void*>(&k_pf_norm_w<8>)
+                     : ne <= 12u ? reinterpret_cast<const void*>(&k_pf_norm_w<12>)
+                     : ne <= 16u ? reinterpret_cast<const void*>(&k_pf_norm_w<16>)
+                     : ne <= 24u ? reinterpret_cast<const void*>(&k_pf_norm_w<24>)
+                     : ne <= 32u ? reinterpret_cast<const void*>(&k_pf_norm_w<32>)
+                                 : nullptr;
+    if (!fn || nsplit > kPfMaxSplits) return set_error(VRT_ERR_INVALID, "prefill norm shape not supported");
+    const uint32_t per = kPfThreads / 64u;
+    VRT_HIP_CHECK(hipLaunchKernel(fn, dim3((rows + per - 1u) / per), dim3(kPfThreads), args, 0, s));
+    return VRT_OK;
+}
+
 static uint32_t pf_pad(uint32_t T) { return (T + kPfTile - 1u) / kPfTile * kPfTile; }
 
 int pf_setup(vrt_g3* g, uint32_t max_t) {
@@ -1196,14 +1248,15 @@ static int pf_attn_launch(const PfAttn& A, dim3 grid, hipStream_t s) {
     void* args[] = {&arg};
     VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_attn<HD>), grid, dim3(256), args, 0, s));
     if (grid.x > 1u)   // some tile has several chunks
-        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_attn_merge<HD>), dim3(grid.y, grid.z),
-                                      dim3(256), args, 0, s));
+        VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_attn_merge<HD>),
+                                      dim3(grid.y, grid.z, pf_merge_groups<HD>()), dim3(256), args, 0, s));
     return VRT_OK;
 }
 
 // Causal local/global attention of one block (k_pf_attn) over the queries in qhi/qlo [T][H hd],
-// written back in place as the attention output.
-static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, _Float16* qhi, _Float16* qlo, hipStream_t s) {
+// written back in place as the attention output, for the query tiles from qt0 on.
+static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, uint32_t qt0, _Float16* qhi, _Float16* qlo,
+                        hipStream_t s) {
     const PfState& p = g->pf;
     const uint32_t H = g->cfg.head_count, hd = g->cfg.head_dim;
     PfAttn A{};
@@ -1226,14 +1279,15 @@ static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, _Float16* 
     A.scale2 = g->P.attn_scale * 1.4426950408889634f;
     const uint32_t qt = (T + 31u) / 32u;
     A.kc = kPfAttKC;
+    A.qt0 = qt0;
     uint32_t nch = 1;
-    for (uint32_t i = 0; i < qt; ++i) {
+    for (uint32_t i = qt0; i < qt; ++i) {
         const uint32_t q0 = 32u * i, ke = std::min(T, q0 + 32u);
         const uint32_t ks = A.window != 0u && q0 + 1u > A.window ? (q0 + 1u - A.window) & ~31u : 0u;
         nch = std::max(nch, (ke - ks + A.kc - 1u) / A.kc);
     }
-    if (qt > p.qtmax || nch > p.maxc) return set_error(VRT_ERR_STATE, "prefill attention workspace too small");
-    const dim3 grid(nch, qt, H);
+    if (qt > p.qtmax || nch > p.maxc || qt0 >= qt) return set_error(VRT_ERR_STATE, "prefill attention workspace too small");
+    const dim3 grid(nch, qt - qt0, H);
     switch (hd) {
     case 32: return pf_attn_launch<32>(A, grid, s);
     case 64: return pf_attn_launch<64>(A, grid, s);
@@ -1283,10 +1337,8 @@ int pf_run(vrt_g3* g, uint32_t T) {
         {   // previous block's FFN output into the residual, then the attention norm
             const float* f = l ? x : nullptr;
             const float* wpost = l ? g->layers[l - 1].post_ffw : nullptr;
-            const float* wnext = Ly.attn_norm;
-            uint32_t blk = l ? l - 1u : 0u;
-            void* args[] = {&h, &f, &s_down, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
+            if (int rc = pf_norm(h, f, s_down, xs, wpost, Ly.attn_norm, d, eps, ahi, alo, st, l ? l - 1u : 0u, T, s))
+                return rc;
         }
         if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, lw ? &lw[l].qkv : nullptr, big, 1, s)) return rc;
         {
@@ -1308,24 +1360,25 @@ int pf_run(vrt_g3* g, uint32_t T) {
             const uint32_t waves = std::min(H + 1u, kPfQkMaxWaves);
             VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_qk), dim3(tp), dim3(64u * waves), args, 0, s));
         }
-        // the attention output replaces q (hi/lo in ahi/alo)
-        if (int rc = pf_attention(g, Ly, T, ahi, alo, s)) return rc;
-        uint32_t so = s_o;
-        if (int rc = pf_gemm(g, ahi, alo, T, qw, {{Ly.wo, d}}, lw ? &lw[l].o : nullptr, x, so, s)) return rc;
-        so = std::max(1u, std::min(so, (qw / 32u) / 2u));
-        {   // attention output into the residual, then the FFN norm
-            const float* f = x;
-            const float* wpost = Ly.post_attn;
-            const float* wnext = Ly.ffn_norm;
-            uint32_t blk = Ly.index;
-            void* args[] = {&h, &f, &so, &xs, &wpost, &wnext, &d, &eps, &ahi, &alo, &st, &blk};
-            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_norm), dim3(T), args)) return rc;
-        }
-        // gelu(gate) * up as f16 hi/lo in `big` (the gate/up GEMM still reads ahi/alo). The last
-        // block's FFN output feeds only the LM head, so there it runs for the last position alone.
+        // The last block's output feeds only the LM head, so past its q/k/v (every position's
+        // keys and values go to the cache) it runs for the last position alone: attention for
+        // that position's query tile, then one row.
         const bool last = l + 1u == L;
         const uint32_t fr = last ? 1u : T;
         const uint64_t a0 = last ? static_cast<uint64_t>(T - 1u) * d : 0u;
+        const uint64_t aq = last ? static_cast<uint64_t>(T - 1u) * qw : 0u;
+        // the attention output replaces q (hi/lo in ahi/alo)
+        if (int rc = pf_attention(g, Ly, T, last ? (T - 1u) / 32u : 0u, ahi, alo, s)) return rc;
+        uint32_t so = last ? pf_splits(1u, d) : s_o;
+        if (int rc = pf_gemm(g, ahi + aq, alo + aq, fr, qw, {{Ly.wo, d}}, lw ? &lw[l].o : nullptr, x, so, s)) return rc;
+        so = std::max(1u, std::min(so, (qw / 32u) / 2u));
+        {   // attention output into the residual, then the FFN norm (the O partials of fr rows)
+            const uint64_t xo = static_cast<uint64_t>(fr) * d;
+            if (int rc = pf_norm(h + a0, x, so, xo, Ly.post_attn, Ly.ffn_norm, d, eps, ahi + a0, alo + a0, st, Ly.index,
+                                 fr, s))
+                return rc;
+        }
+        // gelu(gate) * up as f16 hi/lo in `big` (the gate/up GEMM still reads ahi/alo).
         _Float16* ghi = reinterpret_cast<_Float16*>(big);
         _Float16* glo = ghi + static_cast<uint64_t>(fr) * F;
         if (int rc = pf_gemm_glu(g, ahi + a0, alo + a0, fr, d, Ly.wg, Ly.wu, F, lw ? &lw[l].gu : nullptr, ghi, glo, s))
