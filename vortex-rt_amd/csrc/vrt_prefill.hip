@@ -904,93 +904,100 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_expand(const uint8_t* w0, con
     for (uint32_t k = 0; k < 32u; ++k) dst[k] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(blk[2 + k])));
 }
 
-// The Q8_0 GEMM of k_pf_gemm_q8 on expanded weights (G.wh, G.ws): a K step stages the f16 rows
-// of the tile's W block with plain 16-byte copies (no int8 conversion on the K loop's critical
-// path) and the two block scales per row. Same tiles, splits, LDS layout, K-loop ring and
-// epilogues as k_pf_gemm_q8, with twice the waves: wave group kw (of 2 NWN waves) computes the
-// step's Q8_0 block kw for every tile, so a SIMD runs two waves whose MFMA chains and
-// scale-and-add work overlap; the kw = 1 partial tiles are added to the kw = 0 ones through
-// LDS before the epilogue (sum of the even blocks, then of the odd ones).
-template <int WN, int NWN>
-__global__ void __launch_bounds__(256 * NWN) k_pf_gemm_h(PfGemm G) {
-    constexpr uint32_t NT = 256u * NWN;
+// The Q8_0 GEMM of k_pf_gemm_q8 on expanded weights (G.wh, G.ws): a K step of SB Q8_0 blocks
+// (32 SB wide) stages the f16 rows of the tile's W blocks with plain 16-byte copies (no int8
+// conversion on the K loop's critical path) and the SB block scales per row. Same tiles,
+// splits and epilogues as k_pf_gemm_q8, with KW times the waves: wave group kw (of 2 NWN
+// waves) computes the step's Q8_0 blocks kw, kw + KW, ... for every tile, so a SIMD runs KW
+// waves whose LDS reads, MFMA chains and scale-and-add work overlap; before the epilogue the
+// partial tiles of groups 1..KW-1 are added, in group order, to those of group 0 through LDS.
+// The register ring holds 8 / SB steps in flight (the same bytes for every SB).
+template <int WN, int NWN, int SB, int KW>
+__global__ void __launch_bounds__(128 * NWN * KW) k_pf_gemm_h(PfGemm G) {
+    constexpr uint32_t NT = 128u * NWN * KW;
     constexpr uint32_t BN = 32u * WN * NWN;
-    constexpr uint32_t AU = 2u * kQgBM * 8u / NT;   // A 16-byte units per thread (hi units, then lo)
-    constexpr uint32_t WU = BN * 8u / NT;           // W 16-byte units per thread (8 per row)
-    static_assert(AU >= 1u && 2u * kQgBM * 8u % NT == 0u, "whole A units per thread");
-    static_assert(WU >= 1u && BN * 8u % NT == 0u, "whole W units per thread");
-    static_assert(BN <= NT, "one scale pair per thread");
-    __shared__ __align__(16) unsigned char s_a[2][2][kQgBM * kQgPitch];
-    __shared__ __align__(16) unsigned char s_w[2][BN * kQgPitch];
-    __shared__ float s_sc[2][BN][2];
+    constexpr uint32_t UR = 4u * SB;                   // 16-byte units per staged row
+    constexpr uint32_t PITCH = 16u * UR + 16u;         // LDS row pitch in bytes (padded)
+    constexpr uint32_t AU = 2u * kQgBM * UR / NT;      // A units per thread (hi units, then lo)
+    constexpr uint32_t WU = BN * UR / NT;              // W units per thread
+    constexpr uint32_t AHEAD = 8u / SB;                // steps in flight ahead of the one computed
+    constexpr uint32_t CHUNK = 24u / SB;               // steps per straight-line chunk
+    static_assert((SB == 2 || SB == 4) && (KW == 2 || KW == 4) && SB % KW == 0, "blocks per step, wave groups");
+    static_assert(AU >= 1u && 2u * kQgBM * UR % NT == 0u, "whole A units per thread");
+    static_assert(WU >= 1u && BN * UR % NT == 0u, "whole W units per thread");
+    static_assert(BN <= NT, "one row of scales per thread");
+    __shared__ __align__(16) unsigned char s_a[2][2][kQgBM * PITCH];
+    __shared__ __align__(16) unsigned char s_w[2][BN * PITCH];
+    __shared__ float s_sc[2][BN][SB];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t kh = lane >> 5, l32 = lane & 31u;
     const uint32_t m0 = blockIdx.y * kQgBM, n0 = blockIdx.x * BN;
     const uint32_t nkb = G.K >> 5;
     const uint32_t S = gridDim.z, z = blockIdx.z;
     const uint32_t kb_lo = nkb * z / S, kb_hi = nkb * (z + 1u) / S;
-    const uint32_t nsteps = (kb_hi - kb_lo + 1u) / 2u;
+    const uint32_t nsteps = (kb_hi - kb_lo + SB - 1u) / SB;
     typedef const __attribute__((address_space(1))) v4u* gv4;
     struct Stage {
-        v4u a[AU];   // unit u = AU tid + j: array u / (8 kQgBM), row (u % (8 kQgBM)) / 8, column u % 8
+        v4u a[AU];   // unit u = AU tid + j: array u / (UR kQgBM), row (u % (UR kQgBM)) / UR, column u % UR
         v4u w[WU];
-        float2 sc;
+        float sc[SB];
     };
     // Every load is issued at a clamped, in-bounds address (dead data is zeroed when stored).
     auto load = [&](uint32_t step, Stage& R) {
-        const uint32_t kb = kb_lo + 2u * step;
+        const uint32_t kb = kb_lo + SB * step;
 #pragma unroll
         for (uint32_t j = 0; j < AU; ++j) {
-            const uint32_t u = AU * tid + j, ui = u % (8u * kQgBM), r = ui >> 3, c = ui & 7u;
+            const uint32_t u = AU * tid + j, ui = u % (UR * kQgBM), r = ui / UR, c = ui % UR;
             const uint32_t k = 32u * kb + 8u * c;
             const uint32_t rr = min(m0 + r, G.M - 1u), kk = min(k, 32u * kb_hi - 8u);
             const uint64_t o = (static_cast<uint64_t>(rr) * G.lda + kk) * 2u;
-            R.a[j] = *reinterpret_cast<gv4>(reinterpret_cast<uintptr_t>(u < 8u * kQgBM ? G.ahi : G.alo) + o);
+            R.a[j] = *reinterpret_cast<gv4>(reinterpret_cast<uintptr_t>(u < UR * kQgBM ? G.ahi : G.alo) + o);
         }
 #pragma unroll
         for (uint32_t j = 0; j < WU; ++j) {
-            const uint32_t u = WU * tid + j, r = u >> 3, c = u & 7u;
+            const uint32_t u = WU * tid + j, r = u / UR, c = u % UR;
             const uint32_t rr = min(n0 + r, G.N - 1u), kk = min(32u * kb + 8u * c, 32u * kb_hi - 8u);
             R.w[j] = *reinterpret_cast<gv4>(reinterpret_cast<uintptr_t>(G.wh) + (static_cast<uint64_t>(rr) * G.K + kk) * 2u);
         }
-        {   // the step's two block scales of row tid (clamped to the split's last block)
+        {   // the step's block scales of row tid (clamped to the split's last block)
             typedef const __attribute__((address_space(1))) float* gf;
-            const uint32_t rr = min(n0 + (tid < BN ? tid : 0u), G.N - 1u), bb = min(kb, kb_hi - 1u);
+            const uint32_t rr = min(n0 + (tid < BN ? tid : 0u), G.N - 1u);
             const gf row = reinterpret_cast<gf>(reinterpret_cast<uintptr_t>(G.ws + static_cast<uint64_t>(rr) * nkb));
-            R.sc = make_float2(row[bb], row[min(bb + 1u, kb_hi - 1u)]);
+#pragma unroll
+            for (uint32_t q = 0; q < SB; ++q) R.sc[q] = row[min(kb + q, kb_hi - 1u)];
         }
     };
     auto store = [&](const Stage& R, uint32_t st, uint32_t step) {
-        const uint32_t kb = kb_lo + 2u * step;
+        const uint32_t kb = kb_lo + SB * step;
 #pragma unroll
         for (uint32_t j = 0; j < AU; ++j) {
-            const uint32_t u = AU * tid + j, ui = u % (8u * kQgBM), r = ui >> 3, c = ui & 7u;
+            const uint32_t u = AU * tid + j, ui = u % (UR * kQgBM), r = ui / UR, c = ui % UR;
             const bool live = m0 + r < G.M && 32u * kb + 8u * c < 32u * kb_hi;
-            *reinterpret_cast<v4u*>(&s_a[st][u / (8u * kQgBM)][r * kQgPitch + c * 16u]) =
-                live ? R.a[j] : v4u{0u, 0u, 0u, 0u};
+            *reinterpret_cast<v4u*>(&s_a[st][u / (UR * kQgBM)][r * PITCH + c * 16u]) = live ? R.a[j] : v4u{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (uint32_t j = 0; j < WU; ++j) {
-            const uint32_t u = WU * tid + j, r = u >> 3, c = u & 7u;
+            const uint32_t u = WU * tid + j, r = u / UR, c = u % UR;
             const bool live = n0 + r < G.N && 32u * kb + 8u * c < 32u * kb_hi;
-            *reinterpret_cast<v4u*>(&s_w[st][r * kQgPitch + c * 16u]) = live ? R.w[j] : v4u{0u, 0u, 0u, 0u};
+            *reinterpret_cast<v4u*>(&s_w[st][r * PITCH + c * 16u]) = live ? R.w[j] : v4u{0u, 0u, 0u, 0u};
         }
         if (tid < BN) {
             const bool rl = n0 + tid < G.N;
-            s_sc[st][tid][0] = rl && kb < kb_hi ? R.sc.x : 0.0f;
-            s_sc[st][tid][1] = rl && kb + 1u < kb_hi ? R.sc.y : 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < SB; ++q) s_sc[st][tid][q] = rl && kb + q < kb_hi ? R.sc[q] : 0.0f;
         }
     };
-    const uint32_t kw = wave / (2u * NWN), wv = wave % (2u * NWN);   // block of the step, tile
+    const uint32_t kw = wave / (2u * NWN), wv = wave % (2u * NWN);   // block group of the step, tile
     const uint32_t wm = wv / NWN, wn = wv % NWN;
     float16v acc[WN];
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[j] = float16v{};
     auto compute = [&](uint32_t st) {
-        const unsigned char* pa_hi = &s_a[st][0][(32u * wm + l32) * kQgPitch + 16u * kh];
-        const unsigned char* pa_lo = &s_a[st][1][(32u * wm + l32) * kQgPitch + 16u * kh];
-        {
-            const uint32_t b = kw;
+        const unsigned char* pa_hi = &s_a[st][0][(32u * wm + l32) * PITCH + 16u * kh];
+        const unsigned char* pa_lo = &s_a[st][1][(32u * wm + l32) * PITCH + 16u * kh];
+#pragma unroll
+        for (uint32_t bq = 0; bq < SB / KW; ++bq) {
+            const uint32_t b = kw + KW * bq;
             half8 ah[2], al[2];
 #pragma unroll
             for (uint32_t ks = 0; ks < 2; ++ks) {
@@ -1000,7 +1007,7 @@ __global__ void __launch_bounds__(256 * NWN) k_pf_gemm_h(PfGemm G) {
 #pragma unroll
             for (int j = 0; j < WN; ++j) {
                 const uint32_t nl = 32u * (WN * wn + j) + l32;
-                const unsigned char* pw = &s_w[st][nl * kQgPitch + 64u * b + 16u * kh];
+                const unsigned char* pw = &s_w[st][nl * PITCH + 64u * b + 16u * kh];
                 const half8 w0 = *reinterpret_cast<const half8*>(pw), w1 = *reinterpret_cast<const half8*>(pw + 32u);
                 float16v p = {};
                 p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0], w0, p, 0, 0, 0);
@@ -1013,41 +1020,44 @@ __global__ void __launch_bounds__(256 * NWN) k_pf_gemm_h(PfGemm G) {
             }
         }
     };
-    static_assert(kQgAhead <= kQgChunk, "ring inside a chunk");
-    for (uint32_t i = 0; i < nsteps; i += kQgChunk) {
-        Stage R[kQgAhead];
+    static_assert(AHEAD <= CHUNK, "ring inside a chunk");
+    for (uint32_t i = 0; i < nsteps; i += CHUNK) {
+        Stage R[AHEAD];
         auto clamp = [&](uint32_t j) { return min(i + j, nsteps - 1u); };
 #pragma unroll
-        for (uint32_t u = 0; u < kQgAhead; ++u) load(clamp(u), R[u]);
+        for (uint32_t u = 0; u < AHEAD; ++u) load(clamp(u), R[u]);
 #pragma unroll
-        for (uint32_t u = 0; u < kQgChunk; ++u) {
+        for (uint32_t u = 0; u < CHUNK; ++u) {
             const uint32_t j = i + u;
             if (j < nsteps) {
-                store(R[u % kQgAhead], j & 1u, j);
+                store(R[u % AHEAD], j & 1u, j);
                 __syncthreads();
             }
-            if (u + kQgAhead < kQgChunk) load(clamp(u + kQgAhead), R[u % kQgAhead]);
+            if (u + AHEAD < CHUNK) load(clamp(u + AHEAD), R[u % AHEAD]);
             if (j < nsteps) compute(j & 1u);
         }
     }
-    {   // odd-block partials into the even-block waves (s_w: 2 NWN WN 16 x 64 floats fit)
-        static_assert(2u * NWN * WN * 16u * 64u * 4u <= sizeof(s_w), "reduction area");
+    {   // the other groups' partials into group 0 (s_a: (KW - 1) 2 NWN WN 16 x 64 floats fit)
+        constexpr uint32_t RS = 2u * NWN * WN * 16u * 64u;   // floats per group
+        static_assert((KW - 1u) * RS * 4u <= sizeof(s_a), "reduction area");
         __syncthreads();   // every wave is done reading the LDS stages
-        float* red = reinterpret_cast<float*>(&s_w[0][0]);
-        if (kw == 1u) {
+        float* red = reinterpret_cast<float*>(&s_a[0][0][0]);
+        if (kw != 0u) {
 #pragma unroll
             for (int j = 0; j < WN; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) red[((wv * WN + j) * 16u + r) * 64u + lane] = acc[j][r];
+                for (int r = 0; r < 16; ++r) red[(kw - 1u) * RS + ((wv * WN + j) * 16u + r) * 64u + lane] = acc[j][r];
         }
         __syncthreads();
         if (kw == 0u) {
 #pragma unroll
-            for (int j = 0; j < WN; ++j)
+            for (uint32_t q = 1; q < KW; ++q)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[j][r] += red[((wv * WN + j) * 16u + r) * 64u + lane];
+                for (int j = 0; j < WN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[j][r] += red[(q - 1u) * RS + ((wv * WN + j) * 16u + r) * 64u + lane];
         }
-    }
+    }   // (the GLU epilogue's exchange reuses s_a after a barrier of its own)
     pf_gemm_epilogue<WN, NWN>(G, acc, z, m0, n0, wm, wn, kh, l32, lane, reinterpret_cast<float*>(&s_a[0][0][0]),
                               kw == 0u);
 }
@@ -1065,14 +1075,17 @@ static int pf_launch_q8(const PfGemm& G, uint32_t splits, hipStream_t s) {
     return VRT_OK;
 }
 
-template <int WN, int NWN>
+constexpr int kPfStepBlocks = 4;   // Q8_0 blocks per K step of the 64 x 64 tiles
+constexpr int kPfWaveGroups = 4;   // their wave groups (the 64 x 128 tiles: 2 blocks, 2 groups)
+
+template <int WN, int NWN, int SB, int KW>
 static int pf_launch_h(const PfGemm& G, uint32_t splits, hipStream_t s) {
     constexpr uint32_t BN = 32u * WN * NWN;
     const dim3 grid((G.N + BN - 1u) / BN, (G.M + kQgBM - 1u) / kQgBM, splits);
     PfGemm arg = G;
     void* args[] = {&arg};
-    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_gemm_h<WN, NWN>), grid, dim3(256u * NWN), args,
-                                  0, s));
+    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_gemm_h<WN, NWN, SB, KW>), grid,
+                                  dim3(128u * NWN * KW), args, 0, s));
     return VRT_OK;
 }
 
@@ -1083,7 +1096,7 @@ static int pf_launch_w(PfGemm& G, const PfMatrix* ex, uint32_t splits, hipStream
     if (ex && ex->h) {
         G.wh = static_cast<const _Float16*>(ex->h);
         G.ws = ex->s;
-        return wide ? pf_launch_h<1, 4>(G, splits, s) : pf_launch_h<1, 2>(G, splits, s);
+        return wide ? pf_launch_h<1, 4, 2, 2>(G, splits, s) : pf_launch_h<1, 2, kPfStepBlocks, kPfWaveGroups>(G, splits, s);
     }
     return wide ? pf_launch_q8<1, 4>(G, splits, s) : pf_launch_q8<1, 2>(G, splits, s);
 }
