@@ -234,7 +234,9 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
  * used when the device and shape support it; otherwise, or with VRT_G3_OPT_PERSISTENT = 0,
  * each step is the multi-kernel sequence, replayed from a hipGraph unless
  * VRT_G3_OPT_USE_GRAPH = 0. VRT_G3_OPT_QUERY_PERSISTENT returns VRT_OK when the persistent
- * kernel is available (value ignored). */
+ * kernel is available (value ignored). When the device refuses its cooperative launch (on
+ * ROCm while another live process has made one on the same GPU) the executor continues on the
+ * multi-kernel path and the query reports the refusal. */
 #define VRT_G3_OPT_USE_GRAPH 1
 #define VRT_G3_OPT_PERSISTENT 2
 #define VRT_G3_OPT_QUERY_PERSISTENT 3
@@ -259,6 +261,28 @@ int vrt_g3_read_trace(vrt_g3* g3, uint64_t* out, uint64_t cap, uint32_t* nwg, ui
  * partials. *n receives the word count; synchronises the context's stream. */
 int vrt_g3_read_exchange(vrt_g3* g3, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
+
+/* Batched greedy decode: up to max_seqs independent sequences share the executor's weights, each
+ * with its own KV cache of max_ctx positions (<= context_length). The reference decodes one
+ * sequence (src/gemma3.cpp:1462-1882, one KV cache per model); batching is its roadmap's
+ * "continuous batching" (README.md:190-193), with no implementation to follow. A step advances
+ * n sequences by one position each: sequence seqs[i] consumes tokens[i] at its next position
+ * (a prompt token or the token it generated last) and results[i] receives its greedy next token
+ * and logit (all arrays on the host, n <= max_seqs, distinct ids). Every projection and the
+ * LM head are GEMMs over the n rows on MFMA (the numerics of vrt_g3_prefill), attention runs
+ * per sequence over its own cache. On any error every sequence of the step is reset to
+ * position 0, as the reference resets its cache. */
+typedef struct vrt_g3_batch vrt_g3_batch;
+int vrt_g3_batch_create(vrt_g3* g3, uint32_t max_seqs, uint32_t max_ctx, vrt_g3_batch** out);
+int vrt_g3_batch_destroy(vrt_g3_batch* b);
+/* Sequence seq (or every sequence, seq = 0xffffffff) restarts at position 0. */
+int vrt_g3_batch_reset(vrt_g3_batch* b, uint32_t seq);
+int vrt_g3_batch_step(vrt_g3_batch* b, const uint32_t* seqs, const uint32_t* tokens, uint32_t n,
+                      vrt_argmax_result* results);
+/* Next position of sequence seq. */
+int vrt_g3_batch_position(vrt_g3_batch* b, uint32_t seq, uint32_t* pos);
+/* Logits of row `row` (< n) of the last step (host copy, n floats <= vocab_size). */
+int vrt_g3_batch_logits(vrt_g3_batch* b, uint32_t row, float* host_logits, uint32_t n);
 
 /* Launches the tied LM head + argmax kernel `iters` times back to back between two
  * hipEvents on the context stream (current hidden state) and reports the mean duration. */

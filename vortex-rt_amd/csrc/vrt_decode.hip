@@ -749,8 +749,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         const float scq = mk_rms_scale_pow2(sq_q, hd, g_mk.eps), sck = mk_rms_scale_pow2(sq_k, hd, g_mk.eps);
 #pragma unroll
         for (uint32_t e = 0; e < 4u; ++e) {
-            q[e] = q[e] * scq * wq[e];
-            k[e] = k[e] * sck * wk[e];
+            q[e] = q[e] * (scq * wq[e]);   // values *= scale * weights (src/gemma3.cpp:1097-1102)
+            k[e] = k[e] * (sck * wk[e]);
         }
         // RoPE (NeoX halves): (a, b) = (x[e], x[e + half]) -> (a c - b s, b c + a s)
         float qo[4], ko[4];
@@ -1694,8 +1694,16 @@ int mk_run(vrt_g3* g, uint32_t nsteps) {
         ds.version = mk->version;
     }
     void* args[] = {&nsteps, &tag0};
-    VRT_HIP_CHECK(hipLaunchCooperativeKernel(mk->P.kv_f16 ? mk->fns.f16 : mk->fns.f32, dim3(mk->grid), dim3(kMkThreads),
-                                             args, 0, stream));
+    const hipError_t le = hipLaunchCooperativeKernel(mk->P.kv_f16 ? mk->fns.f16 : mk->fns.f32, dim3(mk->grid),
+                                                     dim3(kMkThreads), args, 0, stream);
+    if (le == hipErrorIllegalState || le == hipErrorCooperativeLaunchTooLarge) {
+        // The device refuses the cooperative launch (on this stack: while another live process
+        // has made one on the same GPU). Nothing ran; the caller takes the multi-kernel path.
+        (void)hipGetLastError();
+        return kMkRefused;
+    }
+    if (le != hipSuccess)
+        return set_error(VRT_ERR_HIP, "hipLaunchCooperativeKernel (persistent decode) failed: %s", hipGetErrorString(le));
     if (!ds.last) VRT_HIP_CHECK(hipEventCreateWithFlags(&ds.last, hipEventDisableTiming));
     VRT_HIP_CHECK(hipEventRecord(ds.last, stream));
     ds.last_stream = stream;

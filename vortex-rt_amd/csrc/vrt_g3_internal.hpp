@@ -122,6 +122,7 @@ struct vrt_g3 {
     uint32_t next_pos = 0;
     bool use_graph = true;
     bool use_persistent = true;  // one cooperative launch per batch of steps (vrt_decode.hip)
+    bool mk_refused = false;     // the device refused a cooperative launch: multi-kernel steps
     vrt::MkState* mk = nullptr;
     uint32_t mk_tag = 1;         // first exchange tag of the next persistent launch
     hipGraphExec_t graph = nullptr;
@@ -135,6 +136,9 @@ namespace vrt {
 // Persistent decode kernel (vrt_decode.hip). mk_setup returns VRT_OK and leaves g->mk null
 // when the configuration or device does not support it (the multi-kernel step is used).
 int mk_setup(vrt_g3* g);
+// Enqueues nsteps steps as one cooperative launch; kMkRefused when the device refuses the
+// cooperative launch (nothing enqueued: the caller runs the steps on the multi-kernel path).
+constexpr int kMkRefused = 1000;
 int mk_run(vrt_g3* g, uint32_t nsteps);
 void mk_destroy(vrt_g3* g);
 int mk_clear_abort(vrt_g3* g);
@@ -147,6 +151,20 @@ int mk_set_kv_f16(vrt_g3* g, bool on);
 // positions from position 0 whose last position runs g3_enqueue_lm.
 int pf_setup(vrt_g3* g, uint32_t max_t);
 int pf_run(vrt_g3* g, uint32_t T);
+// Row-batch building blocks shared by the prefill and the batched decode (vrt_prefill.hip):
+// block l's projections over M rows as (split-K) GEMMs, its gate/up product, the residual
+// norms over rows, embedding rows, and the logits of M rows against the tied embedding table.
+enum PfProj : uint32_t { kProjQkv = 0, kProjO = 1, kProjDown = 2 };
+int pf_project(vrt_g3* g, uint32_t l, uint32_t which, const _Float16* ahi, const _Float16* alo, uint32_t M, float* c,
+               uint32_t splits, uint32_t* used, hipStream_t s);
+int pf_ffn_glu(vrt_g3* g, uint32_t l, const _Float16* ahi, const _Float16* alo, uint32_t M, _Float16* ghi,
+               _Float16* glo, hipStream_t s);
+int pf_norm(float* h, const float* f, uint32_t nsplit, uint64_t sstride, const float* w_post, const float* w_next,
+            uint32_t n, float eps, _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block, uint32_t rows, hipStream_t s,
+            bool into);
+int pf_embed_rows(vrt_g3* g, const uint32_t* tokens, uint32_t rows, float* h, hipStream_t s);
+int pf_lm_logits(vrt_g3* g, const _Float16* xhi, const _Float16* xlo, uint32_t M, float* logits, hipStream_t s);
+uint32_t pf_splits(uint32_t M, uint32_t N);
 // Final residual + output norm + LM head + argmax of the current step (vrt_gemma3.hip).
 int g3_enqueue_lm(vrt_g3* g, hipStream_t s);
 int mk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);

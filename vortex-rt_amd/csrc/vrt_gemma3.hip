@@ -730,7 +730,12 @@ static int g3_capture(vrt_g3* g) {
 
 static int g3_run_steps(vrt_g3* g, uint32_t n) {
     hipStream_t s = g->ctx->stream;
-    if (g->mk && g->use_persistent) return mk_run(g, n);
+    if (g->mk && g->use_persistent) {
+        const int rc = mk_run(g, n);
+        if (rc != kMkRefused) return rc;
+        g->use_persistent = false;   // refused by the device: multi-kernel steps from here on
+        g->mk_refused = true;
+    }
     for (uint32_t i = 0; i < n; ++i) {
         if (g->use_graph) {
             if (!g->graph) { if (int rc = g3_capture(g)) return rc; }
@@ -971,7 +976,9 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
     switch (option) {
     case VRT_G3_OPT_USE_GRAPH: g->use_graph = value != 0; return VRT_OK;
     case VRT_G3_OPT_PERSISTENT: g->use_persistent = value != 0; return VRT_OK;
-    case VRT_G3_OPT_QUERY_PERSISTENT: return g->mk ? VRT_OK : set_error(VRT_ERR_STATE, "persistent decode kernel unavailable");
+    case VRT_G3_OPT_QUERY_PERSISTENT:
+        if (g->mk_refused) return set_error(VRT_ERR_STATE, "persistent decode kernel refused by the device");
+        return g->mk ? VRT_OK : set_error(VRT_ERR_STATE, "persistent decode kernel unavailable");
     case VRT_G3_OPT_TRACE: return mk_set_trace(g, value != 0);
     case VRT_G3_OPT_KV_F16: {
         // the kernels read the flag from their parameter blocks: the captured graph (which holds

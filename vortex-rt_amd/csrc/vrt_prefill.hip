@@ -78,13 +78,14 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_embed(const uint8_t* tok_embd
 // the sum of nsplit partial rows f + s * sstride added in order s = 0, 1, ...):
 // h = f * (scale(f) * w_post) + h (rms_norm_inplace then add_inplace, src/gemma3.cpp:1036-1042,
 // :1703-1711, :1849-1855). Then, with w_next:
-// the GEMM input (h * scale(h)) * w_next as f16 hi/lo (:991-996). nonfinite: lowest block
-// whose residual went non-finite (:1857-1863), reported through st->nonfinite.
+// the GEMM input (h * scale(h)) * w_next as f16 hi/lo (rms_norm_into, :991-996), or with
+// `into` 0 h * (scale(h) * w_next) (rms_norm_inplace, the output norm :1866-1868). nonfinite:
+// lowest block whose residual went non-finite (:1857-1863), reported through st->nonfinite.
 template <uint32_t NE>
 __global__ void __launch_bounds__(kPfThreads) k_pf_norm_w(float* h, const float* f, uint32_t nsplit, uint64_t sstride,
                                                           const float* w_post, const float* w_next, uint32_t n, float eps,
                                                           _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block,
-                                                          uint32_t rows) {
+                                                          uint32_t rows, uint32_t into) {
 #pragma clang fp contract(off)
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t t = blockIdx.x * (kPfThreads / 64u) + (threadIdx.x >> 6);
@@ -149,7 +150,7 @@ __global__ void __launch_bounds__(kPfThreads) k_pf_norm_w(float* h, const float*
     const float sc = pf_rms_scale(wave_red_sum_d(ss), n, eps);
 #pragma unroll
     for (uint32_t k = 0; k < NE; ++k) {
-        const float y = (hv[k] * sc) * wn[k];
+        const float y = into ? (hv[k] * sc) * wn[k] : hv[k] * (sc * wn[k]);
         if (live[k]) pf_split(y, xhi + static_cast<uint64_t>(t) * n + ic[k], xlo + static_cast<uint64_t>(t) * n + ic[k]);
     }
 }
@@ -522,7 +523,7 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
         const float sc = pf_rms_scale(wave_red_sum_d(sq), hd, eps);
 #pragma unroll
         for (uint32_t e = 0; e < 4u; ++e)
-            if (live[e]) xw[ic[e]] = (v[e] * sc) * wv[e];
+            if (live[e]) xw[ic[e]] = v[e] * (sc * wv[e]);   // values *= scale * weights (src/gemma3.cpp:1097-1102)
         // the partners are other lanes' values: a wave's LDS accesses complete in order
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -1121,7 +1122,8 @@ static int pf_gemm(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint32_t
     G.ldc = G.N;
     G.M = M;
     G.K = K;
-    if (K % 32u != 0u || G.N % 32u != 0u) return set_error(VRT_ERR_INVALID, "prefill GEMM shape not supported");
+    // any N: rows past N load clamped, in-bounds rows, are zeroed in LDS and never stored
+    if (K % 32u != 0u || G.N == 0u) return set_error(VRT_ERR_INVALID, "prefill GEMM shape not supported");
     G.c_bs = static_cast<uint64_t>(M) * G.N;
     splits = std::max(1u, std::min(splits, (K / 32u) / 2u));
     return pf_launch_w(G, ex, splits, s);
@@ -1152,17 +1154,18 @@ static int pf_gemm_glu(vrt_g3* g, const _Float16* ahi, const _Float16* alo, uint
 }
 
 // K splits of the 640-row projections (O and down): enough workgroups to cover the CUs.
-static uint32_t pf_splits(uint32_t M, uint32_t N) {
+uint32_t pf_splits(uint32_t M, uint32_t N) {
     const uint32_t tiles = ((M + kQgBM - 1u) / kQgBM) * ((N + 63u) / 64u);
     return std::min(kPfMaxSplits, std::max(1u, 256u / std::max(1u, tiles)));
 }
 
 // k_pf_norm_w over `rows` rows of n <= 2048 elements (elements per lane: the smallest of 4, 8,
 // 12, 16, 24, 32 that covers n).
-static int pf_norm(float* h, const float* f, uint32_t nsplit, uint64_t sstride, const float* w_post, const float* w_next,
-                   uint32_t n, float eps, _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block, uint32_t rows,
-                   hipStream_t s) {
-    void* args[] = {&h, &f, &nsplit, &sstride, &w_post, &w_next, &n, &eps, &xhi, &xlo, &st, &block, &rows};
+int pf_norm(float* h, const float* f, uint32_t nsplit, uint64_t sstride, const float* w_post, const float* w_next,
+            uint32_t n, float eps, _Float16* xhi, _Float16* xlo, G3State* st, uint32_t block, uint32_t rows, hipStream_t s,
+            bool into) {
+    uint32_t in = into ? 1u : 0u;
+    void* args[] = {&h, &f, &nsplit, &sstride, &w_post, &w_next, &n, &eps, &xhi, &xlo, &st, &block, &rows, &in};
     const uint32_t ne = (n + 63u) / 64u;
     const void* fn = ne <= 4u    ? reinterpret_cast<const void*>(&k_pf_norm_w<4>)
                      : ne <= 8u  ? reinterpret_cast<const void*>(&k_pf_norm_w<8>)
@@ -1175,6 +1178,50 @@ static int pf_norm(float* h, const float* f, uint32_t nsplit, uint64_t sstride, 
     const uint32_t per = kPfThreads / 64u;
     VRT_HIP_CHECK(hipLaunchKernel(fn, dim3((rows + per - 1u) / per), dim3(kPfThreads), args, 0, s));
     return VRT_OK;
+}
+
+// Block l's projection `which` over M rows (the building blocks of the batched decode): C =
+// A x W^T with K split over `splits` workgroups (clamped to the K blocks; the count used goes to
+// *used), partial z at c + z * M * N.
+int pf_project(vrt_g3* g, uint32_t l, uint32_t which, const _Float16* ahi, const _Float16* alo, uint32_t M, float* c,
+               uint32_t splits, uint32_t* used, hipStream_t s) {
+    const LayerParams& Ly = g->layers[l];
+    const PfLayerW* lw = g->pf.lw.empty() ? nullptr : &g->pf.lw[l];
+    const uint32_t d = g->cfg.embedding_length, hd = g->cfg.head_dim, qw = g->cfg.head_count * hd;
+    const uint32_t F = g->cfg.feed_forward_length;
+    const uint32_t K = which == kProjQkv ? d : (which == kProjO ? qw : F);
+    *used = std::max(1u, std::min(splits, (K / 32u) / 2u));
+    switch (which) {
+    case kProjQkv: return pf_gemm(g, ahi, alo, M, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, lw ? &lw->qkv : nullptr, c, splits, s);
+    case kProjO: return pf_gemm(g, ahi, alo, M, qw, {{Ly.wo, d}}, lw ? &lw->o : nullptr, c, splits, s);
+    case kProjDown: return pf_gemm(g, ahi, alo, M, F, {{Ly.wd, d}}, lw ? &lw->down : nullptr, c, splits, s);
+    default: return set_error(VRT_ERR_INVALID, "unknown projection %u", which);
+    }
+}
+
+// Block l's gelu_tanh(gate) * up over M rows, as f16 hi/lo [M][F].
+int pf_ffn_glu(vrt_g3* g, uint32_t l, const _Float16* ahi, const _Float16* alo, uint32_t M, _Float16* ghi,
+               _Float16* glo, hipStream_t s) {
+    const LayerParams& Ly = g->layers[l];
+    const PfLayerW* lw = g->pf.lw.empty() ? nullptr : &g->pf.lw[l];
+    return pf_gemm_glu(g, ahi, alo, M, g->cfg.embedding_length, Ly.wg, Ly.wu, g->cfg.feed_forward_length,
+                       lw ? &lw->gu : nullptr, ghi, glo, s);
+}
+
+// Embedding rows of `rows` tokens (device array) into h [rows][d].
+int pf_embed_rows(vrt_g3* g, const uint32_t* tokens, uint32_t rows, float* h, hipStream_t s) {
+    const uint8_t* te = g->P.tok_embd;
+    uint32_t d = g->cfg.embedding_length;
+    float es = g->P.emb_scale;
+    void* args[] = {&te, &tokens, &d, &es, &h};
+    VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_embed), dim3(rows), dim3(kPfThreads), args, 0, s));
+    return VRT_OK;
+}
+
+// Logits of M rows against the tied Q8_0 embedding table: logits [M][vocab] = x W_embd^T, x as
+// f16 hi/lo [M][d] (MFMA on the Q8_0 rows of the arena, one K split).
+int pf_lm_logits(vrt_g3* g, const _Float16* xhi, const _Float16* xlo, uint32_t M, float* logits, hipStream_t s) {
+    return pf_gemm(g, xhi, xlo, M, g->cfg.embedding_length, {{g->P.tok_embd, g->cfg.vocab_size}}, nullptr, logits, 1u, s);
 }
 
 static uint32_t pf_pad(uint32_t T) { return (T + kPfTile - 1u) / kPfTile * kPfTile; }
@@ -1350,7 +1397,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
         {   // previous block's FFN output into the residual, then the attention norm
             const float* f = l ? x : nullptr;
             const float* wpost = l ? g->layers[l - 1].post_ffw : nullptr;
-            if (int rc = pf_norm(h, f, s_down, xs, wpost, Ly.attn_norm, d, eps, ahi, alo, st, l ? l - 1u : 0u, T, s))
+            if (int rc = pf_norm(h, f, s_down, xs, wpost, Ly.attn_norm, d, eps, ahi, alo, st, l ? l - 1u : 0u, T, s, true))
                 return rc;
         }
         if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, lw ? &lw[l].qkv : nullptr, big, 1, s)) return rc;
@@ -1388,7 +1435,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
         {   // attention output into the residual, then the FFN norm (the O partials of fr rows)
             const uint64_t xo = static_cast<uint64_t>(fr) * d;
             if (int rc = pf_norm(h + a0, x, so, xo, Ly.post_attn, Ly.ffn_norm, d, eps, ahi + a0, alo + a0, st, Ly.index,
-                                 fr, s))
+                                 fr, s, true))
                 return rc;
         }
         // gelu(gate) * up as f16 hi/lo in `big` (the gate/up GEMM still reads ahi/alo).

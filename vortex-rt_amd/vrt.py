@@ -101,6 +101,12 @@ SIGNATURES = {
     "vrt_g3_time_lm_head": (_I, [_P, _U32, C.POINTER(_F)]),
     "vrt_g3_read_trace": (_I, [_P, _P, _U64, C.POINTER(_U32), C.POINTER(_U32)]),
     "vrt_g3_read_exchange": (_I, [_P, _U32, _P, _U64, C.POINTER(_U64)]),
+    "vrt_g3_batch_create": (_I, [_P, _U32, _U32, C.POINTER(_P)]),
+    "vrt_g3_batch_destroy": (_I, [_P]),
+    "vrt_g3_batch_reset": (_I, [_P, _U32]),
+    "vrt_g3_batch_step": (_I, [_P, _P, _P, _U32, _P]),
+    "vrt_g3_batch_position": (_I, [_P, _U32, C.POINTER(_U32)]),
+    "vrt_g3_batch_logits": (_I, [_P, _U32, _P, _U32]),
 }
 
 _lib = None
@@ -448,3 +454,78 @@ class Gemma3:
         us = C.c_float()
         check(lib().vrt_g3_time_lm_head(self.h, iters, C.byref(us)))
         return float(us.value)
+
+
+class Gemma3Batch:
+    """Batched greedy decode over independent sequences that share a Gemma3 executor's weights
+    (vrt_g3_batch_*): each sequence has its own KV cache and position."""
+
+    def __init__(self, model: "Gemma3", max_seqs: int, max_ctx: int):
+        self.h = None
+        self.model = model
+        self.max_seqs = max_seqs
+        h = C.c_void_p()
+        check(lib().vrt_g3_batch_create(model.h, max_seqs, max_ctx, C.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib().vrt_g3_batch_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def reset(self, seq=None):
+        check(lib().vrt_g3_batch_reset(self.h, 0xFFFFFFFF if seq is None else seq))
+
+    def position(self, seq: int) -> int:
+        p = C.c_uint32()
+        check(lib().vrt_g3_batch_position(self.h, seq, C.byref(p)))
+        return p.value
+
+    def step(self, seqs, tokens):
+        """One step: sequence seqs[i] consumes tokens[i]; returns (indices, values)."""
+        s = np.ascontiguousarray(seqs, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        if s.size != t.size:
+            raise ValueError("seqs and tokens differ in length")
+        out = np.zeros(s.size, dtype=np.dtype([("index", np.uint32), ("value", np.float32)]))
+        check(lib().vrt_g3_batch_step(self.h, ptr(s), ptr(t), s.size, ptr(out)))
+        return out["index"].copy(), out["value"].copy()
+
+    def logits(self, row: int) -> np.ndarray:
+        out = np.empty(self.model.config.vocab_size, dtype=np.float32)
+        check(lib().vrt_g3_batch_logits(self.h, row, ptr(out), out.size))
+        return out
+
+    def generate(self, prompts, max_new: int, starts=None, eos=None):
+        """Continuous batching: sequence i joins at step starts[i] (default 0), feeds its prompt
+        one token per step, then its own greedy tokens, until max_new tokens or EOS. Returns the
+        generated ids per sequence."""
+        n = len(prompts)
+        if n > self.max_seqs:
+            raise ValueError("more prompts than sequences")
+        starts = [0] * n if starts is None else list(starts)
+        feed = [list(np.asarray(p, dtype=np.uint32)) for p in prompts]
+        gen = [[] for _ in range(n)]
+        done = [False] * n
+        for i in range(n):
+            self.reset(i)
+        step = 0
+        while not all(done):
+            rows = [i for i in range(n) if not done[i] and step >= starts[i]]
+            if rows:
+                toks = [feed[i][0] if feed[i] else gen[i][-1] for i in rows]
+                idx, _ = self.step(rows, toks)
+                for i, r in zip(rows, idx):
+                    if feed[i]:
+                        feed[i].pop(0)
+                        if feed[i]:
+                            continue
+                    gen[i].append(int(r))
+                    if len(gen[i]) >= max_new or (eos is not None and int(r) == eos):
+                        done[i] = True
+            step += 1
+        return [np.asarray(g, dtype=np.uint32) for g in gen]
+
