@@ -243,6 +243,33 @@ def multikernel_leg(ctx, g, prompt, steps: int = 64):
             "us_per_step": round(ms * 1e3 / steps, 1), "tokens_per_s": round(steps / (ms / 1e3), 1)}
 
 
+def batched_leg(ctx, g, cfg, sizes=(1, 8, 32, 64), n_prompt: int = 8, steps: int = 16):
+    """Batched greedy decode (vrt_g3_batch_step): B sequences with their own 8-token prompts advance
+    together, one position per step; after the prompts, `steps` timed steps in which every
+    sequence feeds back its greedy token. Each step includes its host round trip (upload of the
+    step's rows, results back), as a serving loop would see it."""
+    import vrt
+    out = {"workload": f"B independent sequences: {n_prompt}-token prompts fed one per step, then {steps} timed "
+                       f"steps of B greedy tokens (positions {n_prompt}..{n_prompt + steps - 1})", "batches": {}}
+    for B in sizes:
+        b = vrt.Gemma3Batch(g, B, n_prompt + steps + 8)
+        try:
+            prompts = [synth_ids(1000 + i, n_prompt, cfg.vocab_size) for i in range(B)]
+            seqs = list(range(B))
+            idx = None
+            for k in range(n_prompt):
+                idx, _ = b.step(seqs, [int(p[k]) for p in prompts])
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                idx, _ = b.step(seqs, [int(t) for t in idx])
+            dt = time.perf_counter() - t0
+        finally:
+            b.close()
+        out["batches"][str(B)] = {"ms_per_step": round(dt * 1e3 / steps, 3),
+                                  "tokens_per_s": round(B * steps / dt, 1)}
+    return out
+
+
 def copy_calibration(nbytes: int = 1 << 30):
     """A plain device copy of known size for scaling the PMC counters (FETCH_SIZE / WRITE_SIZE
     of this dispatch against nbytes read and nbytes written)."""
@@ -296,6 +323,7 @@ def main():
                     help="skip the standalone matvec / QKV / FFN measurements (single-matvec and layer-block workloads)")
     ap.add_argument("--multikernel", action="store_true",
                     help="also time the multi-kernel (hipGraph) decode path")
+    ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (B sequences) measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
@@ -362,6 +390,7 @@ def main():
     prefill = None if args.no_prefill else prefill_bench(ctx, g, cfg)
     kernels = None if args.no_kernels else kernel_legs(ctx)
     multikernel = multikernel_leg(ctx, g, prompt) if args.multikernel else None
+    batched = None if args.no_batched else batched_leg(ctx, g, cfg)
 
     out = {
         "metric": METRIC,
@@ -405,6 +434,7 @@ def main():
         "prefill": prefill,
         "kernels": kernels,
         "multikernel": multikernel,
+        "batched": batched,
         "cpu_baseline": None,
     }
     g.close()

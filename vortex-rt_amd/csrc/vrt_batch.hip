@@ -161,23 +161,32 @@ __global__ void __launch_bounds__(kBdThreads) k_bd_attn(BdAttn A) {
             A.kc[o] = sk[i];
             A.vc[o] = sv[i];
         }
-    // scores of the chunk's positions
-    for (uint32_t t = c0 + wave; t < c1; t += kBdThreads / 64u) {
-        const uint64_t row = cache0 + static_cast<uint64_t>(t % A.slots) * hd;
-        float kr[4];
+    // scores of the chunk's positions: wave w takes positions c0 + w + 4 i, eight at a time, their
+    // key rows loaded together first (at clamped positions; the current position comes from LDS)
+    constexpr uint32_t kG8 = 8u, nw = kBdThreads / 64u;
+    for (uint32_t t0 = c0 + wave; t0 < c1; t0 += nw * kG8) {
+        float kr[kG8][4];
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) {
-            const uint32_t i = min(lane + 64u * e, hd - 1u);
-            kr[e] = t == p ? sk[i] : A.kc[row + i];
-            if (lane + 64u * e >= hd) kr[e] = 0.0f;
+        for (uint32_t u = 0; u < kG8; ++u) {
+            const uint64_t row = cache0 + static_cast<uint64_t>(min(t0 + nw * u, c1 - 1u) % A.slots) * hd;
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) kr[u][e] = A.kc[row + min(lane + 64u * e, hd - 1u)];
         }
-        for (uint32_t h = 0; h < H; ++h) {
-            float d = 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < kG8; ++u) {
+            const uint32_t t = t0 + nw * u;
+            if (t >= c1) break;
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e)
-                if (lane + 64u * e < hd) d += sx[h * hd + lane + 64u * e] * kr[e];
-            d = wave_sum(d);
-            if (lane == 0u) ssc[h * A.cmax + (t - c0)] = d * A.attn_scale;
+                if (t == p) kr[u][e] = sk[min(lane + 64u * e, hd - 1u)];
+            for (uint32_t h = 0; h < H; ++h) {
+                float d = 0.0f;
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e)
+                    if (lane + 64u * e < hd) d += sx[h * hd + lane + 64u * e] * kr[u][e];
+                d = wave_sum(d);
+                if (lane == 0u) ssc[h * A.cmax + (t - c0)] = d * A.attn_scale;
+            }
         }
     }
     __syncthreads();
@@ -201,14 +210,23 @@ __global__ void __launch_bounds__(kBdThreads) k_bd_attn(BdAttn A) {
         }
     }
     __syncthreads();
-    // weighted values: thread i owns dims i, i + 256, ...
+    // weighted values: thread i owns dims i, i + 256, ...; eight positions' values loaded together
     for (uint32_t i = tid; i < hd; i += kBdThreads) {
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t t = c0; t < c1; ++t) {
-            const float vv = t == p ? sv[i] : A.vc[cache0 + static_cast<uint64_t>(t % A.slots) * hd + i];
+        for (uint32_t t0 = c0; t0 < c1; t0 += kG8) {
+            float vv[kG8];
 #pragma unroll
-            for (uint32_t h = 0; h < 8u; ++h)
-                if (h < H) acc[h] += ssc[h * A.cmax + (t - c0)] * vv;
+            for (uint32_t u = 0; u < kG8; ++u)
+                vv[u] = A.vc[cache0 + static_cast<uint64_t>(min(t0 + u, c1 - 1u) % A.slots) * hd + i];
+#pragma unroll
+            for (uint32_t u = 0; u < kG8; ++u) {
+                const uint32_t t = t0 + u;
+                if (t >= c1) break;
+                const float x = t == p ? sv[i] : vv[u];
+#pragma unroll
+                for (uint32_t h = 0; h < 8u; ++h)
+                    if (h < H) acc[h] += ssc[h * A.cmax + (t - c0)] * x;
+            }
         }
 #pragma unroll
         for (uint32_t h = 0; h < 8u; ++h)
