@@ -324,6 +324,9 @@ def main():
     ap.add_argument("--multikernel", action="store_true",
                     help="also time the multi-kernel (hipGraph) decode path")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (B sequences) measurement")
+    ap.add_argument("--only", choices=("prefill", "batched", "kernels"),
+                    help="run only this leg and print it (no decode timing, so no cooperative launch: for "
+                         "profiling one leg at a time)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
@@ -348,6 +351,14 @@ def main():
     ctx = vrt.Context("")
     g = vrt.Gemma3(ctx, args.model)
     cfg = g.config
+    if args.only:
+        legs = {"prefill": lambda: prefill_bench(ctx, g, cfg), "batched": lambda: batched_leg(ctx, g, cfg),
+                "kernels": lambda: kernel_legs(ctx)}
+        res = legs[args.only]()
+        g.close()
+        ctx.close()
+        print(json.dumps({"only": args.only, args.only: res}))
+        return
     if not g.persistent_available():
         raise SystemExit("[bench] the persistent decode kernel is unavailable for this shape/device")
     prompt = synth.uniform_ids(0, 8, 2, cfg.vocab_size)
