@@ -21,6 +21,12 @@
 //   D  all   h = RMSNorm(o, post_attn) + h, x = RMSNorm(h, ffn_norm), gate/up row pairs,
 //            g = gelu_tanh(gate) * up                                             (:1703-1801)
 //   E  ne    Wd rows -> f
+// Short histories (min(pos + 1, slots) <= kMkFuseHist) replace B and C with one phase on the
+// first nbc workgroups: workgroup w takes query head w % H and a group of output rows, runs head
+// h's attention over the whole history (the same values in every group of the head: the history
+// is short, and the hand-off B -> C it saves costs more), normalises it and computes its rows of
+// the O projection over head h's columns only; D adds the H per-head partials of each row in
+// head order. Every workgroup then produces in A and D.
 // After the last block every workgroup folds f into h; when the step runs the LM head all of
 // them stream an even share of the tied Q8_0 table (staged through LDS with 16-byte loads),
 // keep a local greedy argmax and publish it; the next step (or workgroup 0 at the end of the
@@ -86,6 +92,11 @@ constexpr int kRsrcFlags = 0x00020000;       // raw buffer resource, 32-bit data
 // either system- or device-scope stores and loads.)
 constexpr int kCoherent = 17;                // buffer-load aux bits: sc0 | sc1
 constexpr uint32_t kMarks = 40;              // sub-phase trace marks (the last two: shader clock)
+constexpr uint32_t kMkFuseHeads = 4;         // query heads of the fused attention + O phase, at most
+// Histories up to this length use it: measured on the 270M shape, a step with every block fused
+// takes 339 us at histories 9-28 and 365 us at 41-60 (375 and 387 us unfused), but 409 us at
+// 101-164 (397 us unfused), where the redundant per-group attention costs more than the hand-off.
+constexpr uint32_t kMkFuseHist = 64;
 
 struct MkLayer {
     const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
@@ -114,12 +125,15 @@ struct MkParams {
     uint32_t lm_tile_rows;         // rows per LDS tile
     uint32_t trace_slots;          // phase timestamps per workgroup (0: tracing off)
     uint32_t kv_f16;               // KV cache entries as fp16 (2 bytes)
+    uint32_t fuse_hist;            // histories up to this length run the fused attention + O phase (0: never)
+    uint32_t nbc;                  // workgroups of the fused phase (whole groups of H)
     MkLds lds;
     const uint8_t* tok_embd;
     const uint8_t* arena_end;
     const float* out_norm;
     const float *cos_l, *sin_l, *cos_g, *sin_g;
     u64 *x_qkv, *x_part, *x_o, *x_g, *x_f, *x_am;
+    u64* x_o4;                     // fused phase: the O projection's per-head partials [H][d]
     uint32_t* abort_flag;
     G3State* st;
     uint32_t* tokens;
@@ -248,7 +262,9 @@ __device__ __forceinline__ void attn_split(uint32_t hist, uint32_t max_chunks, u
 }
 
 // Attention workgroups of a block at a position: one per (chunk, query head).
+__device__ __forceinline__ bool mk_fused(uint32_t slots, uint32_t pos) { return min(pos + 1u, slots) <= g_mk.fuse_hist; }
 __device__ __forceinline__ uint32_t n_bunits(uint32_t slots, uint32_t pos) {
+    if (mk_fused(slots, pos)) return 0u;   // the fused phase's workgroups also produce in A and D
     uint32_t nch, clen;
     attn_split(min(pos + 1u, slots), g_mk.max_chunks, g_mk.chunk_min, nch, clen);
     return nch * g_mk.H;
@@ -474,10 +490,10 @@ static_assert(kMkWaves == 8, "sum_waves adds eight wave totals");
 // only its own pairs of h; x goes to x_lds and, if given, to x_glob. `bad` is set when h has a
 // non-finite element (:1857-1863). Ends with a barrier; returns 1 if the gather was abandoned
 // (the same decision in every thread).
-template <int EP, bool INTO>
+template <int EP, bool INTO, int NP = 1>
 __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const float* w_post, const float* w_next,
                                         float* hl, float* x_lds, float* x_glob, uint32_t d, float eps, int& bad,
-                                        bool tr = false, uint32_t mk0 = 31u) {
+                                        bool tr = false, uint32_t mk0 = 31u, uint32_t nparts = 1u) {
 #pragma clang fp contract(off)
     constexpr int P = (EP * 64 + static_cast<int>(kMkThreads) - 1) / static_cast<int>(kMkThreads);
     auto mark = [&](uint32_t k) {
@@ -503,15 +519,30 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
         y[k] = make_float2(0.0f, 0.0f);
     }
     if (ysrc) {
+        // y is the sum of nparts <= NP partial vectors ysrc[q * d ..], added in order q = 0, 1, ...
         const __amdgpu_buffer_rsrc_t r =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(ysrc), 0, static_cast<int>(d * 8u), kRsrcFlags);
-        int off[P];
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(ysrc), 0, static_cast<int>(NP * d * 8u), kRsrcFlags);
+        int off[P * NP];
+        bool lv[P * NP];
 #pragma unroll
-        for (int k = 0; k < P; ++k) off[k] = live[k] ? static_cast<int>(j[k] * 16u) : 0x7ffffff0;   // past: no access
-        float yv[2 * P];
-        const int fail = ll_poll2<P>(r, off, live, tag, yv);
+        for (int k = 0; k < P; ++k)
 #pragma unroll
-        for (int k = 0; k < P; ++k) y[k] = live[k] ? make_float2(yv[2 * k], yv[2 * k + 1]) : make_float2(0.0f, 0.0f);
+            for (int q = 0; q < NP; ++q) {
+                lv[k * NP + q] = live[k] && static_cast<uint32_t>(q) < nparts;
+                off[k * NP + q] = lv[k * NP + q] ? static_cast<int>((q * d + 2u * j[k]) * 8u) : 0x7ffffff0;   // past: no access
+            }
+        float yv[2 * P * NP];
+        const int fail = ll_poll2<P * NP>(r, off, lv, tag, yv);
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            y[k] = lv[k * NP] ? make_float2(yv[2 * k * NP], yv[2 * k * NP + 1]) : make_float2(0.0f, 0.0f);
+#pragma unroll
+            for (int q = 1; q < NP; ++q)
+                if (lv[k * NP + q]) {
+                    y[k].x += yv[2 * (k * NP + q)];
+                    y[k].y += yv[2 * (k * NP + q) + 1];
+                }
+        }
         mark(mk0);
         double sq[2 * P];
 #pragma unroll
@@ -638,7 +669,7 @@ constexpr uint32_t kBLongChunk = 128;              // chunks at least this long 
 // Publishes the unnormalised partial {acc[hd] of head h, m, l} of (c, h).
 // Inlined into the kernel: as a call it would save and restore callee-saved registers through
 // scratch.
-template <bool KVH>
+template <bool KVH, bool fused>
 __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
@@ -651,8 +682,22 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     const uint32_t t_first = pos + 1u - hist;
     uint32_t nch, clen;
     attn_split(hist, g_mk.max_chunks, g_mk.chunk_min, nch, clen);
-    const uint32_t u = bunit_of(w, g_mk.nwg);   // caller guarantees u < H * nch
+    if constexpr (fused) {   // one chunk: the whole (short) history
+        nch = 1u;
+        clen = hist;
+    }
+    const uint32_t u = fused ? w % H : bunit_of(w, g_mk.nwg);   // caller guarantees u < H * nch (fused: w < nbc)
     const uint32_t c = u / H, h = u % H;
+    // fused: this workgroup's O-projection rows over head h's columns, loaded before any wait
+    const uint32_t nbh = hd >> 5;
+    RowBatch<8, 1, 1> orb;
+    if constexpr (fused) {
+        uint32_t v0, v1;
+        split_range(d, g_mk.nbc / H, w / H, v0, v1);
+        const uint8_t* wo = Ly.wo + static_cast<uint64_t>(h) * nbh * 34u;
+        auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
+        batch_load<8, 1, 1>(rowp, nbh, g_mk.arena_end, v0, v1, wave, orb);
+    }
     MK_MARK(6);
     const uint32_t c0 = t_first + c * clen;
     const uint32_t c1 = min(pos + 1u, c0 + clen);
@@ -851,7 +896,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         // this wave's next vector-memory wait in a later phase completes the stores, and every
         // such phase precedes a publication that the next step's attention depends on (vector
         // memory operations complete in issue order), so no wait is needed here.
-        const bool appender = h == 0u && c1 == pos + 1u && uw == 0u;
+        const bool appender = (fused ? w == 0u : h == 0u) && c1 == pos + 1u && uw == 0u;
         if (appender && dlive && !fail) {
             const uint32_t so = ((pos % Ly.slots) * hd + dl) * esz;
             if constexpr (KVH) {   // k and v are already fp16 values: the conversion is exact
@@ -898,17 +943,30 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
 #pragma unroll
         for (uint32_t k = 0; k < kBMaxWaves; ++k)
             if (k < nbw) sacc += f[k] * ra[k * hd + tid];   // the other waves' slots are stale
-        ll_stf(part + h * hd + tid, sacc, tB);
-        if (tid < kLine) {   // this unit's line: m, l, then padding (every word is tagged)
-            float L = 0.0f;
+        float L = 0.0f;
 #pragma unroll
-            for (uint32_t k = 0; k < kBMaxWaves; ++k)
-                if (k < nbw) L += f[k] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lk), k));
-            const float Mu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(M), 0));
-            ll_stf(part + qw + kLine * h + tid, tid == 0u ? Mu : (tid == 1u ? L : 0.0f), tB);
+        for (uint32_t k = 0; k < kBMaxWaves; ++k)
+            if (k < nbw) L += f[k] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lk), k));
+        if constexpr (fused) {
+            // att = acc / l: phase C's merge for one chunk (its weight e^(m - m) is 1); the
+            // softmax check of :1666-1670 by the first group of each head
+            m.xs[tid] = sacc / L;
+            if (tid == 0u && w < H && (!(L > 0.0f) || !__builtin_isfinite(L))) mk_flag_min(g3_code_softmax(l));
+        } else {
+            ll_stf(part + h * hd + tid, sacc, tB);
+            if (tid < kLine) {   // this unit's line: m, l, then padding (every word is tagged)
+                const float Mu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(M), 0));
+                ll_stf(part + qw + kLine * h + tid, tid == 0u ? Mu : (tid == 1u ? L : 0.0f), tB);
+            }
         }
     }
     MK_MARK(10);
+    if constexpr (fused) {   // head h's share of the O projection rows: x_o4[h][row]
+        __syncthreads();
+        u64* out = g_mk.x_o4 + static_cast<uint64_t>(h) * d;
+        batch_consume_x<8, 1, 1>(orb, nbh, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tC); });
+        MK_MARK(14);
+    }
     return true;
 }
 
@@ -1008,7 +1066,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
 
 // Phase D: h = RMSNorm(o, post_attn) + h, x = RMSNorm(h, ffn_norm), gate/up row pairs,
 // g = gelu_tanh(gate) * up (src/gemma3.cpp:1703-1801, shaders/gelu_mul.comp:23-31).
-template <int SD, int EP>
+template <int SD, int EP, bool fused>
 __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
     MK_LOCALS;
@@ -1027,8 +1085,14 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     RowBatch<SD, 1, 2> rb;
     batch_load<SD, 1, 2>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
     int none = 0;
-    if (mk_resid<EP, true>(g_mk.x_o, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps, none, tr, 27u))
+    if constexpr (fused) {   // the fused phase's per-head partials, added in head order
+        if (mk_resid<EP, true, kMkFuseHeads>(g_mk.x_o4, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps,
+                                             none, tr, 27u, H))
+            return false;
+    } else if (mk_resid<EP, true>(g_mk.x_o, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps, none, tr,
+                                  27u)) {
         return false;
+    }
     MK_MARK(17);
     float* gu = m.gu;
     batch_consume_x<SD, 1, 2>(rb, nblk_d, m.xd, [&](uint32_t v, float val) { gu[v - v0] = val; });
@@ -1317,12 +1381,15 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             ok = mk_phase_a<SD, EP>(l, s, tagb, tr);
             MK_TRACE(5u * l + 1u);
             // B, C and E run on a subset of the workgroups; the others skip the call (and its
-            // register save/restore through scratch) entirely
-            ok = ok && (!mk_in_b(l, s) || mk_phase_b<KVH>(l, s, tagb, tr));
+            // register save/restore through scratch) entirely. Short histories run B fused
+            // with the O projection on the first nbc workgroups, and no C.
+            const bool fz = mk_fused(g_mk_layers[l].slots, s);
+            if (fz) ok = ok && (w >= g_mk.nbc || mk_phase_b<KVH, true>(l, s, tagb, tr));
+            else ok = ok && (!mk_in_b(l, s) || mk_phase_b<KVH, false>(l, s, tagb, tr));
             MK_TRACE(5u * l + 2u);
-            ok = ok && (w >= g_mk.nc || mk_phase_c<SA>(l, s, tagb, tr));
+            ok = ok && (fz || w >= g_mk.nc || mk_phase_c<SA>(l, s, tagb, tr));
             MK_TRACE(5u * l + 3u);
-            ok = ok && mk_phase_d<SD, EP>(l, s, tagb, tr);
+            ok = ok && (fz ? mk_phase_d<SD, EP, true>(l, s, tagb, tr) : mk_phase_d<SD, EP, false>(l, s, tagb, tr));
             MK_TRACE(5u * l + 4u);
             ok = ok && (w >= g_mk.ne || mk_phase_e<SF>(l, tagb, tr));
             MK_TRACE(5u * l + 5u);
@@ -1509,6 +1576,12 @@ int mk_setup(vrt_g3* g) {
     P.nc = std::min(nwg - H * max_chunks, (d + std::min(cap_a, kLine / 2u) - 1u) / std::min(cap_a, kLine / 2u));
     P.ne = std::min(nwg, (d + std::min(cap_f, kLine / 2u) - 1u) / std::min(cap_f, kLine / 2u));
     if ((d + P.nc - 1u) / P.nc > cap_a || (d + P.ne - 1u) / P.ne > cap_f) { mk_destroy(g); return VRT_OK; }
+    {   // fused attention + O phase: nc / H row groups per head, one 64-row pass of 8-lane slots
+        const uint32_t ng = P.nc / H;
+        const bool ok = H <= kMkFuseHeads && ng >= 1u && (d + ng - 1u) / ng <= kMkWaves * 8u && hd / 32u <= 8u;
+        P.fuse_hist = ok ? kMkFuseHist : 0u;
+        P.nbc = ok ? ng * H : 0u;
+    }
     P.chunk_min = 32u;
     P.max_chunks = max_chunks;
     P.lm_rows = (c.vocab_size + nwg - 1u) / nwg;
@@ -1557,6 +1630,8 @@ int mk_setup(vrt_g3* g) {
     P.x_part = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
     P.x_o = static_cast<u64*>(p);
+    if (int rc = mk_alloc(mk, static_cast<size_t>(kMkFuseHeads) * d * 8u, &p)) return rc;
+    P.x_o4 = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, F * 8u, &p)) return rc;
     P.x_g = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
@@ -1675,6 +1750,7 @@ int mk_run(vrt_g3* g, uint32_t nsteps) {
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_part, 0, static_cast<size_t>(kMaxChunks) * (qw + kLine * g->cfg.head_count) * 8u,
                                      g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_o, 0, d * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_o4, 0, static_cast<size_t>(kMkFuseHeads) * d * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_g, 0, F * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_f, 0, d * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_am, 0, kLine * mk->grid * 8u, g->ctx->stream));
