@@ -721,15 +721,23 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
         // cached positions [c0, cend); the current position itself comes from registers
         const uint32_t cend = c1 == pos + 1u ? pos : c1;
-        // byte offset of this lane's dims of position t (past the buffer for dead lanes: no access)
-        auto kv_off = [&](uint32_t t) { return dlive ? static_cast<int>(((t % Ly.slots) * hd + dl) * esz) : 0x7ffffff0; };
+        // Byte offset of this lane's dims of position t, past the buffer (a load that returns
+        // zeros) for dead lanes and for positions that are not valid. The positions of a chunk
+        // are consecutive and fewer than `slots`, so their ring index wraps at most once.
+        const uint32_t r0 = c0 % Ly.slots, row_bytes = hd * esz;
+        const uint32_t lane_off = dlive ? dl * esz : 0x7ffffff0u;
+        auto kv_off = [&](uint32_t t, bool valid) {
+            uint32_t sl = r0 + (t - c0);
+            sl = sl >= Ly.slots ? sl - Ly.slots : sl;
+            return static_cast<int>((valid ? sl * row_bytes : 0x7ffffff0u) + lane_off);
+        };
         // this lane's four dims of a cached position, as loaded (fp32 bits, or four fp16 halves
         // that are converted where they are used, so the prefetch of the next group does not wait)
         typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
         using KvReg = typename std::conditional<KVH, v2u, v4u>::type;
-        auto kv_ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t t) -> KvReg {
-            if constexpr (KVH) return __builtin_amdgcn_raw_buffer_load_b64(r, kv_off(t), 0, kCoherent);
-            else return co_ld4(r, kv_off(t));
+        auto kv_ld = [&](__amdgpu_buffer_rsrc_t r, int off) -> KvReg {
+            if constexpr (KVH) return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCoherent);
+            else return co_ld4(r, static_cast<uint32_t>(off));
         };
         auto kv_el = [](const KvReg& x, uint32_t e) -> float {
             if constexpr (KVH) return static_cast<float>(__builtin_bit_cast(half4_t, x)[e]);
@@ -737,17 +745,16 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         };
         // how many of this wave's positions g0 + uw + nbw i fall below g1 (wave-uniform)
         auto nvalid = [&](uint32_t g0, uint32_t g1) { return g1 > g0 + uw ? (g1 - g0 - uw + nbw - 1u) / nbw : 0u; };
+        // positions past a wave's share of a group load zeros: no branch per load, and the
+        // masked positions' value rows are zeros (not stale cache entries) under weight 0
         KvReg kr[kBPos], vr[kBPos];
         {
             const uint32_t nv = nvalid(c0, min(cend, c0 + grp));
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i) {
-                kr[i] = vr[i] = KvReg{};
-                if (i < nv) {
-                    const uint32_t t = c0 + uw + nbw * i;
-                    kr[i] = kv_ld(rk, t);
-                    vr[i] = kv_ld(rv, t);
-                }
+                const int o = kv_off(c0 + uw + nbw * i, i < nv);
+                kr[i] = kv_ld(rk, o);
+                vr[i] = kv_ld(rv, o);
             }
         }
         // norm weights and RoPE factors of this lane's dims
@@ -827,9 +834,9 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             float part[kBPos];
 #pragma unroll
             for (uint32_t i = 0; i < kBPos; ++i) {
-                float p = 0.0f;
+                float p = q[0] * kv_el(kr[i], 0);
 #pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) p += q[e] * kv_el(kr[i], e);
+                for (uint32_t e = 1; e < 4u; ++e) p = fmaf(q[e], kv_el(kr[i], e), p);
                 part[i] = p;
             }
             // lane l: the score of position g0 + uw + nbw (l & 7). The reduction runs in every
@@ -839,9 +846,13 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             // the next group's keys load while this group's softmax and values run
             const uint32_t n0 = g0 + grp;
             const uint32_t nn = n0 < cend ? nvalid(n0, min(cend, n0 + grp)) : 0u;
+            int no[kBPos];
 #pragma unroll
-            for (uint32_t i = 0; i < kBPos; ++i)
-                if (i < nn) kr[i] = kv_ld(rk, n0 + uw + nbw * i);
+            for (uint32_t i = 0; i < kBPos; ++i) no[i] = kv_off(n0 + uw + nbw * i, i < nn);
+            if (nn != 0u) {
+#pragma unroll
+                for (uint32_t i = 0; i < kBPos; ++i) kr[i] = kv_ld(rk, no[i]);
+            }
             if (nv != 0u) {   // this wave has a position in the group
                 float mx = fmaxf(sl, dpp_mov<0xB1>(sl));
                 mx = fmaxf(mx, dpp_mov<0x4E>(mx));
@@ -862,16 +873,17 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                     for (uint32_t e = 0; e < 4u; ++e) {
                         float a = acc[e] * r;
 #pragma unroll
-                        for (uint32_t i = 0; i < kBPos; ++i) a += pw[i] * kv_el(vr[i], e);
+                        for (uint32_t i = 0; i < kBPos; ++i) a = fmaf(pw[i], kv_el(vr[i], e), a);
                         acc[e] = a;
                     }
                     l_run = l_run * r + ls;
                     m_run = m_new;
                 }
             }
+            if (nn != 0u) {
 #pragma unroll
-            for (uint32_t i = 0; i < kBPos; ++i)
-                if (i < nn) vr[i] = kv_ld(rv, n0 + uw + nbw * i);
+                for (uint32_t i = 0; i < kBPos; ++i) vr[i] = kv_ld(rv, no[i]);
+            }
         }
         // the current position, from registers, by the wave whose turn it is
         if (c1 == pos + 1u && uw == (pos - c0) % nbw) {
