@@ -127,6 +127,8 @@ struct MkParams {
     uint32_t kv_f16;               // KV cache entries as fp16 (2 bytes)
     uint32_t fuse_hist;            // histories up to this length run the fused attention + O phase (0: never)
     uint32_t nbc;                  // workgroups of the fused phase (whole groups of H)
+    uint32_t sh_o, sh_f;           // x_o / x_f layout: 2^sh rows per 64-byte line (2: one producer's
+                                   // four rows per line, the other half unused; 3: dense)
     MkLds lds;
     const uint8_t* tok_embd;
     const uint8_t* arena_end;
@@ -249,6 +251,12 @@ __device__ __forceinline__ void split_lines(uint32_t total, uint32_t parts, uint
     split_range((total + kLine - 1u) / kLine, parts, idx, a, b);
     a = min(total, a * kLine);
     b = min(total, b * kLine);
+}
+
+// Word of row v in an exchange buffer that holds 2^sh rows per 64-byte line (sh <= 3): with
+// sh = 2 each producer of four rows owns a line of its own, the line's other half unused.
+__device__ __forceinline__ uint32_t line_word(uint32_t v, uint32_t sh) {
+    return ((v >> sh) << 3) | (v & ((1u << sh) - 1u));
 }
 
 // Attention split of a history of `hist` positions: number of chunks and chunk length.
@@ -493,7 +501,8 @@ static_assert(kMkWaves == 8, "sum_waves adds eight wave totals");
 template <int EP, bool INTO, int NP = 1>
 __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const float* w_post, const float* w_next,
                                         float* hl, float* x_lds, float* x_glob, uint32_t d, float eps, int& bad,
-                                        bool tr = false, uint32_t mk0 = 31u, uint32_t nparts = 1u) {
+                                        bool tr = false, uint32_t mk0 = 31u, uint32_t nparts = 1u,
+                                        uint32_t ysh = 3u) {
 #pragma clang fp contract(off)
     constexpr int P = (EP * 64 + static_cast<int>(kMkThreads) - 1) / static_cast<int>(kMkThreads);
     auto mark = [&](uint32_t k) {
@@ -520,8 +529,9 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
     }
     if (ysrc) {
         // y is the sum of nparts <= NP partial vectors ysrc[q * d ..], added in order q = 0, 1, ...
-        const __amdgpu_buffer_rsrc_t r =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(ysrc), 0, static_cast<int>(NP * d * 8u), kRsrcFlags);
+        // (NP == 1: element v at word line_word(v, ysh); a pair never straddles a line)
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<u64*>(ysrc), 0, static_cast<int>(NP * (d << (3u - ysh)) * 8u), kRsrcFlags);
         int off[P * NP];
         bool lv[P * NP];
 #pragma unroll
@@ -529,7 +539,8 @@ __device__ __forceinline__ int mk_resid(const u64* ysrc, uint32_t tag, const flo
 #pragma unroll
             for (int q = 0; q < NP; ++q) {
                 lv[k * NP + q] = live[k] && static_cast<uint32_t>(q) < nparts;
-                off[k * NP + q] = lv[k * NP + q] ? static_cast<int>((q * d + 2u * j[k]) * 8u) : 0x7ffffff0;   // past: no access
+                off[k * NP + q] = lv[k * NP + q] ? static_cast<int>((q * d + line_word(2u * j[k], ysh)) * 8u)
+                                                 : 0x7ffffff0;   // past: no access
             }
         float yv[2 * P * NP];
         const int fail = ll_poll2<P * NP>(r, off, lv, tag, yv);
@@ -639,7 +650,7 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
     int bad = 0;
     if (mk_resid<EP, true>(l > 0 ? g_mk.x_f : nullptr, tagb + 5u * (l - 1u) + 5u,
                            l > 0 ? g_mk_layers[l - 1u].post_ffw : nullptr, Ly.attn_norm, m.h, m.xa, nullptr, d,
-                           g_mk.eps, bad, tr))
+                           g_mk.eps, bad, tr, 31u, 1u, g_mk.sh_f))
         return false;
     if (bad && w == 0 && tid == 0 && l > 0) mk_flag_min(g3_code_nonfinite(l - 1u));   // :1857-1863
     MK_MARK(3);
@@ -1071,7 +1082,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
     __syncthreads();
     MK_MARK(13);
     u64* out = g_mk.x_o;
-    batch_consume_x<SA, 1, 1>(rb, nblk_a, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tC); });
+    const uint32_t sh = g_mk.sh_o;
+    batch_consume_x<SA, 1, 1>(rb, nblk_a, m.xs, [&](uint32_t v, float val) { ll_stf(out + line_word(v, sh), val, tC); });
     MK_MARK(14);
     return true;
 }
@@ -1102,7 +1114,7 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
                                              none, tr, 27u, H))
             return false;
     } else if (mk_resid<EP, true>(g_mk.x_o, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps, none, tr,
-                                  27u)) {
+                                  27u, 1u, g_mk.sh_o)) {
         return false;
     }
     MK_MARK(17);
@@ -1139,7 +1151,8 @@ __device__ __attribute__((noinline)) bool mk_phase_e(uint32_t l, uint32_t tagb, 
     if (!ll_gather2<kVec / 2>(g_mk.x_g, F, tD, m.xs, kAnyGatherE)) return false;
     MK_MARK(21);
     u64* out = g_mk.x_f;
-    batch_consume_x<SF, 1, 1>(rb, nblk_f, m.xs, [&](uint32_t v, float val) { ll_stf(out + v, val, tE); });
+    const uint32_t sh = g_mk.sh_f;
+    batch_consume_x<SF, 1, 1>(rb, nblk_f, m.xs, [&](uint32_t v, float val) { ll_stf(out + line_word(v, sh), val, tE); });
     MK_MARK(22);
     return true;
 }
@@ -1154,7 +1167,7 @@ __device__ __forceinline__ bool mk_fold(uint32_t tagb) {
     MK_UNIFORM(tagb);
     int bad = 0;
     if (mk_resid<EP, false>(g_mk.x_f, tagb + 5u * (L - 1u) + 5u, g_mk_layers[L - 1u].post_ffw, g_mk.out_norm, m.h, m.xa,
-                            w == 0 ? g_mk.hidden : nullptr, d, g_mk.eps, bad))
+                            w == 0 ? g_mk.hidden : nullptr, d, g_mk.eps, bad, false, 31u, 1u, g_mk.sh_f))
         return false;
     if (bad && w == 0 && tid == 0) mk_flag_min(g3_code_nonfinite(L - 1u));
     return true;
@@ -1588,6 +1601,10 @@ int mk_setup(vrt_g3* g) {
     P.nc = std::min(nwg - H * max_chunks, (d + std::min(cap_a, kLine / 2u) - 1u) / std::min(cap_a, kLine / 2u));
     P.ne = std::min(nwg, (d + std::min(cap_f, kLine / 2u) - 1u) / std::min(cap_f, kLine / 2u));
     if ((d + P.nc - 1u) / P.nc > cap_a || (d + P.ne - 1u) / P.ne > cap_f) { mk_destroy(g); return VRT_OK; }
+    // producers of exactly four rows each get a line of their own (producers on different
+    // XCDs that share a line slow the exchange)
+    P.sh_o = d == 4u * P.nc ? 2u : 3u;
+    P.sh_f = d == 4u * P.ne ? 2u : 3u;
     {   // fused attention + O phase: nc / H row groups per head, one 64-row pass of 8-lane slots
         const uint32_t ng = P.nc / H;
         const bool ok = H <= kMkFuseHeads && ng >= 1u && (d + ng - 1u) / ng <= kMkWaves * 8u && hd / 32u <= 8u;
@@ -1640,13 +1657,13 @@ int mk_setup(vrt_g3* g) {
     P.x_qkv = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, static_cast<size_t>(kMaxChunks) * (qw + kLine * H) * 8u, &p)) return rc;
     P.x_part = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, 2u * d * 8u, &p)) return rc;   // room for the line-per-producer layout
     P.x_o = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, static_cast<size_t>(kMkFuseHeads) * d * 8u, &p)) return rc;
     P.x_o4 = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, F * 8u, &p)) return rc;
     P.x_g = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, d * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, 2u * d * 8u, &p)) return rc;
     P.x_f = static_cast<u64*>(p);
     if (int rc = mk_alloc(mk, kLine * nwg * 8u, &p)) return rc;
     P.x_am = static_cast<u64*>(p);
@@ -1721,19 +1738,23 @@ int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uin
     const uint32_t qw = P.H * P.hd;
     const u64* src = nullptr;
     uint64_t cnt = 0;
+    uint32_t sh = 3u;   // rows per line of the device layout (x_o, x_f): the copy is compacted
     switch (which) {
     case 0: src = P.x_qkv; cnt = qw + 2u * P.hd; break;
     case 1: src = P.x_part; cnt = static_cast<uint64_t>(kMaxChunks) * (qw + kLine * P.H); break;
-    case 2: src = P.x_o; cnt = P.d; break;
+    case 2: src = P.x_o; cnt = P.d; sh = P.sh_o; break;
     case 3: src = P.x_g; cnt = P.F; break;
-    case 4: src = P.x_f; cnt = P.d; break;
+    case 4: src = P.x_f; cnt = P.d; sh = P.sh_f; break;
     case 5: src = P.x_am; cnt = kLine * P.nwg; break;
     default: return set_error(VRT_ERR_INVALID, "unknown exchange buffer %u", which);
     }
     *n = cnt;
     VRT_REQUIRE(cap >= cnt, "exchange buffer needs %llu words", static_cast<unsigned long long>(cnt));
     VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
-    VRT_HIP_CHECK(hipMemcpy(out, src, cnt * 8u, hipMemcpyDeviceToHost));
+    const uint64_t raw_words = cnt << (3u - sh);
+    std::vector<uint64_t> raw(raw_words);
+    VRT_HIP_CHECK(hipMemcpy(raw.data(), src, raw_words * 8u, hipMemcpyDeviceToHost));
+    for (uint64_t v = 0; v < cnt; ++v) out[v] = raw[((v >> sh) << 3) | (v & ((1u << sh) - 1u))];
     return VRT_OK;
 }
 
@@ -1761,10 +1782,10 @@ int mk_run(vrt_g3* g, uint32_t nsteps) {
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_qkv, 0, (qw + 2u * g->cfg.head_dim) * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_part, 0, static_cast<size_t>(kMaxChunks) * (qw + kLine * g->cfg.head_count) * 8u,
                                      g->ctx->stream));
-        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_o, 0, d * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_o, 0, 2u * d * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_o4, 0, static_cast<size_t>(kMkFuseHeads) * d * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_g, 0, F * 8u, g->ctx->stream));
-        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_f, 0, d * 8u, g->ctx->stream));
+        VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_f, 0, 2u * d * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipMemsetAsync(mk->P.x_am, 0, kLine * mk->grid * 8u, g->ctx->stream));
         g->mk_tag = 1u;
     }
