@@ -699,75 +699,114 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     }
     const uint32_t u = fused ? w % H : bunit_of(w, g_mk.nwg);   // caller guarantees u < H * nch (fused: w < nbc)
     const uint32_t c = u / H, h = u % H;
-    // fused: this workgroup's O-projection rows over head h's columns, loaded before any wait
-    const uint32_t nbh = hd >> 5;
-    RowBatch<8, 1, 1> orb;
-    if constexpr (fused) {
-        uint32_t v0, v1;
-        split_range(d, g_mk.nbc / H, w / H, v0, v1);
-        const uint8_t* wo = Ly.wo + static_cast<uint64_t>(h) * nbh * 34u;
-        auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
-        batch_load<8, 1, 1>(rowp, nbh, g_mk.arena_end, v0, v1, wave, orb);
-    }
-    MK_MARK(6);
     const uint32_t c0 = t_first + c * clen;
     const uint32_t c1 = min(pos + 1u, c0 + clen);
     const uint32_t uw = __builtin_amdgcn_readfirstlane(wave);   // scalar: positions and branches on SALU
     // waves taking positions: four (one per SIMD) for short chunks, all eight for long ones
     const uint32_t nbw = clen >= kBLongChunk ? kBMaxWaves : 4u, grp = nbw * kBPos;
     const bool worker = uw < nbw;
+    // With four workers, wave 4 polls q|k|v, normalises and rotates them and hands them to the
+    // workers through LDS, so the workers' key/value loads and the poll wait in different waves'
+    // memory queues (a wave's vector-memory operations complete in issue order). With eight
+    // workers each one polls for itself.
+    const bool shared_q = nbw < kBMaxWaves;
+    const bool poller = shared_q ? uw == nbw : worker;
+    // fused: this workgroup's O-projection rows over head h's columns, loaded before any wait, by
+    // the waves past the poller when they can hold them all (8 rows each)
+    const uint32_t nbh = hd >> 5;
+    RowBatch<8, 1, 1> orb;
+    if constexpr (fused) {
+        uint32_t v0, v1;
+        split_range(d, g_mk.nbc / H, w / H, v0, v1);
+        const uint32_t ow0 = shared_q && v1 - v0 <= (kBMaxWaves - nbw - 1u) * 8u ? nbw + 1u : 0u;
+        const uint8_t* wo = Ly.wo + static_cast<uint64_t>(h) * nbh * 34u;
+        auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
+        orb.live[0] = false;
+        if (uw >= ow0) batch_load<8, 1, 1>(rowp, nbh, g_mk.arena_end, v0, v1, uw - ow0, orb);
+    }
+    MK_MARK(6);
     const uint32_t dl = lane * 4u;                 // this lane's 4 head dims
-    const bool dlive = worker && dl < hd;
+    const bool dlive = dl < hd;
     const bool lo = dl < half;                     // first half of the RoPE pairs
     const uint32_t e0 = lo ? dl : dl - half;       // RoPE index of dim dl
     const int partner = static_cast<int>(lo ? lane + (half >> 2) : lane - (half >> 2));
     float* ra = m.u;                               // [kBMaxWaves][hd] partial sums
     float* rml = m.mw;                             // [kBMaxWaves] m, then [kBMaxWaves] l
+    float* qsh = m.u + kBMaxWaves * hd;            // [3][hd] q, k, v handed from the poller to the workers
     int fail = 0;
-    if (worker) {
-        // this wave's K/V rows of the first group, from the cache (device-coherent)
-        constexpr uint32_t esz = KVH ? 2u : 4u;   // fp16 entries: 8 bytes per lane and position
-        const uint32_t kv_bytes = Ly.slots * hd * esz;
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
-        // cached positions [c0, cend); the current position itself comes from registers
-        const uint32_t cend = c1 == pos + 1u ? pos : c1;
-        // Byte offset of this lane's dims of position t, past the buffer (a load that returns
-        // zeros) for dead lanes and for positions that are not valid. The positions of a chunk
-        // are consecutive and fewer than `slots`, so their ring index wraps at most once.
-        const uint32_t r0 = c0 % Ly.slots, row_bytes = hd * esz;
-        const uint32_t lane_off = dlive ? dl * esz : 0x7ffffff0u;
-        auto kv_off = [&](uint32_t t, bool valid) {
-            uint32_t sl = r0 + (t - c0);
-            sl = sl >= Ly.slots ? sl - Ly.slots : sl;
-            return static_cast<int>((valid ? sl * row_bytes : 0x7ffffff0u) + lane_off);
-        };
-        // this lane's four dims of a cached position, as loaded (fp32 bits, or four fp16 halves
-        // that are converted where they are used, so the prefetch of the next group does not wait)
-        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-        using KvReg = typename std::conditional<KVH, v2u, v4u>::type;
-        auto kv_ld = [&](__amdgpu_buffer_rsrc_t r, int off) -> KvReg {
-            if constexpr (KVH) return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCoherent);
-            else return co_ld4(r, static_cast<uint32_t>(off));
-        };
-        auto kv_el = [](const KvReg& x, uint32_t e) -> float {
-            if constexpr (KVH) return static_cast<float>(__builtin_bit_cast(half4_t, x)[e]);
-            else return __uint_as_float(x[e]);
-        };
-        // how many of this wave's positions g0 + uw + nbw i fall below g1 (wave-uniform)
-        auto nvalid = [&](uint32_t g0, uint32_t g1) { return g1 > g0 + uw ? (g1 - g0 - uw + nbw - 1u) / nbw : 0u; };
-        // positions past a wave's share of a group load zeros: no branch per load, and the
-        // masked positions' value rows are zeros (not stale cache entries) under weight 0
-        KvReg kr[kBPos], vr[kBPos];
-        {
-            const uint32_t nv = nvalid(c0, min(cend, c0 + grp));
+    // K/V cache of this block (device-coherent accesses)
+    constexpr uint32_t esz = KVH ? 2u : 4u;   // fp16 entries: 8 bytes per lane and position
+    const uint32_t kv_bytes = Ly.slots * hd * esz;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
+    // cached positions [c0, cend); the current position itself comes from registers
+    const uint32_t cend = c1 == pos + 1u ? pos : c1;
+    // Byte offset of this lane's dims of position t, past the buffer (a load that returns
+    // zeros) for dead lanes and for positions that are not valid. The positions of a chunk
+    // are consecutive and fewer than `slots`, so their ring index wraps at most once.
+    const uint32_t r0 = c0 % Ly.slots, row_bytes = hd * esz;
+    const uint32_t lane_off = dlive ? dl * esz : 0x7ffffff0u;
+    auto kv_off = [&](uint32_t t, bool valid) {
+        uint32_t sl = r0 + (t - c0);
+        sl = sl >= Ly.slots ? sl - Ly.slots : sl;
+        return static_cast<int>((valid ? sl * row_bytes : 0x7ffffff0u) + lane_off);
+    };
+    // this lane's four dims of a cached position, as loaded (fp32 bits, or four fp16 halves
+    // that are converted where they are used, so the prefetch of the next group does not wait)
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    using KvReg = typename std::conditional<KVH, v2u, v4u>::type;
+    auto kv_ld = [&](__amdgpu_buffer_rsrc_t r, int off) -> KvReg {
+        if constexpr (KVH) return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCoherent);
+        else return co_ld4(r, static_cast<uint32_t>(off));
+    };
+    auto kv_el = [](const KvReg& x, uint32_t e) -> float {
+        if constexpr (KVH) return static_cast<float>(__builtin_bit_cast(half4_t, x)[e]);
+        else return __uint_as_float(x[e]);
+    };
+    // how many of this wave's positions g0 + uw + nbw i fall below g1 (wave-uniform)
+    auto nvalid = [&](uint32_t g0, uint32_t g1) { return g1 > g0 + uw ? (g1 - g0 - uw + nbw - 1u) / nbw : 0u; };
+    // positions past a wave's share of a group load zeros: no branch per load, and the
+    // masked positions' value rows are zeros (not stale cache entries) under weight 0
+    KvReg kr[kBPos], vr[kBPos];
+    if (worker) {   // this wave's K/V rows of the first group
+        const uint32_t nv = nvalid(c0, min(cend, c0 + grp));
 #pragma unroll
-            for (uint32_t i = 0; i < kBPos; ++i) {
-                const int o = kv_off(c0 + uw + nbw * i, i < nv);
-                kr[i] = kv_ld(rk, o);
-                vr[i] = kv_ld(rv, o);
-            }
+        for (uint32_t i = 0; i < kBPos; ++i) {
+            const int o = kv_off(c0 + uw + nbw * i, i < nv);
+            kr[i] = kv_ld(rk, o);
+            vr[i] = kv_ld(rv, o);
         }
+    }
+    // KV append (the current position's k and v, post-norm and post-RoPE): by the poller of
+    // head 0 (fused: of workgroup 0) of the chunk that holds the current position, and with
+    // eight workers by wave 0 after its loop, so that no wait of the loop covers the stores.
+    // Positions < pos are read from the cache by the next step only; this wave's next
+    // vector-memory wait in a later phase completes the stores, and every such phase precedes
+    // a publication that the next step's attention depends on (vector memory operations
+    // complete in issue order), so no wait is needed here.
+    const bool appender = (fused ? w == 0u : h == 0u) && c1 == pos + 1u && (shared_q ? poller : uw == 0u);
+    auto append = [&](const float (&k)[4], const float (&v)[4]) {
+        const uint32_t so = ((pos % Ly.slots) * hd + dl) * esz;
+        if constexpr (KVH) {   // k and v are already fp16 values: the conversion is exact
+            auto pack = [](float a, float b) {
+                return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+            };
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(k[0], k[1]), pack(k[2], k[3])}, rk, static_cast<int>(so), 0,
+                                                  kCoherent);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(v[0], v[1]), pack(v[2], v[3])}, rv, static_cast<int>(so), 0,
+                                                  kCoherent);
+        } else {
+            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(k[0]), __float_as_uint(k[1]),
+                                                       __float_as_uint(k[2]), __float_as_uint(k[3])},
+                                                   rk, static_cast<int>(so), 0, kCoherent);
+            __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                       __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                                   rv, static_cast<int>(so), 0, kCoherent);
+        }
+    };
+    float q[4], k[4], v[4];
+    if (poller) {
         // norm weights and RoPE factors of this lane's dims
         float wq[4], wk[4], cs[4], sn[4];
         {
@@ -792,8 +831,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             const bool live6[6] = {dlive, dlive, dlive, dlive, dlive, dlive};
             fail = ll_poll2<6>(rq, off, live6, tA, qkv);
         }
-        MK_MARK(7);
-        float q[4], k[4], v[4];
+        if (tr && lane == 0u && uw == (shared_q ? nbw : 0u))
+            mk_stamp(g_mk.trace_slots - kMarks + 7u, __builtin_amdgcn_s_memrealtime());
 #pragma unroll
         for (uint32_t e = 0; e < 4u; ++e) {
             q[e] = dlive ? qkv[e] : 0.0f;
@@ -834,7 +873,29 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                 v[e] = static_cast<float>(static_cast<_Float16>(v[e]));
             }
         }
-        MK_MARK(8);
+        if (shared_q) {
+            if (dlive) {
+                *reinterpret_cast<float4*>(qsh + dl) = make_float4(q[0], q[1], q[2], q[3]);
+                *reinterpret_cast<float4*>(qsh + hd + dl) = make_float4(k[0], k[1], k[2], k[3]);
+                *reinterpret_cast<float4*>(qsh + 2u * hd + dl) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+            if (appender && dlive && !fail) append(k, v);
+        }
+    }
+    if (shared_q) {   // the poller's q, k, v reach the workers
+        __syncthreads();
+        if (worker) {
+            const float4 q4 = dlive ? *reinterpret_cast<const float4*>(qsh + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 k4 = dlive ? *reinterpret_cast<const float4*>(qsh + hd + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 v4 =
+                dlive ? *reinterpret_cast<const float4*>(qsh + 2u * hd + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            q[0] = q4.x; q[1] = q4.y; q[2] = q4.z; q[3] = q4.w;
+            k[0] = k4.x; k[1] = k4.y; k[2] = k4.z; k[3] = k4.w;
+            v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
+        }
+    }
+    MK_MARK(8);
+    if (worker) {
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         float m_run = -INFINITY, l_run = 0.0f;
         const float attn_scale = g_mk.attn_scale;
@@ -913,33 +974,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                 m_run = m_new;
             }
         }
-        // KV append (the current position's k and v, post-norm and post-RoPE) by wave 0 of head 0
-        // of the chunk that holds the current position, after the loop so that no wait of the
-        // loop covers the stores. Positions < pos are read from the cache by the next step only;
-        // this wave's next vector-memory wait in a later phase completes the stores, and every
-        // such phase precedes a publication that the next step's attention depends on (vector
-        // memory operations complete in issue order), so no wait is needed here.
-        const bool appender = (fused ? w == 0u : h == 0u) && c1 == pos + 1u && uw == 0u;
-        if (appender && dlive && !fail) {
-            const uint32_t so = ((pos % Ly.slots) * hd + dl) * esz;
-            if constexpr (KVH) {   // k and v are already fp16 values: the conversion is exact
-                auto pack = [](float a, float b) {
-                    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
-                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
-                };
-                __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(k[0], k[1]), pack(k[2], k[3])}, rk, static_cast<int>(so), 0,
-                                                      kCoherent);
-                __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(v[0], v[1]), pack(v[2], v[3])}, rv, static_cast<int>(so), 0,
-                                                      kCoherent);
-            } else {
-                __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(k[0]), __float_as_uint(k[1]),
-                                                           __float_as_uint(k[2]), __float_as_uint(k[3])},
-                                                       rk, static_cast<int>(so), 0, kCoherent);
-                __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]),
-                                                           __float_as_uint(v[2]), __float_as_uint(v[3])},
-                                                       rv, static_cast<int>(so), 0, kCoherent);
-            }
-        }
+        if (!shared_q && appender && dlive && !fail) append(k, v);
         if (dlive) *reinterpret_cast<float4*>(ra + uw * hd + dl) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         if (lane == 0) {
             rml[uw] = m_run;
