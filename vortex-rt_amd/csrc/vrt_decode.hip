@@ -919,11 +919,12 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             const uint32_t n0 = g0 + grp;
             const uint32_t nn = n0 < cend ? nvalid(n0, min(cend, n0 + grp)) : 0u;
             int no[kBPos];
-#pragma unroll
-            for (uint32_t i = 0; i < kBPos; ++i) no[i] = kv_off(n0 + uw + nbw * i, i < nn);
             if (nn != 0u) {
 #pragma unroll
-                for (uint32_t i = 0; i < kBPos; ++i) kr[i] = kv_ld(rk, no[i]);
+                for (uint32_t i = 0; i < kBPos; ++i) {
+                    no[i] = kv_off(n0 + uw + nbw * i, i < nn);
+                    kr[i] = kv_ld(rk, no[i]);
+                }
             }
             if (nv != 0u) {   // this wave has a position in the group
                 float mx = fmaxf(sl, dpp_mov<0xB1>(sl));

@@ -174,47 +174,57 @@ struct LimbLds {
     float* s;
 };
 
-// Cooperative limb build for xs[0..K) (LDS) by all threads of the block. Each wave covers
-// two 32-element blocks per pass (one lane per element). Ends with __syncthreads().
+// Limbs of one element against its block's scale (amax m > 0): x / s = a + b/254 + c/254^2.
+__device__ __forceinline__ void limb3(float v, float m, int8_t& qa, int8_t& qb, int8_t& qc) {
+    const float inv = 127.0f / m;
+    const float r = v * inv;
+    const float a = rintf(r);
+    const float e1 = (r - a) * 254.0f;
+    const float b = fminf(fmaxf(rintf(e1), -127.0f), 127.0f);
+    const float e2 = (e1 - b) * 254.0f;
+    const float c = fminf(fmaxf(rintf(e2), -127.0f), 127.0f);
+    qa = static_cast<int8_t>(fminf(fmaxf(a, -127.0f), 127.0f));
+    qb = static_cast<int8_t>(b);
+    qc = static_cast<int8_t>(c);
+}
+
+// Cooperative limb build for xs[0..K) (LDS) by all threads of the block. A block of 32
+// elements is one 16-lane row of a wave (two elements per lane), so its amax is a DPP
+// reduction within the row and a wave covers four blocks per pass. A non-finite element
+// enters the amax as +inf and makes the block scale NaN. Ends with __syncthreads().
 __device__ __forceinline__ void build_limbs(const float* xs, uint32_t K, LimbLds L) {
     const uint32_t nblk = K >> 5;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nwaves = blockDim.x >> 6;
-    for (uint32_t pair = wave; pair * 2u < nblk; pair += nwaves) {
-        const uint32_t blk = pair * 2u + (lane >> 5);
+    for (uint32_t quad = wave; quad * 4u < nblk; quad += nwaves) {
+        const uint32_t blk = quad * 4u + (lane >> 4);
         const bool live = blk < nblk;
-        const float v = live ? xs[blk * 32u + (lane & 31u)] : 0.0f;
-        // block amax and a non-finite flag over the 32 lanes of this half-wave
-        float m = fabsf(v);
-        float bad = __builtin_isfinite(v) ? 0.0f : 1.0f;
-        for (int off = 16; off > 0; off >>= 1) {
-            m = fmaxf(m, __shfl_xor(m, off));
-            bad = fmaxf(bad, __shfl_xor(bad, off));
-        }
-        int8_t qa = 0, qb = 0, qc = 0;
+        const uint32_t k = blk * 32u + 2u * (lane & 15u);
+        const float2 v = live ? *reinterpret_cast<const float2*>(xs + k) : make_float2(0.0f, 0.0f);
+        auto mag = [](float x) { return __builtin_isfinite(x) ? fabsf(x) : INFINITY; };
+        float m = fmaxf(mag(v.x), mag(v.y));
+        m = fmaxf(m, dpp_mov<0xB1>(m));    // quad_perm [1,0,3,2]
+        m = fmaxf(m, dpp_mov<0x4E>(m));    // quad_perm [2,3,0,1]
+        m = fmaxf(m, dpp_mov<0x141>(m));   // row_half_mirror
+        m = fmaxf(m, dpp_mov<0x140>(m));   // row_mirror: every lane of the row holds its amax
+        int8_t qa0 = 0, qb0 = 0, qc0 = 0, qa1 = 0, qb1 = 0, qc1 = 0;
         float s = 0.0f;
-        if (bad != 0.0f) {
+        if (m == INFINITY) {
             s = __builtin_nanf("");
         } else if (m >= 1e-30f) {
             s = m * (1.0f / 127.0f);
-            const float inv = 127.0f / m;
-            const float r = v * inv;
-            const float a = rintf(r);
-            const float e1 = (r - a) * 254.0f;
-            const float b = fminf(fmaxf(rintf(e1), -127.0f), 127.0f);
-            const float e2 = (e1 - b) * 254.0f;
-            const float c = fminf(fmaxf(rintf(e2), -127.0f), 127.0f);
-            qa = static_cast<int8_t>(fminf(fmaxf(a, -127.0f), 127.0f));
-            qb = static_cast<int8_t>(b);
-            qc = static_cast<int8_t>(c);
+            limb3(v.x, m, qa0, qb0, qc0);
+            limb3(v.y, m, qa1, qb1, qc1);
         }
         if (live) {
-            const uint32_t k = blk * 32u + (lane & 31u);
-            L.a[k] = qa;
-            L.b[k] = qb;
-            L.c[k] = qc;
-            if ((lane & 31u) == 0u) L.s[blk] = s;
+            auto pk = [](int8_t lo, int8_t hi) {
+                return static_cast<uint16_t>(static_cast<uint8_t>(lo) | (static_cast<uint16_t>(static_cast<uint8_t>(hi)) << 8));
+            };
+            *reinterpret_cast<uint16_t*>(L.a + k) = pk(qa0, qa1);
+            *reinterpret_cast<uint16_t*>(L.b + k) = pk(qb0, qb1);
+            *reinterpret_cast<uint16_t*>(L.c + k) = pk(qc0, qc1);
+            if ((lane & 15u) == 0u) L.s[blk] = s;
         }
     }
     __syncthreads();
