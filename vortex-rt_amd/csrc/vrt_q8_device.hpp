@@ -255,19 +255,20 @@ __device__ __forceinline__ float q8_dot(const Q8Raw& r, const XLimb& x) {
 }
 
 // One block's contribution against fp32 activations x[0..31] (LDS, 16-byte aligned): the 32
-// int8 products summed in k order, then scaled: d_w * sum_k q_k x_k.
+// int8 products in four partial sums by k mod 4 (four short FMA chains instead of one of 32),
+// added pairwise, then scaled: d_w * ((s0 + s1) + (s2 + s3)).
 __device__ __forceinline__ float q8_dot_x(const Q8Raw& r, const float* x) {
-    float acc = 0.0f;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int q = static_cast<int>(__builtin_amdgcn_alignbyte(r.d[j + 1], r.d[j], r.sh));
         const float4 xv = *reinterpret_cast<const float4*>(x + 4 * j);
-        acc = fmaf(static_cast<float>((q << 24) >> 24), xv.x, acc);
-        acc = fmaf(static_cast<float>((q << 16) >> 24), xv.y, acc);
-        acc = fmaf(static_cast<float>((q << 8) >> 24), xv.z, acc);
-        acc = fmaf(static_cast<float>(q >> 24), xv.w, acc);
+        a0 = fmaf(static_cast<float>((q << 24) >> 24), xv.x, a0);
+        a1 = fmaf(static_cast<float>((q << 16) >> 24), xv.y, a1);
+        a2 = fmaf(static_cast<float>((q << 8) >> 24), xv.z, a2);
+        a3 = fmaf(static_cast<float>(q >> 24), xv.w, a3);
     }
-    return half_bits_to_float(r.sbits) * acc;
+    return half_bits_to_float(r.sbits) * ((a0 + a1) + (a2 + a3));
 }
 
 // ---- row streaming ----------------------------------------------------------------------
