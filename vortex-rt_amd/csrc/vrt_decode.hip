@@ -645,7 +645,7 @@ __device__ __attribute__((noinline)) bool mk_phase_a(uint32_t l, uint32_t pos, u
                                      : wv + static_cast<uint64_t>(v - qw - hd) * rb_d);
     };
     RowBatch<SD, 1, 1> rb;
-    batch_load<SD, 1, 1>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
+    batch_load<SD, 1, 1>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, kMkWaves, rb);
     MK_MARK(1);
     int bad = 0;
     if (mk_resid<EP, true>(l > 0 ? g_mk.x_f : nullptr, tagb + 5u * (l - 1u) + 5u,
@@ -722,7 +722,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         const uint8_t* wo = Ly.wo + static_cast<uint64_t>(h) * nbh * 34u;
         auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
         orb.live[0] = false;
-        if (uw >= ow0) batch_load<8, 1, 1>(rowp, nbh, g_mk.arena_end, v0, v1, uw - ow0, orb);
+        if (uw >= ow0) batch_load<8, 1, 1>(rowp, nbh, g_mk.arena_end, v0, v1, uw - ow0, kMkWaves, orb);
     }
     MK_MARK(6);
     const uint32_t dl = lane * 4u;                 // this lane's 4 head dims
@@ -1057,7 +1057,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
     const uint8_t* wo = Ly.wo;
     auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
     RowBatch<SA, 1, 1> rb;
-    batch_load<SA, 1, 1>(rowp, nblk_a, g_mk.arena_end, v0, v1, wave, rb);
+    batch_load<SA, 1, 1>(rowp, nblk_a, g_mk.arena_end, v0, v1, wave, kMkWaves, rb);
     float* parts = m.u;
     const uint32_t ntot = nch * part_stride;
     if (ntot <= kPartRoundS) {   // few chunks: one round with fewer polls per thread
@@ -1143,7 +1143,11 @@ __device__ __attribute__((noinline)) bool mk_phase_d(uint32_t l, uint32_t pos, u
     const uint8_t *wg = Ly.wg, *wu = Ly.wu;
     auto rowp = [=](uint32_t v) { return ((v & 1u) ? wu : wg) + static_cast<uint64_t>(v >> 1) * rb_d; };
     RowBatch<SD, 1, 2> rb;
-    batch_load<SD, 1, 2>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, rb);
+    batch_load<SD, 1, 2>(rowp, nblk_d, g_mk.arena_end, v0, v1, wave, kMkWaves, rb);
+    // The fused phase's four partial vectors make this the block's heaviest poll (every
+    // workgroup reads 4 d tagged words per round). Waiting for this wave's weight rows first
+    // starts it when the partials are nearly complete, which measured faster.
+    if constexpr (fused) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     int none = 0;
     if constexpr (fused) {   // the fused phase's per-head partials, added in head order
         if (mk_resid<EP, true, kMkFuseHeads>(g_mk.x_o4, tC, Ly.post_attn, Ly.ffn_norm, m.h, m.xd, nullptr, d, g_mk.eps,
@@ -1183,7 +1187,7 @@ __device__ __attribute__((noinline)) bool mk_phase_e(uint32_t l, uint32_t tagb, 
     const uint8_t* wd = Ly.wd;
     auto rowp = [=](uint32_t v) { return wd + static_cast<uint64_t>(v) * rb_f; };
     RowBatch<SF, 1, 1> rb;
-    batch_load<SF, 1, 1>(rowp, nblk_f, g_mk.arena_end, v0, v1, wave, rb);
+    batch_load<SF, 1, 1>(rowp, nblk_f, g_mk.arena_end, v0, v1, wave, kMkWaves, rb);
     if (!ll_gather2<kVec / 2>(g_mk.x_g, F, tD, m.xs, kAnyGatherE)) return false;
     MK_MARK(21);
     u64* out = g_mk.x_f;
@@ -1242,7 +1246,7 @@ __device__ __attribute__((noinline)) bool mk_phase_lm(uint32_t tagb, uint32_t tL
         if (i < ntiles) (void)issue(i);
     if (!mk_fold<EP>(tagb)) return false;
     MK_MARK(23);
-    build_limbs(m.xa, d, m.L);
+    build_limbs(m.xa, d, m.L, kMkWaves);
     // row slots of LS lanes, LNB blocks per lane: 20-block rows fill 16-lane slots with four
     // lanes holding two blocks, four rows per wave
     constexpr int LS = SD >= 32 ? SD / 2 : SD;

@@ -160,7 +160,7 @@ __global__ void __launch_bounds__(kThreads) k_qkv(G3Params P, LayerParams Lc, co
     const uint32_t v0 = blockIdx.x * per_wg;
     const uint32_t v1 = min(total, v0 + per_wg);
     RowBatch<S, NB, U> batch;
-    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, batch);
+    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, blockDim.x >> 6, batch);
 
     // residual stream entering this block
     float h[kMaxE];
@@ -183,7 +183,7 @@ __global__ void __launch_bounds__(kThreads) k_qkv(G3Params P, LayerParams Lc, co
         }
     }
     __syncthreads();
-    build_limbs(m.xs, d, m.L);
+    build_limbs(m.xs, d, m.L, blockDim.x >> 6);
     XLimb xl[NB];
     lane_limbs<S, NB>(m.L, nblk, xl);
     float* out = P.qkv;
@@ -379,14 +379,14 @@ __global__ void __launch_bounds__(kThreads) k_o(G3Params P, LayerParams Lc) {
     const uint32_t v0 = blockIdx.x * per_wg;
     const uint32_t v1 = min(P.d, v0 + per_wg);
     RowBatch<S, NB, U> batch;
-    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, batch);
+    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, blockDim.x >> 6, batch);
 #pragma unroll
     for (int k = 0; k < kMaxE; ++k) {
         const uint32_t i = threadIdx.x + static_cast<uint32_t>(k) * kThreads;
         if (i < K) m.xs[i] = ra[k];
     }
     __syncthreads();
-    build_limbs(m.xs, K, m.L);
+    build_limbs(m.xs, K, m.L, blockDim.x >> 6);
     XLimb xl[NB];
     lane_limbs<S, NB>(m.L, nblk, xl);
     float* out = P.o;
@@ -426,7 +426,7 @@ __global__ void __launch_bounds__(kThreads) k_gateup(G3Params P, LayerParams Lc)
     const uint32_t v0 = blockIdx.x * per_wg;
     const uint32_t v1 = min(2u * P.F, v0 + per_wg);
     RowBatch<S, NB, U> batch;
-    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, batch);
+    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, blockDim.x >> 6, batch);
 
     const float sc = rms_scale_from(wg_sum_f64(sum_sq(ra, d), red), d, P.eps);
     float h[kMaxE];
@@ -442,7 +442,7 @@ __global__ void __launch_bounds__(kThreads) k_gateup(G3Params P, LayerParams Lc)
         }
     }
     __syncthreads();
-    build_limbs(m.xs, d, m.L);
+    build_limbs(m.xs, d, m.L, blockDim.x >> 6);
     XLimb xl[NB];
     lane_limbs<S, NB>(m.L, nblk, xl);
     float* gu = m.extra;
@@ -474,14 +474,14 @@ __global__ void __launch_bounds__(kThreads) k_down(G3Params P, LayerParams Lc) {
     const uint32_t v0 = blockIdx.x * per_wg;
     const uint32_t v1 = min(P.d, v0 + per_wg);
     RowBatch<S, NB, U> batch;
-    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, batch);
+    batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, blockDim.x >> 6, batch);
 #pragma unroll
     for (int k = 0; k < kMaxE; ++k) {
         const uint32_t i = threadIdx.x + static_cast<uint32_t>(k) * kThreads;
         if (i < K) m.xs[i] = ra[k];
     }
     __syncthreads();
-    build_limbs(m.xs, K, m.L);
+    build_limbs(m.xs, K, m.L, blockDim.x >> 6);
     XLimb xl[NB];
     lane_limbs<S, NB>(m.L, nblk, xl);
     float* out = P.f;
@@ -523,7 +523,7 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
         const uint32_t v1 = min(P.V, v0 + rows_per_wg);
         const uint32_t nw = blockDim.x >> 6;
         RowBatch<S, NB, U> batch;
-        if (run_lm) batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, batch);
+        if (run_lm) batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, blockDim.x >> 6, batch);
 
         const float sc = rms_scale_from(wg_sum_f64(sum_sq(ra, d), red), d, P.eps);
         float h[kMaxE];
@@ -542,7 +542,7 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
         }
         __syncthreads();
         if (run_lm) {
-            build_limbs(m.xs, d, m.L);
+            build_limbs(m.xs, d, m.L, blockDim.x >> 6);
             XLimb xl[NB];
             lane_limbs<S, NB>(m.L, nblk, xl);
             float* logits = P.logits;
@@ -554,7 +554,7 @@ __global__ void __launch_bounds__(kThreads) k_lm(G3Params P, const float* last_p
             constexpr uint32_t RPW = 64u / S;
             const uint32_t ngroups = (v1 > v0) ? (v1 - v0 + RPW - 1u) / RPW : 0u;
             for (uint32_t g0 = (threadIdx.x >> 6) + U * nw; g0 < ngroups; g0 += U * nw) {
-                batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, g0, batch);
+                batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, g0, blockDim.x >> 6, batch);
                 batch_consume<S, NB, U>(batch, nblk, xl, sink);
             }
         }

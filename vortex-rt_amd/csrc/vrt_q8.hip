@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(256) k_matvec(RowSpace rs, uint64_t row_bytes,
               reinterpret_cast<int8_t*>(xs + K) + 2 * K, reinterpret_cast<float*>(reinterpret_cast<int8_t*>(xs + K) + 3 * K)};
     for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) xs[i] = x[i];
     __syncthreads();
-    build_limbs(xs, K, L);
+    build_limbs(xs, K, L, blockDim.x >> 6);
     const uint32_t nblk = K >> 5;
     const uint32_t sl = (threadIdx.x & 63u) % S;
     XLimb xl[NB];
@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(256) k_ffn_gateup(const uint8_t* gate_w, const
               reinterpret_cast<int8_t*>(xs + K) + 2 * K, reinterpret_cast<float*>(reinterpret_cast<int8_t*>(xs + K) + 3 * K)};
     for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) xs[i] = x[i];
     __syncthreads();
-    build_limbs(xs, K, L);
+    build_limbs(xs, K, L, blockDim.x >> 6);
     const uint32_t nblk = K >> 5;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const uint32_t slot = lane / S, sl = lane % S;

@@ -191,12 +191,12 @@ __device__ __forceinline__ void limb3(float v, float m, int8_t& qa, int8_t& qb, 
 // Cooperative limb build for xs[0..K) (LDS) by all threads of the block. A block of 32
 // elements is one 16-lane row of a wave (two elements per lane), so its amax is a DPP
 // reduction within the row and a wave covers four blocks per pass. A non-finite element
-// enters the amax as +inf and makes the block scale NaN. Ends with __syncthreads().
-__device__ __forceinline__ void build_limbs(const float* xs, uint32_t K, LimbLds L) {
+// enters the amax as +inf and makes the block scale NaN. `nwaves` is the workgroup's wave
+// count. Ends with __syncthreads().
+__device__ __forceinline__ void build_limbs(const float* xs, uint32_t K, LimbLds L, uint32_t nwaves) {
     const uint32_t nblk = K >> 5;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t nwaves = blockDim.x >> 6;
     for (uint32_t quad = wave; quad * 4u < nblk; quad += nwaves) {
         const uint32_t blk = quad * 4u + (lane >> 4);
         const bool live = blk < nblk;
@@ -373,14 +373,15 @@ struct RowBatch {
     bool live[U];
 };
 
-// rowp(v) returns the first byte of virtual row v.
+// rowp(v) returns the first byte of virtual row v. Pass U = 1 passes rows to wave group g0;
+// pass u to g0 + u * nwaves (a constant where the workgroup size is one: reading blockDim is
+// a load, and its wait would also wait for the weight loads issued before it).
 template <int S, int NB, int U, typename RowFn>
 __device__ __forceinline__ void batch_load(RowFn&& rowp, uint32_t nblk, const uint8_t* w_end, uint32_t v_begin,
-                                           uint32_t v_end, uint32_t g0, RowBatch<S, NB, U>& rb) {
+                                           uint32_t v_end, uint32_t g0, uint32_t nwaves, RowBatch<S, NB, U>& rb) {
     constexpr uint32_t RPW = 64u / S;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t slot = lane / S, sl = lane % S;
-    const uint32_t nwaves = blockDim.x >> 6;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint32_t g = g0 + static_cast<uint32_t>(u) * nwaves;
