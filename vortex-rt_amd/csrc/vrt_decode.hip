@@ -705,12 +705,15 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     // waves taking positions: four (one per SIMD) for short chunks, all eight for long ones
     const uint32_t nbw = clen >= kBLongChunk ? kBMaxWaves : 4u, grp = nbw * kBPos;
     const bool worker = uw < nbw;
-    // With four workers, wave 4 polls q|k|v, normalises and rotates them and hands them to the
-    // workers through LDS, so the workers' key/value loads and the poll wait in different waves'
-    // memory queues (a wave's vector-memory operations complete in issue order). With eight
-    // workers each one polls for itself.
+    // With four workers, wave 4 polls q and wave 5 polls k and v; they normalise and rotate them
+    // and hand them to the workers through LDS, so the workers' key/value loads and the polls
+    // wait in different waves' memory queues (a wave's vector-memory operations complete in
+    // issue order), and the q and k norms run side by side. With eight workers each one polls
+    // and prepares all three for itself.
     const bool shared_q = nbw < kBMaxWaves;
-    const bool poller = shared_q ? uw == nbw : worker;
+    const bool doq = shared_q ? uw == nbw : worker;        // polls and prepares q
+    const bool dok = shared_q ? uw == nbw + 1u : worker;   // polls and prepares k and v
+    const bool poller = doq || dok;
     // fused: this workgroup's O-projection rows over head h's columns, loaded before any wait, by
     // the waves past the poller when they can hold them all (8 rows each)
     const uint32_t nbh = hd >> 5;
@@ -718,7 +721,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     if constexpr (fused) {
         uint32_t v0, v1;
         split_range(d, g_mk.nbc / H, w / H, v0, v1);
-        const uint32_t ow0 = shared_q && v1 - v0 <= (kBMaxWaves - nbw - 1u) * 8u ? nbw + 1u : 0u;
+        const uint32_t ow0 = shared_q && v1 - v0 <= (kBMaxWaves - nbw - 2u) * 8u ? nbw + 2u : 0u;
         const uint8_t* wo = Ly.wo + static_cast<uint64_t>(h) * nbh * 34u;
         auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
         orb.live[0] = false;
@@ -784,7 +787,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     // vector-memory wait in a later phase completes the stores, and every such phase precedes
     // a publication that the next step's attention depends on (vector memory operations
     // complete in issue order), so no wait is needed here.
-    const bool appender = (fused ? w == 0u : h == 0u) && c1 == pos + 1u && (shared_q ? poller : uw == 0u);
+    const bool appender = (fused ? w == 0u : h == 0u) && c1 == pos + 1u && (shared_q ? dok : uw == 0u);
     auto append = [&](const float (&k)[4], const float (&v)[4]) {
         const uint32_t so = ((pos % Ly.slots) * hd + dl) * esz;
         if constexpr (KVH) {   // k and v are already fp16 values: the conversion is exact
@@ -814,8 +817,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             const VRT_AS_GLOBAL float* st = gp(Ly.global ? g_mk.sin_g : g_mk.sin_l) + static_cast<uint64_t>(pos) * half;
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e) {
-                wq[e] = dlive ? gp(Ly.q_norm)[dl + e] : 0.0f;
-                wk[e] = dlive ? gp(Ly.k_norm)[dl + e] : 0.0f;
+                wq[e] = dlive && doq ? gp(Ly.q_norm)[dl + e] : 0.0f;
+                wk[e] = dlive && dok ? gp(Ly.k_norm)[dl + e] : 0.0f;
                 cs[e] = dlive ? ct[e0 + e] : 0.0f;
                 sn[e] = dlive ? st[e0 + e] : 0.0f;
             }
@@ -828,7 +831,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             const int oq = static_cast<int>((h * hd + dl) * 8u), ok = static_cast<int>((qw + dl) * 8u),
                       ov = static_cast<int>((qw + hd + dl) * 8u);
             const int off[6] = {oq, oq + 16, ok, ok + 16, ov, ov + 16};
-            const bool live6[6] = {dlive, dlive, dlive, dlive, dlive, dlive};
+            const bool lq = dlive && doq, lk = dlive && dok;
+            const bool live6[6] = {lq, lq, lk, lk, lk, lk};
             fail = ll_poll2<6>(rq, off, live6, tA, qkv);
         }
         if (tr && lane == 0u && uw == (shared_q ? nbw : 0u))
@@ -839,33 +843,23 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             k[e] = dlive ? qkv[4 + e] : 0.0f;
             v[e] = dlive ? qkv[8 + e] : 0.0f;
         }
-        // QK-norm: sums of squares of q_h and k over the wave
-        double sq_q = 0.0, sq_k = 0.0;
+        // QK-norm: sums of squares of q_h and of k over the wave
+        auto qk_norm_rope = [&](float (&x)[4], const float (&wx)[4]) {
+            double sq = 0.0;
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) {
-            sq_q += static_cast<double>(q[e]) * static_cast<double>(q[e]);
-            sq_k += static_cast<double>(k[e]) * static_cast<double>(k[e]);
-        }
-        sq_q = wave_red_sum_d(sq_q);
-        sq_k = wave_red_sum_d(sq_k);
-        const float scq = mk_rms_scale_pow2(sq_q, hd, g_mk.eps), sck = mk_rms_scale_pow2(sq_k, hd, g_mk.eps);
+            for (uint32_t e = 0; e < 4u; ++e) sq += static_cast<double>(x[e]) * static_cast<double>(x[e]);
+            const float sc = mk_rms_scale_pow2(wave_red_sum_d(sq), hd, g_mk.eps);
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) {
-            q[e] = q[e] * (scq * wq[e]);   // values *= scale * weights (src/gemma3.cpp:1097-1102)
-            k[e] = k[e] * (sck * wk[e]);
-        }
-        // RoPE (NeoX halves): (a, b) = (x[e], x[e + half]) -> (a c - b s, b c + a s)
-        float qo[4], ko[4];
+            for (uint32_t e = 0; e < 4u; ++e) x[e] = x[e] * (sc * wx[e]);   // values *= scale * weights (src/gemma3.cpp:1097-1102)
+            // RoPE (NeoX halves): (a, b) = (x[e], x[e + half]) -> (a c - b s, b c + a s)
+            float xo[4];
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) {
-            qo[e] = __shfl(q[e], partner);
-            ko[e] = __shfl(k[e], partner);
-        }
+            for (uint32_t e = 0; e < 4u; ++e) xo[e] = __shfl(x[e], partner);
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) {
-            q[e] = lo ? q[e] * cs[e] - qo[e] * sn[e] : q[e] * cs[e] + qo[e] * sn[e];
-            k[e] = lo ? k[e] * cs[e] - ko[e] * sn[e] : k[e] * cs[e] + ko[e] * sn[e];
-        }
+            for (uint32_t e = 0; e < 4u; ++e) x[e] = lo ? x[e] * cs[e] - xo[e] * sn[e] : x[e] * cs[e] + xo[e] * sn[e];
+        };
+        if (doq) qk_norm_rope(q, wq);
+        if (dok) qk_norm_rope(k, wk);
         if constexpr (KVH) {   // the current position's key and value as the cache will hold them
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e) {
@@ -873,16 +867,16 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                 v[e] = static_cast<float>(static_cast<_Float16>(v[e]));
             }
         }
-        if (shared_q) {
-            if (dlive) {
-                *reinterpret_cast<float4*>(qsh + dl) = make_float4(q[0], q[1], q[2], q[3]);
+        if (shared_q && dlive) {
+            if (doq) *reinterpret_cast<float4*>(qsh + dl) = make_float4(q[0], q[1], q[2], q[3]);
+            if (dok) {
                 *reinterpret_cast<float4*>(qsh + hd + dl) = make_float4(k[0], k[1], k[2], k[3]);
                 *reinterpret_cast<float4*>(qsh + 2u * hd + dl) = make_float4(v[0], v[1], v[2], v[3]);
             }
-            if (appender && dlive && !fail) append(k, v);
         }
+        if (shared_q && appender && dlive && !fail) append(k, v);
     }
-    if (shared_q) {   // the poller's q, k, v reach the workers
+    if (shared_q) {   // the pollers' q, k, v reach the workers
         __syncthreads();
         if (worker) {
             const float4 q4 = dlive ? *reinterpret_cast<const float4*>(qsh + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
