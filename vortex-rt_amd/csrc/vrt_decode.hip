@@ -927,8 +927,10 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
                 mx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
                 const float m_new = fmaxf(m_run, mx);
                 if (m_new != -INFINITY) {
-                    const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-                    const float pe = sl == -INFINITY ? 0.0f : expf(sl - m_new);
+                    // softmax weights through the hardware exp2 (__expf): arguments are <= 0 after
+                    // the max subtraction, the weights' relative error stays near 1e-6
+                    const float r = m_run == -INFINITY ? 0.0f : __expf(m_run - m_new);
+                    const float pe = sl == -INFINITY ? 0.0f : __expf(sl - m_new);
                     float pw[kBPos];
                     float ls = 0.0f;
 #pragma unroll
@@ -961,8 +963,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
             const float sc = sp[0] * attn_scale;
             const float m_new = fmaxf(m_run, sc);
             if (m_new != -INFINITY) {
-                const float r = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-                const float pw = sc == -INFINITY ? 0.0f : expf(sc - m_new);
+                const float r = m_run == -INFINITY ? 0.0f : __expf(m_run - m_new);
+                const float pw = sc == -INFINITY ? 0.0f : __expf(sc - m_new);
 #pragma unroll
                 for (uint32_t e = 0; e < 4u; ++e) acc[e] = acc[e] * r + pw * v[e];
                 l_run = l_run * r + pw;
@@ -987,7 +989,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         M = fmaxf(M, dpp_mov<0x4E>(M));
         M = fmaxf(M, dpp_mov<0x141>(M));   // lanes 0..7: the max over the waves
         static_assert(kBMaxWaves <= 8u, "DPP max over one half row (lanes past nbw hold -inf)");
-        const float fk = lane < nbw && mk != -INFINITY ? expf(mk - M) : 0.0f;
+        const float fk = lane < nbw && mk != -INFINITY ? __expf(mk - M) : 0.0f;
         const float lk = lane < nbw ? rml[kBMaxWaves + lane] : 0.0f;
         float f[kBMaxWaves];
 #pragma unroll
@@ -1077,7 +1079,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_c(uint32_t l, uint32_t p
         M = fmaxf(M, dpp_mov<0x4E>(M));
         M = fmaxf(M, dpp_mov<0x141>(M));
         M = fmaxf(M, dpp_mov<0x140>(M));
-        const float e = on ? expf(mq - M) : 0.0f;
+        const float e = on ? __expf(mq - M) : 0.0f;
         double den = on ? static_cast<double>(e) * static_cast<double>(lq) : 0.0;
         den += dpp_d<0xB1, 0xf>(den, false);
         den += dpp_d<0x4E, 0xf>(den, false);
