@@ -27,6 +27,10 @@
 // is short, and the hand-off B -> C it saves costs more), normalises it and computes its rows of
 // the O projection over head h's columns only; D adds the H per-head partials of each row in
 // head order. Every workgroup then produces in A and D.
+// Inside an attention workgroup the roles are split by wave, because a wave's vector-memory
+// operations complete in issue order: waves 0-3 load the history's keys and values and take
+// positions, waves 4 and 5 poll q and k|v and hand them over through LDS, waves 6-7 hold the
+// fused phase's Wo rows. A poll thus never waits behind the key/value loads.
 // After the last block every workgroup folds f into h; when the step runs the LM head all of
 // them stream an even share of the tied Q8_0 table (staged through LDS with 16-byte loads),
 // keep a local greedy argmax and publish it; the next step (or workgroup 0 at the end of the
