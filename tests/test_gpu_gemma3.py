@@ -196,6 +196,28 @@ def test_persistent_split_launches(ctx, tiny_model):
     assert np.array_equal(whole, parts)
 
 
+def test_exchange_buffers_read_back(ctx, tiny_model):
+    """vrt_g3_read_exchange returns each persistent-kernel exchange buffer in row order: after a
+    generation, the last block's q|k|v, gelu(gate)*up and down-projection words all carry that
+    block's tag, and the down projection (one 64-byte line per four-row producer on the device)
+    comes back compacted to d words."""
+    g = vrt.Gemma3(ctx, tiny_model)
+    try:
+        if not g.persistent_available():
+            pytest.skip("persistent kernel unavailable")
+        g.generate(synth.uniform_ids(5, 6, 2, 1000), 4)
+        cfg = g.config
+        sizes = {0: cfg.head_count * cfg.head_dim + 2 * cfg.head_dim, 3: cfg.feed_forward_length,
+                 4: cfg.embedding_length}
+        for which, n in sizes.items():
+            vals, tags = g.read_exchange(which)
+            assert vals.size == n, which
+            assert tags[0] != 0 and np.all(tags == tags[0]), (which, np.unique(tags))
+            assert np.all(np.isfinite(vals)) and np.any(vals != 0.0), which
+    finally:
+        g.close()
+
+
 MEDIUM = dict(n_layers=6, d_model=512, n_heads=4, head_dim=128, ffn=1024, vocab=2000, context=2048, window=64)
 
 
