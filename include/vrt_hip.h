@@ -203,8 +203,9 @@ int vrt_g3_decode(vrt_g3* g3, uint32_t token, uint32_t position, uint32_t top_k,
  * position runs the LM head as vrt_g3_decode would with top_k (0 skips it, 1 is the fused
  * argmax into *out, > 1 keeps the logits for vrt_g3_logits). hidden_out (embedding_length
  * floats, host) may be NULL. Decoding continues at position n. Prompts longer than the
- * batched workspace (min(context_length, 2048) positions) or shapes it does not cover run as
- * serial decode steps. On any error the KV cache is reset. */
+ * batched workspace (min(context_length, 2048) positions) run as consecutive segments of that
+ * many positions, each attending to the earlier ones through the KV cache; shapes the batched
+ * kernels do not cover run as serial decode steps. On any error the KV cache is reset. */
 int vrt_g3_prefill(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t top_k, vrt_argmax_result* out,
                    float* hidden_out);
 

@@ -22,10 +22,12 @@ def _rel(a, b):
     return float(np.max(np.abs(a.astype(np.float64) - b.astype(np.float64))) / max(np.max(np.abs(b)), 1e-30))
 
 
-def _check(ctx, path, prompt, n_cont, top2_margin=1e-4):
+def _check(ctx, path, prompt, n_cont, top2_margin=1e-4, kv_f16=False):
     g = vrt.Gemma3(ctx, path)
-    m = oracle.Model(path)
+    m = oracle.Model(path, kv_f16=kv_f16)
     try:
+        if kv_f16:
+            g.set_kv_f16(True)
         print(f"[pf] {os.path.basename(path)}: prefill of {prompt.size} positions", flush=True)
         (idx, val), hid = g.prefill(prompt, top_k=8, hidden=True)
         logits = g.logits()
@@ -65,6 +67,20 @@ def test_prefill_medium(ctx, model_dir):
     if not os.path.exists(path):
         synth.write_gemma3_gguf(path, seed=21, **MEDIUM)
     _check(ctx, path, synth.uniform_ids(8, 300, 2, MEDIUM["vocab"]), 6)
+
+
+LONG = dict(n_layers=6, d_model=256, n_heads=2, head_dim=64, ffn=512, vocab=1000, context=8192, window=64)
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_prefill_segments(ctx, model_dir, kv_f16):
+    """A prompt longer than the batched workspace (2048 positions) runs as segments of 2048,
+    2048 and 404 positions: a segment's global blocks attend to every earlier position through
+    the KV cache and its local blocks to the window's start rounded down to 32."""
+    path = os.path.join(str(model_dir), "long8k.gguf")
+    if not os.path.exists(path):
+        synth.write_gemma3_gguf(path, seed=23, **LONG)
+    _check(ctx, path, synth.uniform_ids(9, 4500, 2, LONG["vocab"]), 4, kv_f16=kv_f16)
 
 
 def test_prefill_full_shape_512(ctx, full_model):

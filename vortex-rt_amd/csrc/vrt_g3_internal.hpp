@@ -92,10 +92,11 @@ struct PfState {
     void* ahi = nullptr;    // [max_t][max(d, H*hd, F)] GEMM input, f16 high part
     void* alo = nullptr;    //   ... and low part
     float* big = nullptr;   // [max_t][max(H*hd + 2*hd, 2F)] q|k|v rows, then gate|up rows
-    void* khi = nullptr;    // attention keys (Tp x hd, Tp: max_t rounded up to 64), f16 high part
+    void* khi = nullptr;    // attention keys (tkv x hd), f16 high part: a segment's history, then its rows
     void* klo = nullptr;    //   ... and low part
     void* vhi = nullptr;    // attention values (Tp x hd), f16 high part
     void* vlo = nullptr;    //   ... and low part
+    uint32_t tkv = 0;       // key coordinates of khi..vlo: max(max_t, context_length), padded
     uint32_t qtmax = 0;     // 32-query tiles of max_t
     uint32_t maxc = 0;      // key chunks per query tile, at most
     float* opart = nullptr;     // [H][qtmax][maxc][32][hd] attention unit partials
@@ -150,7 +151,9 @@ int mk_set_kv_f16(vrt_g3* g, bool on);
 // Batched prefill (vrt_prefill.hip): workspace for up to max_t positions, and one prefill of T
 // positions from position 0 whose last position runs g3_enqueue_lm.
 int pf_setup(vrt_g3* g, uint32_t max_t);
-int pf_run(vrt_g3* g, uint32_t T);
+// The blocks over the segment of T prompt positions from p0 (earlier positions already in the
+// KV cache); the final segment also runs the LM head of its last position.
+int pf_run(vrt_g3* g, uint32_t T, uint32_t p0 = 0, bool final = true);
 // Row-batch building blocks shared by the prefill and the batched decode (vrt_prefill.hip):
 // block l's projections over M rows as (split-K) GEMMs, its gate/up product, the residual
 // norms over rows, embedding rows, and the logits of M rows against the tied embedding table.

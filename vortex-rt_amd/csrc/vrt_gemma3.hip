@@ -1030,7 +1030,7 @@ extern "C" int vrt_g3_prefill(vrt_g3* g, const uint32_t* tokens, uint32_t n, uin
     if (n > g->cfg.context_length) return set_error(VRT_ERR_STATE, "Gemma 3 context length exceeded");
     for (uint32_t i = 0; i < n; ++i)
         if (tokens[i] >= g->cfg.vocab_size) return g3_fail_reset(g, VRT_ERR_INVALID, "Token id is outside Gemma 3 vocabulary");
-    if (g->pf.max_t == 0u || n > g->pf.max_t) {   // serial decode steps (src/gemma3.cpp:2099-2111)
+    if (g->pf.max_t == 0u) {   // serial decode steps (src/gemma3.cpp:2099-2111)
         g->next_pos = 0;
         for (uint32_t i = 0; i < n; ++i)
             if (int rc = vrt_g3_decode(g, tokens[i], i, i + 1u == n ? top_k : 0u, out, i + 1u == n ? hidden_out : nullptr))
@@ -1041,7 +1041,12 @@ extern "C" int vrt_g3_prefill(vrt_g3* g, const uint32_t* tokens, uint32_t n, uin
     g->next_pos = 0;
     VRT_HIP_CHECK(hipMemcpyAsync(g->P.tokens, tokens, n * 4u, hipMemcpyHostToDevice, s));
     if (int rc = g3_write_ctl(g, n - 1u, top_k ? n - 1u : 0xffffffffu, 0xffffffffu, top_k > 1 ? 1u : 0u)) return rc;
-    if (int rc = pf_run(g, n)) return g3_fail_reset(g, rc, vrt_last_error());
+    // segments of at most max_t positions; each one's attention reads the earlier positions'
+    // keys and values from the cache, and the last one runs the LM head
+    for (uint32_t p0 = 0; p0 < n; p0 += g->pf.max_t) {
+        const uint32_t T = std::min(g->pf.max_t, n - p0);
+        if (int rc = pf_run(g, T, p0, p0 + T == n)) return g3_fail_reset(g, rc, vrt_last_error());
+    }
     if (hidden_out)
         VRT_HIP_CHECK(hipMemcpyAsync(hidden_out, g->P.hidden, g->cfg.embedding_length * 4u, hipMemcpyDeviceToHost, s));
     VRT_HIP_CHECK(hipMemcpyAsync(g->host_res, g->P.results + (n - 1u), sizeof(vrt_argmax_result), hipMemcpyDeviceToHost, s));

@@ -469,23 +469,25 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
                                                             const float* cos_t, const float* sin_t, float eps,
                                                             float* kc, float* vc, uint32_t slots, _Float16* qhi,
                                                             _Float16* qlo, _Float16* khi, _Float16* klo, _Float16* vhi,
-                                                            _Float16* vlo, uint32_t kv_f16) {
+                                                            _Float16* vlo, uint32_t kv_f16, uint32_t p0, uint32_t qo) {
 #pragma clang fp contract(off)
     __shared__ float xs[kPfQkMaxWaves][256];
-    const uint32_t t = blockIdx.x;
+    const uint32_t t = blockIdx.x;           // row of the segment; position p0 + t, key coordinate qo + t
+    const uint32_t kt = qo + t;
     if (t >= T) {   // whole workgroup
         for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
-            const uint64_t ko = pf_kswz(t, i, hd), vo = pf_vswz(t, i, hd);
+            const uint64_t ko = pf_kswz(kt, i, hd), vo = pf_vswz(kt, i, hd);
             khi[ko] = klo[ko] = vhi[vo] = vlo[vo] = static_cast<_Float16>(0.0f);
         }
         return;
     }
+    const uint32_t pos = p0 + t;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t nqkv = (H + 2u) * hd, half = hd >> 1;
     float* row = qkv + static_cast<uint64_t>(t) * nqkv;
     float* xw = xs[wave];
-    const bool keep = t + slots >= T;
-    const uint64_t slot = static_cast<uint64_t>(t % slots) * hd;
+    const bool keep = t + slots >= T;   // the last `slots` positions of the segment reach the ring
+    const uint64_t slot = static_cast<uint64_t>(pos % slots) * hd;
     // Loads are issued at clamped, in-bounds indices and masked afterwards, so each group of
     // them is in flight together (no branch, hence no wait, between them). v first: it is only
     // stored, after the heads.
@@ -502,8 +504,8 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
     float cs[4], sn[4];
 #pragma unroll
     for (uint32_t e = 0; e < 4u; ++e) {
-        cs[e] = cos_t[static_cast<uint64_t>(t) * half + ei[e]];
-        sn[e] = sin_t[static_cast<uint64_t>(t) * half + ei[e]];
+        cs[e] = cos_t[static_cast<uint64_t>(pos) * half + ei[e]];
+        sn[e] = sin_t[static_cast<uint64_t>(pos) * half + ei[e]];
     }
     for (uint32_t hh = wave; hh <= H; hh += nw) {   // H query heads, then the key head
         const float* x = row + hh * hd;
@@ -537,7 +539,7 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
                 pf_split(y2, qhi + o, qlo + o);
             } else {   // fp16 KV: the key as the cache holds it, for the cache and the attention
                 const float kk = kv_f16 ? static_cast<float>(static_cast<_Float16>(y2)) : y2;
-                const uint64_t o = pf_kswz(t, i, hd);
+                const uint64_t o = pf_kswz(kt, i, hd);
                 pf_split(kk, khi + o, klo + o);
                 if (keep) {
                     if (kv_f16) reinterpret_cast<_Float16*>(kc)[slot + i] = static_cast<_Float16>(kk);
@@ -554,8 +556,27 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
             if (kv_f16) reinterpret_cast<_Float16*>(vc)[slot + i] = static_cast<_Float16>(vv);
             else vc[slot + i] = vv;
         }
-        const uint64_t o = pf_vswz(t, i, hd);
+        const uint64_t o = pf_vswz(kt, i, hd);
         pf_split(vv, vhi + o, vlo + o);
+    }
+}
+
+// A segment's history for the attention: key coordinates j < nh hold positions kb + j, read
+// from the block's KV cache (ring slot (kb + j) % slots, fp32 or fp16 entries as the cache
+// holds them) and written in the pf_kswz / pf_vswz layouts as f16 hi/lo, as k_pf_qk writes a
+// segment's own rows. One workgroup per key coordinate.
+__global__ void __launch_bounds__(kPfThreads) k_pf_kv_hist(const float* kc, const float* vc, uint32_t slots, uint32_t kv_f16,
+                                                          uint32_t kb, uint32_t nh, uint32_t hd, _Float16* khi,
+                                                          _Float16* klo, _Float16* vhi, _Float16* vlo) {
+    const uint32_t j = blockIdx.x;
+    if (j >= nh) return;
+    const uint64_t slot = static_cast<uint64_t>((kb + j) % slots) * hd;
+    for (uint32_t i = threadIdx.x; i < hd; i += kPfThreads) {
+        const float k = kv_f16 ? static_cast<float>(reinterpret_cast<const _Float16*>(kc)[slot + i]) : kc[slot + i];
+        const float v = kv_f16 ? static_cast<float>(reinterpret_cast<const _Float16*>(vc)[slot + i]) : vc[slot + i];
+        const uint64_t ko = pf_kswz(j, i, hd), vo = pf_vswz(j, i, hd);
+        pf_split(k, khi + ko, klo + ko);
+        pf_split(v, vhi + vo, vlo + vo);
     }
 }
 
@@ -596,12 +617,15 @@ struct PfAttn {
     G3State* st;
     uint32_t T, H, window, qtmax, maxc, block, kc;
     uint32_t qt0;          // first query tile of the launch (blockIdx.y, merge: blockIdx.x, counts from it)
+    uint32_t qo;           // key coordinate of query row 0 (keys before it: an earlier segment's history)
     float scale2;          // attention scale times log2(e): the scores in base 2
 };
 
-__device__ __forceinline__ void pf_att_range(uint32_t q0, uint32_t T, uint32_t window, uint32_t& ks, uint32_t& ke) {
-    ke = min(T, q0 + 32u);
-    ks = window != 0u && q0 + 1u > window ? (q0 + 1u - window) & ~31u : 0u;
+// Key range [ks, ke) of the query tile whose first row sits at key coordinate qk0, with keys
+// below kend (the key coordinates of a segment's history come first, then its own rows).
+__device__ __forceinline__ void pf_att_range(uint32_t qk0, uint32_t kend, uint32_t window, uint32_t& ks, uint32_t& ke) {
+    ke = min(kend, qk0 + 32u);
+    ks = window != 0u && qk0 + 1u > window ? (qk0 + 1u - window) & ~31u : 0u;
 }
 
 template <uint32_t HD>
@@ -615,12 +639,13 @@ __global__ void __launch_bounds__(256) k_pf_attn(PfAttn A) {
     const uint32_t c = blockIdx.x, i = A.qt0 + blockIdx.y, h = blockIdx.z;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, l32 = lane & 31u, hf = lane >> 5;
     const uint32_t T = A.T, q0 = 32u * i, qw = A.H * HD;
+    const uint32_t qk0 = A.qo + q0;   // the tile's first query in key coordinates
     uint32_t ks, ke;
-    pf_att_range(q0, T, A.window, ks, ke);
+    pf_att_range(qk0, A.qo + T, A.window, ks, ke);
     const uint32_t nch = (ke - ks + A.kc - 1u) / A.kc;
     if (c >= nch) return;   // whole workgroup
     const uint32_t k0 = ks + c * A.kc, k1 = min(ke, k0 + A.kc);
-    const uint32_t q = q0 + l32;
+    const uint32_t q = q0 + l32, qk = qk0 + l32;   // this lane's query: row, key coordinate
     // this wave's k steps of the queries (B operand of S^T), rows past T clamped (never written)
     v4u qb[KW][2];
     {
@@ -698,7 +723,7 @@ __global__ void __launch_bounds__(256) k_pf_attn(PfAttn A) {
         buf ^= 1u;
         // scores in base 2 (scale * log2 e folded in): e_j = 2^(v_j - m) = exp(scale s_j - m ln 2)
         float tmax = -INFINITY;
-        if (kt + 31u < k1 && kt + 31u <= q0 && (A.window == 0u || kt + A.window > q0 + 31u)) {
+        if (kt + 31u < k1 && kt + 31u <= qk0 && (A.window == 0u || kt + A.window > qk0 + 31u)) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {   // every key of the tile visible to every query
                 v[r] *= A.scale2;
@@ -708,7 +733,7 @@ __global__ void __launch_bounds__(256) k_pf_attn(PfAttn A) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t key = kt + 16u * (r / 8) + 8u * hf + (r % 8);
-                const bool ok = key < k1 && key <= q && (A.window == 0u || key + A.window > q);
+                const bool ok = key < k1 && key <= qk && (A.window == 0u || key + A.window > qk);
                 v[r] = ok ? v[r] * A.scale2 : -INFINITY;
                 tmax = fmaxf(tmax, v[r]);
             }
@@ -814,7 +839,7 @@ __global__ void __launch_bounds__(256) k_pf_attn_merge(PfAttn A) {
     constexpr uint32_t NF = HD / 32u / CG;   // float4 per thread
     const uint32_t i = A.qt0 + blockIdx.x, h = blockIdx.y, T = A.T, q0 = 32u * i;
     uint32_t ks, ke;
-    pf_att_range(q0, T, A.window, ks, ke);
+    pf_att_range(A.qo + q0, A.qo + T, A.window, ks, ke);
     const uint32_t nch = (ke - ks + A.kc - 1u) / A.kc;
     const uint32_t r = threadIdx.x >> 3, g = blockIdx.z * 8u + (threadIdx.x & 7u);
     if (nch == 1u || q0 + r >= T) return;
@@ -1250,9 +1275,12 @@ int pf_setup(vrt_g3* g, uint32_t max_t) {
     p.alo = q;
     if (int rc = take(static_cast<size_t>(max_t) * std::max(nqkv, 2u * F) * 4u, &q)) return rc;
     p.big = static_cast<float*>(q);
-    void** kv[] = {&p.khi, &p.klo, &p.vhi, &p.vlo};   // tp x hd f16 each
+    // keys and values of a segment's history and rows (f16 each): prompts longer than max_t run
+    // in segments whose keys reach back to position 0 in a global block
+    p.tkv = static_cast<uint32_t>(std::max<uint64_t>(tp, pf_pad(g->cfg.context_length)));
+    void** kv[] = {&p.khi, &p.klo, &p.vhi, &p.vlo};
     for (void** b : kv)
-        if (int rc = take(static_cast<size_t>(hd) * tp * 2u, b)) return rc;
+        if (int rc = take(static_cast<size_t>(hd) * p.tkv * 2u, b)) return rc;
     p.qtmax = (max_t + 31u) / 32u;
     p.maxc = (max_t + 31u + kPfAttKC - 1u) / kPfAttKC;
     const size_t units = static_cast<size_t>(H) * p.qtmax * p.maxc;
@@ -1316,7 +1344,7 @@ static int pf_attn_launch(const PfAttn& A, dim3 grid, hipStream_t s) {
 // Causal local/global attention of one block (k_pf_attn) over the queries in qhi/qlo [T][H hd],
 // written back in place as the attention output, for the query tiles from qt0 on.
 static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, uint32_t qt0, _Float16* qhi, _Float16* qlo,
-                        hipStream_t s) {
+                        hipStream_t s, uint32_t qo = 0) {
     const PfState& p = g->pf;
     const uint32_t H = g->cfg.head_count, hd = g->cfg.head_dim;
     PfAttn A{};
@@ -1338,15 +1366,20 @@ static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, uint32_t q
     A.block = Ly.index;
     A.scale2 = g->P.attn_scale * 1.4426950408889634f;
     const uint32_t qt = (T + 31u) / 32u;
-    A.kc = kPfAttKC;
     A.qt0 = qt0;
-    uint32_t nch = 1;
+    A.qo = qo;
+    // the longest key range of a query tile (the same ranges as pf_att_range), then a chunk size
+    // that keeps it within maxc chunks (a segment's history can reach back to position 0)
+    uint32_t span = 32;
     for (uint32_t i = qt0; i < qt; ++i) {
-        const uint32_t q0 = 32u * i, ke = std::min(T, q0 + 32u);
-        const uint32_t ks = A.window != 0u && q0 + 1u > A.window ? (q0 + 1u - A.window) & ~31u : 0u;
-        nch = std::max(nch, (ke - ks + A.kc - 1u) / A.kc);
+        const uint32_t qk0 = qo + 32u * i, ke = std::min(qo + T, qk0 + 32u);
+        const uint32_t ks = A.window != 0u && qk0 + 1u > A.window ? (qk0 + 1u - A.window) & ~31u : 0u;
+        span = std::max(span, ke - ks);
     }
-    if (qt > p.qtmax || nch > p.maxc || qt0 >= qt) return set_error(VRT_ERR_STATE, "prefill attention workspace too small");
+    A.kc = std::max(kPfAttKC, (span + 32u * p.maxc - 1u) / (32u * p.maxc) * 32u);
+    const uint32_t nch = (span + A.kc - 1u) / A.kc;
+    if (qt > p.qtmax || nch > p.maxc || qt0 >= qt || pf_pad(qo + T) > p.tkv)
+        return set_error(VRT_ERR_STATE, "prefill attention workspace too small");
     const dim3 grid(nch, qt - qt0, H);
     switch (hd) {
     case 32: return pf_attn_launch<32>(A, grid, s);
@@ -1363,7 +1396,7 @@ static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, uint32_t q
 
 // T prompt positions 0..T-1 on the context's stream; the last one runs the LM head + argmax
 // (results[T-1], logits when want_logits). The caller has reset the step state.
-int pf_run(vrt_g3* g, uint32_t T) {
+int pf_run(vrt_g3* g, uint32_t T, uint32_t p0, bool final) {
     const PfState& p = g->pf;
     hipStream_t s = g->ctx->stream;
     uint32_t d = g->cfg.embedding_length, H = g->cfg.head_count, hd = g->cfg.head_dim;
@@ -1377,13 +1410,15 @@ int pf_run(vrt_g3* g, uint32_t T) {
     float* big = p.big;
     float eps = P.eps;
     G3State* st = P.st;
+    if (T == 0u || T > p.max_t || static_cast<uint64_t>(p0) + T > g->cfg.context_length)
+        return set_error(VRT_ERR_STATE, "prefill segment outside the workspace or the context");
     auto launch = [&](const void* fn, dim3 grid, void** args) -> int {
         VRT_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(kPfThreads), args, 0, s));
         return VRT_OK;
     };
     {
         const uint8_t* te = P.tok_embd;
-        const uint32_t* tok = P.tokens;
+        const uint32_t* tok = P.tokens + p0;
         float es = P.emb_scale;
         void* args[] = {&te, &tok, &d, &es, &h};
         if (int rc = launch(reinterpret_cast<const void*>(&k_pf_embed), dim3(T), args)) return rc;
@@ -1401,6 +1436,22 @@ int pf_run(vrt_g3* g, uint32_t T) {
                 return rc;
         }
         if (int rc = pf_gemm(g, ahi, alo, T, d, {{Ly.wq, qw}, {Ly.wk, hd}, {Ly.wv, hd}}, lw ? &lw[l].qkv : nullptr, big, 1, s)) return rc;
+        // key coordinates: the history this segment's queries can see (from kb: position 0 in a
+        // global block, the window's start rounded down to 32 in a local one), then its rows
+        const uint32_t window = Ly.slots >= g->cfg.context_length ? 0u : Ly.slots;
+        const uint32_t kb = window != 0u && p0 + 1u > window ? (p0 + 1u - window) & ~31u : 0u;
+        uint32_t qo = p0 - kb;
+        if (qo != 0u) {
+            const float* kc = Ly.kc;
+            const float* vc = Ly.vc;
+            uint32_t slots = Ly.slots, kvf = P.kv_f16, kb_ = kb;
+            _Float16* khi = static_cast<_Float16*>(p.khi);
+            _Float16* klo = static_cast<_Float16*>(p.klo);
+            _Float16* vhi = static_cast<_Float16*>(p.vhi);
+            _Float16* vlo = static_cast<_Float16*>(p.vlo);
+            void* args[] = {&kc, &vc, &slots, &kvf, &kb_, &qo, &hd, &khi, &klo, &vhi, &vlo};
+            if (int rc = launch(reinterpret_cast<const void*>(&k_pf_kv_hist), dim3(qo), args)) return rc;
+        }
         {
             const float* qn = Ly.q_norm;
             const float* kn = Ly.k_norm;
@@ -1409,14 +1460,15 @@ int pf_run(vrt_g3* g, uint32_t T) {
             float* kc = Ly.kc;
             float* vc = Ly.vc;
             uint32_t slots = Ly.slots;
-            uint32_t tp = pf_pad(T);
+            // rows past the segment zero the keys and values up to the next 64 key coordinates
+            const uint32_t tp = pf_pad(qo + T) - qo;
             _Float16* khi = static_cast<_Float16*>(p.khi);
             _Float16* klo = static_cast<_Float16*>(p.klo);
             _Float16* vhi = static_cast<_Float16*>(p.vhi);
             _Float16* vlo = static_cast<_Float16*>(p.vlo);
-            uint32_t kvf = P.kv_f16;
+            uint32_t kvf = P.kv_f16, p0_ = p0, qo_ = qo;
             void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &khi, &klo, &vhi, &vlo,
-                            &kvf};
+                            &kvf, &p0_, &qo_};
             const uint32_t waves = std::min(H + 1u, kPfQkMaxWaves);
             VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_pf_qk), dim3(tp), dim3(64u * waves), args, 0, s));
         }
@@ -1424,11 +1476,12 @@ int pf_run(vrt_g3* g, uint32_t T) {
         // keys and values go to the cache) it runs for the last position alone: attention for
         // that position's query tile, then one row.
         const bool last = l + 1u == L;
+        if (last && !final) break;   // an earlier segment: the last block's keys and values are all it leaves
         const uint32_t fr = last ? 1u : T;
         const uint64_t a0 = last ? static_cast<uint64_t>(T - 1u) * d : 0u;
         const uint64_t aq = last ? static_cast<uint64_t>(T - 1u) * qw : 0u;
         // the attention output replaces q (hi/lo in ahi/alo)
-        if (int rc = pf_attention(g, Ly, T, last ? (T - 1u) / 32u : 0u, ahi, alo, s)) return rc;
+        if (int rc = pf_attention(g, Ly, T, last ? (T - 1u) / 32u : 0u, ahi, alo, s, qo)) return rc;
         uint32_t so = last ? pf_splits(1u, d) : s_o;
         if (int rc = pf_gemm(g, ahi + aq, alo + aq, fr, qw, {{Ly.wo, d}}, lw ? &lw[l].o : nullptr, x, so, s)) return rc;
         so = std::max(1u, std::min(so, (qw / 32u) / 2u));
@@ -1446,6 +1499,7 @@ int pf_run(vrt_g3* g, uint32_t T) {
         s_down = std::max(1u, std::min(last ? pf_splits(1u, d) : s_o, (F / 32u) / 2u));
         if (int rc = pf_gemm(g, ghi, glo, fr, F, {{Ly.wd, d}}, lw ? &lw[l].down : nullptr, x, s_down, s)) return rc;
     }
+    if (!final) return VRT_OK;
     {   // last position: its FFN output (the split partials summed in order) and its residual
         // feed the decode step's final norm + LM head
         float* out = P.f;
