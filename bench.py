@@ -137,6 +137,7 @@ def prefill_flops(cfg, T: int) -> int:
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
+PREFILL_SEGMENT = 2048   # positions per batched prefill pass (longer prompts run as segments)
 
 
 def prefill_bench(ctx, g, cfg, T: int = 512, reps: int = 5):
@@ -154,7 +155,8 @@ def prefill_bench(ctx, g, cfg, T: int = 512, reps: int = 5):
     ms = ctx.elapsed_ms(ev0, ev1) / reps
     flops = prefill_flops(cfg, T)
     tflops = flops / (ms / 1e3) / 1e12
-    return {"workload": f"{T}-token prompt, one batched prefill (MFMA Q8_0 GEMMs, causal attention, last-row LM head)",
+    seg = f", in segments of {PREFILL_SEGMENT}" if T > PREFILL_SEGMENT else ""
+    return {"workload": f"{T}-token prompt, one batched prefill{seg} (MFMA Q8_0 GEMMs, causal attention, last-row LM head)",
             "tokens_per_s": round(T / (ms / 1e3), 1), "ms": round(ms, 4), "gflop": round(flops / 1e9, 2),
             "tflops": round(tflops, 2), "mfma_peak_tflops": MFMA_F16_PEAK_TFLOPS,
             "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
@@ -318,7 +320,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-phases", action="store_true", help="skip the traced per-phase split")
     ap.add_argument("--no-long", action="store_true", help="skip the 8192-token long-context measurement")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token batched prefill measurement")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the 512- and 8192-token batched prefill measurements")
     ap.add_argument("--no-kernels", action="store_true",
                     help="skip the standalone matvec / QKV / FFN measurements (single-matvec and layer-block workloads)")
     ap.add_argument("--multikernel", action="store_true",
@@ -399,6 +402,7 @@ def main():
     longctx = None if args.no_long else long_context(ctx, g, cfg)
     longctx16 = None if args.no_long else long_context(ctx, g, cfg, kv_f16=True)
     prefill = None if args.no_prefill else prefill_bench(ctx, g, cfg)
+    prefill_long = None if args.no_prefill else prefill_bench(ctx, g, cfg, T=8192, reps=3)
     kernels = None if args.no_kernels else kernel_legs(ctx)
     multikernel = multikernel_leg(ctx, g, prompt) if args.multikernel else None
     batched = None if args.no_batched else batched_leg(ctx, g, cfg)
@@ -443,6 +447,7 @@ def main():
         "long_context": longctx,
         "long_context_kv_f16": longctx16,
         "prefill": prefill,
+        "prefill_8192": prefill_long,
         "kernels": kernels,
         "multikernel": multikernel,
         "batched": batched,
