@@ -327,7 +327,7 @@ def main():
     ap.add_argument("--multikernel", action="store_true",
                     help="also time the multi-kernel (hipGraph) decode path")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (B sequences) measurement")
-    ap.add_argument("--only", choices=("prefill", "batched", "kernels"),
+    ap.add_argument("--only", choices=("prefill", "prefill_8192", "batched", "kernels"),
                     help="run only this leg and print it (no decode timing, so no cooperative launch: for "
                          "profiling one leg at a time)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -355,7 +355,9 @@ def main():
     g = vrt.Gemma3(ctx, args.model)
     cfg = g.config
     if args.only:
-        legs = {"prefill": lambda: prefill_bench(ctx, g, cfg), "batched": lambda: batched_leg(ctx, g, cfg),
+        legs = {"prefill": lambda: prefill_bench(ctx, g, cfg),
+                "prefill_8192": lambda: prefill_bench(ctx, g, cfg, T=8192, reps=3),
+                "batched": lambda: batched_leg(ctx, g, cfg),
                 "kernels": lambda: kernel_legs(ctx)}
         res = legs[args.only]()
         g.close()
