@@ -33,7 +33,7 @@
 
 namespace vrt {
 
-constexpr uint32_t kPrefillMax = 2048;   // positions of one batched prefill
+constexpr uint32_t kPrefillMax = 2048;   // positions of one batched prefill segment
 
 constexpr int kThreads = 256;
 constexpr int kMaxE = 8;  // vector elements per thread in prologues: d, H*hd, F <= 2048

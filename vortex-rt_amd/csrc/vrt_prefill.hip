@@ -606,7 +606,7 @@ constexpr uint32_t kPfAttKC = 128;   // keys per attention chunk (a multiple of 
 struct PfAttn {
     const _Float16* qhi;   // [T][H * hd] queries, normed and rotated (overwritten by the output)
     const _Float16* qlo;
-    const _Float16* khi;   // keys in pf_kswz order (Tp / 32 tiles)
+    const _Float16* khi;   // keys in pf_kswz order, by key coordinate (32-key tiles)
     const _Float16* klo;
     const _Float16* vhi;   // values in pf_vswz order
     const _Float16* vlo;
@@ -1408,8 +1408,10 @@ static int pf_attention(vrt_g3* g, const LayerParams& Ly, uint32_t T, uint32_t q
     }
 }
 
-// T prompt positions 0..T-1 on the context's stream; the last one runs the LM head + argmax
-// (results[T-1], logits when want_logits). The caller has reset the step state.
+// Prompt positions p0..p0+T-1 on the context's stream (positions before p0 are already in the
+// KV cache). With `final`, the last one runs the LM head + argmax (results[p0+T-1], logits when
+// want_logits); otherwise the segment ends after the last block's keys and values. The caller
+// has reset the step state before the first segment.
 int pf_run(vrt_g3* g, uint32_t T, uint32_t p0, bool final) {
     const PfState& p = g->pf;
     hipStream_t s = g->ctx->stream;
