@@ -83,6 +83,40 @@ def test_prefill_segments(ctx, model_dir, kv_f16):
     _check(ctx, path, synth.uniform_ids(9, 4500, 2, LONG["vocab"]), 4, kv_f16=kv_f16)
 
 
+LC_MODEL = dict(synth.GEMMA3_270M, n_layers=6, vocab=4096, context=8448)
+
+
+def test_prefill_segments_long_context_golden(ctx, model_dir):
+    """An 8192-token prompt at the Gemma-3-270M block shape (6 blocks, window 512, block 5
+    global; head_dim 256) prefilled in four segments of 2048, then 16 teacher-forced decode steps
+    against the oracle's vectors in tests/golden/long_context_6blk.npz (tests/golden/
+    make_long_context.py, the long-context decode test's fixture): greedy ids identical, their
+    logits within the tolerance, the last step's logits and hidden state within the tolerances.
+    The segments' global attention reads up to 6144 earlier positions from the cache, the local
+    blocks' their last 512."""
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "long_context_6blk.npz"))
+    path = os.path.join(str(model_dir), "lc6.gguf")
+    if not os.path.exists(path):
+        synth.write_gemma3_gguf(path, seed=7, **LC_MODEL)
+    n_check = gold["index"].size
+    toks = synth.uniform_ids(8, 8192 + n_check, 2, LC_MODEL["vocab"])
+    scale = np.max(np.abs(gold["last_logits"]))
+    g = vrt.Gemma3(ctx, path)
+    try:
+        print("[pf] 8192-token prefill in segments at the 270M block shape", flush=True)
+        g.prefill(toks[:8192], top_k=0)
+        hid = None
+        for j in range(n_check):
+            p, last = 8192 + j, j == n_check - 1
+            (idx, val), hid = g.decode(int(toks[p]), p, top_k=8 if last else 1, hidden=last)
+            assert idx == int(gold["index"][j]), f"position {p}"
+            assert abs(val - float(gold["value"][j])) <= LOGIT_TOL * scale, f"position {p}"
+        assert _rel(g.logits(), gold["last_logits"]) <= LOGIT_TOL
+        assert _rel(hid, gold["last_hidden"]) <= HIDDEN_TOL
+    finally:
+        g.close()
+
+
 def test_prefill_full_shape_512(ctx, full_model):
     """The 512-token prefill workload at the Gemma-3-270M shape."""
     _check(ctx, full_model, synth.uniform_ids(4, 512, 2, 262144), 2)
