@@ -338,8 +338,8 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the batch-1 token loop is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: this framework runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the batch-1 token loop is single-GPU)", file=sys.stderr)
         sys.exit(2)
 
     import synth

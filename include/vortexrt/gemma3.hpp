@@ -66,7 +66,7 @@ public:
 
     [[nodiscard]] const Gemma3Config& config() const noexcept { return config_; }
 
-    // Lane and fusion policy (src/gemma3.cpp:94-172, :656-671). On this build both are
+    // Lane and fusion policy (src/gemma3.cpp:94-172, :656-671). In this library both are
     // structural rather than tunable: every Q/K/V projection is one fused phase (one launch on
     // the multi-kernel path) and every gate/up pair one phase with the GELU product fused in, so
     // fusion is always on and set_projection_fusion_enabled() leaves it on; matvec row slots

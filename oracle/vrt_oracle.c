@@ -1,7 +1,7 @@
 /*
  * vrt_oracle.c -- CPU restatement of Vortex-RT's Gemma 3 Q8_0 token loop.
  *
- * TEST INFRASTRUCTURE ONLY (see vrt_oracle.h): the checker, never the product.
+ * TEST INFRASTRUCTURE ONLY (see vrt_oracle.h): the oracle, never the product.
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp).
  * Citations are to the reference tree (yannickfan67-ai/Vortex-RT v0.2.0).
  */

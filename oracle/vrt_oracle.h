@@ -1,7 +1,7 @@
 /*
  * vrt_oracle.h -- CPU restatement of Vortex-RT's Gemma 3 Q8_0 token-loop arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: only tests/, the smoke
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle: only tests/, the smoke
  * check in __graft_entry__.py and bench.py's cpu_baseline leg may load it. The
  * product (libvrt_hip.so, libvortexrt.so) never links or calls it.
  *

@@ -802,7 +802,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
     const uint32_t d = c.embedding_length, H = c.head_count, hd = c.head_dim, F = c.feed_forward_length;
     VRT_REQUIRE(d % 32u == 0 && F % 32u == 0 && (H * hd) % 32u == 0, "Gemma 3 widths must be multiples of 32 (Q8_0 blocks)");
     VRT_REQUIRE(d <= 2048u && F <= 2048u && H * hd <= 2048u && hd <= 256u && H <= 8u,
-                "Gemma 3 shape outside this build's kernels: embedding/ffn/attention width <= 2048, head_dim <= 256, heads <= 8");
+                "Gemma 3 shape outside this library's kernels: embedding/ffn/attention width <= 2048, head_dim <= 256, heads <= 8");
     VRT_REQUIRE(desc->arena && desc->layers && desc->output_norm, "vrt_g3_create: null tensor pointer");
     const auto* arena = static_cast<const uint8_t*>(desc->arena);
     auto q8_fits = [&](uint64_t off, uint64_t rows, uint64_t k) {
