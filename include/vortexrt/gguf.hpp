@@ -1,14 +1,13 @@
-// GGUF v2/v3 reader (include/vortexrt/gguf.hpp:14-128 of Vortex-RT): same public API, host only.
+// GGUF v2/v3 reader (include/vortexrt/gguf.hpp:14-128 of Vortex-RT): same public API, host only;
+// the private part is this reader's own (a read-only memory map of the file).
 #pragma once
 
 #include <cstddef>
 #include <cstdint>
 #include <filesystem>
-#include <fstream>
-#include <mutex>
+#include <memory>
 #include <optional>
 #include <string>
-#include <unordered_map>
 #include <variant>
 #include <vector>
 
@@ -62,14 +61,19 @@ struct GgufTensorInfo {
 class GgufFile {
 public:
     explicit GgufFile(const std::filesystem::path& path);
+    ~GgufFile();
+    GgufFile(GgufFile&&) noexcept;
+    GgufFile& operator=(GgufFile&&) noexcept;
+    GgufFile(const GgufFile&) = delete;
+    GgufFile& operator=(const GgufFile&) = delete;
 
-    [[nodiscard]] std::uint32_t version() const noexcept { return version_; }
-    [[nodiscard]] std::uint64_t file_size() const noexcept { return file_size_; }
-    [[nodiscard]] std::uint64_t data_offset() const noexcept { return data_offset_; }
-    [[nodiscard]] std::uint32_t alignment() const noexcept { return alignment_; }
+    [[nodiscard]] std::uint32_t version() const noexcept;
+    [[nodiscard]] std::uint64_t file_size() const noexcept;
+    [[nodiscard]] std::uint64_t data_offset() const noexcept;
+    [[nodiscard]] std::uint32_t alignment() const noexcept;
 
-    [[nodiscard]] const std::vector<GgufMetadata>& metadata() const noexcept { return metadata_; }
-    [[nodiscard]] const std::vector<GgufTensorInfo>& tensors() const noexcept { return tensors_; }
+    [[nodiscard]] const std::vector<GgufMetadata>& metadata() const noexcept;
+    [[nodiscard]] const std::vector<GgufTensorInfo>& tensors() const noexcept;
 
     [[nodiscard]] const GgufValue* find_metadata(const std::string& key) const noexcept;
     [[nodiscard]] const GgufTensorInfo* find_tensor(const std::string& name) const noexcept;
@@ -89,20 +93,11 @@ public:
     void read_data(std::uint64_t offset, void* destination, std::size_t bytes) const;
 
 private:
-    void read_bytes_at(std::uint64_t absolute_offset, void* destination, std::size_t bytes) const;
-
-    std::filesystem::path path_;
-    std::uint32_t version_ = 0;
-    std::uint64_t file_size_ = 0;
-    std::uint64_t data_offset_ = 0;
-    std::uint32_t alignment_ = 32;
-
-    std::vector<GgufMetadata> metadata_;
-    std::vector<GgufTensorInfo> tensors_;
-    std::unordered_map<std::string, std::size_t> metadata_index_;
-    std::unordered_map<std::string, std::size_t> tensor_index_;
-    mutable std::mutex payload_stream_mutex_;
-    mutable std::ifstream payload_stream_;
+    // The file mapped read-only into memory and the header parsed from the mapping (gguf.cpp).
+    // Every read is a bounds-checked copy out of the mapping, so one GgufFile serves concurrent
+    // readers without a lock.
+    struct Image;
+    std::unique_ptr<const Image> image_;
 };
 
 [[nodiscard]] const char* gguf_value_type_name(GgufValueType type) noexcept;

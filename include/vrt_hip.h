@@ -185,6 +185,8 @@ typedef struct vrt_g3_desc {
  * the captured decode-step graph. Shapes are validated as the reference does
  * (src/gemma3.cpp:219-257). */
 int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out);
+/* Fails with VRT_ERR_STATE, destroying nothing, while a vrt_g3_batch created over this executor
+ * is alive: destroy batches first, then the executor, then the context. */
 int vrt_g3_destroy(vrt_g3* g3);
 
 /* Gemma3Model::reset_cache, src/gemma3.cpp:1454-1460. */
@@ -275,6 +277,8 @@ int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
  * position 0, as the reference resets its cache. */
 typedef struct vrt_g3_batch vrt_g3_batch;
 int vrt_g3_batch_create(vrt_g3* g3, uint32_t max_seqs, uint32_t max_ctx, vrt_g3_batch** out);
+/* The batch reads its executor's weights and launches on its context's stream: destroy it
+ * before the executor (vrt_g3_destroy refuses while it is alive). */
 int vrt_g3_batch_destroy(vrt_g3_batch* b);
 /* Sequence seq (or every sequence, seq = 0xffffffff) restarts at position 0. */
 int vrt_g3_batch_reset(vrt_g3_batch* b, uint32_t seq);

@@ -29,6 +29,12 @@ class G3Info(C.Structure):
          ("eos_id", C.c_uint32), ("bos_id", C.c_uint32)]
 
 
+class G3Taps(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "xn", "q_proj", "k_proj", "v_proj", "q_att", "keys", "values", "history", "att")] + \
+        [("hist_cap", C.c_uint32)]
+
+
 _libs = {}
 
 
@@ -70,6 +76,7 @@ def lib(path: str | None = None):
             "or_g3_generate": (I, [P, P, U32, U32, P, P]),
             "or_g3_error": (C.c_char_p, [P]),
             "or_g3_set_kv_f16": (None, [P, I]),
+            "or_g3_set_taps": (None, [P, P]),
             "or_num_threads": (I, []),
         }
         for name, (res, args) in sig.items():
@@ -237,6 +244,26 @@ class Model:
             raise RuntimeError(self.L.or_g3_error(self.h).decode())
         return dict(hidden=hidden, logits=lg, index=int(ai.value) if want_logits else None,
                     value=float(av.value) if want_logits else None)
+
+    def decode_taps(self, token: int, pos: int, hist_cap: int, want_logits: bool = False):
+        """decode() that also returns the attention sub-path's intermediates of every block
+        (or_g3_set_taps): xn, q_proj, k_proj, v_proj, q_att, att, and keys/values [L, history, hd]
+        oldest first (at most hist_cap rows per block), history [L]."""
+        i = self.info
+        nl, d, hd, qd = i.block_count, i.embedding_length, i.head_dim, i.head_count * i.head_dim
+        t = dict(xn=np.zeros((nl, d), np.float32), q_proj=np.zeros((nl, qd), np.float32),
+                 k_proj=np.zeros((nl, hd), np.float32), v_proj=np.zeros((nl, hd), np.float32),
+                 q_att=np.zeros((nl, qd), np.float32), att=np.zeros((nl, qd), np.float32),
+                 keys=np.zeros((nl, hist_cap, hd), np.float32), values=np.zeros((nl, hist_cap, hd), np.float32),
+                 history=np.zeros(nl, np.uint32))
+        taps = G3Taps(**{k: a.ctypes.data for k, a in t.items()}, hist_cap=hist_cap)
+        self.L.or_g3_set_taps(self.h, C.byref(taps))
+        try:
+            r = self.decode(token, pos, want_logits=want_logits)
+        finally:
+            self.L.or_g3_set_taps(self.h, None)
+        r.update(t)
+        return r
 
     def generate(self, prompt, max_new: int):
         pr = np.ascontiguousarray(prompt, dtype=np.uint32)

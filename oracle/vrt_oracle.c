@@ -424,6 +424,8 @@ struct or_g3 {
     uint32_t next_pos;
     uint32_t lanes;
     int kv_f16;
+    int tapping;
+    or_g3_taps taps;
     char err[256];
 };
 
@@ -607,6 +609,17 @@ void or_g3_set_kv_f16(or_g3* m, int on) {
     or_g3_reset(m);
 }
 
+void or_g3_set_taps(or_g3* m, const or_g3_taps* taps) {
+    m->tapping = taps != NULL;
+    if (taps) m->taps = *taps;
+    else memset(&m->taps, 0, sizeof m->taps);
+}
+
+/* Copies n floats into tap array a at row l (row length n), when that tap is set. */
+static void tap_row(float* a, uint32_t l, const float* src, uint32_t n) {
+    if (a) memcpy(a + (size_t)l * n, src, sizeof(float) * n);
+}
+
 /* push_back then pop_front while size > window (src/gemma3.cpp:1590-1600). */
 static int kv_push(or_layer_t* L, const float* k_in, const float* v_in, uint32_t hd, int kv_f16) {
     float kr[512], vr[512];   /* hd <= 512 (checked at open) */
@@ -684,6 +697,12 @@ static int decode_impl(or_g3* m, uint32_t token, uint32_t pos, int want_logits,
         or_q8_matvec_lanes(m->data + L->q, xn, q, d, (uint64_t)H * hd, lanes);
         or_q8_matvec_lanes(m->data + L->k, xn, k, d, hd, lanes);
         or_q8_matvec_lanes(m->data + L->v, xn, v, d, hd, lanes);
+        if (m->tapping) {
+            tap_row(m->taps.xn, l, xn, d);
+            tap_row(m->taps.q_proj, l, q, H * hd);
+            tap_row(m->taps.k_proj, l, k, hd);
+            tap_row(m->taps.v_proj, l, v, hd);
+        }
         or_rms_norm_heads(q, L->q_norm, H, hd, eps);
         or_rms_norm_heads(k, L->k_norm, 1, hd, eps);
         or_apply_rope(q, H, hd, L->global ? gc : lc, L->global ? gs : ls);
@@ -701,7 +720,15 @@ static int decode_impl(or_g3* m, uint32_t token, uint32_t pos, int want_logits,
             K = kbuf;
             V = vbuf;
         }
+        if (m->tapping) {
+            tap_row(m->taps.q_att, l, q, H * hd);
+            const uint32_t cap = m->taps.hist_cap, rows = hist < cap ? hist : cap;
+            if (m->taps.keys) memcpy(m->taps.keys + (size_t)l * cap * hd, K, sizeof(float) * rows * hd);
+            if (m->taps.values) memcpy(m->taps.values + (size_t)l * cap * hd, V, sizeof(float) * rows * hd);
+            if (m->taps.history) m->taps.history[l] = hist;
+        }
         if (or_attention(q, K, V, hist, H, hd, m->attn_scale, att)) { set_err(m->err, sizeof m->err, "Gemma 3 attention softmax failed"); rc = -4; goto done; }
+        if (m->tapping) tap_row(m->taps.att, l, att, H * hd);
         or_q8_matvec_lanes(m->data + L->o, att, o, H * hd, d, lanes);
         or_rms_norm_inplace(o, L->post_attn_norm, d, eps);
         for (uint32_t i = 0; i < d; ++i) o[i] += hidden[i];              /* add_inplace(o, hidden) */

@@ -26,7 +26,15 @@
  *   or_attention         single position returns v; equal keys give the mean of v;
  *                        numpy float64 softmax.
  *   or_g3_*              zero-projection model closed form (hidden = normed scaled
- *                        embedding); window eviction; composition of the pinned parts.
+ *                        embedding); window eviction; composition of the pinned parts;
+ *                        block-wiring invariants (scale absorption, window-1 flow, RoPE base
+ *                        reach, branch norms) with compiled mutants that must fail them.
+ *   attention sub-path   through or_g3_set_taps, per block and step: the query and newest key
+ *   of or_g3_decode      against float64 per-head RMSNorm then NeoX RoPE at the block's base,
+ *                        the newest value equal to the v projection (no norm on v), q.k at the
+ *                        current position unchanged by RoPE (one table for q and k), the cache
+ *                        rows in time order with window eviction, and the output against a
+ *                        float64 softmax(q K^T / sqrt(head_dim)) V.
  * Functions none of these reach are marked "parity unpinned" at their definition.
  */
 #ifndef VRT_ORACLE_H
@@ -116,6 +124,31 @@ const char* or_g3_error(const or_g3* m);
 /* fp16 KV cache: keys and values are rounded with or_f32_to_f16_rne when they enter the cache
  * (every position's attention, the current one's included, reads the cache). Resets the cache. */
 void or_g3_set_kv_f16(or_g3* m, int on);
+
+/* Intermediate values of the attention sub-path, for the parity tests that pin it
+ * (src/gemma3.cpp:1511-1696 computes them inside decode_token and exposes none). While taps
+ * are set, every decode step writes, for each block l (arrays indexed [l][...]):
+ *   xn       [d]          the attention-norm output the q/k/v projections read
+ *   q_proj   [H*hd]       the q projection as the matvec left it (before QK-norm)
+ *   k_proj   [hd], v_proj [hd]   the k and v projections
+ *   q_att    [H*hd]       the query the attention reads (after QK-norm and RoPE)
+ *   keys, values [hist_cap][hd]  the cache rows the attention reads, oldest first
+ *   history  (u32)        how many rows that is (rows past hist_cap are not written)
+ *   att      [H*hd]       the attention output the O projection reads
+ * Any pointer may be NULL. Passing NULL clears the taps. */
+typedef struct or_g3_taps {
+    float* xn;
+    float* q_proj;
+    float* k_proj;
+    float* v_proj;
+    float* q_att;
+    float* keys;
+    float* values;
+    uint32_t* history;
+    float* att;
+    uint32_t hist_cap;
+} or_g3_taps;
+void or_g3_set_taps(or_g3* m, const or_g3_taps* taps);
 /* Threads used by the OpenMP loops (matvec rows). */
 int or_num_threads(void);
 

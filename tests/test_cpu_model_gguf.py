@@ -176,6 +176,53 @@ def test_gguf_against_reference_parser(tmp_path):
     f.close()
 
 
+def _header_only(path, n_tensors=0, array_count=None):
+    """A GGUF v3 header that ends early: n_tensors tensors announced, and when array_count is
+    given one metadata key "a" announcing a u32 array of that many elements."""
+    import struct
+    b = struct.pack("<IIQQ", 0x46554747, 3, n_tensors, 1 if array_count is not None else 0)
+    if array_count is not None:
+        b += struct.pack("<Q", 1) + b"a" + struct.pack("<IIQ", 9, 4, array_count)
+    open(path, "wb").write(b)
+    return path
+
+
+def _limit_errors(tmp_path, run):
+    """run(path) -> error text, for headers just inside and just past the reference's limits:
+    arrays of 2^28 elements (src/gguf.cpp:16, :105-107), 1,000,000 tensors (:334-336)."""
+    out = {}
+    for name, kw in (("array_ok", dict(array_count=1 << 28)), ("array_over", dict(array_count=(1 << 28) + 1)),
+                     ("count_ok", dict(n_tensors=1000000)), ("count_over", dict(n_tensors=1000001))):
+        out[name] = run(_header_only(str(tmp_path / f"{name}.gguf"), **kw))
+    return out
+
+
+def test_cpp_gguf_limits_match_reference(tmp_path):
+    """The C++ reader applies the reference's array-length and header-count limits: a header one
+    past either limit is rejected with the reference's message, one at the limit gets past the
+    check (and then fails at the end of the file)."""
+    def run(p):
+        r = subprocess.run([_cpp("gguf_test"), p], capture_output=True, text=True)
+        assert r.returncode == 1, r.stdout
+        return r.stdout
+    e = _limit_errors(tmp_path, run)
+    assert "GGUF array length exceeds safety limit" in e["array_over"]
+    assert "safety limit" not in e["array_ok"] and "end of GGUF file" in e["array_ok"]
+    assert "GGUF header counts exceed safety limits" in e["count_over"]
+    assert "safety limit" not in e["count_ok"] and "end of GGUF file" in e["count_ok"]
+
+
+@pytest.mark.skipif(not os.path.exists(REF_PROBE), reason="reference GGUF parser probe not built (oracle/Makefile ref)")
+def test_gguf_limits_reference_parser(tmp_path):
+    """The reference's own parser rejects the two over-limit headers with the same messages (the
+    at-limit array is not run through it: it reserves the announced count, 2^28 values)."""
+    for name, kw, msg in (("array_over", dict(array_count=(1 << 28) + 1), "GGUF array length exceeds safety limit"),
+                          ("count_over", dict(n_tensors=1000001), "GGUF header counts exceed safety limits")):
+        p = _header_only(str(tmp_path / f"{name}.gguf"), **kw)
+        r = subprocess.run([REF_PROBE, p], capture_output=True, text=True)
+        assert r.returncode == 1 and msg in r.stdout, (name, r.stdout)
+
+
 # ---- C ABI ---------------------------------------------------------------------------------
 
 def _declared_symbols():

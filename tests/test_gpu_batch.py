@@ -1,11 +1,12 @@
 """Batched greedy decode (vrt_g3_batch_*) against the oracle's single-sequence loop
 (src/gemma3.cpp:1462-1882, one oracle model per sequence). The batched path computes every
 projection and the LM head as MFMA GEMMs over the step's rows (the numerics of the prefill), so
-its logits are held to the prefill's bound: within 1e-3 of max|logit|. Greedy tokens must match
-wherever the oracle's top-2 margin exceeds 1e-4 of the top logit; the sequences are driven with
-the oracle's own tokens (teacher forcing), so one near-tie cannot cascade. Sequences join at
-different steps, so every step mixes rows at different positions, local windows and chunk
-counts."""
+its logits are held to the prefill's bound: within 1e-3 of max|logit|. The sequences are driven
+with the oracle's own tokens (teacher forcing) and every greedy token must be identical to the
+oracle's, as on the single-sequence path. (The oracle's smallest top-2 margin over these rows is
+7.1e-4 of the top logit in the tiny-model cases and 2.9e-3 at the full shape; each row's margin
+is printed with the failure.) Sequences join at different steps, so every step mixes rows at
+different positions, local windows and chunk counts."""
 import numpy as np
 import pytest
 
@@ -16,7 +17,6 @@ import vrt
 pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 1e-3     # of max|logit|, as for the prefill (the same GEMMs and hi/lo activation split)
-MARGIN = 1e-4        # top-2 margin (relative) above which the greedy token must agree
 
 
 def _rel(a, b):
@@ -59,9 +59,9 @@ def _drive(b, runs, starts, check_logits_every=1):
             idx, val = b.step(rows, toks)
             for r, i in enumerate(rows):
                 o = runs[i][1][nxt[i]]
-                where = f"sequence {i} position {nxt[i]} (step {step}, {len(rows)} rows)"
-                if o["margin"] > MARGIN:
-                    assert int(idx[r]) == o["index"], where
+                where = (f"sequence {i} position {nxt[i]} (step {step}, {len(rows)} rows; "
+                         f"oracle top-2 margin {o['margin']:.3g})")
+                assert int(idx[r]) == o["index"], where
                 assert abs(float(val[r]) - o["value"]) <= LOGIT_TOL * float(np.max(np.abs(o["logits"]))), where
                 if checked % check_logits_every == 0:
                     assert _rel(b.logits(r), o["logits"]) <= LOGIT_TOL, where
@@ -152,6 +152,24 @@ def test_batch_reset_and_reuse(ctx, tiny_model):
     finally:
         b.close()
         g.close()
+
+
+def test_batch_destroy_order(ctx, tiny_model):
+    """The executor refuses to be destroyed while a batch over it is alive (the batch reads its
+    weights and stream), and is destroyed once the batch is gone."""
+    g = vrt.Gemma3(ctx, tiny_model)
+    b = vrt.Gemma3Batch(g, 2, 16)
+    try:
+        b.step([0], [5])
+        L = vrt.lib()
+        assert L.vrt_g3_destroy(g.h) == vrt.VRT_ERR_STATE
+        assert "batched decoder" in L.vrt_last_error().decode()
+        idx, _ = b.step([0], [6])          # the batch still runs on the live executor
+        assert 0 <= int(idx[0]) < 1000
+    finally:
+        b.close()
+    g.close()                              # checks vrt_g3_destroy's status
+    assert g.h is None
 
 
 def test_batch_errors(ctx, tiny_model):

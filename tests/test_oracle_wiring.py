@@ -22,6 +22,16 @@ block 5 global):
   ffn_norm and post_ffw_norm do.
 * Zero projections. Every block projection zero: each block is the identity, and the hidden
   state is RMSNorm(embedding(t) * sqrt(d)) * w_out (float64 check).
+* Attention sub-path (src/gemma3.cpp:1557-1696), from the oracle's per-block intermediates
+  (or_g3_set_taps) against float64 restatements of the published operations: the query the
+  attention reads is per-head RMSNorm (Zhang & Sennrich 2019) of the q projection times the
+  q-norm weight, then RoPE (Su et al. 2021, the NeoX half-split pairing (i, i + hd/2)) with
+  inverse frequencies base^(-2i/hd) at the block's base; the newest cached key is the k
+  projection through the same two steps with the k-norm weight; the newest cached value is the v
+  projection bit for bit (no norm on v); per head, q.k of the current position after RoPE equals
+  the dot product before it (true only when q and k turn by one table); earlier cache rows are
+  earlier steps' newest rows, oldest first, min(p + 1, window) of them in local blocks and p + 1
+  in global ones; the attention output is softmax(q K^T / sqrt(hd)) V (Vaswani et al. 2017).
 
 The mutants are compiled from patched copies of oracle/vrt_oracle.c in a temporary directory;
 each must fail at least one invariant, the unpatched oracle must pass them all.
@@ -76,6 +86,7 @@ def models(tmp_path_factory):
         m[f"rope_a_{nl}"] = _model(d, f"rope_a_{nl}", n_layers=nl, rope_global=1.0e6)
         m[f"rope_b_{nl}"] = _model(d, f"rope_b_{nl}", n_layers=nl, rope_global=5.0e4)
     base = _model(d, "base")
+    m["base"] = base
     hd, dm = synth.TINY["head_dim"], synth.TINY["d_model"]
     sizes = {"attn_norm": dm, "attn_q_norm": hd, "attn_k_norm": hd, "post_attention_norm": dm,
              "ffn_norm": dm, "post_ffw_norm": dm}
@@ -94,7 +105,8 @@ def models(tmp_path_factory):
 # ---- runners --------------------------------------------------------------------------------
 
 def oracle_runner(lib_path=None):
-    """(path, tokens) -> [(hidden, logits)] per position, or None if the decode raised."""
+    """(path, tokens) -> [(hidden, logits)] per position, or None if the decode raised. The
+    runner's lib_path attribute names the oracle library it loads (None: the built one)."""
     def run(path, toks):
         m = oracle.Model(path, lib_path=lib_path)
         try:
@@ -107,6 +119,7 @@ def oracle_runner(lib_path=None):
             return None
         finally:
             m.close()
+    run.lib_path = lib_path
     return run
 
 
@@ -198,8 +211,96 @@ def inv_zero_projection(run, m):
     return bad
 
 
+LOCAL_ROPE_BASE = 1.0e4   # src/gemma3.cpp:271-274: local blocks always turn at base 10000
+
+
+def _rms64(x, w, eps):
+    """Per-row RMSNorm in float64: x / sqrt(mean(x^2) + eps) * w."""
+    x = x.astype(np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w.astype(np.float64)
+
+
+def _rope64(x, pos, base):
+    """RoPE of rows x [.., hd] at position pos in float64: pair (i, i + hd/2) turned by
+    pos * base^(-2i/hd)."""
+    hd = x.shape[-1]
+    half = hd // 2
+    ang = pos * np.power(np.float64(base), -2.0 * np.arange(half, dtype=np.float64) / hd)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = x[..., :half], x[..., half:]
+    return np.concatenate([a * c - b * s, b * c + a * s], axis=-1)
+
+
+def _sdpa64(q, keys, values, scale):
+    """Scaled dot-product attention in float64 for heads q [H, hd] over keys/values [T, hd]."""
+    s = (q.astype(np.float64) @ keys.astype(np.float64).T) * scale
+    e = np.exp(s - s.max(axis=-1, keepdims=True))
+    return (e / e.sum(axis=-1, keepdims=True)) @ values.astype(np.float64)
+
+
+def inv_attention_subpath(run, m):
+    path = m["base"]
+    f = gguf.GgufFile.open(path)
+    try:
+        nl = synth.TINY["n_layers"]
+        qn = [f.read_f32(f"blk.{l}.attn_q_norm.weight") for l in range(nl)]
+        kn = [f.read_f32(f"blk.{l}.attn_k_norm.weight") for l in range(nl)]
+    finally:
+        f.close()
+    md = oracle.Model(path, lib_path=run.lib_path)
+    try:
+        info = md.info
+        H, hd, eps, win = info.head_count, info.head_dim, float(info.rms_epsilon), info.sliding_window
+        bases = [info.global_rope_base if (l + 1) % 6 == 0 else LOCAL_ROPE_BASE for l in range(nl)]
+        steps, bad = [], []
+        for p, tok in enumerate(TOKS):
+            try:
+                r = md.decode_taps(tok, p, hist_cap=len(TOKS))
+            except RuntimeError as e:
+                return [f"position {p}: decode failed ({e})"]
+            steps.append(r)
+            for l in range(nl):
+                where = f"position {p} block {l}"
+                glob = (l + 1) % 6 == 0
+                hist = int(r["history"][l])
+                if hist != (p + 1 if glob else min(p + 1, win)):
+                    bad.append(f"{where}: {hist} cached rows")
+                    continue
+                qn64 = _rms64(r["q_proj"][l].reshape(H, hd), qn[l], eps)
+                kn64 = _rms64(r["k_proj"][l], kn[l], eps)
+                q_want = _rope64(qn64, p, bases[l])
+                k_want = _rope64(kn64, p, bases[l])
+                q_att = r["q_att"][l].reshape(H, hd).astype(np.float64)
+                keys, values = r["keys"][l, :hist], r["values"][l, :hist]
+                if np.max(np.abs(q_att - q_want)) > 2e-5 * np.max(np.abs(q_want)):
+                    bad.append(f"{where}: query is not QK-norm then RoPE of the q projection")
+                if np.max(np.abs(keys[-1] - k_want)) > 2e-5 * np.max(np.abs(k_want)):
+                    bad.append(f"{where}: newest key is not QK-norm then RoPE of the k projection")
+                if not np.array_equal(values[-1].view(np.uint32), r["v_proj"][l].view(np.uint32)):
+                    bad.append(f"{where}: newest value is not the v projection")
+                d_rot = q_att @ keys[-1].astype(np.float64)
+                d_raw = qn64 @ kn64
+                if np.max(np.abs(d_rot - d_raw)) > 2e-5 * np.max(np.abs(qn64)) * np.max(np.abs(kn64)) * hd ** 0.5:
+                    bad.append(f"{where}: q.k at the current position changed under RoPE")
+                for t in range(hist - 1):
+                    e = steps[p - (hist - 1) + t]
+                    eh = int(e["history"][l])
+                    if not (np.array_equal(keys[t], e["keys"][l, eh - 1]) and
+                            np.array_equal(values[t], e["values"][l, eh - 1])):
+                        bad.append(f"{where}: cache row {t} is not position {p - (hist - 1) + t}'s entry")
+                        break
+                att_want = _sdpa64(q_att, keys, values, 1.0 / np.sqrt(hd))
+                if np.max(np.abs(r["att"][l].reshape(H, hd) - att_want)) > 1e-5 * np.max(np.abs(values)):
+                    bad.append(f"{where}: attention output is not softmax(q K^T / sqrt(hd)) V")
+            if bad:
+                return bad
+        return bad
+    finally:
+        md.close()
+
+
 INVARIANTS = (inv_scale_absorption, inv_window1_flow, inv_rope_base_global_only, inv_branch_norms,
-              inv_zero_projection)
+              inv_zero_projection, inv_attention_subpath)
 
 
 @pytest.mark.parametrize("inv", INVARIANTS, ids=lambda f: f.__name__)
@@ -224,6 +325,12 @@ MUTANTS = {
     "attn_residual_dropped": [("for (uint32_t i = 0; i < d; ++i) o[i] += hidden[i];", "", 1)],
     "window_on_global_blocks": [("L->cap = (!L->global && m->info.sliding_window)", "L->cap = (m->info.sliding_window)", 1)],
     "embedding_unscaled": [("hidden[i] *= m->emb_scale;", "hidden[i] *= 1.0f;", 1)],
+    "attention_scale_one": [("m->attn_scale = 1.0f / sqrtf((float)m->info.head_dim);", "m->attn_scale = 1.0f;", 1)],
+    "qk_norm_on_v": [("        or_rms_norm_heads(k, L->k_norm, 1, hd, eps);\n",
+                      "        or_rms_norm_heads(k, L->k_norm, 1, hd, eps);\n"
+                      "        or_rms_norm_heads(v, L->k_norm, 1, hd, eps);\n", 1)],
+    "k_on_local_rope_in_global_blocks": [("or_apply_rope(k, 1, hd, L->global ? gc : lc, L->global ? gs : ls);",
+                                          "or_apply_rope(k, 1, hd, lc, ls);", 1)],
 }
 
 

@@ -4,18 +4,25 @@
 // (src/gguf.cpp:312-403, :525-664) so that callers see the same failures.
 #include "vortexrt/gguf.hpp"
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
 #include <bit>
 #include <cstring>
 #include <limits>
 #include <stdexcept>
+#include <unordered_map>
 
 namespace vortexrt {
 namespace {
 
 constexpr std::uint32_t kMagic = 0x46554747u;   // "GGUF" little-endian
 constexpr std::uint64_t kMaxString = 1ull << 30;
-constexpr std::uint64_t kMaxArray = 1ull << 31;
-constexpr std::uint64_t kMaxCount = 1ull << 24;
+constexpr std::uint64_t kMaxArray = 1ull << 28;       // src/gguf.cpp:16
+constexpr std::uint64_t kMaxCount = 1000000ull;       // src/gguf.cpp:334
 constexpr std::uint32_t kMaxDims = 4;
 constexpr int kMaxNesting = 8;
 
@@ -40,15 +47,14 @@ std::optional<Layout> layout_of(std::uint32_t type) {
     }
 }
 
-// Sequential little-endian reader over the header part of the file.
+// Sequential little-endian reader over the mapped header bytes.
 class Cursor {
 public:
-    Cursor(std::ifstream& in, std::uint64_t size) : in_(in), size_(size) {}
+    Cursor(const unsigned char* base, std::uint64_t size) : base_(base), size_(size) {}
 
     void read(void* dst, std::size_t n) {
         if (n > size_ || pos_ > size_ - n) throw std::runtime_error("Unexpected end of GGUF file");
-        in_.read(static_cast<char*>(dst), static_cast<std::streamsize>(n));
-        if (!in_) throw std::runtime_error("Failed while reading GGUF file");
+        if (n) std::memcpy(dst, base_ + pos_, n);
         pos_ += n;
     }
     template <typename T>
@@ -65,9 +71,10 @@ public:
         return s;
     }
     [[nodiscard]] std::uint64_t pos() const noexcept { return pos_; }
+    [[nodiscard]] std::uint64_t remaining() const noexcept { return size_ - pos_; }
 
 private:
-    std::ifstream& in_;
+    const unsigned char* base_;
     std::uint64_t size_;
     std::uint64_t pos_ = 0;
 };
@@ -102,7 +109,9 @@ GgufValue read_value(Cursor& c, GgufValueType type, int depth) {
             const auto n = c.get<std::uint64_t>();
             if (n > kMaxArray) throw std::runtime_error("GGUF array length exceeds safety limit");
             v.array_element_type = static_cast<GgufValueType>(et);
-            v.array.reserve(static_cast<std::size_t>(n));
+            // every element takes at least one byte of the file, so a count the file cannot hold
+            // fails at its end instead of reserving memory for it
+            v.array.reserve(static_cast<std::size_t>(std::min(n, c.remaining())));
             for (std::uint64_t i = 0; i < n; ++i) v.array.push_back(read_value(c, v.array_element_type, depth + 1));
             break;
         }
@@ -143,69 +152,122 @@ std::optional<bool> GgufValue::as_bool() const {
 
 // ---- GgufFile ------------------------------------------------------------------------------
 
-GgufFile::GgufFile(const std::filesystem::path& path) : path_(path) {
+// The whole file mapped read-only (PROT_READ, MAP_PRIVATE) plus the parsed header. A zero-length
+// file is not mapped; its header read fails like any truncated file's.
+struct GgufFile::Image {
+    const unsigned char* bytes = nullptr;
+    std::uint64_t size = 0;
+    std::uint32_t version = 0;
+    std::uint64_t data_offset = 0;
+    std::uint32_t alignment = 32;
+    std::vector<GgufMetadata> metadata;
+    std::vector<GgufTensorInfo> tensors;
+    std::unordered_map<std::string, std::size_t> metadata_at;
+    std::unordered_map<std::string, std::size_t> tensor_at;
+
+    explicit Image(const std::filesystem::path& path) {
+        const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+        if (fd < 0) throw std::runtime_error("Failed to open GGUF file: " + path.string());
+        struct stat st {};
+        if (::fstat(fd, &st) != 0 || st.st_size < 0) {
+            ::close(fd);
+            throw std::runtime_error("Failed to determine GGUF file size");
+        }
+        size = static_cast<std::uint64_t>(st.st_size);
+        if (size) {
+            void* m = ::mmap(nullptr, static_cast<std::size_t>(size), PROT_READ, MAP_PRIVATE, fd, 0);
+            if (m == MAP_FAILED) {
+                ::close(fd);
+                throw std::runtime_error("Failed to open GGUF file: " + path.string());
+            }
+            bytes = static_cast<const unsigned char*>(m);
+        }
+        ::close(fd);   // the mapping keeps the file
+    }
+    ~Image() {
+        if (bytes) ::munmap(const_cast<unsigned char*>(bytes), static_cast<std::size_t>(size));
+    }
+    Image(const Image&) = delete;
+    Image& operator=(const Image&) = delete;
+
+    void parse() {
+        Cursor c(bytes, size);
+        if (c.get<std::uint32_t>() != kMagic) throw std::runtime_error("Invalid GGUF magic");
+        version = c.get<std::uint32_t>();
+        if (version != 2 && version != 3) throw std::runtime_error("Unsupported GGUF version: " + std::to_string(version));
+        const auto n_tensors = c.get<std::uint64_t>();
+        const auto n_meta = c.get<std::uint64_t>();
+        if (n_tensors > kMaxCount || n_meta > kMaxCount) throw std::runtime_error("GGUF header counts exceed safety limits");
+
+        metadata.reserve(static_cast<std::size_t>(n_meta));
+        for (std::uint64_t i = 0; i < n_meta; ++i) {
+            GgufMetadata m;
+            m.key = c.str();
+            const auto t = c.get<std::uint32_t>();
+            if (!valid_type(t)) throw std::runtime_error("GGUF metadata has invalid value type");
+            m.value = read_value(c, static_cast<GgufValueType>(t), 0);
+            metadata_at[m.key] = metadata.size();
+            metadata.push_back(std::move(m));
+        }
+        if (const auto it = metadata_at.find("general.alignment"); it != metadata_at.end()) {
+            const auto v = metadata[it->second].value.as_u64();
+            if (!v || *v > std::numeric_limits<std::uint32_t>::max()) throw std::runtime_error("Invalid general.alignment metadata");
+            alignment = static_cast<std::uint32_t>(*v);
+        }
+        if (alignment == 0) throw std::runtime_error("GGUF alignment must be non-zero");
+        if ((alignment & (alignment - 1u)) != 0) throw std::runtime_error("GGUF alignment must be a power of two");
+
+        tensors.reserve(static_cast<std::size_t>(n_tensors));
+        for (std::uint64_t i = 0; i < n_tensors; ++i) {
+            GgufTensorInfo t;
+            t.name = c.str();
+            const auto nd = c.get<std::uint32_t>();
+            if (nd == 0 || nd > kMaxDims) throw std::runtime_error("GGUF tensor has invalid dimension count");
+            t.dimensions.resize(nd);
+            for (auto& d : t.dimensions) d = c.get<std::uint64_t>();
+            t.type = c.get<std::uint32_t>();
+            t.offset = c.get<std::uint64_t>();
+            tensor_at[t.name] = tensors.size();
+            tensors.push_back(std::move(t));
+        }
+        const std::uint64_t a = alignment;
+        data_offset = (c.pos() + a - 1u) / a * a;
+        if (data_offset > size) throw std::runtime_error("GGUF tensor data offset lies beyond end of file");
+    }
+
+    // Copies bytes [absolute, absolute + n) of the file.
+    void copy(std::uint64_t absolute, void* destination, std::size_t n) const {
+        if (n > size || absolute > size - n) throw std::runtime_error("GGUF read lies beyond end of file");
+        if (n) std::memcpy(destination, bytes + absolute, n);
+    }
+};
+
+GgufFile::GgufFile(const std::filesystem::path& path) {
     static_assert(std::endian::native == std::endian::little, "GGUF reader requires a little-endian host");
-    std::ifstream in(path, std::ios::binary);
-    if (!in) throw std::runtime_error("Failed to open GGUF file: " + path.string());
-    std::error_code ec;
-    file_size_ = std::filesystem::file_size(path, ec);
-    if (ec) throw std::runtime_error("Failed to determine GGUF file size");
-
-    Cursor c(in, file_size_);
-    if (c.get<std::uint32_t>() != kMagic) throw std::runtime_error("Invalid GGUF magic");
-    version_ = c.get<std::uint32_t>();
-    if (version_ != 2 && version_ != 3) throw std::runtime_error("Unsupported GGUF version: " + std::to_string(version_));
-    const auto n_tensors = c.get<std::uint64_t>();
-    const auto n_meta = c.get<std::uint64_t>();
-    if (n_tensors > kMaxCount || n_meta > kMaxCount) throw std::runtime_error("GGUF header counts exceed safety limits");
-
-    metadata_.reserve(static_cast<std::size_t>(n_meta));
-    for (std::uint64_t i = 0; i < n_meta; ++i) {
-        GgufMetadata m;
-        m.key = c.str();
-        const auto t = c.get<std::uint32_t>();
-        if (!valid_type(t)) throw std::runtime_error("GGUF metadata has invalid value type");
-        m.value = read_value(c, static_cast<GgufValueType>(t), 0);
-        metadata_index_[m.key] = metadata_.size();
-        metadata_.push_back(std::move(m));
-    }
-    if (const auto* a = find_metadata("general.alignment")) {
-        const auto v = a->as_u64();
-        if (!v || *v > std::numeric_limits<std::uint32_t>::max()) throw std::runtime_error("Invalid general.alignment metadata");
-        alignment_ = static_cast<std::uint32_t>(*v);
-    }
-    if (alignment_ == 0) throw std::runtime_error("GGUF alignment must be non-zero");
-    if ((alignment_ & (alignment_ - 1u)) != 0) throw std::runtime_error("GGUF alignment must be a power of two");
-
-    tensors_.reserve(static_cast<std::size_t>(n_tensors));
-    for (std::uint64_t i = 0; i < n_tensors; ++i) {
-        GgufTensorInfo t;
-        t.name = c.str();
-        const auto nd = c.get<std::uint32_t>();
-        if (nd == 0 || nd > kMaxDims) throw std::runtime_error("GGUF tensor has invalid dimension count");
-        t.dimensions.resize(nd);
-        for (auto& d : t.dimensions) d = c.get<std::uint64_t>();
-        t.type = c.get<std::uint32_t>();
-        t.offset = c.get<std::uint64_t>();
-        tensor_index_[t.name] = tensors_.size();
-        tensors_.push_back(std::move(t));
-    }
-    const std::uint64_t a = alignment_;
-    data_offset_ = (c.pos() + a - 1u) / a * a;
-    if (data_offset_ > file_size_) throw std::runtime_error("GGUF tensor data offset lies beyond end of file");
-
-    payload_stream_.open(path, std::ios::binary);
-    if (!payload_stream_) throw std::runtime_error("Failed to open GGUF file: " + path.string());
+    auto image = std::make_unique<Image>(path);
+    image->parse();
+    image_ = std::move(image);
 }
 
+GgufFile::~GgufFile() = default;
+GgufFile::GgufFile(GgufFile&&) noexcept = default;
+GgufFile& GgufFile::operator=(GgufFile&&) noexcept = default;
+
+std::uint32_t GgufFile::version() const noexcept { return image_->version; }
+std::uint64_t GgufFile::file_size() const noexcept { return image_->size; }
+std::uint64_t GgufFile::data_offset() const noexcept { return image_->data_offset; }
+std::uint32_t GgufFile::alignment() const noexcept { return image_->alignment; }
+const std::vector<GgufMetadata>& GgufFile::metadata() const noexcept { return image_->metadata; }
+const std::vector<GgufTensorInfo>& GgufFile::tensors() const noexcept { return image_->tensors; }
+
 const GgufValue* GgufFile::find_metadata(const std::string& key) const noexcept {
-    const auto it = metadata_index_.find(key);
-    return it == metadata_index_.end() ? nullptr : &metadata_[it->second].value;
+    const auto it = image_->metadata_at.find(key);
+    return it == image_->metadata_at.end() ? nullptr : &image_->metadata[it->second].value;
 }
 
 const GgufTensorInfo* GgufFile::find_tensor(const std::string& name) const noexcept {
-    const auto it = tensor_index_.find(name);
-    return it == tensor_index_.end() ? nullptr : &tensors_[it->second];
+    const auto it = image_->tensor_at.find(name);
+    return it == image_->tensor_at.end() ? nullptr : &image_->tensors[it->second];
 }
 
 std::optional<std::string> GgufFile::metadata_string(const std::string& key) const {
@@ -232,18 +294,10 @@ std::optional<std::uint64_t> GgufFile::tensor_byte_size(const GgufTensorInfo& te
     return blocks * lay->bytes;
 }
 
-void GgufFile::read_bytes_at(std::uint64_t absolute_offset, void* destination, std::size_t bytes) const {
-    if (bytes > file_size_ || absolute_offset > file_size_ - bytes) throw std::runtime_error("GGUF read lies beyond end of file");
-    std::lock_guard<std::mutex> lock(payload_stream_mutex_);
-    payload_stream_.clear();
-    payload_stream_.seekg(static_cast<std::streamoff>(absolute_offset));
-    payload_stream_.read(static_cast<char*>(destination), static_cast<std::streamsize>(bytes));
-    if (!payload_stream_) throw std::runtime_error("Failed while reading GGUF file");
-}
-
 void GgufFile::read_data(std::uint64_t offset, void* destination, std::size_t bytes) const {
-    if (offset > file_size_ - data_offset_) throw std::runtime_error("GGUF read lies beyond end of file");
-    read_bytes_at(data_offset_ + offset, destination, bytes);
+    const Image& im = *image_;
+    if (offset > im.size - im.data_offset) throw std::runtime_error("GGUF read lies beyond end of file");
+    im.copy(im.data_offset + offset, destination, bytes);
 }
 
 std::vector<std::byte> GgufFile::read_tensor_bytes(const GgufTensorInfo& tensor) const {
@@ -283,11 +337,12 @@ std::vector<float> GgufFile::read_q8_0_row(const GgufTensorInfo& tensor, std::ui
 }
 
 void GgufFile::validate() const {
-    for (const auto& t : tensors_) {
+    const Image& im = *image_;
+    for (const auto& t : im.tensors) {
         const auto n = tensor_byte_size(t);
         if (!n) throw std::runtime_error("Unsupported GGUF tensor type for " + t.name);
-        if (t.offset % alignment_ != 0) throw std::runtime_error("GGUF tensor offset is not aligned: " + t.name);
-        const std::uint64_t room = file_size_ - data_offset_;
+        if (t.offset % im.alignment != 0) throw std::runtime_error("GGUF tensor offset is not aligned: " + t.name);
+        const std::uint64_t room = im.size - im.data_offset;
         if (t.offset > room || *n > room - t.offset) throw std::runtime_error("GGUF tensor data lies beyond end of file: " + t.name);
     }
 }

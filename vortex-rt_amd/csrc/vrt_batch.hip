@@ -386,6 +386,7 @@ extern "C" int vrt_g3_batch_destroy(vrt_g3_batch* B) {
     (void)hipSetDevice(B->g->ctx->device);
     (void)hipStreamSynchronize(B->g->ctx->stream);
     for (void* p : B->allocs) (void)hipFree(p);
+    B->g->live_batches--;
     if (B->host_rows) (void)hipHostFree(B->host_rows);
     if (B->host_res) (void)hipHostFree(B->host_res);
     if (B->host_st) (void)hipHostFree(B->host_st);
@@ -407,6 +408,7 @@ extern "C" int vrt_g3_batch_create(vrt_g3* g, uint32_t max_seqs, uint32_t max_ct
     auto* B = new (std::nothrow) vrt_g3_batch();
     VRT_REQUIRE(B != nullptr, "out of memory");
     B->g = g;
+    g->live_batches++;   // vrt_g3_batch_destroy (also on the failure paths below) gives it back
     B->max_seqs = max_seqs;
     B->max_ctx = max_ctx;
     B->pos.assign(max_seqs, 0u);

@@ -1568,17 +1568,20 @@ static MkFns mk_pick(int sd, int sa, int sf, int ep) {
     return MkFns{};
 }
 
-static int mk_alloc(MkState* mk, size_t bytes, void** out) {
+static int mk_alloc(MkState* mk, hipStream_t stream, size_t bytes, void** out) {
     void* p = nullptr;
     VRT_HIP_CHECK(hipMalloc(&p, bytes + 256));
     mk->allocs.push_back(p);
-    VRT_HIP_CHECK(hipMemset(p, 0, bytes + 256));
+    // zero-filled on the context's (non-blocking) stream, which every later use is ordered on
+    VRT_HIP_CHECK(hipMemsetAsync(p, 0, bytes + 256, stream));
+    VRT_HIP_CHECK(hipStreamSynchronize(stream));
     *out = p;
     return VRT_OK;
 }
 
 void mk_destroy(vrt_g3* g) {
     if (!g || !g->mk) return;
+    (void)hipStreamSynchronize(g->ctx->stream);   // no launch may still use the buffers freed below
     {
         MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
         std::lock_guard<std::mutex> lock(ds.mu);
@@ -1697,24 +1700,24 @@ int mk_setup(vrt_g3* g) {
 
     // exchange buffers
     void* p;
-    if (int rc = mk_alloc(mk, nqkv * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, nqkv * 8u, &p)) return rc;
     P.x_qkv = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, static_cast<size_t>(kMaxChunks) * (qw + kLine * H) * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, static_cast<size_t>(kMaxChunks) * (qw + kLine * H) * 8u, &p)) return rc;
     P.x_part = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, 2u * d * 8u, &p)) return rc;   // room for the line-per-producer layout
+    if (int rc = mk_alloc(mk, g->ctx->stream, 2u * d * 8u, &p)) return rc;   // room for the line-per-producer layout
     P.x_o = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, static_cast<size_t>(kMkFuseHeads) * d * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, static_cast<size_t>(kMkFuseHeads) * d * 8u, &p)) return rc;
     P.x_o4 = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, F * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, F * 8u, &p)) return rc;
     P.x_g = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, 2u * d * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, 2u * d * 8u, &p)) return rc;
     P.x_f = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, kLine * nwg * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, kLine * nwg * 8u, &p)) return rc;
     P.x_am = static_cast<u64*>(p);
-    if (int rc = mk_alloc(mk, 64, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, 64, &p)) return rc;
     P.abort_flag = static_cast<uint32_t*>(p);
     mk->trace_slots = 5u * c.block_count + 3u + kMarks;
-    if (int rc = mk_alloc(mk, static_cast<size_t>(nwg) * mk->trace_slots * 8u, &p)) return rc;
+    if (int rc = mk_alloc(mk, g->ctx->stream, static_cast<size_t>(nwg) * mk->trace_slots * 8u, &p)) return rc;
     P.trace = static_cast<uint64_t*>(p);
     P.trace_slots = 0u;
     std::vector<MkLayer> hl(c.block_count);
@@ -1797,7 +1800,8 @@ int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uin
     VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
     const uint64_t raw_words = cnt << (3u - sh);
     std::vector<uint64_t> raw(raw_words);
-    VRT_HIP_CHECK(hipMemcpy(raw.data(), src, raw_words * 8u, hipMemcpyDeviceToHost));
+    VRT_HIP_CHECK(hipMemcpyAsync(raw.data(), src, raw_words * 8u, hipMemcpyDeviceToHost, g->ctx->stream));
+    VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
     for (uint64_t v = 0; v < cnt; ++v) out[v] = raw[((v >> sh) << 3) | (v & ((1u << sh) - 1u))];
     return VRT_OK;
 }

@@ -131,6 +131,7 @@ struct vrt_g3 {
     uint32_t gen_prompt = 0;     // generation in flight (vrt_g3_start .. vrt_g3_collect)
     uint32_t gen_max = 0;
     uint64_t gen_steps = 0;
+    uint32_t live_batches = 0;   // vrt_g3_batch objects over this executor's weights and stream
 };
 
 namespace vrt {

@@ -659,7 +659,9 @@ static int g3_alloc(vrt_g3* g, size_t bytes, void** out) {
     void* p = nullptr;
     VRT_HIP_CHECK(hipMalloc(&p, bytes + 256));
     g->allocs.push_back(p);
-    VRT_HIP_CHECK(hipMemset(p, 0, bytes + 256));
+    // zero-filled on the context's (non-blocking) stream, which every later use is ordered on
+    VRT_HIP_CHECK(hipMemsetAsync(p, 0, bytes + 256, g->ctx->stream));
+    VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
     *out = p;
     return VRT_OK;
 }
@@ -667,7 +669,10 @@ static int g3_alloc(vrt_g3* g, size_t bytes, void** out) {
 static int g3_upload(vrt_g3* g, const void* host, size_t bytes, const float** out) {
     void* p = nullptr;
     if (int rc = g3_alloc(g, bytes, &p)) return rc;
-    VRT_HIP_CHECK(hipMemcpy(p, host, bytes, hipMemcpyHostToDevice));
+    // on the context's stream and waited for: a pageable-memory hipMemcpy may return before its
+    // DMA lands, and the null stream does not order the non-blocking context stream
+    VRT_HIP_CHECK(hipMemcpyAsync(p, host, bytes, hipMemcpyHostToDevice, g->ctx->stream));
+    VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
     *out = static_cast<const float*>(p);
     return VRT_OK;
 }
@@ -952,6 +957,10 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
 
 extern "C" int vrt_g3_destroy(vrt_g3* g) {
     if (!g) return VRT_OK;
+    // a batched decoder reads this executor's weights and launches on its context's stream
+    if (g->live_batches != 0u)
+        return set_error(VRT_ERR_STATE, "vrt_g3_destroy: %u batched decoder(s) still use this executor; destroy them first",
+                         g->live_batches);
     (void)hipSetDevice(g->ctx->device);
     (void)hipStreamSynchronize(g->ctx->stream);
     if (g->graph) (void)hipGraphExecDestroy(g->graph);

@@ -422,7 +422,8 @@ extern "C" int vrt_ctx_create(const char* selector, vrt_ctx** out) {
     if (e == hipSuccess) {
         c->scratch_bytes = 1u << 16;
         e = hipMalloc(&c->scratch, c->scratch_bytes);
-        if (e == hipSuccess) e = hipMemset(c->scratch, 0, c->scratch_bytes);
+        if (e == hipSuccess) e = hipMemsetAsync(c->scratch, 0, c->scratch_bytes, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     }
     if (e == hipSuccess) {   // this device's copy of the no-allocation FFN workspace (dev is current)
         void* sp = nullptr;
@@ -465,8 +466,12 @@ extern "C" int vrt_alloc(vrt_ctx* ctx, uint64_t bytes, uint32_t kind, void** out
     void* p = nullptr;
     if (kind == VRT_MEM_DEVICE) {
         VRT_HIP_CHECK(hipMalloc(&p, padded));
-        hipError_t e = hipMemset(p, 0, padded);
-        if (e != hipSuccess) { (void)hipFree(p); return set_error(VRT_ERR_HIP, "hipMemset failed: %s", hipGetErrorString(e)); }
+        // The zero-fill goes on the context's stream, which every later copy and kernel of the
+        // context uses: that stream is non-blocking, so a fill on the null stream would not be
+        // ordered before them.
+        hipError_t e = hipMemsetAsync(p, 0, padded, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) { (void)hipFree(p); return set_error(VRT_ERR_HIP, "hipMemsetAsync failed: %s", hipGetErrorString(e)); }
     } else {
         VRT_HIP_CHECK(hipHostMalloc(&p, padded, hipHostMallocDefault));
         std::memset(p, 0, padded);
@@ -478,6 +483,8 @@ extern "C" int vrt_alloc(vrt_ctx* ctx, uint64_t bytes, uint32_t kind, void** out
 extern "C" int vrt_free(vrt_ctx* ctx, void* ptr) {
     VRT_REQUIRE(ctx, "vrt_free: null context");
     if (!ptr) return VRT_OK;
+    // work still queued on the context's stream may read or write the buffer
+    VRT_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     hipPointerAttribute_t attr{};
     VRT_HIP_CHECK(hipPointerGetAttributes(&attr, ptr));
     if (attr.type == hipMemoryTypeHost) {

@@ -354,12 +354,15 @@ class Gemma3:
         check(lib().vrt_g3_create(ctx.h, C.byref(desc), C.byref(h)))
         self.h = h.value
         self.kv_f16 = False
+        self._batches = weakref.WeakSet()   # batched decoders over this executor: closed first
         ctx._children.add(self)
         self._keep.clear()
 
     def close(self):
         if getattr(self, "h", None):
-            lib().vrt_g3_destroy(self.h)
+            for b in list(getattr(self, "_batches", ())):
+                b.close()
+            check(lib().vrt_g3_destroy(self.h))
             self.h = None
         if getattr(self, "arena", None) is not None:
             self.arena.free()
@@ -467,10 +470,11 @@ class Gemma3Batch:
         h = C.c_void_p()
         check(lib().vrt_g3_batch_create(model.h, max_seqs, max_ctx, C.byref(h)))
         self.h = h.value
+        model._batches.add(self)
 
     def close(self):
-        if self.h:
-            lib().vrt_g3_batch_destroy(self.h)
+        if getattr(self, "h", None):
+            check(lib().vrt_g3_batch_destroy(self.h))
             self.h = None
 
     def __del__(self):
