@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import vrt
-from test_oracle_wiring import INVARIANTS, models  # noqa: F401  (fixture)
+from test_oracle_wiring import OUTPUT_INVARIANTS, models  # noqa: F401  (fixture)
 
 pytestmark = pytest.mark.gpu
 
@@ -33,7 +33,7 @@ def gpu_runner(ctx, persistent):
 
 
 @pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "multikernel"])
-@pytest.mark.parametrize("inv", INVARIANTS, ids=lambda f: f.__name__)
+@pytest.mark.parametrize("inv", OUTPUT_INVARIANTS, ids=lambda f: f.__name__)
 def test_hip_path_satisfies_invariant(ctx, models, inv, persistent):  # noqa: F811
     print(f"[wiring] {inv.__name__} persistent={persistent}", flush=True)
     assert inv(gpu_runner(ctx, persistent), models) == []
