@@ -8,10 +8,12 @@ of uniform ids in [2, 262144) from seed 0, then greedy decode with an fp32 KV ca
 prompt is prefilled first (untimed); --steps decode steps at positions 8, 9, ... are timed
 with hipEvents on the library's stream. Inputs are resident in HBM before timing.
 
-The whole decode loop is one kernel, k_decode: a cooperative launch with one workgroup per CU
-that runs every block, the LM head and argmax for each of the launch's steps. The timed region
-is exactly one k_decode launch of --steps steps, so the roofline's launch duration is the
-event-timed region itself.
+The whole decode loop is one persistent kernel: a cooperative launch with one workgroup per CU
+that runs every block, the LM head and argmax for each of the launch's steps. Positions below 64
+run on k_team (four teams of workgroups, each running one phase type of every block); later
+positions on k_decode (every workgroup in every phase). With the default 8-token prompt and up
+to 56 steps the timed region is exactly one k_team launch, so the roofline's launch duration is
+the event-timed region itself; longer runs time one k_team and one k_decode launch together.
 
 Algorithmic bytes per step at position p: every Q8_0 weight byte, the fp32 norm weights, one
 embedding row, plus the fp32 KV rows attention reads (min(p+1, window) positions for local
@@ -47,21 +49,26 @@ def step_bytes(cfg, pos: int, kv_bytes: int = 4) -> int:
     return total
 
 
-TRAFFIC_SUMMARY = os.path.join("profiles", "decode_gemma3_270m_pmc.json")
+# rocprofv3 PMC summaries of the timed dispatch per persistent kernel
+TRAFFIC_SUMMARY = {"k_team": os.path.join("profiles", "decode_team_gemma3_270m_pmc.json"),
+                   "k_decode": os.path.join("profiles", "decode_gemma3_270m_pmc.json")}
 
 
-def load_traffic(steps: int):
-    """HBM bytes per k_decode launch of `steps` steps and where the figure comes from: the
+def load_traffic(steps: int, kernel: str):
+    """HBM bytes per launch of `steps` steps of `kernel` and where the figure comes from: the
     committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE per decode step, calibrated against
     a copy of known size), scaled to `steps`. This run does not measure it."""
-    p = os.path.join(REPO, TRAFFIC_SUMMARY)
+    rel = TRAFFIC_SUMMARY.get(kernel)
+    if rel is None:
+        return None, None
+    p = os.path.join(REPO, rel)
     try:
         with open(p) as fp:
             summary = json.load(fp)
         per_step = summary["hbm_bytes_per_step"]
     except (OSError, ValueError, KeyError):
         return None, None
-    src = (f"{TRAFFIC_SUMMARY}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of k_decode, calibrated, "
+    src = (f"{rel}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of {kernel}, calibrated, "
            f"{per_step / 1e6:.1f} MB per step, scaled to {steps} steps (not measured by this run)")
     if "command" in summary:
         src += f"; command: {summary['command']}"
@@ -69,8 +76,13 @@ def load_traffic(steps: int):
 
 
 def phase_split(g, prompt, cfg, steps: int = 24):
-    """Per-phase time of one decode step from the kernel's own clock marks: each phase's end is
-    the latest workgroup's end timestamp (s_memrealtime, 100 MHz). Median over blocks 1..L-1."""
+    """Per-phase time of one decode step from the kernel's own clock marks (s_memrealtime, 100 MHz),
+    median over blocks 1..L-1. The traced step is position len(prompt), the first of its launch.
+
+    Team kernel (positions below its limit): a phase ends when the last workgroup of its team has
+    published; each phase is timed from the previous phase's end (so it includes its hand-off):
+    A q|k|v, B attention + O, D norms + gate/up + GELU, E down. All-workgroup kernel: phases A..E
+    as that kernel runs them, each phase's end being the latest workgroup's end timestamp."""
     g.set_trace(True)
     g.start(prompt, steps + 1)
     g.step(len(prompt))
@@ -79,13 +91,25 @@ def phase_split(g, prompt, cfg, steps: int = 24):
     g.collect()
     g.set_trace(False)
     L = cfg.block_count
-    mx = tr[:, : 5 * L + 3].max(axis=0) * 10.0 / 1000.0        # us
+    nwg, slots = tr.shape
     out = {}
+    if slots == 2 * L + 3 + 8:   # team kernel: workgroup w in team (w % 8) // 2
+        team = (np.arange(nwg) % 8) // 2
+        pub = np.array([[tr[team == t, L + l].max() for l in range(L)] for t in range(4)]) / 100.0   # us
+        ends = [pub[t, l] for l in range(L) for t in range(4)]          # A0 B0 D0 E0 A1 ...
+        for t, p in enumerate("ABDE"):
+            out[p] = float(np.median([ends[4 * l + t] - ends[4 * l + t - 1] for l in range(1, L)]))
+        out["lm_head"] = float(tr[:, 2 * L + 2].max() / 100.0 - pub[3, L - 1])
+        out["step"] = float((tr[:, 2 * L + 2].max() - tr[:, 2 * L][tr[:, 2 * L] > 0].min()) / 100.0)
+        out["kernel"] = "k_team"
+        return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in out.items()}
+    mx = tr[:, : 5 * L + 3].max(axis=0) * 10.0 / 1000.0        # us
     for k, p in enumerate("ABCDE"):
         out[p] = float(np.median([mx[1 + 5 * l + k] - mx[5 * l + k] for l in range(1, L)]))
     out["lm_head"] = float(mx[5 * L + 2] - mx[5 * L + 1])
     out["step"] = float(mx[5 * L + 2] - mx[0])
-    return {k: round(v, 2) for k, v in out.items()}
+    out["kernel"] = "k_decode"
+    return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in out.items()}
 
 
 def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256, kv_f16: bool = False):
@@ -312,6 +336,21 @@ def cpu_baseline(path, prompt, target_s: float = 12.0):
                       f"the reference's Lavapipe path is not available on this host"}
 
 
+TEAM_POS_LIMIT = 64   # positions below this run on the team kernel (VRT_G3_OPT_TEAM, include/vrt_hip.h)
+
+
+def roofline_kernel(g, cfg, first: int, steps: int) -> str:
+    """The persistent launch(es) that run the timed steps at positions first .. first + steps - 1."""
+    per = f"{cfg.block_count} blocks + tied LM head + argmax per step"
+    last = first + steps - 1
+    if g.team_available() and last < TEAM_POS_LIMIT:
+        return f"k_team (phase-team persistent kernel: {per}, {steps} steps per launch)"
+    if g.team_available() and first < TEAM_POS_LIMIT:
+        return (f"k_team for positions {first}..{TEAM_POS_LIMIT - 1}, then k_decode (all-workgroup persistent "
+                f"kernel) for {TEAM_POS_LIMIT}..{last}: {per}")
+    return f"k_decode (all-workgroup persistent kernel: {per}, {steps} steps per launch)"
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -399,7 +438,9 @@ def main():
     total_bytes = sum(step_bytes(cfg, n_prompt + i) for i in range(args.steps))
     gbps = total_bytes / (ms / 1e3) / 1e9
 
-    traffic, traffic_src = load_traffic(args.steps)
+    rkernel = roofline_kernel(g, cfg, n_prompt, args.steps)
+    single = rkernel.split(" ")[0] if "then" not in rkernel else None
+    traffic, traffic_src = load_traffic(args.steps, single) if single else (None, None)
     phases = None if args.no_phases else phase_split(g, prompt, cfg)
     longctx = None if args.no_long else long_context(ctx, g, cfg)
     longctx16 = None if args.no_long else long_context(ctx, g, cfg, kv_f16=True)
@@ -433,8 +474,7 @@ def main():
         "hbm_gbps": round(gbps, 1),
         "bytes_per_step_mean": int(total_bytes / args.steps),
         "roofline": {
-            "kernel": f"k_decode (persistent: {cfg.block_count} blocks + tied LM head + argmax per step, "
-                      f"{args.steps} steps per launch)",
+            "kernel": rkernel,
             "bound": "hbm",
             "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,

@@ -250,12 +250,23 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
  * reference's README lists an fp16/bf16 KV cache as its next residency step
  * (README.md:190-192); it has no implementation to follow. */
 #define VRT_G3_OPT_KV_F16 5
+/* 1 (default): decode steps at positions below 64 run on the phase-team persistent kernel (four
+ * teams of workgroups, each running one phase type of every block, with one-way hand-offs); later
+ * positions, or all with 0, run on the all-workgroup persistent kernel. Both give the same
+ * results to the stated tolerances. VRT_G3_OPT_QUERY_TEAM returns VRT_OK when the team kernel
+ * is available for the shape and device (value ignored). No reference counterpart. */
+#define VRT_G3_OPT_TEAM 6
+#define VRT_G3_OPT_QUERY_TEAM 7
 
 /* Phase trace of the last persistent launch (tracing tool; no reference counterpart, which
  * only has CLI wall timers, src/gemma_main.cpp:194-232): out[w * slots + k] is the
  * s_memrealtime tick (100 MHz) at which workgroup w finished phase k of the launch's first
  * step: k = 0 step start, 5l + 1 .. 5l + 5 phases A..E of block l, 5L + 1 end of the blocks,
- * 5L + 2 end of the LM head. Entries of phases a workgroup does not run keep older values. */
+ * 5L + 2 end of the LM head. Entries of phases a workgroup does not run keep older values.
+ * When the last launch ran the team kernel (VRT_G3_OPT_TEAM), slots = 2L + 3: k < L the time
+ * workgroup w's team had the inputs of its phase of block k, L + k the time it had published
+ * it, 2L step start, 2L + 1 the LM head's final norm done, 2L + 2 LM head done (0: not run).
+ * Workgroup w belongs to team (w % 8) / 2 (0 q|k|v, 1 attention + O, 2 gate/up, 3 down). */
 int vrt_g3_read_trace(vrt_g3* g3, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);
 
 /* Raw tagged words {fp32 bits | tag << 32} of a persistent-kernel exchange buffer as the last

@@ -197,14 +197,15 @@ def test_persistent_split_launches(ctx, tiny_model):
 
 
 def test_exchange_buffers_read_back(ctx, tiny_model):
-    """vrt_g3_read_exchange returns each persistent-kernel exchange buffer in row order: after a
-    generation, the last block's q|k|v, gelu(gate)*up and down-projection words all carry that
-    block's tag, and the down projection (one 64-byte line per four-row producer on the device)
-    comes back compacted to d words."""
+    """vrt_g3_read_exchange returns each all-workgroup persistent-kernel exchange buffer in row
+    order: after a generation on that kernel (the team kernel off), the last block's q|k|v,
+    gelu(gate)*up and down-projection words all carry that block's tag, and the down projection
+    (one 64-byte line per four-row producer on the device) comes back compacted to d words."""
     g = vrt.Gemma3(ctx, tiny_model)
     try:
         if not g.persistent_available():
             pytest.skip("persistent kernel unavailable")
+        g.set_team(False)
         g.generate(synth.uniform_ids(5, 6, 2, 1000), 4)
         cfg = g.config
         sizes = {0: cfg.head_count * cfg.head_dim + 2 * cfg.head_dim, 3: cfg.feed_forward_length,

@@ -1527,24 +1527,12 @@ struct MkState {
     std::vector<void*> allocs;
 };
 
-// Who last wrote g_mk / g_mk_layers on a device, and the event after its last launch. The
-// event lives while at least one executor with a persistent kernel exists on the device: the
-// last one to go destroys it, so no HIP object outlives the executors (nothing is released by
-// a static destructor at process exit).
-constexpr int kMaxDevices = 64;
-struct MkDeviceSlot {
-    std::mutex mu;
-    const MkState* owner = nullptr;
-    uint64_t version = 0;
-    uint32_t users = 0;            // live executors with a persistent kernel on the device
-    hipEvent_t last = nullptr;
-    hipStream_t last_stream = nullptr;
-};
-// Heap-allocated and never freed: the slots themselves hold no HIP resource once their last
-// executor is gone, and executors released late in process exit may still lock them.
-static MkDeviceSlot* device_slots() {
-    static MkDeviceSlot* s = new MkDeviceSlot[kMaxDevices];
-    return s;
+// One slot per device (vrt_g3_internal.hpp): heap-allocated and never freed. The slots hold no
+// HIP resource once their last executor is gone, and executors released late in process exit
+// may still lock them.
+CoopSlot& coop_slot(int device) {
+    static CoopSlot* s = new CoopSlot[kMaxCoopDevices];
+    return s[device % kMaxCoopDevices];
 }
 
 template <int SD, int SA, int SF, int EP>
@@ -1583,15 +1571,17 @@ void mk_destroy(vrt_g3* g) {
     if (!g || !g->mk) return;
     (void)hipStreamSynchronize(g->ctx->stream);   // no launch may still use the buffers freed below
     {
-        MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
+        CoopSlot& ds = coop_slot(g->ctx->device);
         std::lock_guard<std::mutex> lock(ds.mu);
-        if (ds.owner == g->mk) ds.owner = nullptr;
+        if (ds.owner[kCoopMk] == g->mk) ds.owner[kCoopMk] = nullptr;
         if (g->mk->registered && --ds.users == 0u) {
             // the last executor on the device: its stream is drained by the caller
             if (ds.last) (void)hipEventDestroy(ds.last);
             ds.last = nullptr;
             ds.last_stream = nullptr;
-            ds.version = 0;
+            ds.version[kCoopMk] = 0;
+            ds.version[kCoopTeam] = 0;
+            ds.owner[kCoopTeam] = nullptr;
         }
     }
     for (void* p : g->mk->allocs) (void)hipFree(p);
@@ -1746,7 +1736,7 @@ int mk_setup(vrt_g3* g) {
     mk->grid = nwg;
     g->mk_tag = 1u;
     {
-        MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
+        CoopSlot& ds = coop_slot(g->ctx->device);
         std::lock_guard<std::mutex> lock(ds.mu);
         ++ds.users;
         mk->registered = true;
@@ -1839,16 +1829,16 @@ int mk_run(vrt_g3* g, uint32_t nsteps) {
     }
     uint32_t tag0 = g->mk_tag;
     hipStream_t stream = g->ctx->stream;
-    MkDeviceSlot& ds = device_slots()[g->ctx->device % kMaxDevices];
+    CoopSlot& ds = coop_slot(g->ctx->device);
     std::lock_guard<std::mutex> lock(ds.mu);
     // the parameter block is one per device: order this launch after any other executor's
     if (ds.last && ds.last_stream != stream) VRT_HIP_CHECK(hipStreamWaitEvent(stream, ds.last, 0));
-    if (ds.owner != mk || ds.version != mk->version) {
+    if (ds.owner[kCoopMk] != mk || ds.version[kCoopMk] != mk->version) {
         VRT_HIP_CHECK(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_mk), &mk->P, sizeof(MkParams), 0, hipMemcpyHostToDevice, stream));
         VRT_HIP_CHECK(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_mk_layers), mk->layers.data(), mk->layers.size() * sizeof(MkLayer), 0,
                                              hipMemcpyHostToDevice, stream));
-        ds.owner = mk;
-        ds.version = mk->version;
+        ds.owner[kCoopMk] = mk;
+        ds.version[kCoopMk] = mk->version;
     }
     void* args[] = {&nsteps, &tag0};
     const hipError_t le = hipLaunchCooperativeKernel(mk->P.kv_f16 ? mk->fns.f16 : mk->fns.f32, dim3(mk->grid),

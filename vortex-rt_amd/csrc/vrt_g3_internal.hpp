@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <vector>
 
 #include "vrt_hip.h"
@@ -72,6 +73,24 @@ struct LaunchDesc {
 };
 
 struct MkState;   // persistent decode kernel: exchange buffers and launch shape (vrt_decode.hip)
+struct TkState;   // phase-team decode kernel (vrt_team.hip)
+
+// Cooperative launches on one device. Each persistent kernel keeps its parameter block in
+// constant memory, one per device: `owner` and `version` say which executor's block was last
+// uploaded for each kernel, and `last` is the event after the device's last cooperative launch,
+// on `last_stream`, so a launch from another executor's stream is ordered after it. The event
+// lives while at least one executor with a persistent kernel exists on the device (`users`).
+enum CoopKernel : int { kCoopMk = 0, kCoopTeam = 1, kCoopKinds = 2 };
+struct CoopSlot {
+    std::mutex mu;
+    const void* owner[kCoopKinds] = {nullptr, nullptr};
+    uint64_t version[kCoopKinds] = {0, 0};
+    uint32_t users = 0;
+    hipEvent_t last = nullptr;
+    hipStream_t last_stream = nullptr;
+};
+constexpr int kMaxCoopDevices = 64;
+CoopSlot& coop_slot(int device);   // vrt_decode.hip
 
 // A block's weight matrices expanded once for the prefill GEMMs: the quants as f16 [N][K] and
 // the block scales as fp32 [N][K / 32]. qkv: the q, k, v rows concatenated; gu: the gate and up
@@ -126,6 +145,10 @@ struct vrt_g3 {
     bool mk_refused = false;     // the device refused a cooperative launch: multi-kernel steps
     vrt::MkState* mk = nullptr;
     uint32_t mk_tag = 1;         // first exchange tag of the next persistent launch
+    bool use_team = true;        // positions below the team kernel's history limit run on it (vrt_team.hip)
+    vrt::TkState* tk = nullptr;
+    uint32_t tk_tag = 1;         // first exchange tag of the next team-kernel launch
+    int last_coop = 0;           // kernel of the last persistent launch (vrt::CoopKernel)
     hipGraphExec_t graph = nullptr;
     vrt::PfState pf;             // batched prefill (vrt_prefill.hip)
     uint32_t gen_prompt = 0;     // generation in flight (vrt_g3_start .. vrt_g3_collect)
@@ -172,4 +195,15 @@ uint32_t pf_splits(uint32_t M, uint32_t N);
 // Final residual + output norm + LM head + argmax of the current step (vrt_gemma3.hip).
 int g3_enqueue_lm(vrt_g3* g, hipStream_t s);
 int mk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);
+// Phase-team decode kernel (vrt_team.hip): like mk_setup / mk_run, for the steps whose
+// attention histories stay within tk_hist_limit(g) positions (positions < the limit).
+int tk_setup(vrt_g3* g);
+uint32_t tk_pos_limit(const vrt_g3* g);
+int tk_run(vrt_g3* g, uint32_t nsteps);
+void tk_destroy(vrt_g3* g);
+int tk_read_abort(vrt_g3* g, uint32_t* dst);
+int tk_clear_abort(vrt_g3* g);
+int tk_set_trace(vrt_g3* g, bool on);
+int tk_set_kv_f16(vrt_g3* g, bool on);
+int tk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);
 }  // namespace vrt

@@ -733,13 +733,41 @@ static int g3_capture(vrt_g3* g) {
     return VRT_OK;
 }
 
-static int g3_run_steps(vrt_g3* g, uint32_t n) {
+// Runs n steps from position first. With the persistent kernels: the steps at positions below
+// the team kernel's limit run on it (vrt_team.hip), the rest on the all-workgroup kernel
+// (vrt_decode.hip); both read and leave the same step state, KV cache and token buffer.
+static int g3_run_steps(vrt_g3* g, uint32_t n, uint32_t first) {
     hipStream_t s = g->ctx->stream;
-    if (g->mk && g->use_persistent) {
-        const int rc = mk_run(g, n);
+    if ((g->mk || g->tk) && g->use_persistent) {
+        uint32_t done = 0;
+        const uint32_t lim = g->use_team ? tk_pos_limit(g) : 0u;
+        int rc = VRT_OK;
+        if (first < lim) {
+            const uint32_t k = std::min(n, lim - first);
+            rc = tk_run(g, k);
+            if (rc == VRT_OK) {
+                done = k;
+                g->last_coop = kCoopTeam;
+            }
+        }
+        if (rc == VRT_OK && done < n) {
+            if (g->mk) {
+                rc = mk_run(g, n - done);
+                if (rc == VRT_OK) {
+                    done = n;
+                    g->last_coop = kCoopMk;
+                }
+            } else {
+                rc = kMkRefused;   // no all-workgroup kernel for this shape: the multi-kernel step
+            }
+        }
+        if (rc == VRT_OK) return VRT_OK;
         if (rc != kMkRefused) return rc;
-        g->use_persistent = false;   // refused by the device: multi-kernel steps from here on
-        g->mk_refused = true;
+        if (done == 0u) {
+            g->use_persistent = false;   // refused by the device: multi-kernel steps from here on
+            g->mk_refused = true;
+        }
+        n -= done;
     }
     for (uint32_t i = 0; i < n; ++i) {
         if (g->use_graph) {
@@ -777,15 +805,22 @@ static int g3_fail_reset(vrt_g3* g, int code, const char* msg) {
 static int g3_check_state(vrt_g3* g, G3State* out) {
     VRT_HIP_CHECK(hipMemcpyAsync(g->host_ctl, g->P.st, sizeof(G3State), hipMemcpyDeviceToHost, g->ctx->stream));
     uint32_t* abort_word = &g->host_ctl->pad[0];
+    uint32_t* abort_word_tk = &g->host_ctl->pad[1];
     if (g->mk) {
         if (int rc = mk_read_abort(g, abort_word)) return rc;
     }
+    if (g->tk) {
+        if (int rc = tk_read_abort(g, abort_word_tk)) return rc;
+    }
     VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
     *out = *g->host_ctl;
-    const uint32_t abort_flag = g->mk ? *abort_word : 0u;
-    const G3Failure f = g3_map_failure(out->nonfinite, abort_flag);
-    if (abort_flag != 0u) {
+    const uint32_t abort_mk = g->mk ? *abort_word : 0u, abort_tk = g->tk ? *abort_word_tk : 0u;
+    const G3Failure f = g3_map_failure(out->nonfinite, abort_mk | abort_tk);
+    if (abort_mk != 0u) {
         if (int rc = mk_clear_abort(g)) return rc;
+    }
+    if (abort_tk != 0u) {
+        if (int rc = tk_clear_abort(g)) return rc;
     }
     if (f.code != VRT_OK) return g3_fail_reset(g, f.code, f.msg);
     return VRT_OK;
@@ -949,6 +984,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
     }
     if (int rc = g3_write_ctl(g, 0, 0xffffffffu, 0xffffffffu, 0)) return fail(rc);
     if (int rc = mk_setup(g)) return fail(rc);
+    if (int rc = tk_setup(g)) return fail(rc);
     if (int rc = pf_setup(g, std::min(c.context_length, kPrefillMax))) return fail(rc);
     VRT_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     *out = g;
@@ -965,6 +1001,7 @@ extern "C" int vrt_g3_destroy(vrt_g3* g) {
     (void)hipStreamSynchronize(g->ctx->stream);
     if (g->graph) (void)hipGraphExecDestroy(g->graph);
     mk_destroy(g);
+    tk_destroy(g);
     for (void* p : g->allocs) (void)hipFree(p);
     if (g->host_ctl) (void)hipHostFree(g->host_ctl);
     if (g->host_res) (void)hipHostFree(g->host_res);
@@ -988,7 +1025,13 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
     case VRT_G3_OPT_QUERY_PERSISTENT:
         if (g->mk_refused) return set_error(VRT_ERR_STATE, "persistent decode kernel refused by the device");
         return g->mk ? VRT_OK : set_error(VRT_ERR_STATE, "persistent decode kernel unavailable");
-    case VRT_G3_OPT_TRACE: return mk_set_trace(g, value != 0);
+    case VRT_G3_OPT_TRACE:
+        if (!g->mk && !g->tk) return set_error(VRT_ERR_STATE, "persistent decode kernel unavailable");
+        if (g->mk) { if (int rc = mk_set_trace(g, value != 0)) return rc; }
+        return tk_set_trace(g, value != 0);
+    case VRT_G3_OPT_TEAM: g->use_team = value != 0; return VRT_OK;
+    case VRT_G3_OPT_QUERY_TEAM:
+        return g->tk ? VRT_OK : set_error(VRT_ERR_STATE, "team decode kernel unavailable");
     case VRT_G3_OPT_KV_F16: {
         // the kernels read the flag from their parameter blocks: the captured graph (which holds
         // G3Params by value) is dropped, the persistent kernel's block re-uploaded, the cache reset
@@ -1001,6 +1044,7 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
             g->graph = nullptr;
         }
         if (int rc = mk_set_kv_f16(g, on != 0)) return rc;
+        if (int rc = tk_set_kv_f16(g, on != 0)) return rc;
         return vrt_g3_reset(g);
     }
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
@@ -1016,7 +1060,7 @@ extern "C" int vrt_g3_decode(vrt_g3* g, uint32_t token, uint32_t position, uint3
     hipStream_t s = g->ctx->stream;
     VRT_HIP_CHECK(hipMemcpyAsync(g->P.tokens + position, &token, 4, hipMemcpyHostToDevice, s));
     if (int rc = g3_write_ctl(g, position, top_k ? position : 0xffffffffu, 0xffffffffu, top_k > 1 ? 1u : 0u)) return rc;
-    if (int rc = g3_run_steps(g, 1)) return g3_fail_reset(g, rc, vrt_last_error());
+    if (int rc = g3_run_steps(g, 1, position)) return g3_fail_reset(g, rc, vrt_last_error());
     if (hidden_out)
         VRT_HIP_CHECK(hipMemcpyAsync(hidden_out, g->P.hidden, g->cfg.embedding_length * 4u, hipMemcpyDeviceToHost, s));
     VRT_HIP_CHECK(hipMemcpyAsync(g->host_res, g->P.results + position, sizeof(vrt_argmax_result), hipMemcpyDeviceToHost, s));
@@ -1106,7 +1150,7 @@ extern "C" int vrt_g3_step(vrt_g3* g, uint32_t n) {
     VRT_REQUIRE(g->gen_max != 0, "vrt_g3_step: no generation started");
     const uint64_t total = static_cast<uint64_t>(g->gen_prompt) + g->gen_max - 1u;
     VRT_REQUIRE(g->gen_steps + n <= total, "vrt_g3_step: more steps than the generation needs");
-    if (int rc = g3_run_steps(g, n)) return g3_fail_reset(g, rc, vrt_last_error());
+    if (int rc = g3_run_steps(g, n, static_cast<uint32_t>(g->gen_steps))) return g3_fail_reset(g, rc, vrt_last_error());
     g->gen_steps += n;
     return VRT_OK;
 }
@@ -1157,7 +1201,7 @@ extern "C" int vrt_g3_forced(vrt_g3* g, const uint32_t* tokens, uint32_t n, uint
     g->next_pos = 0;
     VRT_HIP_CHECK(hipMemcpyAsync(g->P.tokens, tokens, n * 4u, hipMemcpyHostToDevice, s));
     if (int rc = g3_write_ctl(g, 0, first_logit_step, 0xffffffffu, 0)) return rc;
-    if (int rc = g3_run_steps(g, n)) return g3_fail_reset(g, rc, vrt_last_error());
+    if (int rc = g3_run_steps(g, n, 0u)) return g3_fail_reset(g, rc, vrt_last_error());
     VRT_HIP_CHECK(hipMemcpyAsync(out, g->P.results, n * sizeof(vrt_argmax_result), hipMemcpyDeviceToHost, s));
     G3State st;
     if (int rc = g3_check_state(g, &st)) return rc;
@@ -1172,6 +1216,7 @@ extern "C" int vrt_g3_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, ui
 
 extern "C" int vrt_g3_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots) {
     VRT_REQUIRE(g && out && nwg && slots, "vrt_g3_read_trace: null argument");
+    if (g->last_coop == kCoopTeam && g->tk) return tk_read_trace(g, out, cap, nwg, slots);
     return mk_read_trace(g, out, cap, nwg, slots);
 }
 

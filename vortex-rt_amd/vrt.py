@@ -21,6 +21,8 @@ OPT_PERSISTENT = 2
 OPT_QUERY_PERSISTENT = 3
 OPT_TRACE = 4
 OPT_KV_F16 = 5
+OPT_TEAM = 6
+OPT_QUERY_TEAM = 7
 
 
 class VrtError(RuntimeError):
@@ -377,6 +379,13 @@ class Gemma3:
     def set_persistent(self, on: bool):
         """Persistent decode kernel (default when available) or the multi-kernel step."""
         check(lib().vrt_g3_set_option(self.h, OPT_PERSISTENT, 1 if on else 0))
+
+    def set_team(self, on: bool):
+        """Phase-team persistent kernel for positions below its limit (default on)."""
+        check(lib().vrt_g3_set_option(self.h, OPT_TEAM, 1 if on else 0))
+
+    def team_available(self) -> bool:
+        return lib().vrt_g3_set_option(self.h, OPT_QUERY_TEAM, 0) == VRT_OK
 
     def set_trace(self, on: bool):
         check(lib().vrt_g3_set_option(self.h, OPT_TRACE, 1 if on else 0))
