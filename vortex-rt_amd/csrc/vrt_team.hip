@@ -73,7 +73,6 @@ constexpr uint32_t kThreads = 512;          // 8 waves: two per SIMD
 constexpr uint32_t kWaves = kThreads / 64;
 constexpr uint32_t kTeams = 4;              // A, B, D, E
 constexpr uint32_t kSpinLimit = 1u << 21;   // polls before a hand-off is declared lost
-constexpr int kPollSleep = 2;               // s_sleep between unsuccessful polls (64 clocks each)
 constexpr int kRsrcFlags = 0x00020000;      // raw buffer resource, 32-bit data format
 constexpr int kCoherent = 17;               // buffer access aux bits: sc0 | sc1 (system scope)
 constexpr uint32_t kLine = 8;               // tagged words per 64-byte line
@@ -102,7 +101,8 @@ struct Layer {
 struct Lds {
     uint32_t x;      // matvec input: A's x, B's head attention, D's x, E's g; the LM head's x
     uint32_t red;    // residual folds: wave totals [waves][4] and flags [waves]
-    uint32_t gu;     // D: the waves' partials of the gate/up rows [waves][64]
+    uint32_t dn;     // A, D: row partials and norm sums of the deferred-norm projections (DnLds)
+    uint32_t scr;    // A, D: each wave's activation limbs of its K blocks
     uint32_t qkv;    // B: q_h, k, v after QK-norm and RoPE
     uint32_t part;   // B: per-wave attention partials [waves][hd], then m [waves], l [waves]
     uint32_t la, lb, lc, ls;   // LM head activation limbs
@@ -120,6 +120,7 @@ struct Params {
     uint32_t lm_tile_rows;
     uint32_t trace_slots;          // stamps per workgroup (0: tracing off)
     uint32_t kv_f16;
+    uint32_t poll_sleep;           // back-off between unsuccessful polls (s_sleep units of 64 clocks)
     Lds lds;
     const uint8_t* tok_embd;
     const uint8_t* arena_end;
@@ -181,6 +182,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t b
 // Polls N 16-byte units (two tagged words each) of up to two buffers until both tags of every
 // live unit equal its tag; unit k reads buffer which[k] at byte off[k]. out[2k], out[2k+1] get
 // the values. Returns 1 if the wait was abandoned (spin limit, or another workgroup's abort).
+// Backs off between two unsuccessful polls: s_sleep of g_tk.poll_sleep (x 64 clocks).
+__device__ __forceinline__ void poll_backoff() {
+    switch (g_tk.poll_sleep) {
+    case 0: break;
+    case 1: __builtin_amdgcn_s_sleep(1); break;
+    case 2: __builtin_amdgcn_s_sleep(2); break;
+    case 4: __builtin_amdgcn_s_sleep(4); break;
+    case 8: __builtin_amdgcn_s_sleep(8); break;
+    default: __builtin_amdgcn_s_sleep(16); break;
+    }
+}
+
 template <int N>
 __device__ __forceinline__ int poll_units(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1, const int (&off)[N],
                                           const bool (&which)[N], const bool (&live)[N], const uint32_t (&tag)[N],
@@ -201,7 +214,7 @@ __device__ __forceinline__ int poll_units(__amdgpu_buffer_rsrc_t r0, __amdgpu_bu
             raise_abort();
             break;
         }
-        __builtin_amdgcn_s_sleep(kPollSleep);
+        poll_backoff();
         __asm__ volatile("" ::: "memory");
 #pragma unroll
         for (int k = 0; k < N; ++k)
@@ -590,8 +603,10 @@ __device__ __forceinline__ uint32_t lm_tile_issue(uint32_t r0, uint32_t r1, uint
 
 // Waits until this wave's tile loads issued before its last `later` tiles are complete.
 __device__ __forceinline__ void lm_wait_tiles(uint32_t later) {
-    static_assert(kLmUnits * (kLmAhead - 1u) <= 15u, "vmcnt immediate");
-    if (later >= 2u) __builtin_amdgcn_s_waitcnt(0x0F70 | (2u * kLmUnits));
+    static_assert(kLmUnits * (kLmAhead - 1u) <= 15u && kLmAhead <= 4u, "vmcnt immediate");
+    // s_waitcnt: vmcnt in bits 3:0, expcnt (7) and lgkmcnt (15) left unconstrained
+    if (later >= 3u) __builtin_amdgcn_s_waitcnt(0x0F70 | (3u * kLmUnits));
+    else if (later == 2u) __builtin_amdgcn_s_waitcnt(0x0F70 | (2u * kLmUnits));
     else if (later == 1u) __builtin_amdgcn_s_waitcnt(0x0F70 | kLmUnits);
     else __builtin_amdgcn_s_waitcnt(0x0F70);
 }
@@ -988,6 +1003,143 @@ __device__ __forceinline__ void load_limb_img(const uint32_t* img, uint32_t b, X
     x.s = __uint_as_float(p[24]);
 }
 
+// ---- projections with the norms applied after the dot products --------------------------------
+
+// A projection of a normed residual fold, x = (h' * rms(h')) * w_next with h' = y * (rms(y) * w_post)
+// + h (src/gemma3.cpp:1703-1718, :991-996), is linear in x, so each output row is
+//     rms(h') * (rms(y) * W (y . w_post . w_next) + W (h . w_next))
+// and the dot products need no global norm: W (h . w_next) runs as soon as h arrives (it is
+// published phases before y), W (y . w_post . w_next) as soon as y arrives, and the two norms come
+// from one reduction round afterwards (sum h'^2 = rms(y)^2 sum a^2 + 2 rms(y) sum a h + sum h^2,
+// a = y . w_post). Layout: one output row per lane (at most 64 rows), the waves splitting the K
+// blocks (wave w: blocks split_range(nblk, kWaves, w), at most KB); lane l of wave w owns the element
+// pair 16 b0 + l of the wave's blocks, so a 32-element block is one 16-lane row of the wave. Each
+// wave turns its elements into activation limbs in a scratch of its own in LDS (block j of the wave at
+// scr + 112 j: a, b, c, then the scale) and every lane dots its row's blocks against them.
+
+constexpr uint32_t kLimbBlkBytes = 112;   // one block's limbs in a wave scratch: 3 x 32 + scale, padded
+
+// The pair of the d-vector that this lane owns in a deferred-norm projection (live: pair exists).
+__device__ __forceinline__ uint32_t dn_pair(uint32_t nblk, bool& live, uint32_t& nb) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t b0, b1;
+    split_range(nblk, kWaves, wave, b0, b1);
+    nb = b1 - b0;
+    live = lane < 16u * nb;
+    return 16u * b0 + (live ? lane : 0u);
+}
+
+// Limbs of the wave's blocks from v (this lane's two elements; 0 where !live) into scr, then this
+// lane's partial dot over the wave's blocks (row_live: the lane has a row).
+template <int KB>
+__device__ __forceinline__ float wave_limbs_dot(float2 v, bool live, uint32_t nb, uint8_t* scr, const RowK<KB>& rb,
+                                                bool row_live) {
+    const uint32_t lane = threadIdx.x & 63u;
+    auto mag = [](float x) { return __builtin_isfinite(x) ? fabsf(x) : INFINITY; };
+    float mm = fmaxf(mag(v.x), mag(v.y));
+    mm = fmaxf(mm, dpp_mov<0xB1>(mm));
+    mm = fmaxf(mm, dpp_mov<0x4E>(mm));
+    mm = fmaxf(mm, dpp_mov<0x141>(mm));
+    mm = fmaxf(mm, dpp_mov<0x140>(mm));   // every lane of a 16-lane row: its block's amax
+    int8_t qa0 = 0, qb0 = 0, qc0 = 0, qa1 = 0, qb1 = 0, qc1 = 0;
+    float sb = 0.0f;
+    if (mm == INFINITY) {
+        sb = __builtin_nanf("");
+    } else if (mm >= 1e-30f) {
+        sb = mm * (1.0f / 127.0f);
+        const float inv = 127.0f * __builtin_amdgcn_rcpf(mm);
+        limb3_r(v.x, inv, qa0, qb0, qc0);
+        limb3_r(v.y, inv, qa1, qb1, qc1);
+    }
+    if (live) {
+        auto pk = [](int8_t lo, int8_t hi) {
+            return static_cast<uint16_t>(static_cast<uint8_t>(lo) | (static_cast<uint16_t>(static_cast<uint8_t>(hi)) << 8));
+        };
+        uint8_t* bp = scr + (lane >> 4) * kLimbBlkBytes + 2u * (lane & 15u);
+        *reinterpret_cast<uint16_t*>(bp) = pk(qa0, qa1);
+        *reinterpret_cast<uint16_t*>(bp + 32) = pk(qb0, qb1);
+        *reinterpret_cast<uint16_t*>(bp + 64) = pk(qc0, qc1);
+        if ((lane & 15u) == 0u) *reinterpret_cast<float*>(scr + (lane >> 4) * kLimbBlkBytes + 96u) = sb;
+    }
+    // the wave's own LDS writes precede its reads (in order within a wave)
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+        if (static_cast<uint32_t>(j) < nb) {
+            const uint32_t* q = reinterpret_cast<const uint32_t*>(scr + j * kLimbBlkBytes);
+            XLimb x;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x.a[i] = static_cast<int>(q[i]);
+                x.b[i] = static_cast<int>(q[8 + i]);
+                x.c[i] = static_cast<int>(q[16 + i]);
+            }
+            x.s = __uint_as_float(q[24]);
+            if (row_live) acc += q8_dot_p(rb.raw[j], x);
+        }
+    return acc;
+}
+
+// Polls this lane's pair of the ny (<= NY) tagged d-vectors src[q d ..] and sums them in order q.
+template <int NY>
+__device__ __forceinline__ int poll_pair_sum(const u64* src, uint32_t ny, uint32_t tag, uint32_t pb, bool live,
+                                             float2& out) {
+    const uint32_t d = g_tk.d;
+    int off[NY];
+    bool which[NY], lv[NY];
+    uint32_t tg[NY];
+#pragma unroll
+    for (int q = 0; q < NY; ++q) {
+        off[q] = static_cast<int>((static_cast<uint32_t>(q) * d + 2u * pb) * 8u);
+        which[q] = false;
+        lv[q] = live && static_cast<uint32_t>(q) < ny;
+        tg[q] = tag;
+    }
+    float v[2 * NY];
+    const __amdgpu_buffer_rsrc_t r = rsrc(src, NY * d * 8u);
+    const int fail = poll_units<NY>(r, r, off, which, lv, tg, v);
+    out = make_float2(0.0f, 0.0f);
+#pragma unroll
+    for (int q = 0; q < NY; ++q)
+        if (lv[q]) {
+            out.x = q == 0 ? v[2 * q] : out.x + v[2 * q];
+            out.y = q == 0 ? v[2 * q + 1] : out.y + v[2 * q + 1];
+        }
+    return fail;
+}
+
+// Per-wave totals of a deferred-norm projection in LDS (dn region): [kWaves][64] row partials of
+// W (h . w_next), the same for W (y . w_post . w_next), [kWaves][4] sums and [kWaves] flags.
+struct DnLds {
+    float* p0;
+    float* p1;
+    float* sums;
+    int* flg;
+};
+__device__ __forceinline__ DnLds dn_lds() {
+    float* b = lds<float>(g_tk.lds.dn);
+    return DnLds{b, b + kWaves * 64u, b + 2u * kWaves * 64u, reinterpret_cast<int*>(b + 2u * kWaves * 64u + 4u * kWaves)};
+}
+
+// The norm scalars from the wave totals (wave order; every thread the same bits).
+__device__ __forceinline__ void dn_scalars(const DnLds& t, bool has_y, float& sc1, float& sc2, int& anyflag) {
+    float syy = 0.0f, saa = 0.0f, sah = 0.0f, shh = 0.0f;
+    int fl = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kWaves; ++k) {
+        const float4 v = *reinterpret_cast<const float4*>(t.sums + 4u * k);
+        syy += v.x;
+        saa += v.y;
+        sah += v.z;
+        shh += v.w;
+        fl |= t.flg[k];
+    }
+    anyflag = fl;
+    const float inv_d = 1.0f / static_cast<float>(g_tk.d);
+    sc1 = has_y ? rms_fast(syy, inv_d, g_tk.eps) : 0.0f;
+    sc2 = rms_fast(has_y ? sc1 * sc1 * saa + 2.0f * sc1 * sah + shh : shh, inv_d, g_tk.eps);
+}
+
 // ---- shapes -------------------------------------------------------------------------------------
 
 // Row-slot width S, blocks per lane NB and passes U of each team's matvec, and EP2 = the residual
@@ -1009,19 +1161,23 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
 #pragma clang fp contract(off)
     nsteps = __builtin_amdgcn_readfirstlane(nsteps);
     tag0 = __builtin_amdgcn_readfirstlane(tag0);
-    const uint32_t w = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t w = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t m = member_of(w), ts = g_tk.tsize;
     const uint32_t d = g_tk.d, hd = g_tk.hd, qw = g_tk.H * hd, nqkv = qw + 2u * hd, L = g_tk.L;
     const uint32_t nblk_d = d >> 5;
     const uint64_t rb_d = static_cast<uint64_t>(nblk_d) * 34u;
     const uint32_t nph = kTagsPerBlock * L + 1u;
     uint32_t v0, v1, e0, e1;
-    split_lines(nqkv, ts, m, v0, v1);
+    split_lines(nqkv, ts, m, v0, v1);   // at most 64 rows: one per lane
     split_lines(d, ts, m, e0, e1);
-    float* x = lds<float>(g_tk.lds.x);
-    const LimbLds Lx{lds<int8_t>(g_tk.lds.la), lds<int8_t>(g_tk.lds.lb), lds<int8_t>(g_tk.lds.lc), lds<float>(g_tk.lds.ls)};
-    RowBatch<C::SA, 1, C::UA> rb;
-    FoldW fw;
+    const bool row_live = lane < v1 - v0;
+    const DnLds t = dn_lds();
+    uint8_t* scr = lds<uint8_t>(g_tk.lds.scr) + wave * C::KBD * kLimbBlkBytes;
+    bool plive;
+    uint32_t pnb;
+    const uint32_t pb = dn_pair(nblk_d, plive, pnb);
+    RowK<C::KBD> rb;
+    float2 wp = make_float2(0.0f, 0.0f), wn = make_float2(0.0f, 0.0f);
     auto load = [&](uint32_t l) {
         const Layer& Ly = g_tk_layers[l];
         const uint8_t *wq = Ly.wq, *wk = Ly.wk, *wv = Ly.wv;
@@ -1030,8 +1186,12 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
                           : (v < qw + hd ? wk + static_cast<uint64_t>(v - qw) * rb_d
                                          : wv + static_cast<uint64_t>(v - qw - hd) * rb_d);
         };
-        batch_load<C::SA, 1, C::UA>(rowp, nblk_d, g_tk.arena_end, v0, v1, wave, kWaves, rb);
-        fw = fold_weights(l > 0u ? g_tk_layers[l - 1u].post_ffw : nullptr, Ly.attn_norm);
+        rowk_load<C::KBD>(rowp, nblk_d, g_tk.arena_end, v0, v1, rb);
+        wn = make_float2(gp(Ly.attn_norm)[2u * pb], gp(Ly.attn_norm)[2u * pb + 1u]);
+        if (l > 0u) {
+            const float* wpost = g_tk_layers[l - 1u].post_ffw;
+            wp = make_float2(gp(wpost)[2u * pb], gp(wpost)[2u * pb + 1u]);
+        }
     };
     load(0);
     StepCtl c = read_ctl();
@@ -1048,27 +1208,80 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
         trace_begin(tr);
         stamp(tr, 2u * L);
         for (uint32_t l = 0; l < L && ok; ++l) {
-            batch_prep<C::SA, 1, C::UA>(rb);
+            const bool mk = tr && l == 1u;
+            rowk_prep<C::KBD>(rb);
+            // stage 1: h, the block's input residual (the scaled embedding row, or hm of block l - 1)
+            float2 h = make_float2(0.0f, 0.0f);
             int fail = 0;
-            if (l > 0u)   // the non-finite check of block l - 1 (:1857-1863)
-                fail = fold_dist<C::EP2, true, 1, true>(g_tk.x_hm, tagof(tagb, l - 1u, kTHm), nullptr, g_tk.x_d, 1u,
-                                                        tagof(tagb, l - 1u, kTD), fw, x, Lx, nullptr, g_tk.x_h, e0, e1,
-                                                        tagof(tagb, l, kTH), m == 0u, g3_code_nonfinite(l - 1u),
-                                                        tr && l == 1u);
-            else
-                fail = fold_dist<C::EP2, false, 0, true>(nullptr, 0u, g_tk.tok_embd + static_cast<uint64_t>(token) * rb_d,
-                                                         nullptr, 0u, 0u, fw, x, Lx, nullptr, g_tk.x_h, e0, e1,
-                                                         tagof(tagb, 0u, kTH), false, 0u);
-            if (fail) { ok = false; break; }
+            if (l == 0u) {
+                if (plive) {
+                    const TK_AS_GLOBAL uint8_t* bq = gp(g_tk.tok_embd) + static_cast<uint64_t>(token) * rb_d + ((2u * pb) >> 5) * 34u;
+                    const float sc = half_bits_to_float(static_cast<uint32_t>(bq[0]) | (static_cast<uint32_t>(bq[1]) << 8));
+                    const uint32_t i = (2u * pb) & 31u;
+                    h.x = (sc * static_cast<float>(static_cast<int8_t>(bq[2 + i]))) * g_tk.emb_scale;   // :1106-1136
+                    h.y = (sc * static_cast<float>(static_cast<int8_t>(bq[3 + i]))) * g_tk.emb_scale;
+                }
+            } else {
+                fail |= poll_pair_sum<1>(g_tk.x_hm, 1u, tagof(tagb, l - 1u, kTHm), pb, plive, h);
+            }
+            const float p0 = wave_limbs_dot<C::KBD>(make_float2(h.x * wn.x, h.y * wn.y), plive, pnb, scr, rb, row_live);
+            submark(mk, 0);
+            // stage 2: y = d of block l - 1
+            float2 a = make_float2(0.0f, 0.0f);
+            float p1 = 0.0f, syy = 0.0f, saa = 0.0f, sah = 0.0f, shh = h.x * h.x + h.y * h.y;
+            if (l > 0u) {
+                float2 y;
+                fail |= poll_pair_sum<1>(g_tk.x_d, 1u, tagof(tagb, l - 1u, kTD), pb, plive, y);
+                submark(mk, 1);
+                a = make_float2(y.x * wp.x, y.y * wp.y);
+                p1 = wave_limbs_dot<C::KBD>(make_float2(a.x * wn.x, a.y * wn.y), plive, pnb, scr, rb, row_live);
+                syy = y.x * y.x + y.y * y.y;
+                saa = a.x * a.x + a.y * a.y;
+                sah = a.x * h.x + a.y * h.y;
+            }
+            wave_sum4(syy, saa, sah, shh);
+            t.p0[wave * 64u + lane] = p0;
+            t.p1[wave * 64u + lane] = p1;
+            const bool wf = __builtin_amdgcn_ballot_w64(fail != 0) != 0u;
+            if (lane == 0u) {
+                *reinterpret_cast<float4*>(t.sums + 4u * wave) = make_float4(syy, saa, sah, shh);
+                t.flg[wave] = wf ? 1 : 0;
+            }
+            submark(mk, 2);
+            __syncthreads();
+            float sc1, sc2;
+            int anyf;
+            dn_scalars(t, l > 0u, sc1, sc2, anyf);
+            if (anyf) { ok = false; break; }
             stamp(tr, l);
-            u64* out = g_tk.x_qkv;
-            const uint32_t tq = tagof(tagb, l, kTQkv);
-            XLimb xl[1];
-            lane_limbs<C::SA, 1>(Lx, nblk_d, xl);
-            batch_consume_p<C::SA, 1, C::UA>(rb, nblk_d, xl, [&](uint32_t v, float val) { st_word(out + v, val, tq); });
+            // h' = y * (rms(y) * w_post) + h, published for team D; a non-finite h' fails block l - 1 (:1857-1863)
+            const float2 hn = make_float2(a.x * sc1 + h.x, a.y * sc1 + h.y);
+            if (l > 0u && m == 0u) {
+                const bool nf = plive && (!__builtin_isfinite(hn.x) || !__builtin_isfinite(hn.y));
+                if (__builtin_amdgcn_ballot_w64(nf) != 0u && lane == 0u) flag_min(g3_code_nonfinite(l - 1u));
+            }
+            if (plive && 2u * pb >= e0 && 2u * pb < e1) {
+                st_word(g_tk.x_h + 2u * pb, hn.x, tagof(tagb, l, kTH));
+                st_word(g_tk.x_h + 2u * pb + 1u, hn.y, tagof(tagb, l, kTH));
+            }
+            if (wave == 0u && row_live) {   // row v0 + lane: rms(h') * (rms(y) * P1 + P0), partials in wave order
+                float q0[kWaves], q1[kWaves];
+#pragma unroll
+                for (uint32_t k = 0; k < kWaves; ++k) {
+                    q0[k] = t.p0[k * 64u + lane];
+                    q1[k] = t.p1[k * 64u + lane];
+                }
+                float P0 = q0[0], P1 = q1[0];
+#pragma unroll
+                for (uint32_t k = 1; k < kWaves; ++k) {
+                    P0 += q0[k];
+                    P1 += q1[k];
+                }
+                st_word(g_tk.x_qkv + v0 + lane, sc2 * (sc1 * P1 + P0), tagof(tagb, l, kTQkv));
+            }
             stamp(tr, L + l);
+            __syncthreads();   // the wave totals are rewritten by the next block
             if (l + 1u < L) load(l + 1u);
-            __syncthreads();   // x is rewritten by the next fold
         }
         if (!ok) break;
         if (s >= c.lm_from) {
@@ -1429,17 +1642,21 @@ __device__ __attribute__((always_inline)) void team_d(uint32_t nsteps, uint32_t 
     split_range(F >> 5, ts, m, gb0, gb1);
     split_lines(d, ts, m, e0, e1);
     const uint32_t p0 = 32u * gb0, p1 = 32u * gb1, v0 = 2u * p0, v1 = 2u * p1;
-    float* x = lds<float>(g_tk.lds.x);
-    float* pr = lds<float>(g_tk.lds.gu);                 // [kWaves][64] row partials
-    const LimbLds Lx{lds<int8_t>(g_tk.lds.la), lds<int8_t>(g_tk.lds.lb), lds<int8_t>(g_tk.lds.lc), lds<float>(g_tk.lds.ls)};
+    const bool row_live = lane < v1 - v0;
+    const DnLds t = dn_lds();
+    uint8_t* scr = lds<uint8_t>(g_tk.lds.scr) + wave * C::KBD * kLimbBlkBytes;
+    bool plive;
+    uint32_t pnb;
+    const uint32_t pb = dn_pair(nblk_d, plive, pnb);
     RowK<C::KBD> rb;
-    FoldW fw;
+    float2 wp = make_float2(0.0f, 0.0f), wn = make_float2(0.0f, 0.0f);
     auto load = [&](uint32_t l) {
         const Layer& Ly = g_tk_layers[l];
         const uint8_t *wg = Ly.wg, *wu = Ly.wu;
         auto rowp = [=](uint32_t v) { return ((v & 1u) ? wu : wg) + static_cast<uint64_t>(v >> 1) * rb_d; };
         rowk_load<C::KBD>(rowp, nblk_d, g_tk.arena_end, v0, v1, rb);
-        fw = fold_weights(Ly.post_attn, Ly.ffn_norm);
+        wp = make_float2(gp(Ly.post_attn)[2u * pb], gp(Ly.post_attn)[2u * pb + 1u]);
+        wn = make_float2(gp(Ly.ffn_norm)[2u * pb], gp(Ly.ffn_norm)[2u * pb + 1u]);
     };
     load(0);
     StepCtl c = read_ctl();
@@ -1456,26 +1673,56 @@ __device__ __attribute__((always_inline)) void team_d(uint32_t nsteps, uint32_t 
         trace_begin(tr);
         stamp(tr, 2u * L);
         for (uint32_t l = 0; l < L && ok; ++l) {
+            const bool mk = tr && l == 1u;
             rowk_prep<C::KBD>(rb);
-            if (fold_dist<C::EP2, true, kMaxHeads, true>(g_tk.x_h, tagof(tagb, l, kTH), nullptr, g_tk.x_o, H,
-                                                         tagof(tagb, l, kTO), fw, x, Lx, nullptr, g_tk.x_hm, e0, e1,
-                                                         tagof(tagb, l, kTHm), false, 0u, tr && l == 1u)) {
-                ok = false;
-                break;
+            // stage 1: h of block l (team A)
+            float2 h;
+            int fail = poll_pair_sum<1>(g_tk.x_h, 1u, tagof(tagb, l, kTH), pb, plive, h);
+            const float q0p = wave_limbs_dot<C::KBD>(make_float2(h.x * wn.x, h.y * wn.y), plive, pnb, scr, rb, row_live);
+            submark(mk, 0);
+            // stage 2: y = the attention output, the per-head O partials added in head order (team B)
+            float2 y;
+            fail |= poll_pair_sum<kMaxHeads>(g_tk.x_o, H, tagof(tagb, l, kTO), pb, plive, y);
+            submark(mk, 1);
+            const float2 a = make_float2(y.x * wp.x, y.y * wp.y);
+            const float q1p = wave_limbs_dot<C::KBD>(make_float2(a.x * wn.x, a.y * wn.y), plive, pnb, scr, rb, row_live);
+            float syy = y.x * y.x + y.y * y.y, saa = a.x * a.x + a.y * a.y, sah = a.x * h.x + a.y * h.y,
+                  shh = h.x * h.x + h.y * h.y;
+            wave_sum4(syy, saa, sah, shh);
+            t.p0[wave * 64u + lane] = q0p;
+            t.p1[wave * 64u + lane] = q1p;
+            const bool wf = __builtin_amdgcn_ballot_w64(fail != 0) != 0u;
+            if (lane == 0u) {
+                *reinterpret_cast<float4*>(t.sums + 4u * wave) = make_float4(syy, saa, sah, shh);
+                t.flg[wave] = wf ? 1 : 0;
             }
-            stamp(tr, l);
-            pr[wave * 64u + lane] = rowk_dot<C::KBD>(rb, Lx, nblk_d);
-            submark(tr && l == 1u, 5);
+            submark(mk, 2);
             __syncthreads();
-            submark(tr && l == 1u, 6);
+            float sc1, sc2;
+            int anyf;
+            dn_scalars(t, true, sc1, sc2, anyf);
+            if (anyf) { ok = false; break; }
+            stamp(tr, l);
+            // hm = y * (rms(y) * post_attn) + h, published for team A of block l + 1 and the LM head
+            if (plive && 2u * pb >= e0 && 2u * pb < e1) {
+                st_word(g_tk.x_hm + 2u * pb, a.x * sc1 + h.x, tagof(tagb, l, kTHm));
+                st_word(g_tk.x_hm + 2u * pb + 1u, a.y * sc1 + h.y, tagof(tagb, l, kTHm));
+            }
             if (wave == 0u && v0 < v1) {
-                // row v0 + lane: the waves' partials in order; gate rows are even, up rows odd
-                float pk[kWaves];
+                // row v0 + lane: rms(hm) * (rms(y) * P1 + P0); gate rows are even, up rows odd
+                float r0[kWaves], r1[kWaves];
 #pragma unroll
-                for (uint32_t k = 0; k < kWaves; ++k) pk[k] = pr[k * 64u + lane];
-                float val = pk[0];
+                for (uint32_t k = 0; k < kWaves; ++k) {
+                    r0[k] = t.p0[k * 64u + lane];
+                    r1[k] = t.p1[k * 64u + lane];
+                }
+                float P0 = r0[0], P1 = r1[0];
 #pragma unroll
-                for (uint32_t k = 1; k < kWaves; ++k) val += pk[k];
+                for (uint32_t k = 1; k < kWaves; ++k) {
+                    P0 += r0[k];
+                    P1 += r1[k];
+                }
+                const float val = sc2 * (sc1 * P1 + P0);
                 const float up = dpp_mov<0xB1>(val);   // even lanes: the odd neighbour's up row
                 // even lane 2 j: g of pair p0 + j (shaders/gelu_mul.comp:23-31)
                 const float gv = (lane & 1u) ? 0.0f : gelu_fast(val) * up;
@@ -1492,8 +1739,9 @@ __device__ __attribute__((always_inline)) void team_d(uint32_t nsteps, uint32_t 
                     st_bits(out + 24u + k, k == 0u ? __float_as_uint(sc) : 0u, tg);
                 }
             }
+            (void)row_live;
             stamp(tr, L + l);
-            __syncthreads();   // the other waves' next loads wait: wave 0's tail has its SIMD
+            __syncthreads();   // the wave totals are rewritten by the next block
             if (l + 1u < L) load(l + 1u);
         }
         if (!ok) break;
@@ -1687,12 +1935,12 @@ int tk_setup(vrt_g3* g) {
     MvShape sd, sb, sf;
     if (!mv_shape(d, &sd) || !mv_shape(hd, &sb) || !mv_shape(F, &sf)) return VRT_OK;
     // capacity (rows) of one batch: waves x rows per wave x passes, read back from the template
-    // (team D: one row per lane over at most one 32-element block of g per workgroup, and at
-    // most kbd K blocks per wave)
+    // (teams A and D: one row per lane, at most kbd K blocks of d per wave; team D: at most one
+    // 32-element block of g per workgroup)
     struct Caps { uint32_t a, b, kbd, e; };
     Caps caps{};
-    if (d == 640) caps = Caps{kWaves * 2u * 2u, kWaves * 8u, 3u, kWaves * 1u * 2u};
-    else caps = Caps{kWaves * 16u * 1u, kWaves * 32u, 1u, kWaves * 8u * 1u};
+    if (d == 640) caps = Caps{64u, kWaves * 8u, 3u, kWaves * 1u * 2u};
+    else caps = Caps{64u, kWaves * 32u, 1u, kWaves * 8u * 1u};
     if (max_lines(nqkv, ts) > caps.a || max_lines(d, ts / H) > caps.b || F / 32u > ts ||
         (d / 32u + kWaves - 1u) / kWaves > caps.kbd || max_lines(d, ts) > caps.e)
         return VRT_OK;
@@ -1715,6 +1963,7 @@ int tk_setup(vrt_g3* g) {
     }
     if (P.lm_tile_rows == 0u) { tk_destroy(g); return VRT_OK; }
     P.kv_f16 = g->P.kv_f16;
+    P.poll_sleep = 1u;   // measured at positions 8..27: 0 and 1 fastest, 2 +1%, 8 +5%, 16 +10%
 
     // LDS layout
     const uint32_t kmax = std::max(std::max(d, qw), F);
@@ -1722,16 +1971,20 @@ int tk_setup(vrt_g3* g) {
     auto take = [&](uint32_t bytes) { const uint32_t o = off; off += (bytes + 15u) & ~15u; return o; };
     P.lds.x = take(std::max(kmax, 33u * (F / 32u)) * 4u);
     P.lds.red = take(4u * kWaves * 4u + kWaves * 4u);
-    P.lds.gu = take(kWaves * 64u * 4u);
-    P.lds.qkv = take(3u * hd * 4u);
-    P.lds.part = take((kWaves * hd + 2u * kWaves) * 4u);
     P.lds.la = take(d);
     P.lds.lb = take(d);
     P.lds.lc = take(d);
     P.lds.ls = take(d / 32u * 4u);
     P.lds.am = take(2u * nwg * 4u);
     P.lds.any = take(kAnySets * kWaves * 4u);
-    P.lds.ring = take(kLmRing * kLmTileBytes);
+    // the LM-head ring overlays the scratch of the block phases (the LM head follows them)
+    const uint32_t blk0 = off;
+    P.lds.dn = take((2u * kWaves * 64u + 4u * kWaves + kWaves) * 4u);
+    P.lds.scr = take(kWaves * 3u * kLimbBlkBytes);
+    P.lds.qkv = take(3u * hd * 4u);
+    P.lds.part = take((kWaves * hd + 2u * kWaves) * 4u);
+    off = std::max(off, blk0 + kLmRing * kLmTileBytes);
+    P.lds.ring = blk0;
     tk->trace_slots = 2u * c.block_count + 3u + kSubMarks;
     P.lds.tr = take(tk->trace_slots * 8u);
     P.lds.total = off;
