@@ -1033,7 +1033,7 @@ __device__ __forceinline__ uint32_t dn_pair(uint32_t nblk, bool& live, uint32_t&
 // lane's partial dot over the wave's blocks (row_live: the lane has a row).
 template <int KB>
 __device__ __forceinline__ float wave_limbs_dot(float2 v, bool live, uint32_t nb, uint8_t* scr, const RowK<KB>& rb,
-                                                bool row_live) {
+                                                bool row_live, uint32_t jb = 0u, uint32_t je = ~0u) {
     const uint32_t lane = threadIdx.x & 63u;
     auto mag = [](float x) { return __builtin_isfinite(x) ? fabsf(x) : INFINITY; };
     float mm = fmaxf(mag(v.x), mag(v.y));
@@ -1062,10 +1062,13 @@ __device__ __forceinline__ float wave_limbs_dot(float2 v, bool live, uint32_t nb
         if ((lane & 15u) == 0u) *reinterpret_cast<float*>(scr + (lane >> 4) * kLimbBlkBytes + 96u) = sb;
     }
     // the wave's own LDS writes precede its reads (in order within a wave)
+    // this lane's blocks: jb + jj < min(je, nb), its weights in rb.raw[jj]
     float acc = 0.0f;
+    const uint32_t jn = min(je, nb);
 #pragma unroll
-    for (int j = 0; j < KB; ++j)
-        if (static_cast<uint32_t>(j) < nb) {
+    for (int jj = 0; jj < KB; ++jj)
+        if (jb + static_cast<uint32_t>(jj) < jn) {
+            const uint32_t j = jb + static_cast<uint32_t>(jj);
             const uint32_t* q = reinterpret_cast<const uint32_t*>(scr + j * kLimbBlkBytes);
             XLimb x;
 #pragma unroll
@@ -1075,9 +1078,43 @@ __device__ __forceinline__ float wave_limbs_dot(float2 v, bool live, uint32_t nb
                 x.c[i] = static_cast<int>(q[16 + i]);
             }
             x.s = __uint_as_float(q[24]);
-            if (row_live) acc += q8_dot_p(rb.raw[j], x);
+            if (row_live) acc += q8_dot_p(rb.raw[jj], x);
         }
     return acc;
+}
+
+// Team A's split of a wave's K blocks over the two halves of the wave: lane l takes row l % 32
+// and, of the wave's nb blocks, [0, ceil(nb / 2)) for l < 32 or [ceil(nb / 2), nb) for l >= 32.
+__device__ __forceinline__ void half_blocks(uint32_t nb, uint32_t& jb, uint32_t& je) {
+    const uint32_t h = (nb + 1u) >> 1;
+    const bool hi = (threadIdx.x & 63u) >= 32u;
+    jb = hi ? h : 0u;
+    je = hi ? nb : h;
+}
+
+// Rows [v0, v1) (at most 32) with row v0 + l % 32 on lane l, each half of the wave loading its
+// share of the wave's blocks (half_blocks), at most KB2 each.
+template <int KB2, typename RowFn>
+__device__ __forceinline__ void rowk_load_half(RowFn&& rowp, uint32_t nblk, const uint8_t* end, uint32_t v0, uint32_t v1,
+                                               RowK<KB2>& rb) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t b0, b1, jb, je;
+    split_range(nblk, kWaves, wave, b0, b1);
+    half_blocks(b1 - b0, jb, je);
+    const uint32_t v = v0 + (lane & 31u);
+    const uint8_t* rp = v < v1 ? rowp(v) : nullptr;
+#pragma unroll
+    for (int jj = 0; jj < KB2; ++jj)
+        if (v < v1 && jb + static_cast<uint32_t>(jj) < je) q8_load(rp + 34u * (b0 + jb + static_cast<uint32_t>(jj)), end, rb.raw[jj]);
+}
+
+// Lanes l < 32: this lane's partial plus the one of lane l + 32. v_permlane32_swap exchanges the
+// upper 32 lanes of one copy of v with the lower 32 lanes of another, so the two results hold v[l]
+// and v[l + 32] in lane l (l < 32); fp addition is commutative, so their sum is the same bits
+// whichever result holds which.
+__device__ __forceinline__ float add_upper_half(float v) {
+    const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
 }
 
 // Polls this lane's pair of the ny (<= NY) tagged d-vectors src[q d ..] and sums them in order q.
@@ -1170,13 +1207,16 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
     uint32_t v0, v1, e0, e1;
     split_lines(nqkv, ts, m, v0, v1);   // at most 64 rows: one per lane
     split_lines(d, ts, m, e0, e1);
-    const bool row_live = lane < v1 - v0;
+    const bool row_live = (lane & 31u) < v1 - v0;   // two lanes per row (half_blocks)
     const DnLds t = dn_lds();
     uint8_t* scr = lds<uint8_t>(g_tk.lds.scr) + wave * C::KBD * kLimbBlkBytes;
     bool plive;
     uint32_t pnb;
     const uint32_t pb = dn_pair(nblk_d, plive, pnb);
-    RowK<C::KBD> rb;
+    uint32_t jb, je;
+    half_blocks(pnb, jb, je);
+    constexpr int KB2 = (C::KBD + 1) / 2;
+    RowK<KB2> rb;
     float2 wp = make_float2(0.0f, 0.0f), wn = make_float2(0.0f, 0.0f);
     auto load = [&](uint32_t l) {
         const Layer& Ly = g_tk_layers[l];
@@ -1186,7 +1226,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
                           : (v < qw + hd ? wk + static_cast<uint64_t>(v - qw) * rb_d
                                          : wv + static_cast<uint64_t>(v - qw - hd) * rb_d);
         };
-        rowk_load<C::KBD>(rowp, nblk_d, g_tk.arena_end, v0, v1, rb);
+        rowk_load_half<KB2>(rowp, nblk_d, g_tk.arena_end, v0, v1, rb);
         wn = make_float2(gp(Ly.attn_norm)[2u * pb], gp(Ly.attn_norm)[2u * pb + 1u]);
         if (l > 0u) {
             const float* wpost = g_tk_layers[l - 1u].post_ffw;
@@ -1209,7 +1249,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
         stamp(tr, 2u * L);
         for (uint32_t l = 0; l < L && ok; ++l) {
             const bool mk = tr && l == 1u;
-            rowk_prep<C::KBD>(rb);
+            rowk_prep<KB2>(rb);
             // stage 1: h, the block's input residual (the scaled embedding row, or hm of block l - 1)
             float2 h = make_float2(0.0f, 0.0f);
             int fail = 0;
@@ -1224,7 +1264,8 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
             } else {
                 fail |= poll_pair_sum<1>(g_tk.x_hm, 1u, tagof(tagb, l - 1u, kTHm), pb, plive, h);
             }
-            const float p0 = wave_limbs_dot<C::KBD>(make_float2(h.x * wn.x, h.y * wn.y), plive, pnb, scr, rb, row_live);
+            const float p0 = add_upper_half(
+                wave_limbs_dot<KB2>(make_float2(h.x * wn.x, h.y * wn.y), plive, pnb, scr, rb, row_live, jb, je));
             submark(mk, 0);
             // stage 2: y = d of block l - 1
             float2 a = make_float2(0.0f, 0.0f);
@@ -1234,7 +1275,8 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
                 fail |= poll_pair_sum<1>(g_tk.x_d, 1u, tagof(tagb, l - 1u, kTD), pb, plive, y);
                 submark(mk, 1);
                 a = make_float2(y.x * wp.x, y.y * wp.y);
-                p1 = wave_limbs_dot<C::KBD>(make_float2(a.x * wn.x, a.y * wn.y), plive, pnb, scr, rb, row_live);
+                p1 = add_upper_half(
+                    wave_limbs_dot<KB2>(make_float2(a.x * wn.x, a.y * wn.y), plive, pnb, scr, rb, row_live, jb, je));
                 syy = y.x * y.x + y.y * y.y;
                 saa = a.x * a.x + a.y * a.y;
                 sah = a.x * h.x + a.y * h.y;
@@ -1264,7 +1306,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
                 st_word(g_tk.x_h + 2u * pb, hn.x, tagof(tagb, l, kTH));
                 st_word(g_tk.x_h + 2u * pb + 1u, hn.y, tagof(tagb, l, kTH));
             }
-            if (wave == 0u && row_live) {   // row v0 + lane: rms(h') * (rms(y) * P1 + P0), partials in wave order
+            if (wave == 0u && lane < v1 - v0) {   // row v0 + lane: rms(h') * (rms(y) * P1 + P0), partials in wave order
                 float q0[kWaves], q1[kWaves];
 #pragma unroll
                 for (uint32_t k = 0; k < kWaves; ++k) {
@@ -1939,8 +1981,8 @@ int tk_setup(vrt_g3* g) {
     // 32-element block of g per workgroup)
     struct Caps { uint32_t a, b, kbd, e; };
     Caps caps{};
-    if (d == 640) caps = Caps{64u, kWaves * 8u, 3u, kWaves * 1u * 2u};
-    else caps = Caps{64u, kWaves * 32u, 1u, kWaves * 8u * 1u};
+    if (d == 640) caps = Caps{32u, kWaves * 8u, 3u, kWaves * 1u * 2u};
+    else caps = Caps{32u, kWaves * 32u, 1u, kWaves * 8u * 1u};
     if (max_lines(nqkv, ts) > caps.a || max_lines(d, ts / H) > caps.b || F / 32u > ts ||
         (d / 32u + kWaves - 1u) / kWaves > caps.kbd || max_lines(d, ts) > caps.e)
         return VRT_OK;
