@@ -406,9 +406,8 @@ __device__ __forceinline__ float wave_sum8_t(const float (&v)[8]) {
     for (int i = 0; i < 2; ++i) b[i] = (b1 ? a[i + 2] : a[i]) + dpp_mov<0x4E>(b1 ? a[i] : a[i + 2]);    // quad_perm [2,3,0,1]
     float c = (b0 ? b[1] : b[0]) + dpp_mov<0xB1>(b0 ? b[0] : b[1]);                                    // quad_perm [1,0,3,2]
     c += dpp_mov<0x128>(c);   // row_ror:8
-    c += swz_xor16(c);
-    c += __shfl_xor(c, 32);
-    return c;
+    c = add_xor16(c);
+    return add_xor32(c);
 }
 
 // Polls 16-byte units (two tagged words each) at byte offsets off[k] of r until both tags of

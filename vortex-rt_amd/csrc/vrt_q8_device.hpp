@@ -31,9 +31,17 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-__device__ __forceinline__ float swz_xor16(float v) {
-    // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10 (within 32 lanes).
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+// v(lane) + v(lane ^ 16) on the VALU: v_permlane16_swap exchanges the odd 16-lane rows of one
+// copy with the even rows of the other, so the two results hold both rows of each pair.
+__device__ __forceinline__ float add_xor16(float v) {
+    const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+}
+
+// v(lane) + v(lane ^ 32) on the VALU, the same way with v_permlane32_swap (wave halves).
+__device__ __forceinline__ float add_xor32(float v) {
+    const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
 }
 
 // Sum over each aligned group of S lanes (S a power of two <= 64). Every lane of a group
@@ -45,7 +53,7 @@ __device__ __forceinline__ float slot_sum(float v) {
     if constexpr (S >= 4) v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
     if constexpr (S >= 8) v += dpp_mov<0x141>(v);   // row_half_mirror
     if constexpr (S >= 16) v += dpp_mov<0x140>(v);  // row_mirror
-    if constexpr (S >= 32) v += swz_xor16(v);
+    if constexpr (S >= 32) v = add_xor16(v);
     return v;
 }
 

@@ -337,9 +337,8 @@ __device__ __forceinline__ float wave_sum8_t(const float (&v)[8]) {
     for (int i = 0; i < 2; ++i) b[i] = (b1 ? a[i + 2] : a[i]) + dpp_mov<0x4E>(b1 ? a[i] : a[i + 2]);    // quad_perm [2,3,0,1]
     float c = (b0 ? b[1] : b[0]) + dpp_mov<0xB1>(b0 ? b[0] : b[1]);                                    // quad_perm [1,0,3,2]
     c += dpp_mov<0x128>(c);   // row_ror:8
-    c += swz_xor16(c);
-    c += __shfl_xor(c, 32);
-    return c;
+    c = add_xor16(c);
+    return add_xor32(c);
 }
 
 // ---- trace -------------------------------------------------------------------------------------
@@ -1108,15 +1107,6 @@ __device__ __forceinline__ void rowk_load_half(RowFn&& rowp, uint32_t nblk, cons
         if (v < v1 && jb + static_cast<uint32_t>(jj) < je) q8_load(rp + 34u * (b0 + jb + static_cast<uint32_t>(jj)), end, rb.raw[jj]);
 }
 
-// Lanes l < 32: this lane's partial plus the one of lane l + 32. v_permlane32_swap exchanges the
-// upper 32 lanes of one copy of v with the lower 32 lanes of another, so the two results hold v[l]
-// and v[l + 32] in lane l (l < 32); fp addition is commutative, so their sum is the same bits
-// whichever result holds which.
-__device__ __forceinline__ float add_upper_half(float v) {
-    const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
-}
-
 // Polls this lane's pair of the ny (<= NY) tagged d-vectors src[q d ..] and sums them in order q.
 template <int NY>
 __device__ __forceinline__ int poll_pair_sum(const u64* src, uint32_t ny, uint32_t tag, uint32_t pb, bool live,
@@ -1264,7 +1254,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
             } else {
                 fail |= poll_pair_sum<1>(g_tk.x_hm, 1u, tagof(tagb, l - 1u, kTHm), pb, plive, h);
             }
-            const float p0 = add_upper_half(
+            const float p0 = add_xor32(
                 wave_limbs_dot<KB2>(make_float2(h.x * wn.x, h.y * wn.y), plive, pnb, scr, rb, row_live, jb, je));
             submark(mk, 0);
             // stage 2: y = d of block l - 1
@@ -1275,7 +1265,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
                 fail |= poll_pair_sum<1>(g_tk.x_d, 1u, tagof(tagb, l - 1u, kTD), pb, plive, y);
                 submark(mk, 1);
                 a = make_float2(y.x * wp.x, y.y * wp.y);
-                p1 = add_upper_half(
+                p1 = add_xor32(
                     wave_limbs_dot<KB2>(make_float2(a.x * wn.x, a.y * wn.y), plive, pnb, scr, rb, row_live, jb, je));
                 syy = y.x * y.x + y.y * y.y;
                 saa = a.x * a.x + a.y * a.y;
