@@ -66,18 +66,17 @@ public:
 
     [[nodiscard]] const Gemma3Config& config() const noexcept { return config_; }
 
-    // Lane and fusion policy (src/gemma3.cpp:94-172, :656-671). In this library both are
-    // structural rather than tunable: every Q/K/V projection is one fused phase (one launch on
-    // the multi-kernel path) and every gate/up pair one phase with the GELU product fused in, so
-    // fusion is always on and set_projection_fusion_enabled() leaves it on; matvec row slots
-    // are sized per matrix from its block count (input_dim / 32 rounded up to a power of two,
-    // wave64), so narrow_q8_lane_count() reports the slot width the narrow projections
-    // (input_dim <= 1024) actually run with, whatever q8_lane_override requested (the override is
-    // validated as the reference validates it).
-    [[nodiscard]] bool projection_fusion_enabled() const noexcept { return true; }
-    void set_projection_fusion_enabled(bool) noexcept {}
-    [[nodiscard]] std::uint32_t narrow_q8_lane_count() const noexcept { return narrow_lanes_; }
-    [[nodiscard]] bool fused_ffn_enabled() const noexcept { return true; }
+    // Lane and fusion policy (src/gemma3.cpp:94-172, :656-671). Fusion is on by default (the
+    // reference's rule for GPU devices); off, every step runs the unfused sequence: q, k, v, gate
+    // and up as separate matvec launches and the GELU product as its own launch
+    // (:1529-1541, :1783-1847). A q8_lane_override of 8, 16, 32 or 64 runs the projections'
+    // rows in slots of that many lanes (a 2048-input row needs at least 16); 0 sizes the slots
+    // per matrix. narrow_q8_lane_count() reports the lanes per row the embedding-width
+    // projections run with. Neither setting changes results beyond the parity tolerances.
+    [[nodiscard]] bool projection_fusion_enabled() const noexcept;
+    void set_projection_fusion_enabled(bool enabled) noexcept;
+    [[nodiscard]] std::uint32_t narrow_q8_lane_count() const noexcept;
+    [[nodiscard]] bool fused_ffn_enabled() const noexcept { return projection_fusion_enabled(); }
 
     // reset_cache(); decode_token(token_id, 0, top_k); reset_cache() (src/gemma3.cpp:1884-1893).
     [[nodiscard]] Gemma3SingleTokenResult run_single_token(std::uint32_t token_id, std::size_t top_k = 8);
@@ -111,7 +110,6 @@ private:
     GgufFile gguf_;
     DeviceContext& context_;
     Gemma3Config config_{};
-    std::uint32_t narrow_lanes_ = 32;
     std::unique_ptr<Buffer> weights_arena_;
     vrt_g3* g3_ = nullptr;
     std::unique_ptr<Gemma3Tokenizer> tokenizer_;

@@ -257,6 +257,21 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
  * is available for the shape and device (value ignored). No reference counterpart. */
 #define VRT_G3_OPT_TEAM 6
 #define VRT_G3_OPT_QUERY_TEAM 7
+/* Projection fusion and the Q8 lane policy (Gemma3Model::set_projection_fusion_enabled and the
+ * q8_lane_override of its constructor, src/gemma3.cpp:94-172, :656-671). FUSION 1 (default): the
+ * fused sequence (the persistent kernels, or on the multi-kernel path one q|k|v launch and one
+ * gate/up launch with the GELU product in its epilogue, as run_q8_triplet / the fused FFN);
+ * 0: every step runs the multi-kernel sequence with q, k, v, gate and up as launches of their
+ * own and the GELU product as a launch after them (:1529-1541, :1783-1847). Q8_LANES 0
+ * (default): row slots sized per matrix; 8, 16, 32 or 64: the projections' rows run in slots of
+ * that many lanes on the multi-kernel path (a 2048-input row needs at least 16), like the
+ * reference's forced narrow pipeline; other values fail as the reference's constructor does.
+ * Both change only the schedule: results agree to the stated tolerances. Either setting drops
+ * the captured step graph. QUERY_Q8_LANES (read with vrt_g3_get_option) gives the lanes per row
+ * the embedding-width projections run with. */
+#define VRT_G3_OPT_FUSION 8
+#define VRT_G3_OPT_Q8_LANES 9
+#define VRT_G3_OPT_QUERY_Q8_LANES 10
 
 /* Phase trace of the last persistent launch (tracing tool; no reference counterpart, which
  * only has CLI wall timers, src/gemma_main.cpp:194-232): out[w * slots + k] is the
@@ -275,6 +290,10 @@ int vrt_g3_read_trace(vrt_g3* g3, uint64_t* out, uint64_t cap, uint32_t* nwg, ui
  * partials. *n receives the word count; synchronises the context's stream. */
 int vrt_g3_read_exchange(vrt_g3* g3, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
+/* Current value of an executor option: USE_GRAPH, PERSISTENT, TEAM, KV_F16, FUSION and Q8_LANES
+ * as last set, QUERY_Q8_LANES as described above (the getters projection_fusion_enabled and
+ * narrow_q8_lane_count of include/vortexrt/gemma3.hpp read these). */
+int vrt_g3_get_option(vrt_g3* g3, uint32_t option, uint32_t* value);
 
 /* Batched greedy decode: up to max_seqs independent sequences share the executor's weights, each
  * with its own KV cache of max_ctx positions (<= context_length). The reference decodes one

@@ -88,3 +88,21 @@ def test_cli_generation_from_bos_and_errors(tiny_model, tmp_path):
     assert err.startswith("vortexrt-gemma: ")
     _, err = _cli(tiny_model, "--q8-lanes", 12, rc=1)
     assert "--q8-lanes" in err
+
+
+@pytest.mark.parametrize("lanes,fusion", [(64, "off"), (32, "off"), (16, "off"), (8, "off"), (8, "on")])
+def test_cli_lane_fusion_loop(tiny_model, lanes, fusion):
+    """The reference CI's lane x fusion loop (.github/workflows/build.yml:105-123): every lane
+    width with projection fusion off, then 8 lanes with it on. The report states the policy that
+    ran, and the generated ids are the oracle's."""
+    out, _ = _cli(tiny_model, "--q8-lanes", lanes, "--projection-fusion", fusion, "--generate", 4)
+    assert "Validation: OK" in out
+    on = fusion == "on"
+    assert f"Narrow Q8 kernel: {lanes} lanes" in out        # 4 blocks per row: every width is instantiated
+    assert f"Projection fusion: {'enabled' if on else 'disabled'}" in out
+    assert f"Fused FFN: {'enabled' if on else 'disabled'}" in out
+    m = oracle.Model(tiny_model)
+    want = m.generate(np.array([2], np.uint32), 4).tolist()
+    m.close()
+    got = [int(x) for x in re.search(r"Generated token ids:((?: \d+)*)\n", out).group(1).split()]
+    assert got == want

@@ -183,6 +183,56 @@ def test_persistent_matches_multikernel(ctx, tiny_model):
     assert np.array_equal(p1, p2)
 
 
+def test_unfused_sequence_equals_fused(ctx, tiny_model):
+    """Projection fusion off runs q, k, v, gate and up as launches of their own and the GELU
+    product as a launch after them (src/gemma3.cpp:1529-1541, :1783-1847). Each row is computed
+    as in the fused multi-kernel step, so a teacher-forced run gives bit-identical greedy
+    results; the option reads back and switching it drops nothing else."""
+    g = vrt.Gemma3(ctx, tiny_model)
+    toks = synth.uniform_ids(5, 40, 2, 1000)
+    g.set_persistent(False)
+    a = g.forced(toks, 0)
+    g.set_persistent(True)
+    g.set_fusion(False)
+    assert g.get_option(vrt.OPT_FUSION) == 0
+    b = g.forced(toks, 0)
+    g.set_fusion(True)
+    c = g.forced(toks, 0)   # back on the persistent kernels
+    g.close()
+    assert np.array_equal(a["index"], b["index"]) and np.array_equal(a["value"], b["value"])
+    assert np.array_equal(a["index"], c["index"])
+
+
+CI_LANE_FUSION = [(64, False), (32, False), (16, False), (8, False), (8, True)]
+
+
+def test_full_shape_lane_fusion_loop(ctx, full_model):
+    """The reference CI's lane x fusion loop (.github/workflows/build.yml:105-123) at the 270M
+    shape: each lane width with fusion off, then 8 lanes with it on. The embedding-width
+    projections run with the requested lanes (20 blocks per row: 3 blocks per lane at 8), and
+    the greedy tokens equal the oracle's."""
+    g = vrt.Gemma3(ctx, full_model)
+    prompt = synth.uniform_ids(0, 8, 2, 262144)
+    m = oracle.Model(full_model)
+    ref = m.generate(prompt, 4)
+    m.close()
+    auto = g.q8_lanes()
+    for lanes, fusion in CI_LANE_FUSION:
+        print(f"[g3] lanes {lanes} fusion {fusion}", flush=True)
+        g.set_q8_lanes(lanes)
+        g.set_fusion(fusion)
+        assert g.q8_lanes() == lanes and g.get_option(vrt.OPT_Q8_LANES) == lanes
+        got = g.generate(prompt, 4)
+        assert np.array_equal(got, ref), (lanes, fusion, got, ref)
+    with pytest.raises(vrt.VrtError):
+        g.set_q8_lanes(12)
+    g.set_q8_lanes(0)
+    g.set_fusion(True)
+    assert g.q8_lanes() == auto
+    assert np.array_equal(g.generate(prompt, 4), ref)
+    g.close()
+
+
 def test_persistent_split_launches(ctx, tiny_model):
     """A generation split over several persistent launches equals one launch."""
     g = vrt.Gemma3(ctx, tiny_model)

@@ -70,13 +70,6 @@ Gemma3Model::Gemma3Model(const std::string& gguf_path, DeviceContext& context, c
         emb.dimensions[1] > std::numeric_limits<std::uint32_t>::max())
         throw std::runtime_error("Unsupported token_embd.weight layout");
     config_.vocab_size = static_cast<std::uint32_t>(emb.dimensions[1]);
-    {   // row-slot width of the narrow projections (input_dim = embedding_length): blocks rounded up to 2^k
-        const std::uint32_t blocks = std::max(1u, config_.embedding_length / 32u);
-        std::uint32_t lanes = 1;
-        while (lanes < blocks && lanes < 64u) lanes <<= 1;
-        narrow_lanes_ = lanes;
-    }
-
     // the tokenizer index (src/gemma3.cpp:289-454): incomplete metadata fails the load
     tokenizer_ = std::make_unique<Gemma3Tokenizer>(gguf_, config_.vocab_size);
     tokenizer_bos_id_ = tokenizer_->bos_id();
@@ -142,10 +135,30 @@ Gemma3Model::Gemma3Model(const std::string& gguf_path, DeviceContext& context, c
     d.layers = layers.data();
     d.eos_token_id = tokenizer_eos_id_;
     check_vrt(vrt_g3_create(context_.handle(), &d, &g3_));
+    if (q8_lane_override != 0u && vrt_g3_set_option(g3_, VRT_G3_OPT_Q8_LANES, q8_lane_override) != VRT_OK) {
+        const std::string msg = vrt_last_error();   // the destructor does not run for a throwing constructor
+        vrt_g3_destroy(g3_);
+        g3_ = nullptr;
+        throw std::runtime_error(msg);
+    }
 }
 
 Gemma3Model::~Gemma3Model() {
     if (g3_) vrt_g3_destroy(g3_);
+}
+
+bool Gemma3Model::projection_fusion_enabled() const noexcept {
+    std::uint32_t v = 1;
+    return vrt_g3_get_option(g3_, VRT_G3_OPT_FUSION, &v) != VRT_OK || v != 0u;
+}
+
+void Gemma3Model::set_projection_fusion_enabled(bool enabled) noexcept {
+    (void)vrt_g3_set_option(g3_, VRT_G3_OPT_FUSION, enabled ? 1u : 0u);
+}
+
+std::uint32_t Gemma3Model::narrow_q8_lane_count() const noexcept {
+    std::uint32_t v = 0;
+    return vrt_g3_get_option(g3_, VRT_G3_OPT_QUERY_Q8_LANES, &v) == VRT_OK ? v : 0u;
 }
 
 void Gemma3Model::reset_cache() { check_vrt(vrt_g3_reset(g3_)); }

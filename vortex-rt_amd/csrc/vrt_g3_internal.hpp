@@ -44,6 +44,7 @@ struct G3Params {
     float* part;
     float* o;
     float* g;
+    float* gu;            // [2F] raw gate and up rows of the unfused sequence (VRT_G3_OPT_FUSION 0)
     float* f;
     float* hidden;
     float* logits;
@@ -70,6 +71,8 @@ struct LaunchDesc {
     const void* fn;
     uint32_t grid;
     size_t smem;
+    uint32_t per_wg;   // rows per workgroup
+    uint32_t S;        // row-slot width (lanes per row)
 };
 
 struct MkState;   // persistent decode kernel: exchange buffers and launch shape (vrt_decode.hip)
@@ -141,6 +144,8 @@ struct vrt_g3 {
     vrt_argmax_result* host_res = nullptr;
     uint32_t next_pos = 0;
     bool use_graph = true;
+    bool fusion = true;          // projection fusion (VRT_G3_OPT_FUSION)
+    uint32_t q8_lanes = 0;       // row-slot width request of the projections, 0 = auto (VRT_G3_OPT_Q8_LANES)
     bool use_persistent = true;  // one cooperative launch per batch of steps (vrt_decode.hip)
     bool mk_refused = false;     // the device refused a cooperative launch: multi-kernel steps
     vrt::MkState* mk = nullptr;

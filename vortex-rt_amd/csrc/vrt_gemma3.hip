@@ -112,8 +112,11 @@ __device__ __forceinline__ void flag_nonfinite(const float (&h)[kMaxE], uint32_t
 // k_qkv
 // =========================================================================================
 
+// Rows [r_begin, r_end) of the virtual rows [Wq | Wk | Wv]: the whole range with projection fusion
+// (one launch, src/gemma3.cpp:1529-1541 run_q8_triplet), one matrix per launch without it.
 template <int S, int NB, int U>
-__global__ void __launch_bounds__(kThreads) k_qkv(G3Params P, LayerParams Lc, const float* prev_post_ffw, uint32_t layer) {
+__global__ void __launch_bounds__(kThreads) k_qkv(G3Params P, LayerParams Lc, const float* prev_post_ffw, uint32_t layer,
+                                                  uint32_t r_begin, uint32_t r_end) {
 #pragma clang fp contract(off)
     __shared__ double red[8];
     if (P.st->stop) return;
@@ -157,8 +160,8 @@ __global__ void __launch_bounds__(kThreads) k_qkv(G3Params P, LayerParams Lc, co
         return b;
     };
     constexpr uint32_t per_wg = (64u / S) * 4u * U;
-    const uint32_t v0 = blockIdx.x * per_wg;
-    const uint32_t v1 = min(total, v0 + per_wg);
+    const uint32_t v0 = r_begin + blockIdx.x * per_wg;
+    const uint32_t v1 = min(min(total, r_end), v0 + per_wg);
     RowBatch<S, NB, U> batch;
     batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, blockDim.x >> 6, batch);
 
@@ -405,8 +408,11 @@ __device__ __forceinline__ float gelu_tanh_g3(float x) {
     return 0.5f * x * (1.0f + tanhf(kSqrt2OverPi * (x + kCubic * cubic)));
 }
 
+// mode 0 (projection fusion): gate/up row pairs with gelu_tanh(gate) * up in the epilogue, as
+// run_q8_pair + gelu_mul. mode 1 / 2: the rows of gate / up alone into P.gu[0, F) / P.gu[F, 2F)
+// (the unfused sequence, src/gemma3.cpp:1820-1847: separate matvecs, then k_gelu_mul).
 template <int S, int NB, int U>
-__global__ void __launch_bounds__(kThreads) k_gateup(G3Params P, LayerParams Lc) {
+__global__ void __launch_bounds__(kThreads) k_gateup(G3Params P, LayerParams Lc, uint32_t mode) {
 #pragma clang fp contract(off)
     __shared__ double red[8];
     if (P.st->stop) return;
@@ -419,12 +425,18 @@ __global__ void __launch_bounds__(kThreads) k_gateup(G3Params P, LayerParams Lc)
     load_vec(P.hres, d, rb);
     load_vec(Lc.post_attn, d, rw);
     load_vec(Lc.ffn_norm, d, rw2);
-    // virtual row v: row v>>1 of gate (v even) or up (v odd)
-    const uint8_t *wg = Lc.wg, *wu = Lc.wu;
-    auto rowp = [=](uint32_t v) { return ((v & 1u) ? wu : wg) + static_cast<uint64_t>(v >> 1) * row_bytes; };
+    // mode 0: virtual row v is row v>>1 of gate (v even) or up (v odd); else row v of one matrix
+    // (offsets from wg, so that no pointer is selected per row)
+    const uint8_t* wg = Lc.wg;
+    const int64_t up_off = Lc.wu - Lc.wg;
+    const uint32_t pair = mode == 0u ? 1u : 0u, fixed_up = mode == 2u ? 1u : 0u;
+    auto rowp = [=](uint32_t v) {
+        const uint32_t is_up = pair ? (v & 1u) : fixed_up;
+        return wg + (is_up ? up_off : 0) + static_cast<int64_t>(static_cast<uint64_t>(v >> pair) * row_bytes);
+    };
     constexpr uint32_t per_wg = (64u / S) * 4u * U;   // even: gate/up pairs stay together
     const uint32_t v0 = blockIdx.x * per_wg;
-    const uint32_t v1 = min(2u * P.F, v0 + per_wg);
+    const uint32_t v1 = min(mode == 0u ? 2u * P.F : P.F, v0 + per_wg);
     RowBatch<S, NB, U> batch;
     batch_load<S, NB, U>(rowp, nblk, P.arena_end, v0, v1, threadIdx.x >> 6, blockDim.x >> 6, batch);
 
@@ -445,6 +457,11 @@ __global__ void __launch_bounds__(kThreads) k_gateup(G3Params P, LayerParams Lc)
     build_limbs(m.xs, d, m.L, blockDim.x >> 6);
     XLimb xl[NB];
     lane_limbs<S, NB>(m.L, nblk, xl);
+    if (mode != 0u) {
+        float* raw = P.gu + (mode - 1u) * P.F;
+        batch_consume<S, NB, U>(batch, nblk, xl, [&](uint32_t v, float val) { raw[v] = val; });
+        return;
+    }
     float* gu = m.extra;
     batch_consume<S, NB, U>(batch, nblk, xl, [&](uint32_t v, float val) { gu[v - v0] = val; });
     __syncthreads();
@@ -453,6 +470,14 @@ __global__ void __launch_bounds__(kThreads) k_gateup(G3Params P, LayerParams Lc)
         const uint32_t j = (r - r0) * 2u;
         P.g[r] = gelu_tanh_g3(gu[j]) * gu[j + 1u];                                   // gelu_mul.comp:23-31
     }
+}
+
+// The GELU product of the unfused sequence: g = gelu_tanh(gate) * up over P.gu.
+__global__ void __launch_bounds__(kThreads) k_gelu_mul(G3Params P) {
+#pragma clang fp contract(off)
+    if (P.st->stop) return;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < P.F; i += gridDim.x * blockDim.x)
+        P.g[i] = gelu_tanh_g3(P.gu[i]) * P.gu[P.F + i];                              // gelu_mul.comp:23-31
 }
 
 // =========================================================================================
@@ -613,13 +638,14 @@ __global__ void __launch_bounds__(kThreads) k_lm_final(G3Params P, uint32_t npar
 
 // ---- dispatch -------------------------------------------------------------------------------
 
+// (lanes per row, blocks per lane) instantiated for every kernel kind, and the extra ones the
+// projections take under a row-slot width request (VRT_G3_OPT_Q8_LANES)
 #define VRT_SHAPES(X) X(1, 1) X(2, 1) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2)
+#define VRT_LANE_SHAPES(X) X(8, 2) X(8, 3) X(8, 4) X(16, 2) X(16, 3) X(16, 4) X(32, 2)
 
 enum KernelKind { KQKV, KO, KGATEUP, KDOWN, KLM };
 
-
-
-template <int S, int NB>
+template <int S, int NB, bool LM>
 static LaunchDesc pick(KernelKind kind, uint32_t rows, uint32_t K, uint32_t extra_per_wg) {
     constexpr uint32_t rpw = 64u / S;
     LaunchDesc ld{};
@@ -628,23 +654,66 @@ static LaunchDesc pick(KernelKind kind, uint32_t rows, uint32_t K, uint32_t extr
     case KO: ld.fn = reinterpret_cast<const void*>(&k_o<S, NB, 1>); break;
     case KGATEUP: ld.fn = reinterpret_cast<const void*>(&k_gateup<S, NB, 1>); break;
     case KDOWN: ld.fn = reinterpret_cast<const void*>(&k_down<S, NB, 1>); break;
-    case KLM: ld.fn = reinterpret_cast<const void*>(&k_lm<S, NB, (S >= 16 ? 4 : 1)>); break;
+    case KLM:
+        if constexpr (LM) ld.fn = reinterpret_cast<const void*>(&k_lm<S, NB, (S >= 16 ? 4 : 1)>);
+        break;
     }
     const uint32_t per_wg = rpw * 4u;
+    ld.per_wg = per_wg;
+    ld.S = S;
     ld.grid = (rows + per_wg - 1u) / per_wg;
     ld.smem = mv_smem_bytes(K, extra_per_wg ? per_wg : 0u);
     return ld;
 }
 
-static bool pick_shape(KernelKind kind, uint32_t rows, uint32_t K, LaunchDesc* out) {
-    MvShape sh;
-    if (!mv_shape(K, &sh) || sh.NB > 2) return false;
+// Row-slot shape of a projection with K inputs. lanes = 0: the shape sized from K (mv_shape).
+// lanes = 8..64: slots of `lanes` lanes, each lane taking ceil(blocks / lanes) blocks of a row;
+// where that exceeds the instantiated blocks per lane the slot widens (a 2048-input row over
+// 8 lanes runs with 16).
+static bool pick_shape(KernelKind kind, uint32_t rows, uint32_t K, LaunchDesc* out, uint32_t lanes = 0) {
     const uint32_t extra = kind == KGATEUP ? 1u : 0u;
+    MvShape sh;
+    if (lanes == 0u || kind == KLM) {
+        if (!mv_shape(K, &sh) || sh.NB > 2) return false;
+    } else {
+        const uint32_t nblk = (K + 31u) / 32u;
+        sh.S = 0;
+        for (uint32_t w = lanes; w <= 64u && sh.S == 0; w *= 2u) {
+            const uint32_t nb = (nblk + w - 1u) / w;
+            if (nb <= (w >= 32u ? 2u : 4u)) { sh.S = static_cast<int>(w); sh.NB = static_cast<int>(nb); }
+        }
+        if (sh.S == 0) return false;
+    }
 #define VRT_PICK(s_, nb_) \
-    if (sh.S == s_ && sh.NB == nb_) { *out = pick<s_, nb_>(kind, rows, K, extra); return true; }
+    if (sh.S == s_ && sh.NB == nb_) { *out = pick<s_, nb_, true>(kind, rows, K, extra); return true; }
     VRT_SHAPES(VRT_PICK)
 #undef VRT_PICK
+#define VRT_PICK(s_, nb_) \
+    if (kind != KLM && sh.S == s_ && sh.NB == nb_) { *out = pick<s_, nb_, false>(kind, rows, K, extra); return true; }
+    VRT_LANE_SHAPES(VRT_PICK)
+#undef VRT_PICK
     return false;
+}
+
+// The projection kernels' shapes for the executor's row-slot request; drops a captured graph.
+static int g3_pick_projections(vrt_g3* g) {
+    const uint32_t d = g->cfg.embedding_length, H = g->cfg.head_count, hd = g->cfg.head_dim;
+    const uint32_t F = g->cfg.feed_forward_length, lanes = g->q8_lanes;
+    LaunchDesc qkv, o, gu, down;
+    if (!pick_shape(KQKV, H * hd + 2u * hd, d, &qkv, lanes) || !pick_shape(KO, d, H * hd, &o, lanes) ||
+        !pick_shape(KGATEUP, 2u * F, d, &gu, lanes) || !pick_shape(KDOWN, d, F, &down, lanes))
+        return set_error(VRT_ERR_INVALID, "no kernel shape for this Gemma 3 configuration");
+    for (const LaunchDesc* ld : {&qkv, &o, &gu, &down})
+        VRT_HIP_CHECK(hipFuncSetAttribute(ld->fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(ld->smem)));
+    g->ld_qkv = qkv;
+    g->ld_o = o;
+    g->ld_gateup = gu;
+    g->ld_down = down;
+    if (g->graph) {
+        (void)hipGraphExecDestroy(g->graph);
+        g->graph = nullptr;
+    }
+    return VRT_OK;
 }
 
 }  // namespace vrt
@@ -677,15 +746,29 @@ static int g3_upload(vrt_g3* g, const void* host, size_t bytes, const float** ou
     return VRT_OK;
 }
 
-// Enqueues one decode step's kernels on `stream`.
+// Enqueues one decode step's kernels on `stream`. With projection fusion a block is q|k|v,
+// attention, O, gate/up with the GELU product, down; without it q, k and v, and gate and up, are
+// launches of their own and the GELU product a launch after them (src/gemma3.cpp:1529-1541,
+// :1783-1847).
 static int g3_enqueue_step(vrt_g3* g, hipStream_t stream) {
     const uint32_t L = g->cfg.block_count;
+    const uint32_t qw = g->cfg.head_count * g->cfg.head_dim, hd = g->cfg.head_dim, F = g->cfg.feed_forward_length;
+    auto grid = [](const LaunchDesc& ld, uint32_t rows) { return dim3((rows + ld.per_wg - 1u) / ld.per_wg); };
     for (uint32_t l = 0; l < L; ++l) {
         LayerParams& Lc = g->layers[l];
         const float* prev_post = l ? g->layers[l - 1].post_ffw : nullptr;
-        {
-            void* args[] = {&g->P, &Lc, &prev_post, &l};
-            VRT_HIP_CHECK(hipLaunchKernel(g->ld_qkv.fn, dim3(g->ld_qkv.grid), dim3(kThreads), args, g->ld_qkv.smem, stream));
+        if (g->fusion) {
+            uint32_t r0 = 0, r1 = qw + 2u * hd;
+            void* args[] = {&g->P, &Lc, &prev_post, &l, &r0, &r1};
+            VRT_HIP_CHECK(hipLaunchKernel(g->ld_qkv.fn, grid(g->ld_qkv, r1), dim3(kThreads), args, g->ld_qkv.smem, stream));
+        } else {
+            const uint32_t cut[4] = {0u, qw, qw + hd, qw + 2u * hd};
+            for (int m = 0; m < 3; ++m) {
+                uint32_t r0 = cut[m], r1 = cut[m + 1];
+                void* args[] = {&g->P, &Lc, &prev_post, &l, &r0, &r1};
+                VRT_HIP_CHECK(hipLaunchKernel(g->ld_qkv.fn, grid(g->ld_qkv, r1 - r0), dim3(kThreads), args, g->ld_qkv.smem,
+                                              stream));
+            }
         }
         {
             void* args[] = {&g->P, &Lc};
@@ -699,7 +782,24 @@ static int g3_enqueue_step(vrt_g3* g, hipStream_t stream) {
         {
             void* args[] = {&g->P, &Lc};
             VRT_HIP_CHECK(hipLaunchKernel(g->ld_o.fn, dim3(g->ld_o.grid), dim3(kThreads), args, g->ld_o.smem, stream));
-            VRT_HIP_CHECK(hipLaunchKernel(g->ld_gateup.fn, dim3(g->ld_gateup.grid), dim3(kThreads), args, g->ld_gateup.smem, stream));
+        }
+        if (g->fusion) {
+            uint32_t mode = 0;
+            void* args[] = {&g->P, &Lc, &mode};
+            VRT_HIP_CHECK(hipLaunchKernel(g->ld_gateup.fn, grid(g->ld_gateup, 2u * F), dim3(kThreads), args,
+                                          g->ld_gateup.smem, stream));
+        } else {
+            for (uint32_t mode = 1; mode <= 2u; ++mode) {
+                void* args[] = {&g->P, &Lc, &mode};
+                VRT_HIP_CHECK(hipLaunchKernel(g->ld_gateup.fn, grid(g->ld_gateup, F), dim3(kThreads), args,
+                                              g->ld_gateup.smem, stream));
+            }
+            void* args[] = {&g->P};
+            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_gelu_mul), dim3((F + kThreads - 1u) / kThreads),
+                                          dim3(kThreads), args, 0, stream));
+        }
+        {
+            void* args[] = {&g->P, &Lc};
             VRT_HIP_CHECK(hipLaunchKernel(g->ld_down.fn, dim3(g->ld_down.grid), dim3(kThreads), args, g->ld_down.smem, stream));
         }
     }
@@ -738,7 +838,9 @@ static int g3_capture(vrt_g3* g) {
 // (vrt_decode.hip); both read and leave the same step state, KV cache and token buffer.
 static int g3_run_steps(vrt_g3* g, uint32_t n, uint32_t first) {
     hipStream_t s = g->ctx->stream;
-    if ((g->mk || g->tk) && g->use_persistent) {
+    // the persistent kernels are the fused sequence at their own row-slot widths: a request for
+    // the unfused sequence or for a slot width runs the multi-kernel steps
+    if ((g->mk || g->tk) && g->use_persistent && g->fusion && g->q8_lanes == 0u) {
         uint32_t done = 0;
         const uint32_t lim = g->use_team ? tk_pos_limit(g) : 0u;
         int rc = VRT_OK;
@@ -893,6 +995,8 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
     P.att = static_cast<float*>(p);
     if (int rc = g3_alloc(g, F * 4u, &p)) return fail(rc);
     P.g = static_cast<float*>(p);
+    if (int rc = g3_alloc(g, 2u * F * 4u, &p)) return fail(rc);
+    P.gu = static_cast<float*>(p);
     if (int rc = g3_alloc(g, static_cast<size_t>(c.vocab_size) * 4u, &p)) return fail(rc);
     P.logits = static_cast<float*>(p);
 
@@ -955,9 +1059,8 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
     P.part = static_cast<float*>(p);
 
     // kernel shapes
-    if (!pick_shape(KQKV, H * hd + 2u * hd, d, &g->ld_qkv) || !pick_shape(KO, d, H * hd, &g->ld_o) ||
-        !pick_shape(KGATEUP, 2u * F, d, &g->ld_gateup) || !pick_shape(KDOWN, d, F, &g->ld_down) ||
-        !pick_shape(KLM, c.vocab_size, d, &g->ld_lm))
+    if (int rc = g3_pick_projections(g)) return fail(rc);
+    if (!pick_shape(KLM, c.vocab_size, d, &g->ld_lm))
         return fail(set_error(VRT_ERR_INVALID, "no kernel shape for this Gemma 3 configuration"));
     {
         // LM head: ~4 workgroups per CU, each a contiguous run of rows
@@ -973,8 +1076,7 @@ extern "C" int vrt_g3_create(vrt_ctx* ctx, const vrt_g3_desc* desc, vrt_g3** out
     }
     if (int rc = g3_alloc(g, static_cast<size_t>(g->ld_lm.grid) * sizeof(LmPartial), &p)) return fail(rc);
     P.lm_part = static_cast<LmPartial*>(p);
-    for (const LaunchDesc* ld : {&g->ld_qkv, &g->ld_o, &g->ld_gateup, &g->ld_down, &g->ld_lm})
-        VRT_HIP_CHECK(hipFuncSetAttribute(ld->fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(ld->smem)));
+    VRT_HIP_CHECK(hipFuncSetAttribute(g->ld_lm.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(g->ld_lm.smem)));
     {
         hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&g->host_ctl), sizeof(G3State), hipHostMallocDefault);
         if (e == hipSuccess)
@@ -1032,6 +1134,30 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
     case VRT_G3_OPT_TEAM: g->use_team = value != 0; return VRT_OK;
     case VRT_G3_OPT_QUERY_TEAM:
         return g->tk ? VRT_OK : set_error(VRT_ERR_STATE, "team decode kernel unavailable");
+    case VRT_G3_OPT_FUSION: {
+        const bool on = value != 0;
+        if (g->fusion == on) return VRT_OK;
+        VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+        g->fusion = on;
+        if (g->graph) {   // the captured sequence changes
+            (void)hipGraphExecDestroy(g->graph);
+            g->graph = nullptr;
+        }
+        return VRT_OK;
+    }
+    case VRT_G3_OPT_Q8_LANES: {
+        if (value != 0u && value != 8u && value != 16u && value != 32u && value != 64u)
+            return set_error(VRT_ERR_INVALID, "Q8 lane override must be 0, 8, 16, 32, or 64");   // src/gemma3.cpp:163-166
+        if (g->q8_lanes == value) return VRT_OK;
+        VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+        const uint32_t old = g->q8_lanes;
+        g->q8_lanes = value;
+        if (int rc = g3_pick_projections(g)) {
+            g->q8_lanes = old;
+            return rc;
+        }
+        return VRT_OK;
+    }
     case VRT_G3_OPT_KV_F16: {
         // the kernels read the flag from their parameter blocks: the captured graph (which holds
         // G3Params by value) is dropped, the persistent kernel's block re-uploaded, the cache reset
@@ -1047,6 +1173,25 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
         if (int rc = tk_set_kv_f16(g, on != 0)) return rc;
         return vrt_g3_reset(g);
     }
+    case VRT_G3_OPT_QUERY_Q8_LANES: return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_Q8_LANES is read with vrt_g3_get_option");
+    default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
+    }
+}
+
+extern "C" int vrt_g3_get_option(vrt_g3* g, uint32_t option, uint32_t* value) {
+    VRT_REQUIRE(g && value, "vrt_g3_get_option: null argument");
+    switch (option) {
+    case VRT_G3_OPT_USE_GRAPH: *value = g->use_graph ? 1u : 0u; return VRT_OK;
+    case VRT_G3_OPT_PERSISTENT: *value = g->use_persistent ? 1u : 0u; return VRT_OK;
+    case VRT_G3_OPT_TEAM: *value = g->use_team ? 1u : 0u; return VRT_OK;
+    case VRT_G3_OPT_KV_F16: *value = g->P.kv_f16; return VRT_OK;
+    case VRT_G3_OPT_FUSION: *value = g->fusion ? 1u : 0u; return VRT_OK;
+    case VRT_G3_OPT_Q8_LANES: *value = g->q8_lanes; return VRT_OK;
+    case VRT_G3_OPT_QUERY_Q8_LANES:
+        // lanes per row of the embedding-width (narrow) projections: the request, widened where a
+        // row has more blocks per lane than instantiated, or with 0 the width sized from d_model
+        *value = g->ld_qkv.S;
+        return VRT_OK;
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
     }
 }

@@ -23,6 +23,9 @@ OPT_TRACE = 4
 OPT_KV_F16 = 5
 OPT_TEAM = 6
 OPT_QUERY_TEAM = 7
+OPT_FUSION = 8
+OPT_Q8_LANES = 9
+OPT_QUERY_Q8_LANES = 10
 
 
 class VrtError(RuntimeError):
@@ -100,6 +103,7 @@ SIGNATURES = {
     "vrt_g3_collect": (_I, [_P, _P, C.POINTER(_U32)]),
     "vrt_g3_forced": (_I, [_P, _P, _U32, _U32, _P]),
     "vrt_g3_set_option": (_I, [_P, _U32, _U32]),
+    "vrt_g3_get_option": (_I, [_P, _U32, C.POINTER(_U32)]),
     "vrt_g3_time_lm_head": (_I, [_P, _U32, C.POINTER(_F)]),
     "vrt_g3_read_trace": (_I, [_P, _P, _U64, C.POINTER(_U32), C.POINTER(_U32)]),
     "vrt_g3_read_exchange": (_I, [_P, _U32, _P, _U64, C.POINTER(_U64)]),
@@ -389,6 +393,23 @@ class Gemma3:
 
     def set_trace(self, on: bool):
         check(lib().vrt_g3_set_option(self.h, OPT_TRACE, 1 if on else 0))
+
+    def get_option(self, option: int) -> int:
+        v = C.c_uint32()
+        check(lib().vrt_g3_get_option(self.h, option, C.byref(v)))
+        return int(v.value)
+
+    def set_fusion(self, on: bool):
+        """Projection fusion (default on); off runs the unfused multi-kernel sequence."""
+        check(lib().vrt_g3_set_option(self.h, OPT_FUSION, 1 if on else 0))
+
+    def set_q8_lanes(self, lanes: int):
+        """Row-slot width request of the projections: 0 (auto), 8, 16, 32 or 64."""
+        check(lib().vrt_g3_set_option(self.h, OPT_Q8_LANES, lanes))
+
+    def q8_lanes(self) -> int:
+        """Lanes per row the embedding-width projections run with."""
+        return self.get_option(OPT_QUERY_Q8_LANES)
 
     def set_kv_f16(self, on: bool):
         """fp16 KV cache (keys and values rounded to fp16 as they enter it); resets the cache."""
