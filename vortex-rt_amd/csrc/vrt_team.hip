@@ -83,7 +83,12 @@ constexpr uint32_t kLmUnits = 3;            // 16-byte LM-head loads per thread 
 constexpr uint32_t kLmRing = 4;             // LM-head tile slots in LDS
 constexpr uint32_t kLmAhead = kLmRing - 1u; // tiles in flight while one is computed
 constexpr uint32_t kLmTileBytes = kLmUnits * kThreads * 16u;
-constexpr uint32_t kLdsBytes = 144u * 1024u;
+// matrix-core LM head: every wave streams its own 8-row tiles through a ring of its own
+constexpr uint32_t kLmWaveRows = 8;
+constexpr uint32_t kLmWaveLoads = 6;        // 1 KB direct-to-LDS loads per wave tile
+constexpr uint32_t kLmWaveSlot = kLmWaveLoads * 1024u;
+constexpr uint32_t kLmWaveRing = 3;         // slots per wave: two tiles in flight while one is computed
+constexpr uint32_t kLdsBytes = 159u * 1024u;
 constexpr uint32_t kMaxLayers = 64;
 constexpr uint32_t kAnySets = 4;
 
@@ -625,9 +630,115 @@ __device__ __forceinline__ bool final_fold(uint32_t tagb, const FoldW& fw) {
     return !fail;
 }
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// The tied LM head on the matrix cores (v_mfma_i32_16x16x32_i8) for rows of NB Q8_0 blocks. Every
+// wave streams its own tiles of 8 rows (rows (w + i nwg) * 64 + 8 wave ..) into a ring of its own
+// with direct-to-LDS loads, so the loop has no workgroup barrier: a wave waits only for its own
+// loads. For block j the A operand holds the activation limbs block-diagonally: row m = 4 q + t of
+// A is limb t (t < 3) of x's block j when q = j % 4, and zero otherwise; the B operand is the 32
+// quants of row n & 7 (lane n + 16 g: quants 8 g .. 8 g + 7; columns 8-15 repeat rows 0-7). After
+// the blocks of group G (4G .. 4G + 3), C[4 q + t][n] is the limb-t dot product of block 4G + q
+// with row n, held by lane n + 16 q, which combines the three limb products as q8_dot does and
+// scales them by the block scales; the four lanes of a row then add their groups' sums.
+template <int NB, int EP2>
+__device__ __forceinline__ bool lm_waves(uint32_t tagb, uint32_t want_logits, bool tr, const FoldW& fw, float& bv,
+                                         uint32_t& bi) {
+#pragma clang fp contract(off)
+    constexpr uint32_t NG = (NB + 3) / 4;
+    constexpr uint32_t kRound = kWaves * kLmWaveRows;   // rows per workgroup round
+    const uint32_t w = blockIdx.x, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t n = lane & 15u, grp = lane >> 4;
+    const uint32_t nwg = g_tk.nwg, V = g_tk.V;
+    const uint32_t rb = static_cast<uint32_t>(NB) * 34u;
+    const uint64_t first = static_cast<uint64_t>(w) * kRound + wave * kLmWaveRows;
+    const uint64_t stride = static_cast<uint64_t>(kRound) * nwg;
+    const uint32_t nt = first < V ? static_cast<uint32_t>((V - first + stride - 1u) / stride) : 0u;
+    auto row0 = [&](uint32_t i) { return static_cast<uint32_t>(first + static_cast<uint64_t>(i) * stride); };
+    uint8_t* ring = lds<uint8_t>(g_tk.lds.ring) + wave * (kLmWaveRing * kLmWaveSlot);
+    auto slot = [&](uint32_t i) { return ring + (i % kLmWaveRing) * kLmWaveSlot; };
+    // rows [r0, r1) as the 16-byte units of their aligned span, unit u at slot byte 16 u; units past
+    // the span re-load its last unit (16 readable bytes follow the table). Non-temporal.
+    auto issue = [&](uint32_t i) {
+        const uint32_t r0 = row0(i), r1 = min(V, r0 + kLmWaveRows);
+        const uintptr_t s0 = reinterpret_cast<uintptr_t>(g_tk.tok_embd) + static_cast<uint64_t>(r0) * rb;
+        const uintptr_t a0 = s0 & ~uintptr_t(15);
+        const uint32_t n16 = static_cast<uint32_t>(((s0 - a0) + static_cast<uint64_t>(r1 - r0) * rb + 15u) / 16u);
+        uint8_t* dst = slot(i);
+#pragma unroll
+        for (uint32_t k = 0; k < kLmWaveLoads; ++k) {
+            const uint32_t u = lane + 64u * k;
+            __builtin_amdgcn_global_load_lds((const TK_AS_GLOBAL void*)(a0 + static_cast<uintptr_t>(u < n16 ? u : n16 - 1u) * 16u),
+                                             (__attribute__((address_space(3))) void*)(dst + 1024u * k), 16, 0, 2 /* nt */);
+        }
+    };
+#pragma unroll
+    for (uint32_t i = 0; i + 1u < kLmWaveRing; ++i)
+        if (i < nt) issue(i);
+    if (!final_fold<EP2>(tagb, fw)) return false;
+    stamp(tr, 2u * g_tk.L + 1u);
+    long aop[NB];
+    {
+        const uint32_t q = n >> 2, limb = n & 3u;
+        const int8_t* src = lds<int8_t>(limb == 0u ? g_tk.lds.la : (limb == 1u ? g_tk.lds.lb : g_tk.lds.lc));
+#pragma unroll
+        for (uint32_t j = 0; j < static_cast<uint32_t>(NB); ++j)
+            aop[j] = (q == (j & 3u) && limb < 3u) ? *reinterpret_cast<const long*>(src + 32u * j + 8u * grp) : 0;
+    }
+    float sx[NG];   // activation scale of this lane's block in each group
+    {
+        const float* ls = lds<float>(g_tk.lds.ls);
+#pragma unroll
+        for (uint32_t G = 0; G < NG; ++G) sx[G] = 4u * G + grp < static_cast<uint32_t>(NB) ? ls[4u * G + grp] : 0.0f;
+    }
+    const float inv254 = 1.0f / 254.0f, inv64516 = 1.0f / 64516.0f;
+    for (uint32_t i = 0; i < nt; ++i) {
+        // this wave's loads of tile i are complete: at most those of tile i + 1 are outstanding
+        static_assert(kLmWaveLoads <= 15u && kLmWaveRing == 3u, "vmcnt immediate");
+        if (i + 1u < nt) __builtin_amdgcn_s_waitcnt(0x0F70 | kLmWaveLoads);
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        // slot (i + 2) % 3 held tile i - 1, whose reads this wave has consumed
+        if (i + 2u < nt) issue(i + 2u);
+        const uint32_t r0 = row0(i);
+        const uint8_t* tile = slot(i);
+        const uint32_t pre = static_cast<uint32_t>((reinterpret_cast<uintptr_t>(g_tk.tok_embd) + static_cast<uint64_t>(r0) * rb) & 15u);
+        const uint32_t rbase = pre + (n & 7u) * rb;
+        v4i acc[NG];
+#pragma unroll
+        for (uint32_t G = 0; G < NG; ++G) acc[G] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t j = 0; j < static_cast<uint32_t>(NB); ++j) {
+            const uint32_t addr = rbase + 34u * j + 2u + 8u * grp;
+            const uint32_t* q = reinterpret_cast<const uint32_t*>(tile + (addr & ~3u));
+            const uint32_t sh = addr & 3u, d0 = q[0], d1 = q[1], d2 = q[2];
+            const long bop = static_cast<long>(__builtin_amdgcn_alignbyte(d1, d0, sh)) |
+                             (static_cast<long>(__builtin_amdgcn_alignbyte(d2, d1, sh)) << 32);
+            acc[j / 4u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[j], bop, acc[j / 4u], 0, 0, 0);
+        }
+        float part = 0.0f;
+#pragma unroll
+        for (uint32_t G = 0; G < NG; ++G) {
+            const uint32_t j = 4u * G + grp;
+            if (j < static_cast<uint32_t>(NB)) {
+                const float dw = half_bits_to_float(*reinterpret_cast<const uint16_t*>(tile + rbase + 34u * j));
+                const float t = fmaf(static_cast<float>(acc[G][2]), inv64516,
+                                     fmaf(static_cast<float>(acc[G][1]), inv254, static_cast<float>(acc[G][0])));
+                part += dw * sx[G] * t;
+            }
+        }
+        const float tot = add_xor32(add_xor16(part));
+        const uint32_t v = r0 + lane;
+        if (lane < kLmWaveRows && v < V) {
+            if (want_logits) gp(g_tk.logits)[v] = tot;
+            if (am_better(tot, v, bv, bi)) { bv = tot; bi = v; }
+        }
+    }
+    return true;
+}
+
 // Final norm, tied Q8_0 LM head over this workgroup's tiles, local greedy argmax published with
 // tag tLM (src/gemma3.cpp:1138-1185, shaders/argmax.comp:30-43).
-template <int SD, int EP2>
+template <int SD, int EP2, int LMB>
 __device__ __attribute__((noinline)) bool phase_lm(uint32_t tagb, uint32_t tLM, uint32_t want_logits, bool tr) {
 #pragma clang fp contract(off)
     tagb = __builtin_amdgcn_readfirstlane(tagb);
@@ -642,61 +753,65 @@ __device__ __attribute__((noinline)) bool phase_lm(uint32_t tagb, uint32_t tLM, 
     const uint32_t tiles = (g_tk.V + TR - 1u) / TR;
     const uint32_t ntiles = w < tiles ? (tiles - w + nwg - 1u) / nwg : 0u;
     auto tile_row = [&](uint32_t ti) { return (w + ti * nwg) * TR; };
-    uint8_t* ring = lds<uint8_t>(g_tk.lds.ring);
-    auto issue = [&](uint32_t ti) {
-        const uint32_t r0 = tile_row(ti);
-        return lm_tile_issue(r0, min(g_tk.V, r0 + TR), rb_d, ring + (ti % kLmRing) * kLmTileBytes);
-    };
     const FoldW fw = fold_weights(g_tk_layers[g_tk.L - 1u].post_ffw, g_tk.out_norm);
-#pragma unroll
-    for (uint32_t i = 0; i < kLmAhead; ++i)
-        if (i < ntiles) (void)issue(i);
-    if (!final_fold<EP2>(tagb, fw)) return false;
-    stamp(tr, 2u * g_tk.L + 1u);
-    const LimbLds Lm{lds<int8_t>(g_tk.lds.la), lds<int8_t>(g_tk.lds.lb), lds<int8_t>(g_tk.lds.lc), lds<float>(g_tk.lds.ls)};
-    // row slots of LS lanes, LNB blocks per lane (20-block rows: 16-lane slots, four lanes with two)
-    constexpr int LS = SD >= 32 ? SD / 2 : SD;
-    constexpr int LNB = SD / LS;
-    XLimb xl[LNB];
-    lane_limbs<LS, LNB>(Lm, nblk_d, xl);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
-    constexpr uint32_t RPW = 64u / LS;
-    const uint32_t slot = lane / LS, sl = lane % LS;
-    for (uint32_t ti = 0; ti < ntiles; ++ti) {
-        const uint32_t t0 = tile_row(ti), t1 = min(g_tk.V, t0 + TR);
-        const uint8_t* tile = ring + (ti % kLmRing) * kLmTileBytes;
-        const uint32_t pre_cur = static_cast<uint32_t>(
-            (reinterpret_cast<uintptr_t>(g_tk.tok_embd) + static_cast<uint64_t>(t0) * rb_d) & 15u);
-        lm_wait_tiles(min(kLmAhead - 1u, ntiles - 1u - ti));
-        __syncthreads();   // tile ti is in LDS for every wave; every wave is done with tile ti - 1
-        if (ti + kLmAhead < ntiles) (void)issue(ti + kLmAhead);
-        const uint32_t nrows = t1 - t0;
-        for (uint32_t rg = wave * RPW; rg < nrows; rg += kWaves * RPW) {
-            const uint32_t r = rg + slot;
-            const bool live = r < nrows;
-            float acc = 0.0f;
+    if constexpr (LMB > 0) {
+        if (!lm_waves<LMB, EP2>(tagb, want_logits, tr, fw, bv, bi)) return false;
+    } else {
+        uint8_t* ring = lds<uint8_t>(g_tk.lds.ring);
+        auto issue = [&](uint32_t ti) {
+            const uint32_t r0 = tile_row(ti);
+            return lm_tile_issue(r0, min(g_tk.V, r0 + TR), rb_d, ring + (ti % kLmRing) * kLmTileBytes);
+        };
 #pragma unroll
-            for (int b = 0; b < LNB; ++b) {
-                const uint32_t blk = sl + static_cast<uint32_t>(b) * LS;
-                if (live && blk < nblk_d) {
-                    Q8Raw raw;
-                    q8_load_lds(tile, pre_cur + r * static_cast<uint32_t>(rb_d) + 34u * blk, raw);
-                    acc += q8_dot(raw, xl[b]);
+        for (uint32_t i = 0; i < kLmAhead; ++i)
+            if (i < ntiles) (void)issue(i);
+        if (!final_fold<EP2>(tagb, fw)) return false;
+        stamp(tr, 2u * g_tk.L + 1u);
+        const LimbLds Lm{lds<int8_t>(g_tk.lds.la), lds<int8_t>(g_tk.lds.lb), lds<int8_t>(g_tk.lds.lc), lds<float>(g_tk.lds.ls)};
+        // row slots of LS lanes, LNB blocks per lane (20-block rows: 16-lane slots, four lanes with two)
+        constexpr int LS = SD >= 32 ? SD / 2 : SD;
+        constexpr int LNB = SD / LS;
+        XLimb xl[LNB];
+        lane_limbs<LS, LNB>(Lm, nblk_d, xl);
+        constexpr uint32_t RPW = 64u / LS;
+        const uint32_t slot = lane / LS, sl = lane % LS;
+        for (uint32_t ti = 0; ti < ntiles; ++ti) {
+            const uint32_t t0 = tile_row(ti), t1 = min(g_tk.V, t0 + TR);
+            const uint8_t* tile = ring + (ti % kLmRing) * kLmTileBytes;
+            const uint32_t pre_cur = static_cast<uint32_t>(
+                (reinterpret_cast<uintptr_t>(g_tk.tok_embd) + static_cast<uint64_t>(t0) * rb_d) & 15u);
+            lm_wait_tiles(min(kLmAhead - 1u, ntiles - 1u - ti));
+            __syncthreads();   // tile ti is in LDS for every wave; every wave is done with tile ti - 1
+            if (ti + kLmAhead < ntiles) (void)issue(ti + kLmAhead);
+            const uint32_t nrows = t1 - t0;
+            for (uint32_t rg = wave * RPW; rg < nrows; rg += kWaves * RPW) {
+                const uint32_t r = rg + slot;
+                const bool live = r < nrows;
+                float acc = 0.0f;
+    #pragma unroll
+                for (int b = 0; b < LNB; ++b) {
+                    const uint32_t blk = sl + static_cast<uint32_t>(b) * LS;
+                    if (live && blk < nblk_d) {
+                        Q8Raw raw;
+                        q8_load_lds(tile, pre_cur + r * static_cast<uint32_t>(rb_d) + 34u * blk, raw);
+                        acc += q8_dot(raw, xl[b]);
+                    }
                 }
-            }
-            float tot;
-            if constexpr (LS == 64) {
-                const float hsum = slot_sum<32>(acc);
-                tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 0)) +
-                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 32));
-            } else {
-                tot = slot_sum<LS>(acc);
-            }
-            if (live && sl == 0u) {
-                const uint32_t v = t0 + r;
-                if (want_logits) gp(g_tk.logits)[v] = tot;
-                if (am_better(tot, v, bv, bi)) { bv = tot; bi = v; }
+                float tot;
+                if constexpr (LS == 64) {
+                    const float hsum = slot_sum<32>(acc);
+                    tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 0)) +
+                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsum), 32));
+                } else {
+                    tot = slot_sum<LS>(acc);
+                }
+                if (live && sl == 0u) {
+                    const uint32_t v = t0 + r;
+                    if (want_logits) gp(g_tk.logits)[v] = tot;
+                    if (am_better(tot, v, bv, bi)) { bv = tot; bi = v; }
+                }
             }
         }
     }
@@ -1171,8 +1286,9 @@ __device__ __forceinline__ void dn_scalars(const DnLds& t, bool has_y, float& sc
 
 // Row-slot width S, blocks per lane NB and passes U of each team's matvec, and EP2 = the residual
 // pairs per lane of the fold (d / 128 rounded up).
-template <int SA_, int UA_, int SB_, int SD_, int KBD_, int SE_, int NBE_, int UE_, int EP2_>
+template <int SA_, int UA_, int SB_, int SD_, int KBD_, int SE_, int NBE_, int UE_, int EP2_, int LMB_ = 0>
 struct Cfg {
+    static constexpr int LMB = LMB_;             // LM head on the matrix cores for rows of LMB blocks (0: row slots)
     static constexpr int SA = SA_, UA = UA_;     // q|k|v rows: K = d
     static constexpr int SB = SB_;               // Wo rows over one head: K = head_dim
     static constexpr int SD = SD_;               // LM head row slots: K = d
@@ -1317,7 +1433,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
         }
         if (!ok) break;
         if (s >= c.lm_from) {
-            ok = phase_lm<C::SD, C::EP2>(tagb, tagb + nph, c.want_logits, tr);
+            ok = phase_lm<C::SD, C::EP2, C::LMB>(tagb, tagb + nph, c.want_logits, tr);
             prev_tag = tagb + nph;
         } else {
             // a prompt step: no LM head, but the next step may only start once the last block's
@@ -1648,7 +1764,7 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
         }
         if (!ok) break;
         if (s >= c.lm_from) {
-            ok = phase_lm<C::SD, C::EP2>(tagb, tagb + nph, c.want_logits, tr);
+            ok = phase_lm<C::SD, C::EP2, C::LMB>(tagb, tagb + nph, c.want_logits, tr);
             prev_tag = tagb + nph;
         }
         load(0, s + 1u);
@@ -1778,7 +1894,7 @@ __device__ __attribute__((always_inline)) void team_d(uint32_t nsteps, uint32_t 
         }
         if (!ok) break;
         if (s >= c.lm_from) {
-            ok = phase_lm<C::SD, C::EP2>(tagb, tagb + nph, c.want_logits, tr);
+            ok = phase_lm<C::SD, C::EP2, C::LMB>(tagb, tagb + nph, c.want_logits, tr);
             prev_tag = tagb + nph;
         }
         load(0);
@@ -1849,7 +1965,7 @@ __device__ __attribute__((always_inline)) void team_e(uint32_t nsteps, uint32_t 
         }
         if (!ok) break;
         if (s >= c.lm_from) {
-            ok = phase_lm<C::SD, C::EP2>(tagb, tagb + nph, c.want_logits, tr);
+            ok = phase_lm<C::SD, C::EP2, C::LMB>(tagb, tagb + nph, c.want_logits, tr);
             prev_tag = tagb + nph;
         }
         load(0);
@@ -1876,6 +1992,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_team(uint32_t nsteps, uint32_t 
 struct TkFns {
     const void* f32 = nullptr;
     const void* f16 = nullptr;
+    uint32_t lm_blocks = 0;   // blocks per row of the matrix-core LM head (0: row-slot LM head)
 };
 
 struct TkState {
@@ -1892,14 +2009,15 @@ struct TkState {
 
 template <class C>
 static TkFns tk_fn() {
-    return TkFns{reinterpret_cast<const void*>(&tk::k_team<C, false>), reinterpret_cast<const void*>(&tk::k_team<C, true>)};
+    return TkFns{reinterpret_cast<const void*>(&tk::k_team<C, false>), reinterpret_cast<const void*>(&tk::k_team<C, true>),
+                 static_cast<uint32_t>(C::LMB)};
 }
 
 // Instantiated shapes: (d, heads x head_dim, FFN) -> row slots, passes and residual pairs.
 static TkFns tk_pick(uint32_t d, uint32_t H, uint32_t hd, uint32_t F) {
     using namespace tk;
     // Gemma-3-270M: d 640 (20 blocks: 32-lane slots), Wo over one 256-wide head (8 blocks), FFN 2048
-    if (d == 640 && H == 4 && hd == 256 && F == 2048) return tk_fn<Cfg<32, 2, 8, 32, 3, 64, 1, 2, 5>>();
+    if (d == 640 && H == 4 && hd == 256 && F == 2048) return tk_fn<Cfg<32, 2, 8, 32, 3, 64, 1, 2, 5, 20>>();
     // test shape: d 128 (4 blocks), 2 x 64 heads (2 blocks), FFN 256 (8 blocks)
     if (d == 128 && H == 2 && hd == 64 && F == 256) return tk_fn<Cfg<4, 1, 2, 4, 1, 8, 1, 1, 1>>();
     return TkFns{};
@@ -2015,7 +2133,12 @@ int tk_setup(vrt_g3* g) {
     P.lds.scr = take(kWaves * 3u * kLimbBlkBytes);
     P.lds.qkv = take(3u * hd * 4u);
     P.lds.part = take((kWaves * hd + 2u * kWaves) * 4u);
-    off = std::max(off, blk0 + kLmRing * kLmTileBytes);
+    if (fns.lm_blocks != 0u) {   // per-wave rings of 8-row tiles
+        if (fns.lm_blocks != d / 32u || kLmWaveRows * rb + 16u > kLmWaveSlot) { tk_destroy(g); return VRT_OK; }
+        off = std::max(off, blk0 + kWaves * kLmWaveRing * kLmWaveSlot);
+    } else {
+        off = std::max(off, blk0 + kLmRing * kLmTileBytes);
+    }
     P.lds.ring = blk0;
     tk->trace_slots = 2u * c.block_count + 3u + kSubMarks;
     P.lds.tr = take(tk->trace_slots * 8u);
