@@ -234,6 +234,144 @@ __global__ void __launch_bounds__(kBdThreads) k_bd_attn(BdAttn A) {
     }
 }
 
+constexpr uint32_t kBdShort = 32;   // rows whose histories are all this short take k_bd_attn_short
+
+// Histories of at most kBdShort positions: one workgroup per (head h, row b) runs the head's whole
+// attention and writes its output, with no chunk partials to merge. The cached key and value rows
+// are loaded first, before the q|k|v split partials are added, so the loads overlap. Waves 0 and 1
+// apply QK-norm and NeoX RoPE to q_h and k (src/gemma3.cpp:1045-1104, :1371-1424); the head-0
+// workgroup appends k and v at slot pos % slots (:1590-1600). The scores (wave w: positions
+// t_first + w + 4 u), the maximum, e^(s - m) with their double sum, the weighted values (thread per
+// dimension, positions in order) and the division follow k_bd_attn and k_bd_merge for one chunk
+// (:1602-1696). The current position's k and v come from LDS, never from the cache.
+__global__ void __launch_bounds__(kBdThreads) k_bd_attn_short(BdAttn A) {
+#pragma clang fp contract(off)
+    __shared__ float sq[256], sk[256], sv[256];
+    __shared__ float ssc[kBdShort];
+    __shared__ double s_l;
+    const uint32_t h = blockIdx.x, b = blockIdx.y;
+    const uint32_t H = A.H, hd = A.hd, half = hd >> 1, nq = (H + 2u) * hd;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t p = A.pos[b], sqn = A.seq[b];
+    const uint32_t n_full = min(p + 1u, A.slots), t_first = p + 1u - n_full;
+    const uint32_t n_hist = min(n_full, kBdShort);   // the host sends no longer history here
+    const uint64_t cache0 = static_cast<uint64_t>(sqn) * A.slots * hd;
+    const uint32_t di = min(tid, hd - 1u);
+    // cached key rows (wave w: positions t_first + w + 4 u; lane: dims lane + 64 e) and value rows
+    // (thread: its dimension, every position), at clamped in-bounds positions
+    float kr[8][4], vv[kBdShort];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+        const uint64_t row = cache0 + static_cast<uint64_t>(min(t_first + wave + 4u * u, p) % A.slots) * hd;
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) kr[u][e] = A.kc[row + min(lane + 64u * e, hd - 1u)];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kBdShort; ++u)
+        vv[u] = A.vc[cache0 + static_cast<uint64_t>(min(t_first + u, p) % A.slots) * hd + di];
+    float rc[4], rs[4];   // RoPE table entries of the dims lane + 64 e (waves 0 and 1 use them)
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {
+        const uint32_t ic = min(lane + 64u * e, hd - 1u), ei = ic < half ? ic : ic - half;
+        rc[e] = A.cos_t[static_cast<uint64_t>(p) * half + ei];
+        rs[e] = A.sin_t[static_cast<uint64_t>(p) * half + ei];
+    }
+    {   // q of head h, k and v: the split partials added in order
+        const float* src = A.qkv + static_cast<uint64_t>(b) * nq;
+        float pq[kBdMaxSplits], pk[kBdMaxSplits], pw[kBdMaxSplits];
+#pragma unroll
+        for (uint32_t z = 0; z < kBdMaxSplits; ++z) {
+            const uint64_t o = static_cast<uint64_t>(min(z, A.nsplit - 1u)) * A.sstride;
+            pq[z] = src[o + h * hd + di];
+            pk[z] = src[o + H * hd + di];
+            pw[z] = src[o + (H + 1u) * hd + di];
+        }
+        float a = 0.0f, c = 0.0f, e = 0.0f;
+#pragma unroll
+        for (uint32_t z = 0; z < kBdMaxSplits; ++z)
+            if (z < A.nsplit) { a += pq[z]; c += pk[z]; e += pw[z]; }
+        if (tid < hd) { sq[tid] = a; sk[tid] = c; sv[tid] = e; }
+    }
+    __syncthreads();
+    if (wave < 2u) {   // QK-norm and RoPE of q_h (wave 0) and k (wave 1); lane l: dims l + 64 e
+        float* x = wave == 0u ? sq : sk;
+        const float* w = wave == 0u ? A.q_norm : A.k_norm;
+        uint32_t ic[4], ei[4];
+        bool live[4];
+        float v[4], wv[4];
+        double ss = 0.0;
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            live[e] = lane + 64u * e < hd;
+            ic[e] = min(lane + 64u * e, hd - 1u);
+            ei[e] = ic[e] < half ? ic[e] : ic[e] - half;
+            wv[e] = w[ic[e]];
+            v[e] = live[e] ? x[ic[e]] : 0.0f;
+            ss += static_cast<double>(v[e]) * static_cast<double>(v[e]);
+        }
+        const double tot = wave_red_sum_d(ss);
+        const float sc = 1.0f / sqrtf(static_cast<float>(tot / static_cast<double>(hd)) + A.eps);   // :1087-1093
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e)
+            if (live[e]) x[ic[e]] = v[e] * (sc * wv[e]);
+        __builtin_amdgcn_wave_barrier();   // a wave's LDS accesses complete in order
+        float y[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const float a = x[ei[e]], bb = x[ei[e] + half];
+            y[e] = ic[e] < half ? a * rc[e] - bb * rs[e] : bb * rc[e] + a * rs[e];
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e)
+            if (live[e]) x[ic[e]] = y[e];
+    }
+    __syncthreads();
+    if (h == 0u && tid < hd) {   // KV append of this row's position
+        const uint64_t o = cache0 + static_cast<uint64_t>(p % A.slots) * hd + tid;
+        A.kc[o] = sk[tid];
+        A.vc[o] = sv[tid];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t t = t_first + wave + 4u * u;
+        if (t > p) break;
+        float d = 0.0f;
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e)
+            if (lane + 64u * e < hd) d += sq[lane + 64u * e] * (t == p ? sk[lane + 64u * e] : kr[u][e]);
+        d = wave_sum(d);
+        if (lane == 0u) ssc[t - t_first] = d * A.attn_scale;
+    }
+    __syncthreads();
+    if (wave == 0u) {   // m = max, e = exp(s - m), l = sum e (double)
+        float mx = lane < n_hist ? ssc[lane] : -INFINITY;
+        mx = wave_max(mx);
+        double l = 0.0;
+        if (lane < n_hist) {
+            const float e = expf(ssc[lane] - mx);
+            ssc[lane] = e;
+            l = e;
+        }
+        l = wave_sum_f64(l);
+        if (lane == 0u) s_l = l;
+    }
+    __syncthreads();
+    if (tid < hd) {
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < kBdShort; ++u)
+            if (u < n_hist) acc += ssc[u] * (t_first + u == p ? sv[tid] : vv[u]);
+        const double den = static_cast<double>(static_cast<float>(s_l));
+        if (tid == 0u && (!(den > 0.0) || !__builtin_isfinite(den))) atomicMin(&A.st->nonfinite, g3_code_softmax(A.block));
+        const float v = static_cast<float>(static_cast<double>(acc) / den);
+        const uint64_t o = static_cast<uint64_t>(b) * H * hd + h * hd + tid;
+        const _Float16 hi = static_cast<_Float16>(v);
+        A.ohi[o] = hi;
+        A.olo[o] = static_cast<_Float16>(v - static_cast<float>(hi));
+    }
+}
+
 // One workgroup per (head h, row b): att = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c over the
 // row's non-empty chunks (sums in double, chunk order), as f16 hi/lo into the O projection's
 // input; a denominator that is not > 0 and finite flags the block (src/gemma3.cpp:1666-1670).
@@ -546,11 +684,18 @@ static int bd_enqueue(vrt_g3_batch* B, uint32_t n, hipStream_t s) {
         A.block = l;
         {
             void* args[] = {&A};
-            const size_t lds = static_cast<size_t>((H + 2u) * hd + H * BL.cmax) * 4u;
-            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_bd_attn), dim3(BL.G, n), dim3(kBdThreads), args,
-                                          lds, s));
-            VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_bd_merge), dim3(H, n), dim3(kBdThreads), args,
-                                          0, s));
+            uint32_t nh_max = 0;   // longest history of the step's rows in this block
+            for (uint32_t i = 0; i < n; ++i) nh_max = std::max(nh_max, std::min(B->host_rows[kBdMaxRows + i] + 1u, BL.slots));
+            if (nh_max <= kBdShort && hd <= 256u) {
+                VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_bd_attn_short), dim3(H, n), dim3(kBdThreads),
+                                              args, 0, s));
+            } else {
+                const size_t lds = static_cast<size_t>((H + 2u) * hd + H * BL.cmax) * 4u;
+                VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_bd_attn), dim3(BL.G, n), dim3(kBdThreads), args,
+                                              lds, s));
+                VRT_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(&k_bd_merge), dim3(H, n), dim3(kBdThreads), args,
+                                              0, s));
+            }
         }
         uint32_t s_o = 1;
         if (int rc = pf_project(g, l, kProjO, B->ahi, B->alo, n, B->x, std::min(kBdMaxSplits, pf_splits(n, d)), &s_o, s))
