@@ -1136,6 +1136,9 @@ static int pf_launch_w(PfGemm& G, const PfMatrix* ex, uint32_t splits, hipStream
     if (ex && ex->h) {
         G.wh = static_cast<const _Float16*>(ex->h);
         G.ws = ex->s;
+        // one row tile (the batched decode's rows): 32-column tiles, twice the workgroups (1.256 ->
+        // 1.211 ms per step of 64 sequences); the GLU epilogue pairs gate and up inside 64 columns
+        if (!G.glu && G.M <= kQgBM) return pf_launch_h<1, 1, kPfStepBlocks, kPfWaveGroups>(G, splits, s);
         return wide ? pf_launch_h<1, 4, 2, 2>(G, splits, s) : pf_launch_h<1, 2, kPfStepBlocks, kPfWaveGroups>(G, splits, s);
     }
     return wide ? pf_launch_q8<1, 4>(G, splits, s) : pf_launch_q8<1, 2>(G, splits, s);
