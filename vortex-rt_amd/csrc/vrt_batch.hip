@@ -515,6 +515,9 @@ static int bd_alloc(vrt_g3_batch* B, size_t bytes, void** out) {
     void* p = nullptr;
     VRT_HIP_CHECK(hipMalloc(&p, bytes + 256));
     B->allocs.push_back(p);
+    // zero-filled on the executor's context stream (non-blocking), which every later use is ordered on
+    VRT_HIP_CHECK(hipMemsetAsync(p, 0, bytes + 256, B->g->ctx->stream));
+    VRT_HIP_CHECK(hipStreamSynchronize(B->g->ctx->stream));
     *out = p;
     return VRT_OK;
 }
