@@ -233,6 +233,52 @@ def test_full_shape_lane_fusion_loop(ctx, full_model):
     g.close()
 
 
+def test_team_kernel_matches_allworkgroup_kernel(ctx, tiny_model):
+    """Positions below 64 run on the phase-team kernel, later ones on the all-workgroup kernel.
+    Teacher-forced over 100 positions (crossing 64 inside one launch), team on and off give the
+    same greedy tokens and logits within the logit tolerance (float sums with v_rsq and the
+    deferred norms against double sums); a generation across the boundary gives the same
+    tokens."""
+    g = vrt.Gemma3(ctx, tiny_model)
+    assert g.team_available(), "team kernel not built for the test shape"
+    toks = synth.uniform_ids(91, 100, 2, 1000)
+    g.set_team(True)
+    a = g.forced(toks, 0)
+    g.set_team(False)
+    b = g.forced(toks, 0)
+    assert np.array_equal(a["index"], b["index"])
+    assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"]))
+    prompt = synth.uniform_ids(92, 20, 2, 1000)
+    g.set_team(False)
+    mk = g.generate(prompt, 70)
+    g.set_team(True)
+    tk = g.generate(prompt, 70)
+    g.close()
+    assert np.array_equal(tk, mk)
+
+
+def test_team_phase_trace(ctx, tiny_model):
+    """The team kernel's phase trace of a launch whose first step runs the LM head: every
+    workgroup stamps its team's input and publish of every block in order, the final norm and
+    the LM head after the blocks, and the slots match the documented layout (2L + 3 + 8)."""
+    g = vrt.Gemma3(ctx, tiny_model)
+    L = int(g.config.block_count)
+    g.set_trace(True)
+    g.generate(synth.uniform_ids(93, 1, 2, 1000), 4)   # the traced first step runs the LM head
+    tr = g.read_trace().astype(np.int64)
+    g.set_trace(False)
+    g.close()
+    nwg, slots = tr.shape
+    assert slots == 2 * L + 3 + 8, slots
+    assert nwg % 8 == 0
+    for w in range(nwg):
+        ins, pubs = tr[w, :L], tr[w, L:2 * L]
+        assert np.all(ins > 0) and np.all(pubs >= ins), w
+        assert np.all(np.diff(ins) > 0) and np.all(np.diff(pubs) > 0), w
+        start, fold, lm = tr[w, 2 * L], tr[w, 2 * L + 1], tr[w, 2 * L + 2]
+        assert start <= ins[0] and pubs[-1] <= fold <= lm, w
+
+
 def test_persistent_split_launches(ctx, tiny_model):
     """A generation split over several persistent launches equals one launch."""
     g = vrt.Gemma3(ctx, tiny_model)
