@@ -250,11 +250,14 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
  * reference's README lists an fp16/bf16 KV cache as its next residency step
  * (README.md:190-192); it has no implementation to follow. */
 #define VRT_G3_OPT_KV_F16 5
-/* 1 (default): decode steps at positions below 64 run on the phase-team persistent kernel (four
+/* 1 (default): decode steps at short histories run on the phase-team persistent kernel (four
  * teams of workgroups, each running one phase type of every block, with one-way hand-offs); later
  * positions, or all with 0, run on the all-workgroup persistent kernel. Both give the same
  * results to the stated tolerances. VRT_G3_OPT_QUERY_TEAM returns VRT_OK when the team kernel
- * is available for the shape and device (value ignored). No reference counterpart. */
+ * is available for the shape and device (value ignored). VRT_G3_OPT_QUERY_TEAM_POSITIONS (read
+ * with vrt_g3_get_option) gives the position below which steps run on the team kernel (0 when it
+ * is unavailable): 136 at the Gemma-3-270M shape with fp32 KV entries, 208 with fp16 ones. No
+ * reference counterpart. */
 #define VRT_G3_OPT_TEAM 6
 #define VRT_G3_OPT_QUERY_TEAM 7
 /* Projection fusion and the Q8 lane policy (Gemma3Model::set_projection_fusion_enabled and the
@@ -272,6 +275,7 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
 #define VRT_G3_OPT_FUSION 8
 #define VRT_G3_OPT_Q8_LANES 9
 #define VRT_G3_OPT_QUERY_Q8_LANES 10
+#define VRT_G3_OPT_QUERY_TEAM_POSITIONS 11
 
 /* Phase trace of the last persistent launch (tracing tool; no reference counterpart, which
  * only has CLI wall timers, src/gemma_main.cpp:194-232): out[w * slots + k] is the
@@ -291,7 +295,7 @@ int vrt_g3_read_trace(vrt_g3* g3, uint64_t* out, uint64_t cap, uint32_t* nwg, ui
 int vrt_g3_read_exchange(vrt_g3* g3, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
 /* Current value of an executor option: USE_GRAPH, PERSISTENT, TEAM, KV_F16, FUSION and Q8_LANES
- * as last set, QUERY_Q8_LANES as described above (the getters projection_fusion_enabled and
+ * as last set, QUERY_Q8_LANES and QUERY_TEAM_POSITIONS as described above (the getters projection_fusion_enabled and
  * narrow_q8_lane_count of include/vortexrt/gemma3.hpp read these). */
 int vrt_g3_get_option(vrt_g3* g3, uint32_t option, uint32_t* value);
 

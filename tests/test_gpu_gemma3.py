@@ -234,27 +234,56 @@ def test_full_shape_lane_fusion_loop(ctx, full_model):
 
 
 def test_team_kernel_matches_allworkgroup_kernel(ctx, tiny_model):
-    """Positions below 64 run on the phase-team kernel, later ones on the all-workgroup kernel.
-    Teacher-forced over 100 positions (crossing 64 inside one launch), team on and off give the
+    """The phase-team kernel holds the first 64 history positions in registers and the rest in
+    LDS (passes of 64, an online softmax per wave); at head_dim 64 the tiny model's whole
+    256-position context fits, so every step runs on it. Teacher-forced over 250 positions (the
+    register pass and three LDS passes, the current position in each), team on and off give the
     same greedy tokens and logits within the logit tolerance (float sums with v_rsq and the
-    deferred norms against double sums); a generation across the boundary gives the same
-    tokens."""
+    deferred norms against double sums), with fp32 and fp16 entries; a generation gives the
+    same tokens."""
     g = vrt.Gemma3(ctx, tiny_model)
     assert g.team_available(), "team kernel not built for the test shape"
-    toks = synth.uniform_ids(91, 100, 2, 1000)
-    g.set_team(True)
-    a = g.forced(toks, 0)
-    g.set_team(False)
-    b = g.forced(toks, 0)
-    assert np.array_equal(a["index"], b["index"])
-    assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"]))
+    assert g.team_positions() == 256, g.team_positions()
+    toks = synth.uniform_ids(91, 250, 2, 1000)
+    for f16 in (False, True):
+        g.set_kv_f16(f16)
+        g.set_team(True)
+        a = g.forced(toks, 0)
+        g.set_team(False)
+        b = g.forced(toks, 0)
+        assert np.array_equal(a["index"], b["index"]), f16
+        assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"])), f16
+    g.set_kv_f16(False)
     prompt = synth.uniform_ids(92, 20, 2, 1000)
     g.set_team(False)
-    mk = g.generate(prompt, 70)
+    mk = g.generate(prompt, 150)
     g.set_team(True)
-    tk = g.generate(prompt, 70)
+    tk = g.generate(prompt, 150)
     g.close()
     assert np.array_equal(tk, mk)
+
+
+def test_team_kernel_history_limit_full_shape(ctx, full_model):
+    """At the Gemma-3-270M shape the team kernel takes histories up to 136 positions with fp32
+    entries (64 in registers, 72 in LDS) and 208 with fp16 ones; later steps run on the
+    all-workgroup kernel. Teacher-forced across each limit, team on and off give the same greedy
+    tokens and logits within the tolerance."""
+    g = vrt.Gemma3(ctx, full_model)
+    try:
+        assert g.team_available()
+        for f16, limit in ((False, 136), (True, 208)):
+            g.set_kv_f16(f16)
+            assert g.team_positions() == limit, (f16, g.team_positions())
+            toks = synth.uniform_ids(94, limit + 12, 2, 262144)
+            print(f"[g3] full shape, {toks.size} forced steps, fp16 KV {f16}, team on/off", flush=True)
+            g.set_team(True)
+            a = g.forced(toks, 0)
+            g.set_team(False)
+            b = g.forced(toks, 0)
+            assert np.array_equal(a["index"], b["index"]), f16
+            assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"])), f16
+    finally:
+        g.close()
 
 
 def test_team_phase_trace(ctx, tiny_model):

@@ -1174,6 +1174,8 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
         return vrt_g3_reset(g);
     }
     case VRT_G3_OPT_QUERY_Q8_LANES: return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_Q8_LANES is read with vrt_g3_get_option");
+    case VRT_G3_OPT_QUERY_TEAM_POSITIONS:
+        return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_TEAM_POSITIONS is read with vrt_g3_get_option");
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
     }
 }
@@ -1192,6 +1194,7 @@ extern "C" int vrt_g3_get_option(vrt_g3* g, uint32_t option, uint32_t* value) {
         // row has more blocks per lane than instantiated, or with 0 the width sized from d_model
         *value = g->ld_qkv.S;
         return VRT_OK;
+    case VRT_G3_OPT_QUERY_TEAM_POSITIONS: *value = tk_pos_limit(g); return VRT_OK;
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
     }
 }

@@ -29,10 +29,13 @@
 // LM head fused with the greedy argmax (as the all-workgroup persistent kernel does), and the
 // next step starts from the argmax partials.
 //
-// Histories. Team B keeps a head's whole history in registers: eight waves of eight positions,
-// so the kernel runs positions < 64 (the host sends later positions to the all-workgroup kernel,
-// whose attention splits long histories into chunks). Each head is computed by tsize/H
-// workgroups, each producing its group of Wo rows over that head's columns.
+// Histories. Team B keeps a head's whole history on chip: the first 64 positions in registers
+// (eight waves of eight), the next hist_lds in LDS (direct-to-LDS loads issued with the register
+// loads, one phase ahead; 72 positions of fp32 entries at head_dim 256, 144 of fp16 ones). Each
+// wave runs an online softmax over its eight positions of every 64-position pass. The host sends
+// later positions to the all-workgroup kernel, whose attention splits long histories into
+// chunks. Each head is computed by tsize/H workgroups, each producing its group of Wo rows over
+// that head's columns.
 //
 // Buffer reuse without double buffering: every exchange buffer is written once per block, and
 // a team rewrites a buffer for block l + 1 only after consuming data that every reader of the
@@ -108,8 +111,10 @@ struct Lds {
     uint32_t red;    // residual folds: wave totals [waves][4] and flags [waves]
     uint32_t dn;     // A, D: row partials and norm sums of the deferred-norm projections (DnLds)
     uint32_t scr;    // A, D: each wave's activation limbs of its K blocks
-    uint32_t qkv;    // B: q_h, k, v after QK-norm and RoPE
-    uint32_t part;   // B: per-wave attention partials [waves][hd], then m [waves], l [waves]
+    uint32_t qkv;    // B: q_h after QK-norm and RoPE (shares am: the argmax partials are read before)
+    uint32_t kvc;    // B: the current position's k and v after QK-norm and RoPE
+    uint32_t kvx;    // B: key rows, then value rows, of history positions 64 .. 64 + hist_lds - 1
+    uint32_t part;   // B: per-wave attention partials [waves][hd], then m [waves], l [waves] (shares x)
     uint32_t la, lb, lc, ls;   // LM head activation limbs
     uint32_t am;     // argmax partials [2 * nwg]
     uint32_t any;    // workgroup OR flags
@@ -125,6 +130,7 @@ struct Params {
     uint32_t lm_tile_rows;
     uint32_t trace_slots;          // stamps per workgroup (0: tracing off)
     uint32_t kv_f16;
+    uint32_t hist_lds;             // history positions past the registers held in LDS (multiple of 8)
     uint32_t poll_sleep;           // back-off between unsuccessful polls (s_sleep units of 64 clocks)
     Lds lds;
     const uint8_t* tok_embd;
@@ -1497,7 +1503,8 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
     const bool lo = dl < half;
     const uint32_t e0 = lo ? dl : dl - half;       // RoPE index of dim dl
     const int partner = static_cast<int>(lo ? lane + (half >> 2) : lane - (half >> 2));
-    float* qkv_s = lds<float>(g_tk.lds.qkv);       // [3][hd]
+    float* q_s = lds<float>(g_tk.lds.qkv);         // [hd] q_h
+    float* kv_s = lds<float>(g_tk.lds.kvc);        // [2][hd] the current position's k, v
     float* part = lds<float>(g_tk.lds.part);       // [kWaves][hd], then m [kWaves], l [kWaves]
     const LimbLds Lx{lds<int8_t>(g_tk.lds.la), lds<int8_t>(g_tk.lds.lb), lds<int8_t>(g_tk.lds.lc), lds<float>(g_tk.lds.ls)};
     constexpr uint32_t esz = KVH ? 2u : 4u;
@@ -1507,6 +1514,15 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
         if constexpr (KVH) return static_cast<float>(__builtin_bit_cast(half4_t, v)[e]);
         else return __uint_as_float(v[e]);
     };
+    // History positions 64 .. 64 + hist_lds - 1 sit in LDS: key row of position 64 + j at
+    // kvx + j * rowb, value rows after the hist_lds key rows. LDS pass p >= 1 of wave j covers
+    // positions 64 p + 8 j + i (i < 8); the wave loads exactly those rows (direct-to-LDS, 1 KB
+    // = ppi rows per load, 16 bytes per lane) and is their only reader, so no barrier orders
+    // the loads: a wave waits for its own.
+    const uint32_t hist_lds = g_tk.hist_lds;
+    const uint32_t rowb = hd * esz, ppi = 1024u / rowb, lpp = 64u / ppi;
+    uint8_t* kvk = lds<uint8_t>(g_tk.lds.kvx);
+    uint8_t* kvv = kvk + hist_lds * rowb;
     RowBatch<C::SB, 1, 1> orb;
     KvReg kr[kBPos], vr[kBPos];
     // Wo rows of block l (head h's blocks) and this wave's cached key/value rows at position pos
@@ -1530,6 +1546,20 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
             } else {
                 kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, kCoherent);
                 vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, kCoherent);
+            }
+        }
+        // the cached positions 64 .. past the registers (up to hist_lds of them); lanes past the
+        // last cached position repeat it into slots that are masked or hold the current position
+        const uint32_t ncached = min(hist - 1u, kHistMax + hist_lds);
+        for (uint32_t i0 = kHistMax + kBPos * wave; i0 < ncached; i0 += kHistMax) {
+            for (uint32_t i = 0; i < kBPos && i0 + i < ncached; i += ppi) {
+                const uint32_t idx = min(i0 + i + lane / lpp, ncached - 1u);
+                const uint64_t go = static_cast<uint64_t>((t_first + idx) % Ly.slots) * rowb + (lane % lpp) * 16u;
+                const uint32_t so = (i0 + i - kHistMax) * rowb;
+                __builtin_amdgcn_global_load_lds((const TK_AS_GLOBAL void*)(reinterpret_cast<const uint8_t*>(Ly.kc) + go),
+                                                 (__attribute__((address_space(3))) void*)(kvk + so), 16, 0, kCoherent);
+                __builtin_amdgcn_global_load_lds((const TK_AS_GLOBAL void*)(reinterpret_cast<const uint8_t*>(Ly.vc) + go),
+                                                 (__attribute__((address_space(3))) void*)(kvv + so), 16, 0, kCoherent);
             }
         }
     };
@@ -1611,8 +1641,8 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                     }
                 }
                 if (dlive) {
-                    *reinterpret_cast<float4*>(qkv_s + (isq ? 0u : hd) + dl) = make_float4(xv[0], xv[1], xv[2], xv[3]);
-                    if (!isq) *reinterpret_cast<float4*>(qkv_s + 2u * hd + dl) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+                    *reinterpret_cast<float4*>((isq ? q_s : kv_s) + dl) = make_float4(xv[0], xv[1], xv[2], xv[3]);
+                    if (!isq) *reinterpret_cast<float4*>(kv_s + hd + dl) = make_float4(vv[0], vv[1], vv[2], vv[3]);
                 }
                 if (!isq && m == 0u && dlive && !fail) {   // KV append of the current position
                     const uint32_t kv_bytes = Ly.slots * hd * esz;
@@ -1637,68 +1667,98 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
             }
             if (blk_any(fail, kAnyB)) { ok = false; break; }
             stamp(tr, l);
-            // this wave's positions: 8 wave + i < hist; the current one is hist - 1
+            // this wave's positions: 8 wave + i < hist from the registers, then 64 p + 8 wave + i
+            // (p >= 1) from LDS; the current one, hist - 1, from kv_s
             const uint32_t ci = hist - 1u;
             const bool has = kBPos * wave < hist;
             if (has) {
-                const float4 q4 = dlive ? *reinterpret_cast<const float4*>(qkv_s + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const float4 q4 = dlive ? *reinterpret_cast<const float4*>(q_s + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 const float q[4] = {q4.x, q4.y, q4.z, q4.w};
-                if (ci / kBPos == wave) {   // the current position's key and value replace slot ci % 8
-                    const float4 k4 = dlive ? *reinterpret_cast<const float4*>(qkv_s + hd + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    const float4 v4 = dlive ? *reinterpret_cast<const float4*>(qkv_s + 2u * hd + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    KvReg kc, vc;
+                KvReg kc, vc;   // the current position's key and value as the cache holds them
+                {
+                    const float4 k4 = dlive ? *reinterpret_cast<const float4*>(kv_s + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    const float4 v4 = dlive ? *reinterpret_cast<const float4*>(kv_s + hd + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                     if constexpr (KVH) {
-                        kc = v2u{static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(k4.x))) |
-                                     (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(k4.y))) << 16),
-                                 static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(k4.z))) |
-                                     (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(k4.w))) << 16)};
-                        vc = v2u{static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v4.x))) |
-                                     (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v4.y))) << 16),
-                                 static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v4.z))) |
-                                     (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v4.w))) << 16)};
+                        auto pack = [](float a, float b) {
+                            return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+                                   (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+                        };
+                        kc = v2u{pack(k4.x, k4.y), pack(k4.z, k4.w)};
+                        vc = v2u{pack(v4.x, v4.y), pack(v4.z, v4.w)};
                     } else {
                         kc = v4u{__float_as_uint(k4.x), __float_as_uint(k4.y), __float_as_uint(k4.z), __float_as_uint(k4.w)};
                         vc = v4u{__float_as_uint(v4.x), __float_as_uint(v4.y), __float_as_uint(v4.z), __float_as_uint(v4.w)};
                     }
+                }
+                if (ci / kBPos == wave) {   // the current position replaces register slot ci % 8
                     const uint32_t cs = ci % kBPos;
 #pragma unroll
                     for (uint32_t i = 0; i < kBPos; ++i)
                         if (i == cs) { kr[i] = kc; vr[i] = vc; }
                 }
-                float sp[kBPos];
-#pragma unroll
-                for (uint32_t i = 0; i < kBPos; ++i) {
-                    float p = q[0] * kv_el(kr[i], 0);
-#pragma unroll
-                    for (uint32_t e = 1; e < 4u; ++e) p = fmaf(q[e], kv_el(kr[i], e), p);
-                    sp[i] = p;
-                }
-                const float st = wave_sum8_t(sp);
+                // online softmax of the wave's positions, one pass of eight at a time: running
+                // maximum wm, sum wl and accumulator wacc over this lane's four dims (the first pass
+                // leaves exactly that pass's softmax terms: alpha = 0 against wl = wacc = 0)
+                float wm = -INFINITY, wl = 0.0f, wacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 const uint32_t pl = lane & 7u;
-                const float sl = kBPos * wave + pl < hist ? st * g_tk.attn_scale : -INFINITY;
-                float mx = fmaxf(sl, dpp_mov<0xB1>(sl));
-                mx = fmaxf(mx, dpp_mov<0x4E>(mx));
-                mx = fmaxf(mx, dpp_mov<0x141>(mx));
-                mx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));   // >= one finite score
-                const float pe = sl == -INFINITY ? 0.0f : __expf(sl - mx);
-                float pw[kBPos], ls = 0.0f;
+                auto pass = [&](const KvReg (&kk)[kBPos], const KvReg (&vv)[kBPos], uint32_t b0) {
+                    float sp[kBPos];
 #pragma unroll
-                for (uint32_t i = 0; i < kBPos; ++i) {
-                    pw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), i));
-                    ls += pw[i];
+                    for (uint32_t i = 0; i < kBPos; ++i) {
+                        float p = q[0] * kv_el(kk[i], 0);
+#pragma unroll
+                        for (uint32_t e = 1; e < 4u; ++e) p = fmaf(q[e], kv_el(kk[i], e), p);
+                        sp[i] = p;
+                    }
+                    const float st = wave_sum8_t(sp);
+                    const float sl = b0 + pl < hist ? st * g_tk.attn_scale : -INFINITY;
+                    float mx = fmaxf(sl, dpp_mov<0xB1>(sl));
+                    mx = fmaxf(mx, dpp_mov<0x4E>(mx));
+                    mx = fmaxf(mx, dpp_mov<0x141>(mx));
+                    mx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));   // >= one finite score
+                    const float mn = fmaxf(wm, mx);
+                    const float alpha = __expf(wm - mn);
+                    const float pe = sl == -INFINITY ? 0.0f : __expf(sl - mn);
+                    float pw[kBPos], ls = 0.0f;
+#pragma unroll
+                    for (uint32_t i = 0; i < kBPos; ++i) {
+                        pw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), i));
+                        ls += pw[i];
+                    }
+#pragma unroll
+                    for (uint32_t e = 0; e < 4u; ++e) {
+                        float a = 0.0f;
+#pragma unroll
+                        for (uint32_t i = 0; i < kBPos; ++i) a = fmaf(pw[i], kv_el(vv[i], e), a);
+                        wacc[e] = wacc[e] * alpha + a;
+                    }
+                    wl = wl * alpha + ls;
+                    wm = mn;
+                };
+                pass(kr, vr, kBPos * wave);
+                if (hist > kHistMax && hist_lds != 0u) {
+                    __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's direct-to-LDS rows
+                    const uint32_t lo_b = dlive ? dl * esz : 0u;
+                    for (uint32_t b0 = kHistMax + kBPos * wave; b0 < hist; b0 += kHistMax) {
+                        KvReg kk[kBPos], vv[kBPos];
+#pragma unroll
+                        for (uint32_t i = 0; i < kBPos; ++i) {
+                            const uint32_t idx = b0 + i;
+                            const uint32_t so = min(idx - kHistMax, hist_lds - 1u) * rowb + lo_b;
+                            const KvReg kl = *reinterpret_cast<const KvReg*>(kvk + so);
+                            const KvReg vl = *reinterpret_cast<const KvReg*>(kvv + so);
+                            // slots past the history hold stale bytes: zeros keep their (masked)
+                            // terms finite, as the registers' out-of-range loads do
+                            kk[i] = idx == ci ? kc : (idx < hist ? kl : KvReg{});
+                            vv[i] = idx == ci ? vc : (idx < hist ? vl : KvReg{});
+                        }
+                        pass(kk, vv, b0);
+                    }
                 }
-                float acc[4];
-#pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) {
-                    float a = 0.0f;
-#pragma unroll
-                    for (uint32_t i = 0; i < kBPos; ++i) a = fmaf(pw[i], kv_el(vr[i], e), a);
-                    acc[e] = a;
-                }
-                if (dlive) *reinterpret_cast<float4*>(part + wave * hd + dl) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                if (dlive) *reinterpret_cast<float4*>(part + wave * hd + dl) = make_float4(wacc[0], wacc[1], wacc[2], wacc[3]);
                 if (lane == 0u) {
-                    part[kWaves * hd + wave] = mx;
-                    part[kWaves * hd + kWaves + wave] = ls;
+                    part[kWaves * hd + wave] = wm;
+                    part[kWaves * hd + kWaves + wave] = wl;
                 }
             }
             submark(tr && l == 1u, 5);
@@ -2003,6 +2063,7 @@ struct TkState {
     uint32_t grid = 0;
     uint32_t trace_slots = 0;
     uint32_t pos_limit = 0;        // steps at positions below this run here
+    uint32_t hist_lds[2] = {0, 0}; // LDS history rows past the registers: fp32, fp16 entries
     bool registered = false;
     std::vector<void*> allocs;
 };
@@ -2119,20 +2180,36 @@ int tk_setup(vrt_g3* g) {
     const uint32_t kmax = std::max(std::max(d, qw), F);
     uint32_t off = 0;
     auto take = [&](uint32_t bytes) { const uint32_t o = off; off += (bytes + 15u) & ~15u; return o; };
-    P.lds.x = take(std::max(kmax, 33u * (F / 32u)) * 4u);
+    // x also holds team B's per-wave partials and am team B's q_h during the blocks
+    P.lds.x = take(std::max(std::max(kmax, 33u * (F / 32u)), kWaves * hd + 2u * kWaves) * 4u);
+    P.lds.part = P.lds.x;
     P.lds.red = take(4u * kWaves * 4u + kWaves * 4u);
     P.lds.la = take(d);
     P.lds.lb = take(d);
     P.lds.lc = take(d);
     P.lds.ls = take(d / 32u * 4u);
-    P.lds.am = take(2u * nwg * 4u);
+    P.lds.am = take(std::max(2u * nwg, hd) * 4u);
+    P.lds.qkv = P.lds.am;
     P.lds.any = take(kAnySets * kWaves * 4u);
-    // the LM-head ring overlays the scratch of the block phases (the LM head follows them)
+    tk->trace_slots = 2u * c.block_count + 3u + kSubMarks;
+    P.lds.tr = take(tk->trace_slots * 8u);
+    // the block phases' scratch (teams A and D: dn, scr; team B: the current k and v, then the
+    // history rows past the registers) and the LM-head ring overlay each other: the LM head
+    // follows the blocks, and a workgroup runs one team
     const uint32_t blk0 = off;
     P.lds.dn = take((2u * kWaves * 64u + 4u * kWaves + kWaves) * 4u);
     P.lds.scr = take(kWaves * 3u * kLimbBlkBytes);
-    P.lds.qkv = take(3u * hd * 4u);
-    P.lds.part = take((kWaves * hd + 2u * kWaves) * 4u);
+    const uint32_t end_ad = off;
+    off = blk0;
+    P.lds.kvc = take(2u * hd * 4u);
+    P.lds.kvx = off;
+    // LDS history rows (key and value) for fp32 and fp16 entries: whole 1 KB loads of rows, in
+    // multiples of 8 positions (one wave's share of a pass)
+    for (uint32_t f = 0; f < 2u; ++f) {
+        const uint32_t rowb = hd * (f ? 2u : 4u);
+        tk->hist_lds[f] = 1024u % rowb == 0u && P.lds.kvx < kLdsBytes ? (kLdsBytes - P.lds.kvx) / (2u * rowb) / 8u * 8u : 0u;
+    }
+    off = std::max(end_ad, P.lds.kvx);
     if (fns.lm_blocks != 0u) {   // per-wave rings of 8-row tiles
         if (fns.lm_blocks != d / 32u || kLmWaveRows * rb + 16u > kLmWaveSlot) { tk_destroy(g); return VRT_OK; }
         off = std::max(off, blk0 + kWaves * kLmWaveRing * kLmWaveSlot);
@@ -2140,8 +2217,6 @@ int tk_setup(vrt_g3* g) {
         off = std::max(off, blk0 + kLmRing * kLmTileBytes);
     }
     P.lds.ring = blk0;
-    tk->trace_slots = 2u * c.block_count + 3u + kSubMarks;
-    P.lds.tr = take(tk->trace_slots * 8u);
     P.lds.total = off;
     if (off > kLdsBytes) { tk_destroy(g); return VRT_OK; }
 
@@ -2189,7 +2264,8 @@ int tk_setup(vrt_g3* g) {
     }
     tk->fns = fns;
     tk->grid = nwg;
-    tk->pos_limit = std::min(c.context_length, kHistMax);
+    P.hist_lds = tk->hist_lds[P.kv_f16 ? 1 : 0];
+    tk->pos_limit = std::min(c.context_length, kHistMax + P.hist_lds);
     g->tk_tag = 1u;
     {
         CoopSlot& ds = coop_slot(g->ctx->device);
@@ -2210,6 +2286,8 @@ int tk_set_trace(vrt_g3* g, bool on) {
 int tk_set_kv_f16(vrt_g3* g, bool on) {
     if (!g->tk) return VRT_OK;
     g->tk->P.kv_f16 = on ? 1u : 0u;
+    g->tk->P.hist_lds = g->tk->hist_lds[on ? 1 : 0];
+    g->tk->pos_limit = std::min(g->cfg.context_length, tk::kHistMax + g->tk->P.hist_lds);
     ++g->tk->version;
     return VRT_OK;
 }

@@ -26,6 +26,7 @@ OPT_QUERY_TEAM = 7
 OPT_FUSION = 8
 OPT_Q8_LANES = 9
 OPT_QUERY_Q8_LANES = 10
+OPT_QUERY_TEAM_POSITIONS = 11
 
 
 class VrtError(RuntimeError):
@@ -390,6 +391,10 @@ class Gemma3:
 
     def team_available(self) -> bool:
         return lib().vrt_g3_set_option(self.h, OPT_QUERY_TEAM, 0) == VRT_OK
+
+    def team_positions(self) -> int:
+        """Steps at positions below this run on the team kernel (0: unavailable)."""
+        return self.get_option(OPT_QUERY_TEAM_POSITIONS)
 
     def set_trace(self, on: bool):
         check(lib().vrt_g3_set_option(self.h, OPT_TRACE, 1 if on else 0))
