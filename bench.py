@@ -9,11 +9,13 @@ prompt is prefilled first (untimed); --steps decode steps at positions 8, 9, ...
 with hipEvents on the library's stream. Inputs are resident in HBM before timing.
 
 The whole decode loop is one persistent kernel: a cooperative launch with one workgroup per CU
-that runs every block, the LM head and argmax for each of the launch's steps. Positions below 64
-run on k_team (four teams of workgroups, each running one phase type of every block); later
-positions on k_decode (every workgroup in every phase). With the default 8-token prompt and up
-to 56 steps the timed region is exactly one k_team launch, so the roofline's launch duration is
-the event-timed region itself; longer runs time one k_team and one k_decode launch together.
+that runs every block, the LM head and argmax for each of the launch's steps. Positions below
+the team kernel's limit (136 with fp32 KV at this shape: histories of up to 64 positions in
+registers and 72 in LDS) run on k_team (four teams of workgroups, each running one phase type of
+every block); later positions on k_decode (every workgroup in every phase). With the default
+8-token prompt and up to 128 steps the timed region is exactly one k_team launch, so the
+roofline's launch duration is the event-timed region itself; longer runs time one k_team and one
+k_decode launch together.
 
 Algorithmic bytes per step at position p: every Q8_0 weight byte, the fp32 norm weights, one
 embedding row, plus the fp32 KV rows attention reads (min(p+1, window) positions for local
@@ -336,18 +338,17 @@ def cpu_baseline(path, prompt, target_s: float = 12.0):
                       f"the reference's Lavapipe path is not available on this host"}
 
 
-TEAM_POS_LIMIT = 64   # positions below this run on the team kernel (VRT_G3_OPT_TEAM, include/vrt_hip.h)
-
-
 def roofline_kernel(g, cfg, first: int, steps: int) -> str:
-    """The persistent launch(es) that run the timed steps at positions first .. first + steps - 1."""
+    """The persistent launch(es) that run the timed steps at positions first .. first + steps - 1
+    (steps below g.team_positions() run on the team kernel, VRT_G3_OPT_QUERY_TEAM_POSITIONS)."""
     per = f"{cfg.block_count} blocks + tied LM head + argmax per step"
     last = first + steps - 1
-    if g.team_available() and last < TEAM_POS_LIMIT:
+    limit = g.team_positions() if g.team_available() else 0
+    if last < limit:
         return f"k_team (phase-team persistent kernel: {per}, {steps} steps per launch)"
-    if g.team_available() and first < TEAM_POS_LIMIT:
-        return (f"k_team for positions {first}..{TEAM_POS_LIMIT - 1}, then k_decode (all-workgroup persistent "
-                f"kernel) for {TEAM_POS_LIMIT}..{last}: {per}")
+    if first < limit:
+        return (f"k_team for positions {first}..{limit - 1}, then k_decode (all-workgroup persistent "
+                f"kernel) for {limit}..{last}: {per}")
     return f"k_decode (all-workgroup persistent kernel: {per}, {steps} steps per launch)"
 
 

@@ -250,6 +250,11 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
  * reference's README lists an fp16/bf16 KV cache as its next residency step
  * (README.md:190-192); it has no implementation to follow. */
 #define VRT_G3_OPT_KV_F16 5
+/* 1: the KV cache holds bfloat16 keys and values (IEEE round to nearest even of the fp32 k and
+ * v, as for KV_F16; 8 exponent bits, 7 mantissa bits), 2 bytes per element. KV_F16 and KV_BF16
+ * select one format: setting either to 1 replaces the other, setting the one in use to 0
+ * returns to fp32. Switching resets the cache. Same roadmap item (README.md:190-192). */
+#define VRT_G3_OPT_KV_BF16 12
 /* 1 (default): decode steps at short histories run on the phase-team persistent kernel (four
  * teams of workgroups, each running one phase type of every block, with one-way hand-offs); later
  * positions, or all with 0, run on the all-workgroup persistent kernel. Both give the same
@@ -294,7 +299,7 @@ int vrt_g3_read_trace(vrt_g3* g3, uint64_t* out, uint64_t cap, uint32_t* nwg, ui
  * partials. *n receives the word count; synchronises the context's stream. */
 int vrt_g3_read_exchange(vrt_g3* g3, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
-/* Current value of an executor option: USE_GRAPH, PERSISTENT, TEAM, KV_F16, FUSION and Q8_LANES
+/* Current value of an executor option: USE_GRAPH, PERSISTENT, TEAM, KV_F16, KV_BF16, FUSION and Q8_LANES
  * as last set, QUERY_Q8_LANES and QUERY_TEAM_POSITIONS as described above (the getters projection_fusion_enabled and
  * narrow_q8_lane_count of include/vortexrt/gemma3.hpp read these). */
 int vrt_g3_get_option(vrt_g3* g3, uint32_t option, uint32_t* value);

@@ -53,6 +53,9 @@ def lib(path: str | None = None):
             "or_f16_to_f32": (F, [C.c_uint16]),
             "or_f32_to_f16_rne": (C.c_uint16, [F]),
             "or_f32_to_f16_rne_n": (None, [P, U64, P]),
+            "or_f32_to_bf16_rne": (C.c_uint16, [F]),
+            "or_f32_to_bf16_rne_n": (None, [P, U64, P]),
+            "or_bf16_to_f32": (F, [C.c_uint16]),
             "or_q8_quantize_a": (None, [P, U64, U32, P]),
             "or_q8_quantize_b": (None, [P, U64, U32, P]),
             "or_q8_dequant": (None, [P, U64, P]),
@@ -76,6 +79,7 @@ def lib(path: str | None = None):
             "or_g3_generate": (I, [P, P, U32, U32, P, P]),
             "or_g3_error": (C.c_char_p, [P]),
             "or_g3_set_kv_f16": (None, [P, I]),
+            "or_g3_set_kv_format": (None, [P, I]),
             "or_g3_set_taps": (None, [P, P]),
             "or_num_threads": (I, []),
         }
@@ -105,6 +109,18 @@ def f32_to_f16_rne(x: np.ndarray) -> np.ndarray:
 
 def f16_to_f32(h: int) -> float:
     return float(lib().or_f16_to_f32(C.c_uint16(h)))
+
+
+def f32_to_bf16_rne(x: np.ndarray) -> np.ndarray:
+    """bfloat16 bits of float32 values, round to nearest even (the bf16 KV rounding)."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().or_f32_to_bf16_rne_n(_p(a), a.size, _p(out))
+    return out
+
+
+def bf16_to_f32(h: int) -> float:
+    return float(lib().or_bf16_to_f32(C.c_uint16(h)))
 
 
 def quantize(w: np.ndarray, variant: str = "a") -> np.ndarray:
@@ -210,7 +226,8 @@ def attention(q, keys, values, heads, head_dim, scale):
 class Model:
     """The whole-model oracle (src/gemma3.cpp executor restated) over a GGUF file."""
 
-    def __init__(self, path: str, lanes: int = 8, lib_path: str | None = None, kv_f16: bool = False):
+    def __init__(self, path: str, lanes: int = 8, lib_path: str | None = None, kv_f16: bool = False,
+                 kv_bf16: bool = False):
         self.L = lib(lib_path)
         err = C.create_string_buffer(512)
         self.h = self.L.or_g3_open(str(path).encode(), lanes, err, 512)
@@ -218,6 +235,8 @@ class Model:
             raise RuntimeError(err.value.decode())
         if kv_f16:
             self.L.or_g3_set_kv_f16(self.h, 1)
+        if kv_bf16:
+            self.L.or_g3_set_kv_format(self.h, 2)
         info = G3Info()
         self.L.or_g3_get_info(self.h, C.byref(info))
         self.info = info

@@ -72,6 +72,30 @@ void or_f32_to_f16_rne_n(const float* x, uint64_t n, uint16_t* out) {
     for (uint64_t i = 0; i < n; ++i) out[i] = or_f32_to_f16_rne(x[i]);
 }
 
+/* bf16 (the upper half of an fp32) by round to nearest even of the lower 16 bits; NaN stays a
+ * quiet NaN of the same sign; a carry out of the mantissa moves into the exponent (finite
+ * values at the top round to infinity). The bf16 KV cache format: the reference's README lists
+ * an fp16/bf16 cache as a roadmap item (README.md:190-192) with no arithmetic to follow, so this
+ * is IEEE RNE to bfloat16. */
+uint16_t or_f32_to_bf16_rne(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    const uint32_t rem = x & 0xffffu, hi = x >> 16;
+    return (uint16_t)(hi + (rem > 0x8000u || (rem == 0x8000u && (hi & 1u))));
+}
+
+void or_f32_to_bf16_rne_n(const float* x, uint64_t n, uint16_t* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = or_f32_to_bf16_rne(x[i]);
+}
+
+float or_bf16_to_f32(uint16_t h) {
+    const uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
 float or_f16_to_f32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
     uint32_t exponent = (h >> 10) & 31u;
@@ -423,7 +447,7 @@ struct or_g3 {
     float *inv_local, *inv_global;
     uint32_t next_pos;
     uint32_t lanes;
-    int kv_f16;
+    int kv_fmt;   /* KV cache entries: 0 fp32, 1 fp16, 2 bf16 */
     int tapping;
     or_g3_taps taps;
     char err[256];
@@ -604,10 +628,12 @@ void or_g3_reset(or_g3* m) {
     m->next_pos = 0;
 }
 
-void or_g3_set_kv_f16(or_g3* m, int on) {
-    m->kv_f16 = on != 0;
+void or_g3_set_kv_format(or_g3* m, int fmt) {
+    m->kv_fmt = fmt == 1 || fmt == 2 ? fmt : 0;
     or_g3_reset(m);
 }
+
+void or_g3_set_kv_f16(or_g3* m, int on) { or_g3_set_kv_format(m, on ? 1 : 0); }
 
 void or_g3_set_taps(or_g3* m, const or_g3_taps* taps) {
     m->tapping = taps != NULL;
@@ -621,14 +647,21 @@ static void tap_row(float* a, uint32_t l, const float* src, uint32_t n) {
 }
 
 /* push_back then pop_front while size > window (src/gemma3.cpp:1590-1600). */
-static int kv_push(or_layer_t* L, const float* k_in, const float* v_in, uint32_t hd, int kv_f16) {
+static int kv_push(or_layer_t* L, const float* k_in, const float* v_in, uint32_t hd, int kv_fmt) {
     float kr[512], vr[512];   /* hd <= 512 (checked at open) */
     const float* k = k_in;
     const float* v = v_in;
-    if (kv_f16) {   /* the fp16 cache holds the rounded values */
+    if (kv_fmt == 1) {   /* the fp16 cache holds the rounded values */
         for (uint32_t i = 0; i < hd; ++i) {
             kr[i] = or_f16_to_f32(or_f32_to_f16_rne(k_in[i]));
             vr[i] = or_f16_to_f32(or_f32_to_f16_rne(v_in[i]));
+        }
+        k = kr;
+        v = vr;
+    } else if (kv_fmt == 2) {   /* and the bf16 cache its rounded values */
+        for (uint32_t i = 0; i < hd; ++i) {
+            kr[i] = or_bf16_to_f32(or_f32_to_bf16_rne(k_in[i]));
+            vr[i] = or_bf16_to_f32(or_f32_to_bf16_rne(v_in[i]));
         }
         k = kr;
         v = vr;
@@ -707,7 +740,7 @@ static int decode_impl(or_g3* m, uint32_t token, uint32_t pos, int want_logits,
         or_rms_norm_heads(k, L->k_norm, 1, hd, eps);
         or_apply_rope(q, H, hd, L->global ? gc : lc, L->global ? gs : ls);
         or_apply_rope(k, 1, hd, L->global ? gc : lc, L->global ? gs : ls);
-        if (kv_push(L, k, v, hd, m->kv_f16)) { set_err(m->err, sizeof m->err, "out of memory"); rc = -3; goto done; }
+        if (kv_push(L, k, v, hd, m->kv_fmt)) { set_err(m->err, sizeof m->err, "out of memory"); rc = -3; goto done; }
         const uint32_t hist = L->count;
         const float *K = L->keys, *V = L->vals;
         if (L->cap && L->start) { /* gather the ring in time order */

@@ -14,6 +14,10 @@
  *   or_f32_to_f16        numpy float16 (IEEE RNE) on every non-tie, non-carry input;
  *                        closed-form tie (half-up) and carry-loss cases; golden bytes.
  *   or_f16_to_f32        exhaustive over all 65536 halves against numpy float16.
+ *   or_f32_to_bf16_rne   nearest of the two neighbouring bf16 values chosen in float64
+ *                        (ties to the even one), on random and constructed tie/carry/
+ *                        subnormal/inf/NaN inputs; or_bf16_to_f32 exhaustive against the
+ *                        16-bit shift into a float32.
  *   or_q8_quantize_*     numpy float32 rint/division; |q|<=127 and the amax element
  *                        quantises to +-127; golden bytes.
  *   or_q8_matvec_lanes   exact float64 dot (products are exact in float64) within the
@@ -55,6 +59,11 @@ float or_f16_to_f32(uint16_t h);                 /* src/gguf.cpp:203-235 */
  * a roadmap item (README.md:190-192) without an implementation. Bulk form for the pins. */
 uint16_t or_f32_to_f16_rne(float f);
 void or_f32_to_f16_rne_n(const float* x, uint64_t n, uint16_t* out);
+/* IEEE round to nearest even to bfloat16 (NaN -> quiet NaN), and its exact inverse: the bf16
+ * KV cache format. */
+uint16_t or_f32_to_bf16_rne(float f);
+void or_f32_to_bf16_rne_n(const float* x, uint64_t n, uint16_t* out);
+float or_bf16_to_f32(uint16_t h);
 
 /* ---- Q8_0 quantisers: 34-byte blocks {f16 scale LE, int8 q[32]} along k ---- */
 /* Variant A, src/q8_test_main.cpp:93-124: q = nearbyint(v / (amax/127)), fp32 scale. */
@@ -124,6 +133,9 @@ const char* or_g3_error(const or_g3* m);
 /* fp16 KV cache: keys and values are rounded with or_f32_to_f16_rne when they enter the cache
  * (every position's attention, the current one's included, reads the cache). Resets the cache. */
 void or_g3_set_kv_f16(or_g3* m, int on);
+/* KV cache entries: 0 fp32, 1 fp16 (as or_g3_set_kv_f16), 2 bf16 (or_f32_to_bf16_rne as they
+ * enter the cache). Resets the cache. */
+void or_g3_set_kv_format(or_g3* m, int fmt);
 
 /* Intermediate values of the attention sub-path, for the parity tests that pin it
  * (src/gemma3.cpp:1511-1696 computes them inside decode_token and exposes none). While taps

@@ -239,21 +239,21 @@ def test_team_kernel_matches_allworkgroup_kernel(ctx, tiny_model):
     256-position context fits, so every step runs on it. Teacher-forced over 250 positions (the
     register pass and three LDS passes, the current position in each), team on and off give the
     same greedy tokens and logits within the logit tolerance (float sums with v_rsq and the
-    deferred norms against double sums), with fp32 and fp16 entries; a generation gives the
-    same tokens."""
+    deferred norms against double sums), with fp32, fp16 and bf16 entries; a generation gives
+    the same tokens."""
     g = vrt.Gemma3(ctx, tiny_model)
     assert g.team_available(), "team kernel not built for the test shape"
     assert g.team_positions() == 256, g.team_positions()
     toks = synth.uniform_ids(91, 250, 2, 1000)
-    for f16 in (False, True):
-        g.set_kv_f16(f16)
+    for fmt in ("f32", "f16", "bf16"):
+        g.set_kv_format(fmt)
         g.set_team(True)
         a = g.forced(toks, 0)
         g.set_team(False)
         b = g.forced(toks, 0)
-        assert np.array_equal(a["index"], b["index"]), f16
-        assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"])), f16
-    g.set_kv_f16(False)
+        assert np.array_equal(a["index"], b["index"]), fmt
+        assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"])), fmt
+    g.set_kv_format("f32")
     prompt = synth.uniform_ids(92, 20, 2, 1000)
     g.set_team(False)
     mk = g.generate(prompt, 150)
@@ -265,23 +265,23 @@ def test_team_kernel_matches_allworkgroup_kernel(ctx, tiny_model):
 
 def test_team_kernel_history_limit_full_shape(ctx, full_model):
     """At the Gemma-3-270M shape the team kernel takes histories up to 136 positions with fp32
-    entries (64 in registers, 72 in LDS) and 208 with fp16 ones; later steps run on the
+    entries (64 in registers, 72 in LDS) and 208 with fp16 or bf16 ones; later steps run on the
     all-workgroup kernel. Teacher-forced across each limit, team on and off give the same greedy
     tokens and logits within the tolerance."""
     g = vrt.Gemma3(ctx, full_model)
     try:
         assert g.team_available()
-        for f16, limit in ((False, 136), (True, 208)):
-            g.set_kv_f16(f16)
-            assert g.team_positions() == limit, (f16, g.team_positions())
+        for fmt, limit in (("f32", 136), ("f16", 208), ("bf16", 208)):
+            g.set_kv_format(fmt)
+            assert g.team_positions() == limit, (fmt, g.team_positions())
             toks = synth.uniform_ids(94, limit + 12, 2, 262144)
-            print(f"[g3] full shape, {toks.size} forced steps, fp16 KV {f16}, team on/off", flush=True)
+            print(f"[g3] full shape, {toks.size} forced steps, {fmt} KV, team on/off", flush=True)
             g.set_team(True)
             a = g.forced(toks, 0)
             g.set_team(False)
             b = g.forced(toks, 0)
-            assert np.array_equal(a["index"], b["index"]), f16
-            assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"])), f16
+            assert np.array_equal(a["index"], b["index"]), fmt
+            assert np.max(np.abs(a["value"] - b["value"])) <= LOGIT_TOL * np.max(np.abs(b["value"])), fmt
     finally:
         g.close()
 

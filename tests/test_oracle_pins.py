@@ -98,6 +98,58 @@ def test_f16_rne_against_numpy():
     assert np.all((got[nan] & 0x7c00) == 0x7c00) and np.all((got[nan] & 0x3ff) != 0)
 
 
+def _bf16_nearest(x: np.ndarray) -> np.ndarray:
+    """bfloat16 bits of finite float32 values by the definition of round to nearest even: of
+    the two bf16 values around x (its top 16 bits, and one ulp further from zero, with 2^128 in
+    place of the value past the largest finite one), the nearer in exact float64 arithmetic, the
+    one with an even last bit on a tie."""
+    bits = x.view(np.uint32)
+    lo = (bits >> 16).astype(np.uint32)
+    hi = lo + 1
+    mag = np.abs(x.astype(np.float64))
+    v_lo = np.abs((lo << 16).view(np.float32).astype(np.float64))
+    hi_bits = (hi << 16).astype(np.uint32)
+    v_hi = np.where((hi & 0x7fff) == 0x7f80, 2.0 ** 128, np.abs(hi_bits.view(np.float32).astype(np.float64)))
+    d_lo, d_hi = mag - v_lo, v_hi - mag
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & ((lo & 1) == 1))
+    return np.where(pick_hi, hi, lo).astype(np.uint16)
+
+
+def test_bf16_rne_against_definition():
+    """or_f32_to_bf16_rne (the bf16 KV rounding) against the definition of round to nearest
+    even, computed independently in float64 (_bf16_nearest): every midpoint between neighbouring
+    bf16 values of a sweep of exponents (ties, to the even neighbour) and its float32 neighbours,
+    the carry into the exponent, the largest finite values (rounding to infinity), subnormals,
+    signed zeros, infinities and 4M random bit patterns; NaN stays a quiet NaN. or_bf16_to_f32
+    is the exact 16-bit shift for every bf16 bit pattern."""
+    rng = np.random.default_rng(12)
+    top = rng.integers(0, 0x7f80, size=1 << 16, dtype=np.uint32)
+    mids = ((top << 16) | 0x8000).astype(np.uint32).view(np.float32)          # exact ties
+    near = np.concatenate([np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))])
+    edges = np.array([0x00000000, 0x00008000, 0x00018000, 0x00007fff, 0x3f7fffff, 0x3f7f8000, 0x3f7f7fff,
+                      0x7f7f7fff, 0x7f7f8000, 0x7f7fffff, 0x7f800000, 0x00800000, 0x007fffff],
+                     dtype=np.uint32).view(np.float32)
+    rand = rng.integers(0, 2 ** 32, size=1 << 22, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([mids, near, edges, rand])
+    x = np.concatenate([x, -x])
+    got = oracle.f32_to_bf16_rne(x)
+    nan = np.isnan(x)
+    fin = np.isfinite(x)
+    assert np.array_equal(got[fin], _bf16_nearest(x[fin]))
+    inf = ~fin & ~nan
+    assert np.array_equal(got[inf], (x[inf].view(np.uint32) >> 16).astype(np.uint16))
+    assert np.all((got[nan] & 0x7f80) == 0x7f80) and np.all((got[nan] & 0x40) != 0)
+    # a tie rounds to the even neighbour: 1 + 2^-8 (between 1 and 1 + 2^-7) -> 1; the odd one up
+    assert oracle.f32_to_bf16_rne(np.array([1 + 2.0 ** -8], np.float32))[0] == 0x3f80
+    assert oracle.f32_to_bf16_rne(np.array([1 + 3 * 2.0 ** -8], np.float32))[0] == 0x3f82
+    for h in range(1 << 16):
+        f = np.float32(oracle.bf16_to_f32(h))
+        if np.isnan(f):
+            assert (h & 0x7f80) == 0x7f80 and (h & 0x7f) != 0
+        else:
+            assert int(f.view(np.uint32)) == h << 16, h
+
+
 def test_f16_encode_golden():
     """Hand-derived codes (ties, carries, subnormals, overflow) kept in tests/golden."""
     import json

@@ -128,7 +128,7 @@ struct MkParams {
     uint32_t lm_rows;              // LM-head rows per workgroup
     uint32_t lm_tile_rows;         // rows per LDS tile
     uint32_t trace_slots;          // phase timestamps per workgroup (0: tracing off)
-    uint32_t kv_f16;               // KV cache entries as fp16 (2 bytes)
+    uint32_t kv16;               // KV cache entries: 0 fp32, 1 fp16, 2 bf16
     uint32_t fuse_hist;            // histories up to this length run the fused attention + O phase (0: never)
     uint32_t nbc;                  // workgroups of the fused phase (whole groups of H)
     uint32_t sh_o, sh_f;           // x_o / x_f layout: 2^sh rows per 64-byte line (2: one producer's
@@ -687,9 +687,10 @@ constexpr uint32_t kBLongChunk = 128;              // chunks at least this long 
 // Publishes the unnormalised partial {acc[hd] of head h, m, l} of (c, h).
 // Inlined into the kernel: as a call it would save and restore callee-saved registers through
 // scratch.
-template <bool KVH, bool fused>
+template <typename KE, bool fused>
 __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t pos, uint32_t tagb, bool tr) {
 #pragma clang fp contract(off)
+    constexpr bool KVH = sizeof(KE) == 2;   // 16-bit entries: KE is _Float16 or __bf16
     MK_LOCALS;
     MK_UNIFORM(l);
     MK_UNIFORM(tagb);
@@ -745,7 +746,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     float* qsh = m.u + kBMaxWaves * hd;            // [3][hd] q, k, v handed from the poller to the workers
     int fail = 0;
     // K/V cache of this block (device-coherent accesses)
-    constexpr uint32_t esz = KVH ? 2u : 4u;   // fp16 entries: 8 bytes per lane and position
+    constexpr uint32_t esz = KVH ? 2u : 4u;   // 16-bit entries: 8 bytes per lane and position
     const uint32_t kv_bytes = Ly.slots * hd * esz;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(Ly.kc, 0, kv_bytes, kRsrcFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(Ly.vc, 0, kv_bytes, kRsrcFlags);
@@ -763,7 +764,7 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     };
     // this lane's four dims of a cached position, as loaded (fp32 bits, or four fp16 halves
     // that are converted where they are used, so the prefetch of the next group does not wait)
-    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    typedef KE half4_t __attribute__((ext_vector_type(4)));
     using KvReg = typename std::conditional<KVH, v2u, v4u>::type;
     auto kv_ld = [&](__amdgpu_buffer_rsrc_t r, int off) -> KvReg {
         if constexpr (KVH) return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCoherent);
@@ -797,10 +798,10 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
     const bool appender = (fused ? w == 0u : h == 0u) && c1 == pos + 1u && (shared_q ? dok : uw == 0u);
     auto append = [&](const float (&k)[4], const float (&v)[4]) {
         const uint32_t so = ((pos % Ly.slots) * hd + dl) * esz;
-        if constexpr (KVH) {   // k and v are already fp16 values: the conversion is exact
+        if constexpr (KVH) {   // k and v are already 16-bit values: the conversion is exact
             auto pack = [](float a, float b) {
-                return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
-                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+                return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<KE>(a))) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<KE>(b))) << 16);
             };
             __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(k[0], k[1]), pack(k[2], k[3])}, rk, static_cast<int>(so), 0,
                                                   kCoherent);
@@ -870,8 +871,8 @@ __device__ __attribute__((always_inline)) bool mk_phase_b(uint32_t l, uint32_t p
         if constexpr (KVH) {   // the current position's key and value as the cache will hold them
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e) {
-                k[e] = static_cast<float>(static_cast<_Float16>(k[e]));
-                v[e] = static_cast<float>(static_cast<_Float16>(v[e]));
+                k[e] = static_cast<float>(static_cast<KE>(k[e]));
+                v[e] = static_cast<float>(static_cast<KE>(v[e]));
             }
         }
         if (shared_q && dlive) {
@@ -1385,7 +1386,7 @@ __device__ __attribute__((noinline)) void mk_embed(uint32_t token) {
     __syncthreads();   // the next residual fold reads h before its first barrier
 }
 
-template <int SD, int SA, int SF, int EP, bool KVH>
+template <int SD, int SA, int SF, int EP, typename KE>
 __global__ void __launch_bounds__(kMkThreads, 1)
 k_decode(uint32_t nsteps, uint32_t tag0) {
     const uint32_t w = blockIdx.x;
@@ -1452,8 +1453,8 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
             // register save/restore through scratch) entirely. Short histories run B fused
             // with the O projection on the first nbc workgroups, and no C.
             const bool fz = mk_fused(g_mk_layers[l].slots, s);
-            if (fz) ok = ok && (w >= g_mk.nbc || mk_phase_b<KVH, true>(l, s, tagb, tr));
-            else ok = ok && (!mk_in_b(l, s) || mk_phase_b<KVH, false>(l, s, tagb, tr));
+            if (fz) ok = ok && (w >= g_mk.nbc || mk_phase_b<KE, true>(l, s, tagb, tr));
+            else ok = ok && (!mk_in_b(l, s) || mk_phase_b<KE, false>(l, s, tagb, tr));
             MK_TRACE(5u * l + 2u);
             ok = ok && (fz || w >= g_mk.nc || mk_phase_c<SA>(l, s, tagb, tr));
             MK_TRACE(5u * l + 3u);
@@ -1512,13 +1513,14 @@ k_decode(uint32_t nsteps, uint32_t tag0) {
 struct MkFns {
     const void* f32 = nullptr;
     const void* f16 = nullptr;
+    const void* bf16 = nullptr;
 };
 
 struct MkState {
     MkParams P{};
     std::vector<MkLayer> layers;   // host image of g_mk_layers
     uint64_t version = 1;          // bumped whenever P changes
-    MkFns fns{};                   // k_decode for fp32 and fp16 KV entries
+    MkFns fns{};                   // k_decode for fp32, fp16 and bf16 KV entries
     size_t lds_bytes = 0;
     uint32_t grid = 0;
     uint32_t trace_slots = 0;      // slots per workgroup when tracing is enabled
@@ -1536,8 +1538,9 @@ CoopSlot& coop_slot(int device) {
 
 template <int SD, int SA, int SF, int EP>
 static MkFns mk_fn() {
-    return MkFns{reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP, false>),
-                 reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP, true>)};
+    return MkFns{reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP, float>),
+                 reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP, _Float16>),
+                 reinterpret_cast<const void*>(&k_decode<SD, SA, SF, EP, __bf16>)};
 }
 
 // Row-slot widths of the three matvec input lengths (d, H * head_dim, FFN) and the residual
@@ -1726,7 +1729,7 @@ int mk_setup(vrt_g3* g) {
     P.logits = g->P.logits;
     P.hidden = g->P.hidden;
 
-    for (const void* fn : {fns.f32, fns.f16}) {   // both KV element types must fit a CU
+    for (const void* fn : {fns.f32, fns.f16, fns.bf16}) {   // every KV element type must fit a CU
         int per_cu = 0;
         VRT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kMkThreads, 0));
         if (per_cu < 1) { mk_destroy(g); return VRT_OK; }
@@ -1750,9 +1753,9 @@ int mk_set_trace(vrt_g3* g, bool on) {
     return VRT_OK;
 }
 
-int mk_set_kv_f16(vrt_g3* g, bool on) {
+int mk_set_kv_format(vrt_g3* g, uint32_t fmt) {
     if (!g->mk) return VRT_OK;
-    g->mk->P.kv_f16 = on ? 1u : 0u;
+    g->mk->P.kv16 = fmt;
     ++g->mk->version;
     return VRT_OK;
 }
@@ -1840,7 +1843,7 @@ int mk_run(vrt_g3* g, uint32_t nsteps) {
         ds.version[kCoopMk] = mk->version;
     }
     void* args[] = {&nsteps, &tag0};
-    const hipError_t le = hipLaunchCooperativeKernel(mk->P.kv_f16 ? mk->fns.f16 : mk->fns.f32, dim3(mk->grid),
+    const hipError_t le = hipLaunchCooperativeKernel(mk->P.kv16 == 2u ? mk->fns.bf16 : (mk->P.kv16 ? mk->fns.f16 : mk->fns.f32), dim3(mk->grid),
                                                      dim3(kMkThreads), args, 0, stream);
     if (le == hipErrorIllegalState || le == hipErrorCooperativeLaunchTooLarge) {
         // The device refuses the cooperative launch (on this stack: while another live process

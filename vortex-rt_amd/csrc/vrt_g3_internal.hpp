@@ -31,7 +31,7 @@ struct LmPartial {
 struct G3Params {
     uint32_t d, H, hd, F, V, L, ctx_len, eos;
     float eps, emb_scale, attn_scale;
-    uint32_t kv_f16;      // KV cache entries as fp16 (VRT_G3_OPT_KV_F16)
+    uint32_t kv16;        // KV cache entries: 0 fp32, 1 fp16, 2 bf16 (VRT_G3_OPT_KV_F16 / _KV_BF16)
     const uint8_t* arena_end;
     const uint8_t* tok_embd;
     G3State* st;
@@ -58,7 +58,7 @@ struct G3Params {
 struct LayerParams {
     const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
     const float *attn_norm, *q_norm, *k_norm, *post_attn, *ffn_norm, *post_ffw;
-    float* kc;            // [slots][hd] fp32, or fp16 in the first half of the buffer (kv_f16)
+    float* kc;            // [slots][hd] fp32, or 16-bit entries in the first half of the buffer (kv16 != 0)
     float* vc;
     uint32_t slots;       // KV slots: window for local layers, context_length otherwise
     uint32_t global;
@@ -176,7 +176,7 @@ int mk_clear_abort(vrt_g3* g);
 int mk_read_abort(vrt_g3* g, uint32_t* dst);
 int mk_read_exchange(vrt_g3* g, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int mk_set_trace(vrt_g3* g, bool on);
-int mk_set_kv_f16(vrt_g3* g, bool on);
+int mk_set_kv_format(vrt_g3* g, uint32_t fmt);
 // Batched prefill (vrt_prefill.hip): workspace for up to max_t positions, and one prefill of T
 // positions from position 0 whose last position runs g3_enqueue_lm.
 int pf_setup(vrt_g3* g, uint32_t max_t);
@@ -209,6 +209,6 @@ void tk_destroy(vrt_g3* g);
 int tk_read_abort(vrt_g3* g, uint32_t* dst);
 int tk_clear_abort(vrt_g3* g);
 int tk_set_trace(vrt_g3* g, bool on);
-int tk_set_kv_f16(vrt_g3* g, bool on);
+int tk_set_kv_format(vrt_g3* g, uint32_t fmt);
 int tk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_t* slots);
 }  // namespace vrt

@@ -239,24 +239,25 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
         }
         __syncthreads();
     }
-    // fp16 KV: the current position's key and value as the cache will hold them
-    if (P.kv_f16) {
+    // 16-bit KV: the current position's key and value as the cache will hold them
+    const uint32_t fmt = P.kv16;
+    if (fmt) {
         for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
-            sk[i] = static_cast<float>(static_cast<_Float16>(sk[i]));
-            sv[i] = static_cast<float>(static_cast<_Float16>(sv[i]));
+            sk[i] = kv16_float(kv16_bits(sk[i], fmt), fmt);
+            sv[i] = kv16_float(kv16_bits(sv[i], fmt), fmt);
         }
         __syncthreads();
     }
     // KV append (slot of this position); the current position is read from LDS below
     const uint32_t slot_cur = pos % Lc.slots;
-    _Float16* kh = reinterpret_cast<_Float16*>(Lc.kc);
-    _Float16* vh = reinterpret_cast<_Float16*>(Lc.vc);
+    uint16_t* kh = reinterpret_cast<uint16_t*>(Lc.kc);
+    uint16_t* vh = reinterpret_cast<uint16_t*>(Lc.vc);
     if (blockIdx.x == 0)
         for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
             const uint64_t o = static_cast<uint64_t>(slot_cur) * hd + i;
-            if (P.kv_f16) {
-                kh[o] = static_cast<_Float16>(sk[i]);
-                vh[o] = static_cast<_Float16>(sv[i]);
+            if (fmt) {
+                kh[o] = kv16_bits(sk[i], fmt);
+                vh[o] = kv16_bits(sv[i], fmt);
             } else {
                 Lc.kc[o] = sk[i];
                 Lc.vc[o] = sv[i];
@@ -274,7 +275,7 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t i = lane + 64u * j;
-                kr[j] = i >= hd ? 0.0f : (t == pos ? sk[i] : (P.kv_f16 ? static_cast<float>(kh[row + i]) : Lc.kc[row + i]));
+                kr[j] = i >= hd ? 0.0f : (t == pos ? sk[i] : (fmt ? kv16_float(kh[row + i], fmt) : Lc.kc[row + i]));
             }
             for (uint32_t h = 0; h < H; ++h) {
                 float p = 0.0f;
@@ -307,7 +308,7 @@ __global__ void __launch_bounds__(kThreads) k_attn(G3Params P, LayerParams Lc) {
             float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             for (uint32_t t = c0; t < c1; ++t) {
                 const uint64_t vo = static_cast<uint64_t>(t % Lc.slots) * hd + i;
-                const float vv = (t == pos) ? sv[i] : (P.kv_f16 ? static_cast<float>(vh[vo]) : Lc.vc[vo]);
+                const float vv = (t == pos) ? sv[i] : (fmt ? kv16_float(vh[vo], fmt) : Lc.vc[vo]);
 #pragma unroll
                 for (uint32_t h = 0; h < 8u; ++h)
                     if (h < H) acc[h] += sc[h * Lc.chunk_max + (t - c0)] * vv;
@@ -1119,6 +1120,22 @@ extern "C" int vrt_g3_reset(vrt_g3* g) {
     return VRT_OK;
 }
 
+// KV cache entries: 0 fp32, 1 fp16, 2 bf16. The kernels read the format from their parameter
+// blocks: the captured graph (which holds G3Params by value) is dropped, the persistent kernels'
+// blocks re-uploaded, the cache reset.
+static int g3_set_kv_format(vrt_g3* g, uint32_t fmt) {
+    if (g->P.kv16 == fmt) return VRT_OK;
+    VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
+    g->P.kv16 = fmt;
+    if (g->graph) {
+        (void)hipGraphExecDestroy(g->graph);
+        g->graph = nullptr;
+    }
+    if (int rc = mk_set_kv_format(g, fmt)) return rc;
+    if (int rc = tk_set_kv_format(g, fmt)) return rc;
+    return vrt_g3_reset(g);
+}
+
 extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
     VRT_REQUIRE(g, "vrt_g3_set_option: null executor");
     switch (option) {
@@ -1158,21 +1175,8 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
         }
         return VRT_OK;
     }
-    case VRT_G3_OPT_KV_F16: {
-        // the kernels read the flag from their parameter blocks: the captured graph (which holds
-        // G3Params by value) is dropped, the persistent kernel's block re-uploaded, the cache reset
-        const uint32_t on = value != 0 ? 1u : 0u;
-        if (g->P.kv_f16 == on) return VRT_OK;
-        VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
-        g->P.kv_f16 = on;
-        if (g->graph) {
-            (void)hipGraphExecDestroy(g->graph);
-            g->graph = nullptr;
-        }
-        if (int rc = mk_set_kv_f16(g, on != 0)) return rc;
-        if (int rc = tk_set_kv_f16(g, on != 0)) return rc;
-        return vrt_g3_reset(g);
-    }
+    case VRT_G3_OPT_KV_F16: return g3_set_kv_format(g, value != 0 ? 1u : (g->P.kv16 == 1u ? 0u : g->P.kv16));
+    case VRT_G3_OPT_KV_BF16: return g3_set_kv_format(g, value != 0 ? 2u : (g->P.kv16 == 2u ? 0u : g->P.kv16));
     case VRT_G3_OPT_QUERY_Q8_LANES: return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_Q8_LANES is read with vrt_g3_get_option");
     case VRT_G3_OPT_QUERY_TEAM_POSITIONS:
         return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_TEAM_POSITIONS is read with vrt_g3_get_option");
@@ -1186,7 +1190,8 @@ extern "C" int vrt_g3_get_option(vrt_g3* g, uint32_t option, uint32_t* value) {
     case VRT_G3_OPT_USE_GRAPH: *value = g->use_graph ? 1u : 0u; return VRT_OK;
     case VRT_G3_OPT_PERSISTENT: *value = g->use_persistent ? 1u : 0u; return VRT_OK;
     case VRT_G3_OPT_TEAM: *value = g->use_team ? 1u : 0u; return VRT_OK;
-    case VRT_G3_OPT_KV_F16: *value = g->P.kv_f16; return VRT_OK;
+    case VRT_G3_OPT_KV_F16: *value = g->P.kv16 == 1u ? 1u : 0u; return VRT_OK;
+    case VRT_G3_OPT_KV_BF16: *value = g->P.kv16 == 2u ? 1u : 0u; return VRT_OK;
     case VRT_G3_OPT_FUSION: *value = g->fusion ? 1u : 0u; return VRT_OK;
     case VRT_G3_OPT_Q8_LANES: *value = g->q8_lanes; return VRT_OK;
     case VRT_G3_OPT_QUERY_Q8_LANES:

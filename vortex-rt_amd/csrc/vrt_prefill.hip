@@ -456,8 +456,8 @@ __device__ __forceinline__ uint64_t pf_vswz(uint32_t t, uint32_t d, uint32_t hd)
 // 1045-1104), NeoX RoPE at position t (:1371-1424), in place (q also as f16 hi/lo rows of
 // qhi/qlo); then k and v go to the KV cache slot t % slots when position t is still in the
 // window after the prompt (the serial loop's eviction leaves exactly those, :1590-1600); with
-// kv_f16 the cache holds fp16 and k and v are rounded to fp16 first (the attention below then
-// sees the cached values, as the serial loop does). The attention operands as f16 hi/lo: k and
+// kv16 (1 fp16, 2 bf16) the cache holds 16-bit entries and k and v are rounded to them first
+// (the attention below then sees the cached values, as the serial loop does). The attention operands as f16 hi/lo: k and
 // v in the pf_kswz / pf_vswz tile layouts. One
 // workgroup per position t < Tp: those with t >= T write the zero padding keys and values
 // (keys past the prompt are masked, and zero values keep the masked products zero).
@@ -469,7 +469,7 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
                                                             const float* cos_t, const float* sin_t, float eps,
                                                             float* kc, float* vc, uint32_t slots, _Float16* qhi,
                                                             _Float16* qlo, _Float16* khi, _Float16* klo, _Float16* vhi,
-                                                            _Float16* vlo, uint32_t kv_f16, uint32_t p0, uint32_t qo) {
+                                                            _Float16* vlo, uint32_t kv16, uint32_t p0, uint32_t qo) {
 #pragma clang fp contract(off)
     __shared__ float xs[kPfQkMaxWaves][256];
     const uint32_t t = blockIdx.x;           // row of the segment; position p0 + t, key coordinate qo + t
@@ -537,12 +537,12 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
             if (hh < H) {   // the query, [T][H * hd]
                 const uint64_t o = static_cast<uint64_t>(t) * H * hd + hh * hd + i;
                 pf_split(y2, qhi + o, qlo + o);
-            } else {   // fp16 KV: the key as the cache holds it, for the cache and the attention
-                const float kk = kv_f16 ? static_cast<float>(static_cast<_Float16>(y2)) : y2;
+            } else {   // 16-bit KV: the key as the cache holds it, for the cache and the attention
+                const float kk = kv16 ? kv16_float(kv16_bits(y2, kv16), kv16) : y2;
                 const uint64_t o = pf_kswz(kt, i, hd);
                 pf_split(kk, khi + o, klo + o);
                 if (keep) {
-                    if (kv_f16) reinterpret_cast<_Float16*>(kc)[slot + i] = static_cast<_Float16>(kk);
+                    if (kv16) reinterpret_cast<uint16_t*>(kc)[slot + i] = kv16_bits(kk, kv16);
                     else kc[slot + i] = kk;
                 }
             }
@@ -551,9 +551,9 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
     }
     for (uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {   // v is not normed
         const float vv0 = i == vi ? vr : row[(H + 1u) * hd + i];
-        const float vv = kv_f16 ? static_cast<float>(static_cast<_Float16>(vv0)) : vv0;
+        const float vv = kv16 ? kv16_float(kv16_bits(vv0, kv16), kv16) : vv0;
         if (keep) {
-            if (kv_f16) reinterpret_cast<_Float16*>(vc)[slot + i] = static_cast<_Float16>(vv);
+            if (kv16) reinterpret_cast<uint16_t*>(vc)[slot + i] = kv16_bits(vv, kv16);
             else vc[slot + i] = vv;
         }
         const uint64_t o = pf_vswz(kt, i, hd);
@@ -562,18 +562,18 @@ __global__ void __launch_bounds__(kPfQkMaxWaves * 64) k_pf_qk(float* qkv, uint32
 }
 
 // A segment's history for the attention: key coordinates j < nh hold positions kb + j, read
-// from the block's KV cache (ring slot (kb + j) % slots, fp32 or fp16 entries as the cache
+// from the block's KV cache (ring slot (kb + j) % slots, fp32 or 16-bit entries as the cache
 // holds them) and written in the pf_kswz / pf_vswz layouts as f16 hi/lo, as k_pf_qk writes a
 // segment's own rows. One workgroup per key coordinate.
-__global__ void __launch_bounds__(kPfThreads) k_pf_kv_hist(const float* kc, const float* vc, uint32_t slots, uint32_t kv_f16,
+__global__ void __launch_bounds__(kPfThreads) k_pf_kv_hist(const float* kc, const float* vc, uint32_t slots, uint32_t kv16,
                                                           uint32_t kb, uint32_t nh, uint32_t hd, _Float16* khi,
                                                           _Float16* klo, _Float16* vhi, _Float16* vlo) {
     const uint32_t j = blockIdx.x;
     if (j >= nh) return;
     const uint64_t slot = static_cast<uint64_t>((kb + j) % slots) * hd;
     for (uint32_t i = threadIdx.x; i < hd; i += kPfThreads) {
-        const float k = kv_f16 ? static_cast<float>(reinterpret_cast<const _Float16*>(kc)[slot + i]) : kc[slot + i];
-        const float v = kv_f16 ? static_cast<float>(reinterpret_cast<const _Float16*>(vc)[slot + i]) : vc[slot + i];
+        const float k = kv16 ? kv16_float(reinterpret_cast<const uint16_t*>(kc)[slot + i], kv16) : kc[slot + i];
+        const float v = kv16 ? kv16_float(reinterpret_cast<const uint16_t*>(vc)[slot + i], kv16) : vc[slot + i];
         const uint64_t ko = pf_kswz(j, i, hd), vo = pf_vswz(j, i, hd);
         pf_split(k, khi + ko, klo + ko);
         pf_split(v, vhi + vo, vlo + vo);
@@ -1463,7 +1463,7 @@ int pf_run(vrt_g3* g, uint32_t T, uint32_t p0, bool final) {
         if (qo != 0u) {
             const float* kc = Ly.kc;
             const float* vc = Ly.vc;
-            uint32_t slots = Ly.slots, kvf = P.kv_f16, kb_ = kb;
+            uint32_t slots = Ly.slots, kvf = P.kv16, kb_ = kb;
             _Float16* khi = static_cast<_Float16*>(p.khi);
             _Float16* klo = static_cast<_Float16*>(p.klo);
             _Float16* vhi = static_cast<_Float16*>(p.vhi);
@@ -1485,7 +1485,7 @@ int pf_run(vrt_g3* g, uint32_t T, uint32_t p0, bool final) {
             _Float16* klo = static_cast<_Float16*>(p.klo);
             _Float16* vhi = static_cast<_Float16*>(p.vhi);
             _Float16* vlo = static_cast<_Float16*>(p.vlo);
-            uint32_t kvf = P.kv_f16, p0_ = p0, qo_ = qo;
+            uint32_t kvf = P.kv16, p0_ = p0, qo_ = qo;
             void* args[] = {&big, &T, &H, &hd, &qn, &kn, &ct, &sn, &eps, &kc, &vc, &slots, &ahi, &alo, &khi, &klo, &vhi, &vlo,
                             &kvf, &p0_, &qo_};
             const uint32_t waves = std::min(H + 1u, kPfQkMaxWaves);

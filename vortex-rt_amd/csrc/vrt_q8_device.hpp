@@ -139,6 +139,15 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);   // v_cvt_f32_f16, exact
 }
 
+// 16-bit KV cache entries, fmt 1 fp16 and 2 bf16: IEEE round to nearest even into the entry
+// (v_cvt_f16_f32 / v_cvt_pk_bf16_f32), exact back to fp32.
+__device__ __forceinline__ uint16_t kv16_bits(float x, uint32_t fmt) {
+    return fmt == 2u ? __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)) : __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+__device__ __forceinline__ float kv16_float(uint16_t b, uint32_t fmt) {
+    return fmt == 2u ? __uint_as_float(static_cast<uint32_t>(b) << 16) : static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
 // ---- Q8_0 block loads ------------------------------------------------------------------
 
 struct Q8Raw {

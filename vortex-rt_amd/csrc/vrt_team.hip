@@ -129,7 +129,7 @@ struct Params {
     uint32_t nwg, tsize;           // workgroups; workgroups per team
     uint32_t lm_tile_rows;
     uint32_t trace_slots;          // stamps per workgroup (0: tracing off)
-    uint32_t kv_f16;
+    uint32_t kv16;                 // KV cache entries: 0 fp32, 1 fp16, 2 bf16
     uint32_t hist_lds;             // history positions past the registers held in LDS (multiple of 8)
     uint32_t poll_sleep;           // back-off between unsuccessful polls (s_sleep units of 64 clocks)
     Lds lds;
@@ -1483,7 +1483,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
 // eight positions (scores reduced and transposed together: lane l holds position l & 7's), the
 // waves' partials are merged in wave order, att = acc / l (:1602-1696), and the workgroup's Wo
 // rows over head h's blocks are published as x_o[h][row].
-template <class C, bool KVH>
+template <class C, typename KE>
 __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t tag0) {
 #pragma clang fp contract(off)
     nsteps = __builtin_amdgcn_readfirstlane(nsteps);
@@ -1507,8 +1507,9 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
     float* kv_s = lds<float>(g_tk.lds.kvc);        // [2][hd] the current position's k, v
     float* part = lds<float>(g_tk.lds.part);       // [kWaves][hd], then m [kWaves], l [kWaves]
     const LimbLds Lx{lds<int8_t>(g_tk.lds.la), lds<int8_t>(g_tk.lds.lb), lds<int8_t>(g_tk.lds.lc), lds<float>(g_tk.lds.ls)};
+    constexpr bool KVH = sizeof(KE) == 2;   // 16-bit entries: KE is _Float16 or __bf16
     constexpr uint32_t esz = KVH ? 2u : 4u;
-    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    typedef KE half4_t __attribute__((ext_vector_type(4)));
     using KvReg = typename std::conditional<KVH, v2u, v4u>::type;
     auto kv_el = [](const KvReg& v, uint32_t e) -> float {
         if constexpr (KVH) return static_cast<float>(__builtin_bit_cast(half4_t, v)[e]);
@@ -1635,8 +1636,8 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                     if (!isq) {
 #pragma unroll
                         for (uint32_t e = 0; e < 4u; ++e) {
-                            xv[e] = static_cast<float>(static_cast<_Float16>(xv[e]));
-                            vv[e] = static_cast<float>(static_cast<_Float16>(vv[e]));
+                            xv[e] = static_cast<float>(static_cast<KE>(xv[e]));
+                            vv[e] = static_cast<float>(static_cast<KE>(vv[e]));
                         }
                     }
                 }
@@ -1650,8 +1651,8 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                     const int so = static_cast<int>(((pos % Ly.slots) * hd + dl) * esz);
                     if constexpr (KVH) {
                         auto pack = [](float a, float b) {
-                            return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
-                                   (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+                            return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<KE>(a))) |
+                                   (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<KE>(b))) << 16);
                         };
                         __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(xv[0], xv[1]), pack(xv[2], xv[3])}, rk, so, 0, kCoherent);
                         __builtin_amdgcn_raw_buffer_store_b64(v2u{pack(vv[0], vv[1]), pack(vv[2], vv[3])}, rv, so, 0, kCoherent);
@@ -1680,8 +1681,8 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                     const float4 v4 = dlive ? *reinterpret_cast<const float4*>(kv_s + hd + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                     if constexpr (KVH) {
                         auto pack = [](float a, float b) {
-                            return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
-                                   (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+                            return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<KE>(a))) |
+                                   (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<KE>(b))) << 16);
                         };
                         kc = v2u{pack(k4.x, k4.y), pack(k4.z, k4.w)};
                         vc = v2u{pack(v4.x, v4.y), pack(v4.z, v4.w)};
@@ -1739,20 +1740,23 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                 if (hist > kHistMax && hist_lds != 0u) {
                     __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's direct-to-LDS rows
                     const uint32_t lo_b = dlive ? dl * esz : 0u;
+                    // the LDS rows replace the register rows (consumed above; the next block's
+                    // are loaded after this block)
                     for (uint32_t b0 = kHistMax + kBPos * wave; b0 < hist; b0 += kHistMax) {
-                        KvReg kk[kBPos], vv[kBPos];
 #pragma unroll
                         for (uint32_t i = 0; i < kBPos; ++i) {
                             const uint32_t idx = b0 + i;
                             const uint32_t so = min(idx - kHistMax, hist_lds - 1u) * rowb + lo_b;
                             const KvReg kl = *reinterpret_cast<const KvReg*>(kvk + so);
                             const KvReg vl = *reinterpret_cast<const KvReg*>(kvv + so);
-                            // slots past the history hold stale bytes: zeros keep their (masked)
-                            // terms finite, as the registers' out-of-range loads do
-                            kk[i] = idx == ci ? kc : (idx < hist ? kl : KvReg{});
-                            vv[i] = idx == ci ? vc : (idx < hist ? vl : KvReg{});
+                            // slots past the history hold stale bytes: their scores are masked
+                            // (each position's score sums its own products only), and zero values
+                            // keep their weight-0 terms finite, as the registers' out-of-range
+                            // loads do
+                            kr[i] = idx == ci ? kc : kl;
+                            vr[i] = idx == ci ? vc : (idx < hist ? vl : KvReg{});
                         }
-                        pass(kk, vv, b0);
+                        pass(kr, vr, b0);
                     }
                 }
                 if (dlive) *reinterpret_cast<float4*>(part + wave * hd + dl) = make_float4(wacc[0], wacc[1], wacc[2], wacc[3]);
@@ -2033,11 +2037,11 @@ __device__ __attribute__((always_inline)) void team_e(uint32_t nsteps, uint32_t 
     }
 }
 
-template <class C, bool KVH>
+template <class C, typename KE>
 __global__ void __launch_bounds__(kThreads, 1) k_team(uint32_t nsteps, uint32_t tag0) {
     switch (team_of(blockIdx.x)) {
     case 0: team_a<C>(nsteps, tag0); break;
-    case 1: team_b<C, KVH>(nsteps, tag0); break;
+    case 1: team_b<C, KE>(nsteps, tag0); break;
     case 2: team_d<C>(nsteps, tag0); break;
     default: team_e<C>(nsteps, tag0); break;
     }
@@ -2052,6 +2056,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_team(uint32_t nsteps, uint32_t 
 struct TkFns {
     const void* f32 = nullptr;
     const void* f16 = nullptr;
+    const void* bf16 = nullptr;
     uint32_t lm_blocks = 0;   // blocks per row of the matrix-core LM head (0: row-slot LM head)
 };
 
@@ -2063,15 +2068,15 @@ struct TkState {
     uint32_t grid = 0;
     uint32_t trace_slots = 0;
     uint32_t pos_limit = 0;        // steps at positions below this run here
-    uint32_t hist_lds[2] = {0, 0}; // LDS history rows past the registers: fp32, fp16 entries
+    uint32_t hist_lds[2] = {0, 0}; // LDS history rows past the registers: fp32, 16-bit entries
     bool registered = false;
     std::vector<void*> allocs;
 };
 
 template <class C>
 static TkFns tk_fn() {
-    return TkFns{reinterpret_cast<const void*>(&tk::k_team<C, false>), reinterpret_cast<const void*>(&tk::k_team<C, true>),
-                 static_cast<uint32_t>(C::LMB)};
+    return TkFns{reinterpret_cast<const void*>(&tk::k_team<C, float>), reinterpret_cast<const void*>(&tk::k_team<C, _Float16>),
+                 reinterpret_cast<const void*>(&tk::k_team<C, __bf16>), static_cast<uint32_t>(C::LMB)};
 }
 
 // Instantiated shapes: (d, heads x head_dim, FFN) -> row slots, passes and residual pairs.
@@ -2173,7 +2178,7 @@ int tk_setup(vrt_g3* g) {
         P.lm_tile_rows = static_cast<uint32_t>(std::min<uint64_t>((c.vocab_size + nwg - 1u) / nwg, tr));
     }
     if (P.lm_tile_rows == 0u) { tk_destroy(g); return VRT_OK; }
-    P.kv_f16 = g->P.kv_f16;
+    P.kv16 = g->P.kv16;
     P.poll_sleep = 1u;   // measured at positions 8..27: 0 and 1 fastest, 2 +1%, 8 +5%, 16 +10%
 
     // LDS layout
@@ -2257,14 +2262,14 @@ int tk_setup(vrt_g3* g) {
     P.results = g->P.results;
     P.logits = g->P.logits;
     P.hidden = g->P.hidden;
-    for (const void* fn : {fns.f32, fns.f16}) {
+    for (const void* fn : {fns.f32, fns.f16, fns.bf16}) {
         int per_cu = 0;
         VRT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0));
         if (per_cu < 1) { tk_destroy(g); return VRT_OK; }
     }
     tk->fns = fns;
     tk->grid = nwg;
-    P.hist_lds = tk->hist_lds[P.kv_f16 ? 1 : 0];
+    P.hist_lds = tk->hist_lds[P.kv16 ? 1 : 0];
     tk->pos_limit = std::min(c.context_length, kHistMax + P.hist_lds);
     g->tk_tag = 1u;
     {
@@ -2283,10 +2288,10 @@ int tk_set_trace(vrt_g3* g, bool on) {
     return VRT_OK;
 }
 
-int tk_set_kv_f16(vrt_g3* g, bool on) {
+int tk_set_kv_format(vrt_g3* g, uint32_t fmt) {
     if (!g->tk) return VRT_OK;
-    g->tk->P.kv_f16 = on ? 1u : 0u;
-    g->tk->P.hist_lds = g->tk->hist_lds[on ? 1 : 0];
+    g->tk->P.kv16 = fmt;
+    g->tk->P.hist_lds = g->tk->hist_lds[fmt != 0u ? 1 : 0];
     g->tk->pos_limit = std::min(g->cfg.context_length, tk::kHistMax + g->tk->P.hist_lds);
     ++g->tk->version;
     return VRT_OK;
@@ -2346,7 +2351,7 @@ int tk_run(vrt_g3* g, uint32_t nsteps) {
         ds.version[kCoopTeam] = tk->version;
     }
     void* args[] = {&nsteps, &tag0};
-    const hipError_t le = hipLaunchCooperativeKernel(tk->P.kv_f16 ? tk->fns.f16 : tk->fns.f32, dim3(tk->grid),
+    const hipError_t le = hipLaunchCooperativeKernel(tk->P.kv16 == 2u ? tk->fns.bf16 : (tk->P.kv16 ? tk->fns.f16 : tk->fns.f32), dim3(tk->grid),
                                                      dim3(tk::kThreads), args, 0, stream);
     if (le == hipErrorIllegalState || le == hipErrorCooperativeLaunchTooLarge) {
         (void)hipGetLastError();

@@ -21,6 +21,7 @@ OPT_PERSISTENT = 2
 OPT_QUERY_PERSISTENT = 3
 OPT_TRACE = 4
 OPT_KV_F16 = 5
+OPT_KV_BF16 = 12
 OPT_TEAM = 6
 OPT_QUERY_TEAM = 7
 OPT_FUSION = 8
@@ -360,7 +361,7 @@ class Gemma3:
         h = C.c_void_p()
         check(lib().vrt_g3_create(ctx.h, C.byref(desc), C.byref(h)))
         self.h = h.value
-        self.kv_f16 = False
+        self.kv_f16 = False    # 16-bit KV entries (fp16 or bf16)
         self._batches = weakref.WeakSet()   # batched decoders over this executor: closed first
         ctx._children.add(self)
         self._keep.clear()
@@ -417,9 +418,40 @@ class Gemma3:
         return self.get_option(OPT_QUERY_Q8_LANES)
 
     def set_kv_f16(self, on: bool):
-        """fp16 KV cache (keys and values rounded to fp16 as they enter it); resets the cache."""
-        check(lib().vrt_g3_set_option(self.h, OPT_KV_F16, 1 if on else 0))
+        """fp16 KV cache (keys and values rounded to fp16 as they enter it); resets the cache.
+        Off: fp32 entries."""
+        if on:
+            check(lib().vrt_g3_set_option(self.h, OPT_KV_F16, 1))
+        else:
+            self.set_kv_format("f32")
         self.kv_f16 = bool(on)
+
+    def set_kv_bf16(self, on: bool):
+        """bf16 KV cache (keys and values rounded to bfloat16 as they enter it); resets the
+        cache. Off: fp32 entries."""
+        if on:
+            check(lib().vrt_g3_set_option(self.h, OPT_KV_BF16, 1))
+        else:
+            self.set_kv_format("f32")
+        self.kv_f16 = bool(on)
+
+    def set_kv_format(self, fmt: str):
+        """KV cache entries "f32", "f16" or "bf16" (resets the cache when it changes)."""
+        if fmt == "f16":
+            check(lib().vrt_g3_set_option(self.h, OPT_KV_F16, 1))
+        elif fmt == "bf16":
+            check(lib().vrt_g3_set_option(self.h, OPT_KV_BF16, 1))
+        elif fmt == "f32":
+            check(lib().vrt_g3_set_option(self.h, OPT_KV_F16, 0))
+            check(lib().vrt_g3_set_option(self.h, OPT_KV_BF16, 0))
+        else:
+            raise ValueError(f"unknown KV format {fmt!r}")
+        self.kv_f16 = fmt != "f32"
+
+    def kv_format(self) -> str:
+        if self.get_option(OPT_KV_BF16):
+            return "bf16"
+        return "f16" if self.get_option(OPT_KV_F16) else "f32"
 
     def read_trace(self) -> np.ndarray:
         """[nwg, slots] s_memrealtime ticks (100 MHz) of the last persistent launch's first step."""
