@@ -263,18 +263,20 @@ def test_team_kernel_matches_allworkgroup_kernel(ctx, tiny_model):
     assert np.array_equal(tk, mk)
 
 
-def test_team_kernel_history_limit_full_shape(ctx, full_model):
-    """At the Gemma-3-270M shape the team kernel takes histories up to 136 positions with fp32
-    entries (64 in registers, 72 in LDS) and 208 with fp16 or bf16 ones; later steps run on the
-    all-workgroup kernel. Teacher-forced across each limit, team on and off give the same greedy
-    tokens and logits within the tolerance."""
+def test_team_kernel_history_modes_full_shape(ctx, full_model):
+    """At the Gemma-3-270M shape every workgroup of a head holds the whole history on chip up
+    to 136 positions with fp32 entries (64 in registers, 72 in LDS) and 208 with fp16 or bf16
+    ones; longer histories split into 16 chunks per head whose partials the head's workgroups
+    exchange and merge, so the team kernel takes every position. Teacher-forced across the
+    switch, team on and off (the all-workgroup kernel) give the same greedy tokens and logits
+    within the tolerance."""
     g = vrt.Gemma3(ctx, full_model)
     try:
         assert g.team_available()
-        for fmt, limit in (("f32", 136), ("f16", 208), ("bf16", 208)):
+        for fmt, switch in (("f32", 136), ("f16", 208), ("bf16", 208)):
             g.set_kv_format(fmt)
-            assert g.team_positions() == limit, (fmt, g.team_positions())
-            toks = synth.uniform_ids(94, limit + 12, 2, 262144)
+            assert g.team_positions() == int(g.config.context_length), (fmt, g.team_positions())
+            toks = synth.uniform_ids(94, switch + 12, 2, 262144)
             print(f"[g3] full shape, {toks.size} forced steps, {fmt} KV, team on/off", flush=True)
             g.set_team(True)
             a = g.forced(toks, 0)

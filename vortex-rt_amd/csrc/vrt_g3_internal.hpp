@@ -204,7 +204,10 @@ int mk_read_trace(vrt_g3* g, uint64_t* out, uint64_t cap, uint32_t* nwg, uint32_
 // attention histories stay within tk_hist_limit(g) positions (positions < the limit).
 int tk_setup(vrt_g3* g);
 uint32_t tk_pos_limit(const vrt_g3* g);
-int tk_run(vrt_g3* g, uint32_t nsteps);
+uint32_t tk_chunk_from(const vrt_g3* g);
+// chunked: the variant for steps at positions from tk_chunk_from(g) on (histories longer than a
+// workgroup holds on chip); the other one for earlier steps.
+int tk_run(vrt_g3* g, uint32_t nsteps, bool chunked);
 void tk_destroy(vrt_g3* g);
 int tk_read_abort(vrt_g3* g, uint32_t* dst);
 int tk_clear_abort(vrt_g3* g);

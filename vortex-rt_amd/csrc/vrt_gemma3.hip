@@ -844,12 +844,15 @@ static int g3_run_steps(vrt_g3* g, uint32_t n, uint32_t first) {
     if ((g->mk || g->tk) && g->use_persistent && g->fusion && g->q8_lanes == 0u) {
         uint32_t done = 0;
         const uint32_t lim = g->use_team ? tk_pos_limit(g) : 0u;
+        const uint32_t pch = g->use_team ? tk_chunk_from(g) : 0u;   // team steps from here: chunked variant
         int rc = VRT_OK;
-        if (first < lim) {
-            const uint32_t k = std::min(n, lim - first);
-            rc = tk_run(g, k);
+        while (rc == VRT_OK && done < n && first + done < lim) {
+            const uint32_t p = first + done;
+            const bool ch = p >= pch;
+            const uint32_t k = std::min(n - done, (ch ? lim : std::min(lim, pch)) - p);
+            rc = tk_run(g, k, ch);
             if (rc == VRT_OK) {
-                done = k;
+                done += k;
                 g->last_coop = kCoopTeam;
             }
         }

@@ -29,13 +29,15 @@
 // LM head fused with the greedy argmax (as the all-workgroup persistent kernel does), and the
 // next step starts from the argmax partials.
 //
-// Histories. Team B keeps a head's whole history on chip: the first 64 positions in registers
-// (eight waves of eight), the next hist_lds in LDS (direct-to-LDS loads issued with the register
-// loads, one phase ahead; 72 positions of fp32 entries at head_dim 256, 144 of fp16 ones). Each
-// wave runs an online softmax over its eight positions of every 64-position pass. The host sends
-// later positions to the all-workgroup kernel, whose attention splits long histories into
-// chunks. Each head is computed by tsize/H workgroups, each producing its group of Wo rows over
-// that head's columns.
+// Histories. Each head is computed by tsize/H workgroups, each producing its group of Wo rows
+// over that head's columns. While a head's history fits on chip, every one of them attends over
+// all of it: the first 64 positions in registers (eight waves of eight), the next hist_lds in
+// LDS (direct-to-LDS loads issued with the register loads, one phase ahead; 72 positions of fp32
+// entries at head_dim 256, 144 of 16-bit ones). Longer histories split into tsize/H chunks, one
+// per workgroup of the head, laid out the same way (passes past the LDS rows load when they
+// run); the chunks' partials {acc, max, sum} go through x_p and every workgroup of the head
+// merges them in chunk order. Each wave runs an online softmax over its eight positions of every
+// 64-position pass.
 //
 // Buffer reuse without double buffering: every exchange buffer is written once per block, and
 // a team rewrites a buffer for block l + 1 only after consuming data that every reader of the
@@ -82,6 +84,7 @@ constexpr uint32_t kLine = 8;               // tagged words per 64-byte line
 constexpr uint32_t kBPos = 8;               // attention positions per wave
 constexpr uint32_t kHistMax = kWaves * kBPos;   // longest history (positions) a block can attend to
 constexpr uint32_t kMaxHeads = 4;           // query heads (partials summed by team D)
+constexpr uint32_t kPartUnits = 4;          // 16-byte polls per thread of a head's chunk accumulators
 constexpr uint32_t kLmUnits = 3;            // 16-byte LM-head loads per thread per tile
 constexpr uint32_t kLmRing = 4;             // LM-head tile slots in LDS
 constexpr uint32_t kLmAhead = kLmRing - 1u; // tiles in flight while one is computed
@@ -138,6 +141,7 @@ struct Params {
     const float* out_norm;
     const float *cos_l, *sin_l, *cos_g, *sin_g;
     u64 *x_h, *x_qkv, *x_o, *x_hm, *x_g, *x_d, *x_am;   // x_o: [H][d] per-head partials
+    u64* x_p;                      // [H][tsize / H][hd + 8] attention chunk partials {acc, M, l} (chunked histories)
     uint32_t* abort_flag;
     G3State* st;
     uint32_t* tokens;
@@ -163,8 +167,8 @@ __device__ __forceinline__ uint32_t member_of(uint32_t w) { return (w >> 3) * 2u
 
 // tags of block l's buffers in the step whose base is tagb; the argmax partials of that step
 // take tagb + nph (the next step's base, which no buffer of that step uses)
-constexpr uint32_t kTagsPerBlock = 6;
-enum : uint32_t { kTH = 1, kTQkv = 2, kTO = 3, kTHm = 4, kTG = 5, kTD = 6 };
+constexpr uint32_t kTagsPerBlock = 7;
+enum : uint32_t { kTH = 1, kTQkv = 2, kTO = 3, kTHm = 4, kTG = 5, kTD = 6, kTP = 7 };
 __device__ __forceinline__ uint32_t tagof(uint32_t tagb, uint32_t l, uint32_t k) { return tagb + kTagsPerBlock * l + k; }
 
 // ---- tagged exchange ---------------------------------------------------------------------
@@ -1483,7 +1487,7 @@ __device__ __attribute__((always_inline)) void team_a(uint32_t nsteps, uint32_t 
 // eight positions (scores reduced and transposed together: lane l holds position l & 7's), the
 // waves' partials are merged in wave order, att = acc / l (:1602-1696), and the workgroup's Wo
 // rows over head h's blocks are published as x_o[h][row].
-template <class C, typename KE>
+template <class C, typename KE, bool CH>
 __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t tag0) {
 #pragma clang fp contract(off)
     nsteps = __builtin_amdgcn_readfirstlane(nsteps);
@@ -1495,7 +1499,13 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
     const uint32_t half = hd >> 1, nbh = hd >> 5;
     const uint64_t rb_a = static_cast<uint64_t>(qw >> 5) * 34u;
     const uint32_t nph = kTagsPerBlock * L + 1u;
-    const uint32_t h = m % H, grp = m / H, ngrp = ts / H;
+    // head h and row group grp of member m. With an even team half per head count, the H heads
+    // of one group sit on one XCD (member parity = XCD parity): a history chunk's key and value
+    // rows, read by the H workgroups of its group, then come from one L2.
+    const uint32_t ngrp = ts / H;
+    const bool pair = (ts / 2u) % H == 0u;
+    const uint32_t h = pair ? (m >> 1) % H : m % H;
+    const uint32_t grp = pair ? ((m >> 1) / H) * 2u + (m & 1u) : m / H;
     uint32_t o0, o1;
     split_lines(d, ngrp, grp, o0, o1);
     const uint32_t dl = lane * 4u;                 // this lane's 4 head dims
@@ -1515,32 +1525,47 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
         if constexpr (KVH) return static_cast<float>(__builtin_bit_cast(half4_t, v)[e]);
         else return __uint_as_float(v[e]);
     };
-    // History positions 64 .. 64 + hist_lds - 1 sit in LDS: key row of position 64 + j at
-    // kvx + j * rowb, value rows after the hist_lds key rows. LDS pass p >= 1 of wave j covers
-    // positions 64 p + 8 j + i (i < 8); the wave loads exactly those rows (direct-to-LDS, 1 KB
-    // = ppi rows per load, 16 bytes per lane) and is their only reader, so no barrier orders
-    // the loads: a wave waits for its own.
+    // The history of a block is positions [0, hist) by age (index i is position t_first + i,
+    // ring slot (t_first + i) % slots; the current one is hist - 1). A workgroup attends over
+    // its share [hb, he): the whole history while it fits on chip (64 + hist_lds positions),
+    // else chunk grp of ngrp equal chunks, whose partials the head's ngrp workgroups exchange
+    // and merge (x_p). Share positions hb + 64 .. hb + 64 + hist_lds - 1 sit in LDS: key row of
+    // position hb + 64 + j at kvx + j * rowb, value rows after the hist_lds key rows. Pass p >= 1
+    // of wave j covers share positions 64 p + 8 j + i (i < 8); the wave loads exactly those rows
+    // (direct-to-LDS, 1 KB = ppi rows per load, 16 bytes per lane) and is their only reader, so
+    // no barrier orders the loads: a wave waits for its own. Passes past the LDS rows load into
+    // registers when they run.
     const uint32_t hist_lds = g_tk.hist_lds;
     const uint32_t rowb = hd * esz, ppi = 1024u / rowb, lpp = 64u / ppi;
     uint8_t* kvk = lds<uint8_t>(g_tk.lds.kvx);
     uint8_t* kvv = kvk + hist_lds * rowb;
+    struct Geo {
+        uint32_t hist, t_first, hb, he;
+        bool chunked;
+    };
+    auto geo = [&](const Layer& Ly, uint32_t pos) {
+        Geo G;
+        G.hist = min(pos + 1u, Ly.slots);
+        G.t_first = pos + 1u - G.hist;
+        G.chunked = CH && G.hist > kHistMax + hist_lds;
+        const uint32_t cs = G.chunked ? (G.hist + ngrp - 1u) / ngrp : G.hist;
+        G.hb = G.chunked ? min(G.hist, grp * cs) : 0u;
+        G.he = min(G.hist, G.hb + cs);
+        return G;
+    };
     RowBatch<C::SB, 1, 1> orb;
     KvReg kr[kBPos], vr[kBPos];
-    // Wo rows of block l (head h's blocks) and this wave's cached key/value rows at position pos
-    auto load = [&](uint32_t l, uint32_t pos) {
-        const Layer& Ly = g_tk_layers[l];
-        const uint8_t* wo = Ly.wo + static_cast<uint64_t>(h) * nbh * 34u;
-        auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
-        batch_load<C::SB, 1, 1>(rowp, nbh, g_tk.arena_end, o0, o1, wave, kWaves, orb);
-        const uint32_t hist = min(pos + 1u, Ly.slots), t_first = pos + 1u - hist;
+    // this wave's eight rows of share positions b0 .. b0 + 7 from the cache (cached positions
+    // below he only: the others, and the current position, load zeros)
+    auto load_rows = [&](const Layer& Ly, const Geo& G, uint32_t b0) {
         const uint32_t kv_bytes = Ly.slots * hd * esz;
         const __amdgpu_buffer_rsrc_t rk = rsrc(Ly.kc, kv_bytes), rv = rsrc(Ly.vc, kv_bytes);
         const uint32_t lane_off = dlive ? dl * esz : 0x7ffffff0u;
 #pragma unroll
         for (uint32_t i = 0; i < kBPos; ++i) {
-            const uint32_t idx = kBPos * wave + i;     // cached positions only (the current one is hist - 1)
-            const uint32_t t = t_first + idx;
-            const int o = static_cast<int>(idx + 1u < hist ? (t % Ly.slots) * hd * esz + lane_off : 0x7ffffff0u);
+            const uint32_t idx = b0 + i;
+            const int o = static_cast<int>(idx < G.he && idx + 1u < G.hist ? ((G.t_first + idx) % Ly.slots) * hd * esz + lane_off
+                                                                            : 0x7ffffff0u);
             if constexpr (KVH) {
                 kr[i] = __builtin_amdgcn_raw_buffer_load_b64(rk, o, 0, kCoherent);
                 vr[i] = __builtin_amdgcn_raw_buffer_load_b64(rv, o, 0, kCoherent);
@@ -1549,14 +1574,24 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                 vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, kCoherent);
             }
         }
-        // the cached positions 64 .. past the registers (up to hist_lds of them); lanes past the
-        // last cached position repeat it into slots that are masked or hold the current position
-        const uint32_t ncached = min(hist - 1u, kHistMax + hist_lds);
-        for (uint32_t i0 = kHistMax + kBPos * wave; i0 < ncached; i0 += kHistMax) {
+    };
+    // Wo rows of block l (head h's blocks) and this wave's cached key/value rows at position pos
+    auto load = [&](uint32_t l, uint32_t pos) {
+        const Layer& Ly = g_tk_layers[l];
+        const uint8_t* wo = Ly.wo + static_cast<uint64_t>(h) * nbh * 34u;
+        auto rowp = [=](uint32_t v) { return wo + static_cast<uint64_t>(v) * rb_a; };
+        batch_load<C::SB, 1, 1>(rowp, nbh, g_tk.arena_end, o0, o1, wave, kWaves, orb);
+        const Geo G = geo(Ly, pos);
+        load_rows(Ly, G, G.hb + kBPos * wave);
+        // the cached share positions hb + 64 .. past the registers (up to hist_lds of them); lanes
+        // past the last one repeat it into slots that are masked or hold the current position
+        const uint32_t ncached = min(min(G.he, G.hist - 1u), G.hb + kHistMax + hist_lds);
+        const uint32_t t_first = G.t_first;
+        for (uint32_t i0 = G.hb + kHistMax + kBPos * wave; i0 < ncached; i0 += kHistMax) {
             for (uint32_t i = 0; i < kBPos && i0 + i < ncached; i += ppi) {
                 const uint32_t idx = min(i0 + i + lane / lpp, ncached - 1u);
                 const uint64_t go = static_cast<uint64_t>((t_first + idx) % Ly.slots) * rowb + (lane % lpp) * 16u;
-                const uint32_t so = (i0 + i - kHistMax) * rowb;
+                const uint32_t so = (i0 + i - G.hb - kHistMax) * rowb;
                 __builtin_amdgcn_global_load_lds((const TK_AS_GLOBAL void*)(reinterpret_cast<const uint8_t*>(Ly.kc) + go),
                                                  (__attribute__((address_space(3))) void*)(kvk + so), 16, 0, kCoherent);
                 __builtin_amdgcn_global_load_lds((const TK_AS_GLOBAL void*)(reinterpret_cast<const uint8_t*>(Ly.vc) + go),
@@ -1581,7 +1616,8 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
         const uint32_t pos = s;
         for (uint32_t l = 0; l < L && ok; ++l) {
             const Layer& Ly = g_tk_layers[l];
-            const uint32_t hist = min(pos + 1u, Ly.slots);
+            const Geo G = geo(Ly, pos);
+            const uint32_t hist = G.hist, he = G.he;
             const uint32_t tA = tagof(tagb, l, kTQkv);
             batch_prep<C::SB, 1, 1>(orb);
             int fail = 0;
@@ -1668,10 +1704,11 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
             }
             if (blk_any(fail, kAnyB)) { ok = false; break; }
             stamp(tr, l);
-            // this wave's positions: 8 wave + i < hist from the registers, then 64 p + 8 wave + i
-            // (p >= 1) from LDS; the current one, hist - 1, from kv_s
+            // this wave's share positions: hb + 8 wave + i from the registers, then hb + 64 p +
+            // 8 wave + i (p >= 1) from LDS or, past the LDS rows, loaded now; the current one,
+            // hist - 1, from kv_s
             const uint32_t ci = hist - 1u;
-            const bool has = kBPos * wave < hist;
+            const bool has = kBPos * wave < he - G.hb;
             if (has) {
                 const float4 q4 = dlive ? *reinterpret_cast<const float4*>(q_s + dl) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 const float q[4] = {q4.x, q4.y, q4.z, q4.w};
@@ -1691,8 +1728,9 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                         vc = v4u{__float_as_uint(v4.x), __float_as_uint(v4.y), __float_as_uint(v4.z), __float_as_uint(v4.w)};
                     }
                 }
-                if (ci / kBPos == wave) {   // the current position replaces register slot ci % 8
-                    const uint32_t cs = ci % kBPos;
+                // the current position replaces its register row (ci in this wave's first group)
+                if (ci >= G.hb + kBPos * wave && ci < G.hb + kBPos * wave + kBPos) {
+                    const uint32_t cs = ci - G.hb - kBPos * wave;
 #pragma unroll
                     for (uint32_t i = 0; i < kBPos; ++i)
                         if (i == cs) { kr[i] = kc; vr[i] = vc; }
@@ -1712,7 +1750,7 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                         sp[i] = p;
                     }
                     const float st = wave_sum8_t(sp);
-                    const float sl = b0 + pl < hist ? st * g_tk.attn_scale : -INFINITY;
+                    const float sl = b0 + pl < he ? st * g_tk.attn_scale : -INFINITY;
                     float mx = fmaxf(sl, dpp_mov<0xB1>(sl));
                     mx = fmaxf(mx, dpp_mov<0x4E>(mx));
                     mx = fmaxf(mx, dpp_mov<0x141>(mx));
@@ -1736,25 +1774,32 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                     wl = wl * alpha + ls;
                     wm = mn;
                 };
-                pass(kr, vr, kBPos * wave);
-                if (hist > kHistMax && hist_lds != 0u) {
+                pass(kr, vr, G.hb + kBPos * wave);
+                if (he - G.hb > kHistMax) {
                     __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's direct-to-LDS rows
                     const uint32_t lo_b = dlive ? dl * esz : 0u;
-                    // the LDS rows replace the register rows (consumed above; the next block's
-                    // are loaded after this block)
-                    for (uint32_t b0 = kHistMax + kBPos * wave; b0 < hist; b0 += kHistMax) {
+                    // the LDS rows (or the rows loaded now) replace the register rows (consumed
+                    // above; the next block's are loaded after this block)
+                    for (uint32_t b0 = G.hb + kHistMax + kBPos * wave; b0 < he; b0 += kHistMax) {
+                        const uint32_t j0 = b0 - G.hb - kHistMax;   // LDS row of the group's first position
+                        if (j0 < hist_lds) {
 #pragma unroll
-                        for (uint32_t i = 0; i < kBPos; ++i) {
-                            const uint32_t idx = b0 + i;
-                            const uint32_t so = min(idx - kHistMax, hist_lds - 1u) * rowb + lo_b;
-                            const KvReg kl = *reinterpret_cast<const KvReg*>(kvk + so);
-                            const KvReg vl = *reinterpret_cast<const KvReg*>(kvv + so);
-                            // slots past the history hold stale bytes: their scores are masked
-                            // (each position's score sums its own products only), and zero values
-                            // keep their weight-0 terms finite, as the registers' out-of-range
-                            // loads do
-                            kr[i] = idx == ci ? kc : kl;
-                            vr[i] = idx == ci ? vc : (idx < hist ? vl : KvReg{});
+                            for (uint32_t i = 0; i < kBPos; ++i) {
+                                const uint32_t so = (j0 + i) * rowb + lo_b;
+                                const KvReg kl = *reinterpret_cast<const KvReg*>(kvk + so);
+                                const KvReg vl = *reinterpret_cast<const KvReg*>(kvv + so);
+                                // rows past the share hold stale bytes: their scores are masked
+                                // (each position's score sums its own products only), and zero
+                                // values keep their weight-0 terms finite, as the registers'
+                                // out-of-range loads do
+                                kr[i] = b0 + i == ci ? kc : kl;
+                                vr[i] = b0 + i == ci ? vc : (b0 + i < he ? vl : KvReg{});
+                            }
+                        } else if constexpr (CH) {
+                            load_rows(Ly, G, b0);
+#pragma unroll
+                            for (uint32_t i = 0; i < kBPos; ++i)
+                                if (b0 + i == ci) { kr[i] = kc; vr[i] = vc; }
                         }
                         pass(kr, vr, b0);
                     }
@@ -1768,8 +1813,10 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
             submark(tr && l == 1u, 5);
             __syncthreads();
             submark(tr && l == 1u, 6);
-            // merge the waves in order: att = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j
-            const uint32_t nw = (hist + kBPos - 1u) / kBPos;
+            // merge the waves in order: sum_j e^(m_j - M) acc_j and sum_j e^(m_j - M) l_j over the
+            // waves that hold positions (none for an empty chunk: M = -inf, sums 0)
+            const uint32_t nw = (he - G.hb + kBPos - 1u) / kBPos;
+            float M = -INFINITY, num = 0.0f, den = 0.0f;
             if (tid < hd) {   // whole waves (head_dim is a multiple of 64)
                 float mj[kWaves], lj[kWaves], aj[kWaves];
 #pragma unroll
@@ -1779,16 +1826,75 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                     lj[j] = on ? part[kWaves * hd + kWaves + j] : 0.0f;
                     aj[j] = on ? part[j * hd + tid] : 0.0f;
                 }
-                float M = mj[0];
+                M = mj[0];
 #pragma unroll
                 for (uint32_t j = 1; j < kWaves; ++j) M = fmaxf(M, mj[j]);
-                float num = 0.0f, den = 0.0f;
 #pragma unroll
                 for (uint32_t j = 0; j < kWaves; ++j) {
                     const float f = j < nw ? __expf(mj[j] - M) : 0.0f;
                     num += f * aj[j];
                     den += f * lj[j];
                 }
+            }
+            if (CH && G.chunked) {
+                // the head's chunks: publish this one's {acc, M, l} (x_p[h][grp]), gather all
+                // ngrp, merge them in chunk order (the same bits in every workgroup of the head)
+                const uint32_t pst = hd + 8u;   // words per chunk partial (M, l at hd, hd + 1)
+                u64* xp = g_tk.x_p + static_cast<uint64_t>(h) * ngrp * pst;
+                const uint32_t tP = tagof(tagb, l, kTP);
+                if (tid < hd) {
+                    st_word(xp + grp * pst + tid, num, tP);
+                    if (tid == 0u) {
+                        st_word(xp + grp * pst + hd, M, tP);
+                        st_word(xp + grp * pst + hd + 1u, den, tP);
+                    }
+                }
+                float* cp = lds<float>(g_tk.lds.kvx);   // [ngrp][hd] acc, then [ngrp][2] M, l
+                const uint32_t upc = hd / 2u, nun = ngrp * upc;   // 16-byte units of the accumulators
+                const __amdgpu_buffer_rsrc_t rp = rsrc(xp, ngrp * pst * 8u);
+                int pfail;
+                {
+                    int off[kPartUnits + 1u];
+                    bool which[kPartUnits + 1u], live[kPartUnits + 1u];
+                    uint32_t tg[kPartUnits + 1u];
+#pragma unroll
+                    for (uint32_t k = 0; k < kPartUnits; ++k) {
+                        const uint32_t u = tid + kThreads * k, c = u / upc, j = u % upc;
+                        live[k] = u < nun;
+                        which[k] = false;
+                        tg[k] = tP;
+                        off[k] = static_cast<int>((c * pst + 2u * j) * 8u);
+                    }
+                    live[kPartUnits] = tid < ngrp;   // and chunk tid's M and l
+                    which[kPartUnits] = false;
+                    tg[kPartUnits] = tP;
+                    off[kPartUnits] = static_cast<int>((tid * pst + hd) * 8u);
+                    float pv[2u * (kPartUnits + 1u)];
+                    pfail = poll_units<kPartUnits + 1u>(rp, rp, off, which, live, tg, pv);
+#pragma unroll
+                    for (uint32_t k = 0; k < kPartUnits; ++k) {
+                        const uint32_t u = tid + kThreads * k, c = u / upc, j = u % upc;
+                        if (live[k]) *reinterpret_cast<float2*>(cp + c * hd + 2u * j) = make_float2(pv[2 * k], pv[2 * k + 1]);
+                    }
+                    if (live[kPartUnits])
+                        *reinterpret_cast<float2*>(cp + ngrp * hd + 2u * tid) =
+                            make_float2(pv[2 * kPartUnits], pv[2 * kPartUnits + 1]);
+                }
+                if (blk_any(pfail, kAnyB)) { ok = false; break; }
+                if (tid < hd) {
+                    float Mx = -INFINITY;
+                    for (uint32_t c = 0; c < ngrp; ++c) Mx = fmaxf(Mx, cp[ngrp * hd + 2u * c]);
+                    num = 0.0f;
+                    den = 0.0f;
+                    for (uint32_t c = 0; c < ngrp; ++c) {
+                        const float mc = cp[ngrp * hd + 2u * c];
+                        const float f = mc == -INFINITY ? 0.0f : __expf(mc - Mx);
+                        num += f * cp[c * hd + tid];
+                        den += f * cp[ngrp * hd + 2u * c + 1u];
+                    }
+                }
+            }
+            if (tid < hd) {
                 const float att = num * __builtin_amdgcn_rcpf(den);
                 if (tid == 0u && grp == 0u && (!(den > 0.0f) || !__builtin_isfinite(den))) flag_min(g3_code_softmax(l));   // :1666-1670
                 // activation limbs of the head's 32-element blocks (each one half of a wave)
@@ -2037,11 +2143,13 @@ __device__ __attribute__((always_inline)) void team_e(uint32_t nsteps, uint32_t 
     }
 }
 
-template <class C, typename KE>
+// CH: the variant for steps whose histories may exceed what a workgroup holds on chip (team B
+// then splits them into chunks per head); the other variant leaves that code out, for registers.
+template <class C, typename KE, bool CH>
 __global__ void __launch_bounds__(kThreads, 1) k_team(uint32_t nsteps, uint32_t tag0) {
     switch (team_of(blockIdx.x)) {
     case 0: team_a<C>(nsteps, tag0); break;
-    case 1: team_b<C, KE>(nsteps, tag0); break;
+    case 1: team_b<C, KE, CH>(nsteps, tag0); break;
     case 2: team_d<C>(nsteps, tag0); break;
     default: team_e<C>(nsteps, tag0); break;
     }
@@ -2054,9 +2162,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_team(uint32_t nsteps, uint32_t 
 // =============================================================================================
 
 struct TkFns {
-    const void* f32 = nullptr;
+    const void* f32 = nullptr;     // histories held on chip, per KV entry type
     const void* f16 = nullptr;
     const void* bf16 = nullptr;
+    const void* f32c = nullptr;    // and with chunked histories
+    const void* f16c = nullptr;
+    const void* bf16c = nullptr;
     uint32_t lm_blocks = 0;   // blocks per row of the matrix-core LM head (0: row-slot LM head)
 };
 
@@ -2069,14 +2180,20 @@ struct TkState {
     uint32_t trace_slots = 0;
     uint32_t pos_limit = 0;        // steps at positions below this run here
     uint32_t hist_lds[2] = {0, 0}; // LDS history rows past the registers: fp32, 16-bit entries
+    bool chunked = false;          // longer histories run as chunks per head (any position)
     bool registered = false;
     std::vector<void*> allocs;
 };
 
 template <class C>
 static TkFns tk_fn() {
-    return TkFns{reinterpret_cast<const void*>(&tk::k_team<C, float>), reinterpret_cast<const void*>(&tk::k_team<C, _Float16>),
-                 reinterpret_cast<const void*>(&tk::k_team<C, __bf16>), static_cast<uint32_t>(C::LMB)};
+    return TkFns{reinterpret_cast<const void*>(&tk::k_team<C, float, false>),
+                 reinterpret_cast<const void*>(&tk::k_team<C, _Float16, false>),
+                 reinterpret_cast<const void*>(&tk::k_team<C, __bf16, false>),
+                 reinterpret_cast<const void*>(&tk::k_team<C, float, true>),
+                 reinterpret_cast<const void*>(&tk::k_team<C, _Float16, true>),
+                 reinterpret_cast<const void*>(&tk::k_team<C, __bf16, true>),
+                 static_cast<uint32_t>(C::LMB)};
 }
 
 // Instantiated shapes: (d, heads x head_dim, FFN) -> row slots, passes and residual pairs.
@@ -2121,6 +2238,11 @@ void tk_destroy(vrt_g3* g) {
 }
 
 uint32_t tk_pos_limit(const vrt_g3* g) { return g->tk ? g->tk->pos_limit : 0u; }
+
+uint32_t tk_chunk_from(const vrt_g3* g) {
+    if (!g->tk) return 0u;
+    return g->tk->chunked ? tk::kHistMax + g->tk->P.hist_lds : g->tk->pos_limit;
+}
 
 int tk_setup(vrt_g3* g) {
     using namespace tk;
@@ -2241,6 +2363,8 @@ int tk_setup(vrt_g3* g) {
     P.x_d = static_cast<u64*>(p);
     if (int rc = tk_alloc(tk, st, kLine * nwg * 8u, &p)) return rc;
     P.x_am = static_cast<u64*>(p);
+    if (int rc = tk_alloc(tk, st, static_cast<size_t>(ts) * (hd + 8u) * 8u, &p)) return rc;
+    P.x_p = static_cast<u64*>(p);
     if (int rc = tk_alloc(tk, st, 64, &p)) return rc;
     P.abort_flag = static_cast<uint32_t*>(p);
     if (int rc = tk_alloc(tk, st, static_cast<size_t>(nwg) * tk->trace_slots * 8u, &p)) return rc;
@@ -2262,7 +2386,7 @@ int tk_setup(vrt_g3* g) {
     P.results = g->P.results;
     P.logits = g->P.logits;
     P.hidden = g->P.hidden;
-    for (const void* fn : {fns.f32, fns.f16, fns.bf16}) {
+    for (const void* fn : {fns.f32, fns.f16, fns.bf16, fns.f32c, fns.f16c, fns.bf16c}) {
         int per_cu = 0;
         VRT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0));
         if (per_cu < 1) { tk_destroy(g); return VRT_OK; }
@@ -2270,7 +2394,13 @@ int tk_setup(vrt_g3* g) {
     tk->fns = fns;
     tk->grid = nwg;
     P.hist_lds = tk->hist_lds[P.kv16 ? 1 : 0];
-    tk->pos_limit = std::min(c.context_length, kHistMax + P.hist_lds);
+    // longer histories split into ts / H chunks per head when a workgroup can gather a head's
+    // chunk partials (kPartUnits accumulator polls per thread, one more for M and l) and hold
+    // them in the LDS history rows
+    const uint32_t ngrp = ts / H;
+    tk->chunked = ngrp * (hd / 2u) <= kPartUnits * kThreads && ngrp <= kThreads &&
+                  P.lds.kvx + ngrp * (hd + 2u) * 4u <= kLdsBytes;
+    tk->pos_limit = tk->chunked ? c.context_length : std::min(c.context_length, kHistMax + P.hist_lds);
     g->tk_tag = 1u;
     {
         CoopSlot& ds = coop_slot(g->ctx->device);
@@ -2292,7 +2422,8 @@ int tk_set_kv_format(vrt_g3* g, uint32_t fmt) {
     if (!g->tk) return VRT_OK;
     g->tk->P.kv16 = fmt;
     g->tk->P.hist_lds = g->tk->hist_lds[fmt != 0u ? 1 : 0];
-    g->tk->pos_limit = std::min(g->cfg.context_length, tk::kHistMax + g->tk->P.hist_lds);
+    g->tk->pos_limit = g->tk->chunked ? g->cfg.context_length
+                                      : std::min(g->cfg.context_length, tk::kHistMax + g->tk->P.hist_lds);
     ++g->tk->version;
     return VRT_OK;
 }
@@ -2320,7 +2451,7 @@ int tk_clear_abort(vrt_g3* g) {
     return VRT_OK;
 }
 
-int tk_run(vrt_g3* g, uint32_t nsteps) {
+int tk_run(vrt_g3* g, uint32_t nsteps, bool chunked) {
     TkState* tk = g->tk;
     if (nsteps == 0) return VRT_OK;
     const uint32_t nph = tk::kTagsPerBlock * g->cfg.block_count + 1u;
@@ -2333,7 +2464,8 @@ int tk_run(vrt_g3* g, uint32_t nsteps) {
                         std::make_pair(static_cast<void*>(P.x_o), tk::kMaxHeads * P.d),
                         std::make_pair(static_cast<void*>(P.x_hm), P.d), std::make_pair(static_cast<void*>(P.x_g), P.F),
                         std::make_pair(static_cast<void*>(P.x_d), P.d),
-                        std::make_pair(static_cast<void*>(P.x_am), tk::kLine * tk->grid)})
+                        std::make_pair(static_cast<void*>(P.x_am), tk::kLine * tk->grid),
+                        std::make_pair(static_cast<void*>(P.x_p), P.tsize * (P.hd + 8u))})
             VRT_HIP_CHECK(hipMemsetAsync(pr.first, 0, static_cast<size_t>(pr.second) * 8u, g->ctx->stream));
         VRT_HIP_CHECK(hipStreamSynchronize(g->ctx->stream));
         g->tk_tag = 1u;
@@ -2351,7 +2483,10 @@ int tk_run(vrt_g3* g, uint32_t nsteps) {
         ds.version[kCoopTeam] = tk->version;
     }
     void* args[] = {&nsteps, &tag0};
-    const hipError_t le = hipLaunchCooperativeKernel(tk->P.kv16 == 2u ? tk->fns.bf16 : (tk->P.kv16 ? tk->fns.f16 : tk->fns.f32), dim3(tk->grid),
+    const TkFns& F = tk->fns;
+    const void* fn = tk->P.kv16 == 2u ? (chunked ? F.bf16c : F.bf16)
+                                      : (tk->P.kv16 ? (chunked ? F.f16c : F.f16) : (chunked ? F.f32c : F.f32));
+    const hipError_t le = hipLaunchCooperativeKernel(fn, dim3(tk->grid),
                                                      dim3(tk::kThreads), args, 0, stream);
     if (le == hipErrorIllegalState || le == hipErrorCooperativeLaunchTooLarge) {
         (void)hipGetLastError();
