@@ -85,6 +85,7 @@ constexpr uint32_t kBPos = 8;               // attention positions per wave
 constexpr uint32_t kHistMax = kWaves * kBPos;   // longest history (positions) a block can attend to
 constexpr uint32_t kMaxHeads = 4;           // query heads (partials summed by team D)
 constexpr uint32_t kPartUnits = 4;          // 16-byte polls per thread of a head's chunk accumulators
+constexpr uint32_t kMaxTeamChunks = 64;     // history chunks per head (one lane of a wave each)
 constexpr uint32_t kLmUnits = 3;            // 16-byte LM-head loads per thread per tile
 constexpr uint32_t kLmRing = 4;             // LM-head tile slots in LDS
 constexpr uint32_t kLmAhead = kLmRing - 1u; // tiles in flight while one is computed
@@ -1849,6 +1850,7 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                         st_word(xp + grp * pst + hd + 1u, den, tP);
                     }
                 }
+                submark(tr && l == 1u, 3);
                 float* cp = lds<float>(g_tk.lds.kvx);   // [ngrp][hd] acc, then [ngrp][2] M, l
                 const uint32_t upc = hd / 2u, nun = ngrp * upc;   // 16-byte units of the accumulators
                 const __amdgpu_buffer_rsrc_t rp = rsrc(xp, ngrp * pst * 8u);
@@ -1881,16 +1883,34 @@ __device__ __attribute__((always_inline)) void team_b(uint32_t nsteps, uint32_t 
                             make_float2(pv[2 * kPartUnits], pv[2 * kPartUnits + 1]);
                 }
                 if (blk_any(pfail, kAnyB)) { ok = false; break; }
+                submark(tr && l == 1u, 4);
                 if (tid < hd) {
-                    float Mx = -INFINITY;
-                    for (uint32_t c = 0; c < ngrp; ++c) Mx = fmaxf(Mx, cp[ngrp * hd + 2u * c]);
+                    // chunk weights: lane c holds chunk c's max, weight e^(M_c - M) and l_c
+                    const bool cl = lane < ngrp;
+                    const float2 ml = cl ? *reinterpret_cast<const float2*>(cp + ngrp * hd + 2u * lane) : make_float2(-INFINITY, 0.0f);
+                    const float Mx = wave_max(ml.x);
+                    const float f = ml.x == -INFINITY ? 0.0f : __expf(ml.x - Mx);
+                    const float fl = f * ml.y;
+                    // sums in chunk order, four accumulator rows loaded together
                     num = 0.0f;
                     den = 0.0f;
-                    for (uint32_t c = 0; c < ngrp; ++c) {
-                        const float mc = cp[ngrp * hd + 2u * c];
-                        const float f = mc == -INFINITY ? 0.0f : __expf(mc - Mx);
-                        num += f * cp[c * hd + tid];
-                        den += f * cp[ngrp * hd + 2u * c + 1u];
+                    auto fc = [&](float v, uint32_t c) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), c)); };
+                    uint32_t c = 0;
+                    for (; c + 4u <= ngrp; c += 4u) {
+                        const float a0 = cp[c * hd + tid], a1 = cp[(c + 1u) * hd + tid];
+                        const float a2 = cp[(c + 2u) * hd + tid], a3 = cp[(c + 3u) * hd + tid];
+                        num += fc(f, c) * a0;
+                        num += fc(f, c + 1u) * a1;
+                        num += fc(f, c + 2u) * a2;
+                        num += fc(f, c + 3u) * a3;
+                        den += fc(fl, c);
+                        den += fc(fl, c + 1u);
+                        den += fc(fl, c + 2u);
+                        den += fc(fl, c + 3u);
+                    }
+                    for (; c < ngrp; ++c) {
+                        num += fc(f, c) * cp[c * hd + tid];
+                        den += fc(fl, c);
                     }
                 }
             }
@@ -2398,7 +2418,7 @@ int tk_setup(vrt_g3* g) {
     // chunk partials (kPartUnits accumulator polls per thread, one more for M and l) and hold
     // them in the LDS history rows
     const uint32_t ngrp = ts / H;
-    tk->chunked = ngrp * (hd / 2u) <= kPartUnits * kThreads && ngrp <= kThreads &&
+    tk->chunked = ngrp * (hd / 2u) <= kPartUnits * kThreads && ngrp <= kMaxTeamChunks &&
                   P.lds.kvx + ngrp * (hd + 2u) * 4u <= kLdsBytes;
     tk->pos_limit = tk->chunked ? c.context_length : std::min(c.context_length, kHistMax + P.hist_lds);
     g->tk_tag = 1u;
