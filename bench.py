@@ -9,13 +9,12 @@ prompt is prefilled first (untimed); --steps decode steps at positions 8, 9, ...
 with hipEvents on the library's stream. Inputs are resident in HBM before timing.
 
 The whole decode loop is one persistent kernel: a cooperative launch with one workgroup per CU
-that runs every block, the LM head and argmax for each of the launch's steps. Positions below
-the team kernel's limit (136 with fp32 KV at this shape: histories of up to 64 positions in
-registers and 72 in LDS) run on k_team (four teams of workgroups, each running one phase type of
-every block); later positions on k_decode (every workgroup in every phase). With the default
-8-token prompt and up to 128 steps the timed region is exactly one k_team launch, so the
-roofline's launch duration is the event-timed region itself; longer runs time one k_team and one
-k_decode launch together.
+that runs every block, the LM head and argmax for each of the launch's steps. At this shape every
+position runs on k_team (four teams of workgroups, each running one phase type of every block):
+its on-chip variant while a head's history fits in a workgroup (136 positions with fp32 KV: 64
+in registers and 72 in LDS), its chunked variant after that. With the default 8-token prompt and
+up to 128 steps the timed region is exactly one k_team launch, so the roofline's launch duration
+is the event-timed region itself; longer runs time two launches together.
 
 Algorithmic bytes per step at position p: every Q8_0 weight byte, the fp32 norm weights, one
 embedding row, plus the fp32 KV rows attention reads (min(p+1, window) positions for local
@@ -344,8 +343,12 @@ def roofline_kernel(g, cfg, first: int, steps: int) -> str:
     per = f"{cfg.block_count} blocks + tied LM head + argmax per step"
     last = first + steps - 1
     limit = g.team_positions() if g.team_available() else 0
-    if last < limit:
+    chunked = min(g.team_chunked_from(), limit) if limit else 0
+    if last < limit and (last < chunked or first >= chunked):
         return f"k_team (phase-team persistent kernel: {per}, {steps} steps per launch)"
+    if last < limit:
+        return (f"k_team for positions {first}..{chunked - 1}, then its chunked-history variant for "
+                f"{chunked}..{last}: {per}")
     if first < limit:
         return (f"k_team for positions {first}..{limit - 1}, then k_decode (all-workgroup persistent "
                 f"kernel) for {limit}..{last}: {per}")

@@ -261,8 +261,9 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
  * results to the stated tolerances. VRT_G3_OPT_QUERY_TEAM returns VRT_OK when the team kernel
  * is available for the shape and device (value ignored). VRT_G3_OPT_QUERY_TEAM_POSITIONS (read
  * with vrt_g3_get_option) gives the position below which steps run on the team kernel (0 when it
- * is unavailable): 136 at the Gemma-3-270M shape with fp32 KV entries, 208 with fp16 ones. No
- * reference counterpart. */
+ * is unavailable): the context length at the shapes it is built for, where histories longer
+ * than a workgroup holds on chip (136 positions of fp32 KV entries at the Gemma-3-270M shape, 208
+ * of 16-bit ones) split into chunks per head. No reference counterpart. */
 #define VRT_G3_OPT_TEAM 6
 #define VRT_G3_OPT_QUERY_TEAM 7
 /* Projection fusion and the Q8 lane policy (Gemma3Model::set_projection_fusion_enabled and the
@@ -281,6 +282,10 @@ int vrt_g3_forced(vrt_g3* g3, const uint32_t* tokens, uint32_t n, uint32_t first
 #define VRT_G3_OPT_Q8_LANES 9
 #define VRT_G3_OPT_QUERY_Q8_LANES 10
 #define VRT_G3_OPT_QUERY_TEAM_POSITIONS 11
+/* Read with vrt_g3_get_option: the position from which team-kernel steps run its chunked
+ * variant (histories split across a head's workgroups); equal to QUERY_TEAM_POSITIONS when the
+ * shape has none. Each variant is its own launch. */
+#define VRT_G3_OPT_QUERY_TEAM_CHUNKED 13
 
 /* Phase trace of the last persistent launch (tracing tool; no reference counterpart, which
  * only has CLI wall timers, src/gemma_main.cpp:194-232): out[w * slots + k] is the
@@ -300,7 +305,7 @@ int vrt_g3_read_trace(vrt_g3* g3, uint64_t* out, uint64_t cap, uint32_t* nwg, ui
 int vrt_g3_read_exchange(vrt_g3* g3, uint32_t which, uint64_t* out, uint64_t cap, uint64_t* n);
 int vrt_g3_set_option(vrt_g3* g3, uint32_t option, uint32_t value);
 /* Current value of an executor option: USE_GRAPH, PERSISTENT, TEAM, KV_F16, KV_BF16, FUSION and Q8_LANES
- * as last set, QUERY_Q8_LANES and QUERY_TEAM_POSITIONS as described above (the getters projection_fusion_enabled and
+ * as last set, QUERY_Q8_LANES, QUERY_TEAM_POSITIONS and QUERY_TEAM_CHUNKED as described above (the getters projection_fusion_enabled and
  * narrow_q8_lane_count of include/vortexrt/gemma3.hpp read these). */
 int vrt_g3_get_option(vrt_g3* g3, uint32_t option, uint32_t* value);
 

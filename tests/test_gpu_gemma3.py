@@ -276,6 +276,7 @@ def test_team_kernel_history_modes_full_shape(ctx, full_model):
         for fmt, switch in (("f32", 136), ("f16", 208), ("bf16", 208)):
             g.set_kv_format(fmt)
             assert g.team_positions() == int(g.config.context_length), (fmt, g.team_positions())
+            assert g.team_chunked_from() == switch, (fmt, g.team_chunked_from())
             toks = synth.uniform_ids(94, switch + 12, 2, 262144)
             print(f"[g3] full shape, {toks.size} forced steps, {fmt} KV, team on/off", flush=True)
             g.set_team(True)

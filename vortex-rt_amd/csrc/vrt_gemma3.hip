@@ -1183,6 +1183,8 @@ extern "C" int vrt_g3_set_option(vrt_g3* g, uint32_t option, uint32_t value) {
     case VRT_G3_OPT_QUERY_Q8_LANES: return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_Q8_LANES is read with vrt_g3_get_option");
     case VRT_G3_OPT_QUERY_TEAM_POSITIONS:
         return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_TEAM_POSITIONS is read with vrt_g3_get_option");
+    case VRT_G3_OPT_QUERY_TEAM_CHUNKED:
+        return set_error(VRT_ERR_INVALID, "VRT_G3_OPT_QUERY_TEAM_CHUNKED is read with vrt_g3_get_option");
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
     }
 }
@@ -1203,6 +1205,7 @@ extern "C" int vrt_g3_get_option(vrt_g3* g, uint32_t option, uint32_t* value) {
         *value = g->ld_qkv.S;
         return VRT_OK;
     case VRT_G3_OPT_QUERY_TEAM_POSITIONS: *value = tk_pos_limit(g); return VRT_OK;
+    case VRT_G3_OPT_QUERY_TEAM_CHUNKED: *value = tk_chunk_from(g); return VRT_OK;
     default: return set_error(VRT_ERR_INVALID, "unknown executor option %u", option);
     }
 }

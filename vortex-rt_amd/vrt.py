@@ -28,6 +28,7 @@ OPT_FUSION = 8
 OPT_Q8_LANES = 9
 OPT_QUERY_Q8_LANES = 10
 OPT_QUERY_TEAM_POSITIONS = 11
+OPT_QUERY_TEAM_CHUNKED = 13
 
 
 class VrtError(RuntimeError):
@@ -396,6 +397,10 @@ class Gemma3:
     def team_positions(self) -> int:
         """Steps at positions below this run on the team kernel (0: unavailable)."""
         return self.get_option(OPT_QUERY_TEAM_POSITIONS)
+
+    def team_chunked_from(self) -> int:
+        """Team-kernel steps from this position on run its chunked-history variant."""
+        return self.get_option(OPT_QUERY_TEAM_CHUNKED)
 
     def set_trace(self, on: bool):
         check(lib().vrt_g3_set_option(self.h, OPT_TRACE, 1 if on else 0))
