@@ -370,9 +370,9 @@ def main():
     ap.add_argument("--multikernel", action="store_true",
                     help="also time the multi-kernel (hipGraph) decode path")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (B sequences) measurement")
-    ap.add_argument("--only", choices=("prefill", "prefill_8192", "batched", "kernels"),
-                    help="run only this leg and print it (no decode timing, so no cooperative launch: for "
-                         "profiling one leg at a time)")
+    ap.add_argument("--only", choices=("prefill", "prefill_8192", "batched", "kernels", "long_context"),
+                    help="run only this leg and print it (for profiling one leg at a time; all but "
+                         "long_context make no cooperative launch)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the PMC calibration dispatch) and exit")
     ap.add_argument("--model", default=os.environ.get("VRT_BENCH_MODEL", "/tmp/vrt_bench/gemma3_270m_q8_seed0.gguf"))
@@ -401,7 +401,8 @@ def main():
         legs = {"prefill": lambda: prefill_bench(ctx, g, cfg),
                 "prefill_8192": lambda: prefill_bench(ctx, g, cfg, T=8192, reps=3),
                 "batched": lambda: batched_leg(ctx, g, cfg),
-                "kernels": lambda: kernel_legs(ctx)}
+                "kernels": lambda: kernel_legs(ctx),
+                "long_context": lambda: long_context(ctx, g, cfg)}
         res = legs[args.only]()
         g.close()
         ctx.close()
