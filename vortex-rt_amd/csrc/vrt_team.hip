@@ -90,9 +90,11 @@ constexpr uint32_t kLmUnits = 3;            // 16-byte LM-head loads per thread 
 constexpr uint32_t kLmRing = 4;             // LM-head tile slots in LDS
 constexpr uint32_t kLmAhead = kLmRing - 1u; // tiles in flight while one is computed
 constexpr uint32_t kLmTileBytes = kLmUnits * kThreads * 16u;
-// matrix-core LM head: every wave streams its own 8-row tiles through a ring of its own
-constexpr uint32_t kLmWaveRows = 8;
-constexpr uint32_t kLmWaveLoads = 6;        // 1 KB direct-to-LDS loads per wave tile
+// matrix-core LM head: each of the first kLmWaves waves streams its own 16-row tiles through a
+// ring of its own
+constexpr uint32_t kLmWaves = 4;
+constexpr uint32_t kLmWaveRows = 16;
+constexpr uint32_t kLmWaveLoads = 11;       // 1 KB direct-to-LDS loads per wave tile
 constexpr uint32_t kLmWaveSlot = kLmWaveLoads * 1024u;
 constexpr uint32_t kLmWaveRing = 3;         // slots per wave: two tiles in flight while one is computed
 constexpr uint32_t kLdsBytes = 159u * 1024u;
@@ -643,12 +645,13 @@ __device__ __forceinline__ bool final_fold(uint32_t tagb, const FoldW& fw) {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// The tied LM head on the matrix cores (v_mfma_i32_16x16x32_i8) for rows of NB Q8_0 blocks. Every
-// wave streams its own tiles of 8 rows (rows (w + i nwg) * 64 + 8 wave ..) into a ring of its own
-// with direct-to-LDS loads, so the loop has no workgroup barrier: a wave waits only for its own
-// loads. For block j the A operand holds the activation limbs block-diagonally: row m = 4 q + t of
-// A is limb t (t < 3) of x's block j when q = j % 4, and zero otherwise; the B operand is the 32
-// quants of row n & 7 (lane n + 16 g: quants 8 g .. 8 g + 7; columns 8-15 repeat rows 0-7). After
+// The tied LM head on the matrix cores (v_mfma_i32_16x16x32_i8) for rows of NB Q8_0 blocks. Each of
+// waves 0 .. kLmWaves - 1 streams its own tiles of 16 rows (rows (w + i nwg) * 64 + 16 wave ..) into
+// a ring of its own with direct-to-LDS loads, so the loop has no workgroup barrier: a wave waits
+// only for its own loads (the other waves only join the argmax). For block j the A operand holds
+// the activation limbs block-diagonally: row m = 4 q + t of A is limb t (t < 3) of x's block j when
+// q = j % 4, and zero otherwise; the B operand is the 32 quants of row n (lane n + 16 g: quants
+// 8 g .. 8 g + 7), so one product covers the tile's 16 rows. After
 // the blocks of group G (4G .. 4G + 3), C[4 q + t][n] is the limb-t dot product of block 4G + q
 // with row n, held by lane n + 16 q, which combines the three limb products as q8_dot does and
 // scales them by the block scales; the four lanes of a row then add their groups' sums.
@@ -657,14 +660,14 @@ __device__ __forceinline__ bool lm_waves(uint32_t tagb, uint32_t want_logits, bo
                                          uint32_t& bi) {
 #pragma clang fp contract(off)
     constexpr uint32_t NG = (NB + 3) / 4;
-    constexpr uint32_t kRound = kWaves * kLmWaveRows;   // rows per workgroup round
+    constexpr uint32_t kRound = kLmWaves * kLmWaveRows;   // rows per workgroup round
     const uint32_t w = blockIdx.x, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u, grp = lane >> 4;
     const uint32_t nwg = g_tk.nwg, V = g_tk.V;
     const uint32_t rb = static_cast<uint32_t>(NB) * 34u;
     const uint64_t first = static_cast<uint64_t>(w) * kRound + wave * kLmWaveRows;
     const uint64_t stride = static_cast<uint64_t>(kRound) * nwg;
-    const uint32_t nt = first < V ? static_cast<uint32_t>((V - first + stride - 1u) / stride) : 0u;
+    const uint32_t nt = wave < kLmWaves && first < V ? static_cast<uint32_t>((V - first + stride - 1u) / stride) : 0u;
     auto row0 = [&](uint32_t i) { return static_cast<uint32_t>(first + static_cast<uint64_t>(i) * stride); };
     uint8_t* ring = lds<uint8_t>(g_tk.lds.ring) + wave * (kLmWaveRing * kLmWaveSlot);
     auto slot = [&](uint32_t i) { return ring + (i % kLmWaveRing) * kLmWaveSlot; };
@@ -713,7 +716,7 @@ __device__ __forceinline__ bool lm_waves(uint32_t tagb, uint32_t want_logits, bo
         const uint32_t r0 = row0(i);
         const uint8_t* tile = slot(i);
         const uint32_t pre = static_cast<uint32_t>((reinterpret_cast<uintptr_t>(g_tk.tok_embd) + static_cast<uint64_t>(r0) * rb) & 15u);
-        const uint32_t rbase = pre + (n & 7u) * rb;
+        const uint32_t rbase = pre + (n % kLmWaveRows) * rb;
         v4i acc[NG];
 #pragma unroll
         for (uint32_t G = 0; G < NG; ++G) acc[G] = v4i{0, 0, 0, 0};
@@ -2359,7 +2362,7 @@ int tk_setup(vrt_g3* g) {
     off = std::max(end_ad, P.lds.kvx);
     if (fns.lm_blocks != 0u) {   // per-wave rings of 8-row tiles
         if (fns.lm_blocks != d / 32u || kLmWaveRows * rb + 16u > kLmWaveSlot) { tk_destroy(g); return VRT_OK; }
-        off = std::max(off, blk0 + kWaves * kLmWaveRing * kLmWaveSlot);
+        off = std::max(off, blk0 + kLmWaves * kLmWaveRing * kLmWaveSlot);
     } else {
         off = std::max(off, blk0 + kLmRing * kLmTileBytes);
     }
