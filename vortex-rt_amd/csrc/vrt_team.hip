@@ -2360,7 +2360,7 @@ int tk_setup(vrt_g3* g) {
         tk->hist_lds[f] = 1024u % rowb == 0u && P.lds.kvx < kLdsBytes ? (kLdsBytes - P.lds.kvx) / (2u * rowb) / 8u * 8u : 0u;
     }
     off = std::max(end_ad, P.lds.kvx);
-    if (fns.lm_blocks != 0u) {   // per-wave rings of 8-row tiles
+    if (fns.lm_blocks != 0u) {   // per-wave rings of 16-row tiles (waves 0 .. kLmWaves - 1)
         if (fns.lm_blocks != d / 32u || kLmWaveRows * rb + 16u > kLmWaveSlot) { tk_destroy(g); return VRT_OK; }
         off = std::max(off, blk0 + kLmWaves * kLmWaveRing * kLmWaveSlot);
     } else {
