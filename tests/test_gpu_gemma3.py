@@ -289,6 +289,34 @@ def test_team_kernel_history_modes_full_shape(ctx, full_model):
         g.close()
 
 
+RAGGED_VOCAB = dict(synth.GEMMA3_270M, n_layers=3, vocab=4099, context=512)
+
+
+def test_team_lm_head_ragged_vocab(ctx, model_dir):
+    """The team kernel's LM head at the 270M block width streams the table in 16-row tiles, each
+    wave its own. With 4099 rows the last tile holds 3 rows, and most workgroups have no tile.
+    Teacher-forced over 40 positions against the oracle: the greedy token, every logit and the
+    hidden state of each step."""
+    path = os.path.join(str(model_dir), "ragged_vocab.gguf")
+    if not os.path.exists(path):
+        synth.write_gemma3_gguf(path, seed=33, **RAGGED_VOCAB)
+    toks = synth.uniform_ids(35, 40, 2, RAGGED_VOCAB["vocab"])
+    g = vrt.Gemma3(ctx, path)
+    m = oracle.Model(path)
+    try:
+        assert g.team_available(), "team kernel not built for the 270M block width"
+        print(f"[g3] ragged vocabulary ({RAGGED_VOCAB['vocab']} rows), {toks.size} forced steps", flush=True)
+        for i, t in enumerate(toks):
+            r = m.decode(int(t), i, want_logits=True, logits=True)
+            (idx, _), hid = g.decode(int(t), i, top_k=8, hidden=True)
+            assert idx == r["index"], f"step {i}: gpu {idx} oracle {r['index']}"
+            assert _rel(g.logits(), r["logits"]) <= LOGIT_TOL, f"step {i}"
+            assert _rel(hid, r["hidden"]) <= HIDDEN_TOL, f"step {i}"
+    finally:
+        m.close()
+        g.close()
+
+
 def test_team_phase_trace(ctx, tiny_model):
     """The team kernel's phase trace of a launch whose first step runs the LM head: every
     workgroup stamps its team's input and publish of every block in order, the final norm and
