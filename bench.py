@@ -19,6 +19,11 @@ is the event-timed region itself; longer runs time two launches together.
 Algorithmic bytes per step at position p: every Q8_0 weight byte, the fp32 norm weights, one
 embedding row, plus the fp32 KV rows attention reads (min(p+1, window) positions for local
 blocks, p+1 for global ones), each counted once.
+
+The line also carries the long-context legs (an 8192-token prompt, then 256 timed steps) with
+fp32, fp16 and bf16 KV entries, the 512- and 8192-token prefills, batched decode at 1-64
+sequences, the standalone kernels and the oracle's CPU rate; --no-* switches each one off and
+--only runs a single leg.
 """
 import argparse
 import json
@@ -113,16 +118,16 @@ def phase_split(g, prompt, cfg, steps: int = 24):
     return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in out.items()}
 
 
-def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256, kv_f16: bool = False):
+def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256, kv: str = "f32"):
     """The long-context workload: an n_prompt-token prompt of uniform ids (seed 1) prefilled
-    untimed, then `steps` greedy decode steps timed with events (positions n_prompt..). With
-    kv_f16 the executor's KV cache holds fp16 entries (2 bytes per element)."""
-    if kv_f16:
-        g.set_kv_f16(True)
+    untimed, then `steps` greedy decode steps timed with events (positions n_prompt..). kv is
+    the KV cache's entry type: "f32", or "f16" / "bf16" (2 bytes per element)."""
+    if kv != "f32":
+        g.set_kv_format(kv)
         try:
             return long_context(ctx, g, cfg, n_prompt, steps)
         finally:
-            g.set_kv_f16(False)
+            g.set_kv_format("f32")
     prompt = synth_ids(1, n_prompt, cfg.vocab_size)
     g.start(prompt, steps + 1)
     g.step(n_prompt)
@@ -136,7 +141,7 @@ def long_context(ctx, g, cfg, n_prompt: int = 8192, steps: int = 256, kv_f16: bo
     toks = g.collect()
     if toks.size < steps + 1:
         raise SystemExit(f"[bench] long context: EOS after {toks.size} generated tokens; the timed steps did not all run")
-    kvb = 2 if g.kv_f16 else 4
+    kvb = 4 if g.kv_format() == "f32" else 2
     total = sum(step_bytes(cfg, n_prompt + i, kvb) for i in range(steps))
     gbps = total / (ms / 1e3) / 1e9
     return {"workload": f"{n_prompt}-token prompt (untimed prefill), {steps} timed greedy decode steps at positions "
@@ -448,7 +453,8 @@ def main():
     traffic, traffic_src = load_traffic(args.steps, single) if single else (None, None)
     phases = None if args.no_phases else phase_split(g, prompt, cfg)
     longctx = None if args.no_long else long_context(ctx, g, cfg)
-    longctx16 = None if args.no_long else long_context(ctx, g, cfg, kv_f16=True)
+    longctx16 = None if args.no_long else long_context(ctx, g, cfg, kv="f16")
+    longctxbf16 = None if args.no_long else long_context(ctx, g, cfg, kv="bf16")
     prefill = None if args.no_prefill else prefill_bench(ctx, g, cfg)
     prefill_long = None if args.no_prefill else prefill_bench(ctx, g, cfg, T=8192, reps=3)
     kernels = None if args.no_kernels else kernel_legs(ctx)
@@ -493,6 +499,7 @@ def main():
         "phase_us_per_step": phases,
         "long_context": longctx,
         "long_context_kv_f16": longctx16,
+        "long_context_kv_bf16": longctxbf16,
         "prefill": prefill,
         "prefill_8192": prefill_long,
         "kernels": kernels,
