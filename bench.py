@@ -347,7 +347,7 @@ def roofline_kernel(g, cfg, first: int, steps: int) -> str:
     (steps below g.team_positions() run on the team kernel, VRT_G3_OPT_QUERY_TEAM_POSITIONS)."""
     per = f"{cfg.block_count} blocks + tied LM head + argmax per step"
     last = first + steps - 1
-    limit = g.team_positions() if g.team_available() else 0
+    limit = g.team_positions() if g.team_available() and g.team_enabled() else 0
     chunked = min(g.team_chunked_from(), limit) if limit else 0
     if last < limit and (last < chunked or first >= chunked):
         return f"k_team (phase-team persistent kernel: {per}, {steps} steps per launch)"
@@ -375,6 +375,8 @@ def main():
     ap.add_argument("--multikernel", action="store_true",
                     help="also time the multi-kernel (hipGraph) decode path")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-decode (B sequences) measurement")
+    ap.add_argument("--no-team", action="store_true",
+                    help="decode on the all-workgroup persistent kernel k_decode (the team kernel switched off)")
     ap.add_argument("--only", choices=("prefill", "prefill_8192", "batched", "kernels", "long_context"),
                     help="run only this leg and print it (for profiling one leg at a time; all but "
                          "long_context make no cooperative launch)")
@@ -402,6 +404,8 @@ def main():
     ctx = vrt.Context("")
     g = vrt.Gemma3(ctx, args.model)
     cfg = g.config
+    if args.no_team:
+        g.set_team(False)
     if args.only:
         legs = {"prefill": lambda: prefill_bench(ctx, g, cfg),
                 "prefill_8192": lambda: prefill_bench(ctx, g, cfg, T=8192, reps=3),

@@ -394,6 +394,10 @@ class Gemma3:
     def team_available(self) -> bool:
         return lib().vrt_g3_set_option(self.h, OPT_QUERY_TEAM, 0) == VRT_OK
 
+    def team_enabled(self) -> bool:
+        """Whether steps may run on the team kernel (set_team; it runs them when also available)."""
+        return bool(self.get_option(OPT_TEAM))
+
     def team_positions(self) -> int:
         """Steps at positions below this run on the team kernel (0: unavailable)."""
         return self.get_option(OPT_QUERY_TEAM_POSITIONS)
